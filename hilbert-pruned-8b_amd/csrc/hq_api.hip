@@ -1,0 +1,431 @@
+// hq_api.hip - C ABI of the gfx950 quantized matmul path (include/hq.h): weight residency,
+// argument checking and kernel dispatch. Every entry point validates shapes, alignment and ids on
+// the host before a kernel is launched, so no launch can read or write outside its buffers.
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <vector>
+
+#include "hq.h"
+#include "hq_llama.h"
+#include "hq_internal.h"
+#include "hq_kernels.h"
+
+struct hq_mat {
+    hq_dev_mat m;
+    int device;
+    void *alloc;
+    size_t bytes;
+};
+
+// ------------------------------------------------------------------------------------ errors
+static thread_local char g_err[512] = "";
+
+static int fail(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return -1;
+}
+
+#define HIPCK(call)                                                                                         \
+    do {                                                                                                    \
+        hipError_t e_ = (call);                                                                             \
+        if (e_ != hipSuccess) return fail("HIP %s failed: %s (%s:%d)", #call, hipGetErrorString(e_), __FILE__, \
+                                          __LINE__);                                                        \
+    } while (0)
+
+extern "C" const char *hq_last_error(void) { return g_err; }
+
+extern "C" int hq_internal_fail(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return -1;
+}
+
+// ------------------------------------------------------------------------------------ device
+static int use_device(int device) {
+    int cur = -1;
+    HIPCK(hipGetDevice(&cur));
+    if (cur != device) HIPCK(hipSetDevice(device));
+    return 0;
+}
+
+extern "C" int hq_device_count(int *count) {
+    HIPCK(hipGetDeviceCount(count));
+    return 0;
+}
+
+extern "C" int hq_device_name(int device, char *name, size_t name_len, char *arch, size_t arch_len) {
+    hipDeviceProp_t p;
+    HIPCK(hipGetDeviceProperties(&p, device));
+    if (name && name_len) snprintf(name, name_len, "%s", p.name);
+    if (arch && arch_len) snprintf(arch, arch_len, "%s", p.gcnArchName);
+    return 0;
+}
+
+extern "C" int hq_device_init(int device) {
+    int n = 0;
+    HIPCK(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) return fail("hq: device %d not found (%d visible)", device, n);
+    HIPCK(hipSetDevice(device));
+    hipDeviceProp_t p;
+    HIPCK(hipGetDeviceProperties(&p, device));
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
+        return fail("hq: device %d is %s; this library is built for gfx950 (MI355X)", device, p.gcnArchName);
+    return 0;
+}
+
+// ------------------------------------------------------------------------------------ residency
+static uint32_t block_values(int t) { return t == HQ_GGML_Q8_0 ? 32u : t == HQ_GGML_Q4_K ? 256u : 0u; }
+static uint32_t block_bytes(int t) { return t == HQ_GGML_Q8_0 ? 34u : t == HQ_GGML_Q4_K ? 144u : 0u; }
+
+// Storage row of Hugging Face row r (llama.cpp q/k interleave; reference src/model.c:283-289).
+static uint32_t storage_row(uint32_t rows, uint32_t perm_heads, uint32_t r) {
+    if (!perm_heads) return r;
+    const uint32_t hd = rows / perm_heads, half = hd / 2, within = r % hd;
+    return (r - within) + 2 * (within % half) + within / half;
+}
+
+static size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+extern "C" int hq_mat_upload(const hq_wmat_t *w, int device, hq_mat **out) {
+    *out = nullptr;
+    if (!w || !w->data) return fail("hq_mat_upload: no matrix");
+    if (w->dtype != HQ_DT_GGML) return fail("hq_mat_upload: dtype %d is not a GGUF block type", w->dtype);
+    const uint32_t per = block_values(w->ggml_type);
+    if (!per) return fail("hq_mat_upload: ggml type %d is not supported (Q8_0 = 8, Q4_K = 12)", w->ggml_type);
+    if (w->rows == 0 || w->cols == 0 || w->cols % per)
+        return fail("hq_mat_upload: shape [%u, %u] is not a whole number of %u-value blocks per row", w->rows, w->cols,
+                    per);
+    if (w->rows > (1u << 30) || w->cols > (1u << 24)) return fail("hq_mat_upload: shape [%u, %u] too large", w->rows, w->cols);
+    if (w->perm_heads && (w->rows % w->perm_heads || (w->rows / w->perm_heads) % 2))
+        return fail("hq_mat_upload: %u rows do not split into %u heads of even size", w->rows, w->perm_heads);
+    if (use_device(device)) return -1;
+    const size_t rb = (size_t)(w->cols / per) * block_bytes(w->ggml_type);
+    const uint8_t *src = (const uint8_t *)w->data;
+    hq_mat *m = (hq_mat *)calloc(1, sizeof *m);
+    if (!m) return fail("hq_mat_upload: out of host memory");
+    m->device = device;
+    m->m.type = w->ggml_type;
+    m->m.rows = w->rows;
+    m->m.cols = w->cols;
+    m->m.row_bytes = rb;
+    std::vector<uint8_t> host;
+    if (w->ggml_type == HQ_GGML_Q4_K) {
+        m->bytes = rb * w->rows;
+        host.resize(m->bytes);
+        for (uint32_t r = 0; r < w->rows; r++)
+            memcpy(host.data() + (size_t)r * rb, src + (size_t)storage_row(w->rows, w->perm_heads, r) * rb, rb);
+    } else {
+        const size_t K = w->cols, nb = K / 32, ldd = round_up(nb, 8);
+        const size_t qbytes = round_up((size_t)w->rows * K, 256);
+        m->m.ldd = (int)ldd;
+        m->bytes = qbytes + (size_t)w->rows * ldd * 2;
+        host.assign(m->bytes, 0);
+        uint16_t *dpl = (uint16_t *)(host.data() + qbytes);
+        for (uint32_t r = 0; r < w->rows; r++) {
+            const uint8_t *row = src + (size_t)storage_row(w->rows, w->perm_heads, r) * rb;
+            uint8_t *q = host.data() + (size_t)r * K;
+            for (size_t b = 0; b < nb; b++) {
+                const uint8_t *blk = row + 34 * b;
+                dpl[(size_t)r * ldd + b] = (uint16_t)(blk[0] | (blk[1] << 8));
+                for (int j = 0; j < 32; j++) q[32 * b + j] = blk[2 + j] ^ 0x80u;
+            }
+        }
+    }
+    hipError_t e = hipMalloc(&m->alloc, m->bytes);
+    if (e != hipSuccess) {
+        free(m);
+        return fail("hq_mat_upload: hipMalloc(%zu) failed: %s", m->bytes, hipGetErrorString(e));
+    }
+    e = hipMemcpy(m->alloc, host.data(), m->bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(m->alloc);
+        free(m);
+        return fail("hq_mat_upload: copy failed: %s", hipGetErrorString(e));
+    }
+    m->m.qs = (const uint8_t *)m->alloc;
+    m->m.d = w->ggml_type == HQ_GGML_Q8_0 ? (const uint16_t *)((const uint8_t *)m->alloc +
+                                                                 round_up((size_t)w->rows * w->cols, 256))
+                                          : nullptr;
+    *out = m;
+    return 0;
+}
+
+extern "C" void hq_mat_free(hq_mat *m) {
+    if (!m) return;
+    if (use_device(m->device) == 0) (void)hipFree(m->alloc);
+    free(m);
+}
+
+extern "C" int hq_mat_shape(const hq_mat *m, uint32_t *rows, uint32_t *cols, int *ggml_type) {
+    if (!m) return fail("hq_mat_shape: no matrix");
+    if (rows) *rows = m->m.rows;
+    if (cols) *cols = m->m.cols;
+    if (ggml_type) *ggml_type = m->m.type;
+    return 0;
+}
+
+extern "C" size_t hq_mat_device_bytes(const hq_mat *m) { return m ? m->bytes : 0; }
+
+extern "C" int hq_mat_download(const hq_mat *m, void *out, size_t nbytes) {
+    if (!m || !out) return fail("hq_mat_download: null argument");
+    const size_t rb = m->m.row_bytes, total = rb * m->m.rows;
+    if (nbytes < total) return fail("hq_mat_download: need %zu bytes, got %zu", total, nbytes);
+    if (use_device(m->device)) return -1;
+    std::vector<uint8_t> host(m->bytes);
+    HIPCK(hipMemcpy(host.data(), m->alloc, m->bytes, hipMemcpyDeviceToHost));
+    uint8_t *dst = (uint8_t *)out;
+    if (m->m.type == HQ_GGML_Q4_K) {
+        memcpy(dst, host.data(), total);
+        return 0;
+    }
+    const size_t K = m->m.cols, nb = K / 32, ldd = (size_t)m->m.ldd;
+    const uint16_t *dpl = (const uint16_t *)(host.data() + round_up((size_t)m->m.rows * K, 256));
+    for (uint32_t r = 0; r < m->m.rows; r++)
+        for (size_t b = 0; b < nb; b++) {
+            uint8_t *blk = dst + (size_t)r * rb + 34 * b;
+            const uint16_t d = dpl[(size_t)r * ldd + b];
+            blk[0] = (uint8_t)d, blk[1] = (uint8_t)(d >> 8);
+            for (int j = 0; j < 32; j++) blk[2 + j] = host[(size_t)r * K + 32 * b + j] ^ 0x80u;
+        }
+    return 0;
+}
+
+// ------------------------------------------------------------------------------------ compute
+static hipStream_t S(void *s) { return (hipStream_t)s; }
+
+static int aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+extern "C" int hq_dequant_f32(const hq_mat *W, uint32_t row0, uint32_t nrows, float *out, void *stream) {
+    if (!W || !out) return fail("hq_dequant_f32: null argument");
+    if (row0 > W->m.rows || nrows > W->m.rows - row0)
+        return fail("hq_dequant_f32: rows [%u, %u) outside [0, %u)", row0, row0 + nrows, W->m.rows);
+    if (!aligned(out, 16)) return fail("hq_dequant_f32: output must be 16-byte aligned");
+    if (nrows == 0) return 0;
+    if (use_device(W->device)) return -1;
+    HIPCK(hq_launch_dequant(&W->m, row0, nullptr, nrows, out, S(stream)));
+    return 0;
+}
+
+extern "C" int hq_gemm(const hq_mat *W, const uint16_t *A, int M, void *C, int c_is_f32, int accumulate, void *stream) {
+    if (!W || !A || !C) return fail("hq_gemm: null argument");
+    if (M < 1) return fail("hq_gemm: M = %d", M);
+    if (!aligned(A, 16)) return fail("hq_gemm: A must be 16-byte aligned");
+    if (!aligned(C, c_is_f32 ? 4 : 2)) return fail("hq_gemm: C is misaligned");
+    if (use_device(W->device)) return -1;
+    if (M == 1) HIPCK(hq_launch_gemv(&W->m, A, C, c_is_f32, accumulate, S(stream)));
+    else HIPCK(hq_launch_gemm(&W->m, A, M, C, c_is_f32, accumulate, S(stream)));
+    return 0;
+}
+
+extern "C" int hq_gemv(const hq_mat *W, const uint16_t *a, void *c, int c_is_f32, int accumulate, void *stream) {
+    return hq_gemm(W, a, 1, c, c_is_f32, accumulate, stream);
+}
+
+extern "C" int hq_gather_dot_dev(const hq_mat *head, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
+                                 void *stream) {
+    if (!head || !H || !ids || !out) return fail("hq_gather_dot: null argument");
+    if (B < 0 || k < 0 || (long)B * k > (1l << 30)) return fail("hq_gather_dot: B = %d, k = %d", B, k);
+    if (!aligned(H, 16)) return fail("hq_gather_dot: H must be 16-byte aligned");
+    if ((long)B * k == 0) return 0;
+    if (use_device(head->device)) return -1;
+    HIPCK(hq_launch_gather(&head->m, H, ids, B, k, out, S(stream)));
+    return 0;
+}
+
+// Library-owned staging buffers for host-pointer entry points, per device.
+namespace {
+struct Staging {  // slots: 0 ids / x fp32, 1 x fp16, 2 y fp32, 3 embedding ids
+    void *buf[4] = {nullptr, nullptr, nullptr, nullptr};
+    size_t cap[4] = {0, 0, 0, 0};
+};
+std::mutex g_staging_mu;
+std::vector<Staging> g_staging;
+
+int staging(int device, int slot, size_t bytes, void **p) {
+    std::lock_guard<std::mutex> lk(g_staging_mu);
+    if ((int)g_staging.size() <= device) g_staging.resize(device + 1);
+    Staging &s = g_staging[device];
+    if (s.cap[slot] < bytes) {
+        if (s.buf[slot]) HIPCK(hipFree(s.buf[slot]));
+        s.buf[slot] = nullptr;
+        s.cap[slot] = 0;
+        HIPCK(hipMalloc(&s.buf[slot], bytes));
+        s.cap[slot] = bytes;
+    }
+    *p = s.buf[slot];
+    return 0;
+}
+}  // namespace
+
+extern "C" int hq_gather_dot(const hq_mat *head, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
+                             void *stream) {
+    if (!head || !ids) return fail("hq_gather_dot: null argument");
+    if (B < 0 || k < 0 || (long)B * k > (1l << 30)) return fail("hq_gather_dot: B = %d, k = %d", B, k);
+    const size_t n = (size_t)B * k;
+    for (size_t i = 0; i < n; i++)
+        if (ids[i] >= head->m.rows) return fail("hq_gather_dot: readout id %u out of range", ids[i]);
+    if (n == 0) return 0;
+    if (use_device(head->device)) return -1;
+    void *d_ids;
+    if (staging(head->device, 0, n * sizeof(uint32_t), &d_ids)) return -1;
+    HIPCK(hipMemcpyAsync(d_ids, ids, n * sizeof(uint32_t), hipMemcpyHostToDevice, S(stream)));
+    return hq_gather_dot_dev(head, H, (const uint32_t *)d_ids, B, k, out, stream);
+}
+
+extern "C" int hq_embed_f32(const hq_mat *W, const uint32_t *ids, int n, float *out, void *stream) {
+    if (!W || !ids || !out) return fail("hq_embed_f32: null argument");
+    if (n < 0) return fail("hq_embed_f32: n = %d", n);
+    for (int i = 0; i < n; i++)
+        if (ids[i] >= W->m.rows) return fail("hq_embed_f32: token %u out of range", ids[i]);
+    if (!aligned(out, 16)) return fail("hq_embed_f32: output must be 16-byte aligned");
+    if (n == 0) return 0;
+    if (use_device(W->device)) return -1;
+    void *d_ids;
+    if (staging(W->device, 3, (size_t)n * sizeof(uint32_t), &d_ids)) return -1;
+    HIPCK(hipMemcpyAsync(d_ids, ids, (size_t)n * sizeof(uint32_t), hipMemcpyHostToDevice, S(stream)));
+    HIPCK(hq_launch_dequant(&W->m, 0, (const uint32_t *)d_ids, (uint32_t)n, out, S(stream)));
+    return 0;
+}
+
+extern "C" int hq_matmul_host(const hq_mat *W, const float *x, size_t T, float *y, bool accumulate) {
+    if (!W || !x || !y) return fail("hq_matmul_host: null argument");
+    if (T == 0) return 0;
+    if (T > (1u << 24)) return fail("hq_matmul_host: T = %zu", T);
+    const size_t K = W->m.cols, N = W->m.rows;
+    if (use_device(W->device)) return -1;
+    void *dx, *dh, *dy;
+    if (staging(W->device, 0, T * K * sizeof(float), &dx) || staging(W->device, 1, T * K * 2, &dh) ||
+        staging(W->device, 2, T * N * sizeof(float), &dy))
+        return -1;
+    HIPCK(hipMemcpy(dx, x, T * K * sizeof(float), hipMemcpyHostToDevice));
+    if (accumulate) HIPCK(hipMemcpy(dy, y, T * N * sizeof(float), hipMemcpyHostToDevice));
+    HIPCK(hq_launch_f32_to_f16((const float *)dx, (uint16_t *)dh, T * K, nullptr));
+    if (hq_gemm(W, (const uint16_t *)dh, (int)T, dy, 1, accumulate ? 1 : 0, nullptr)) return -1;
+    HIPCK(hipMemcpy(y, dy, T * N * sizeof(float), hipMemcpyDeviceToHost));
+    return 0;
+}
+
+// ------------------------------------------------------------------------------------ plumbing
+extern "C" int hq_malloc(void **p, size_t n) {
+    HIPCK(hipMalloc(p, n ? n : 16));
+    return 0;
+}
+extern "C" int hq_free(void *p) {
+    HIPCK(hipFree(p));
+    return 0;
+}
+extern "C" int hq_memcpy_h2d(void *dst, const void *src, size_t n, void *stream) {
+    HIPCK(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, S(stream)));
+    HIPCK(hipStreamSynchronize(S(stream)));
+    return 0;
+}
+extern "C" int hq_memcpy_d2h(void *dst, const void *src, size_t n, void *stream) {
+    HIPCK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, S(stream)));
+    HIPCK(hipStreamSynchronize(S(stream)));
+    return 0;
+}
+extern "C" int hq_memset(void *dst, int value, size_t n, void *stream) {
+    HIPCK(hipMemsetAsync(dst, value, n, S(stream)));
+    return 0;
+}
+extern "C" int hq_stream_create(void **stream) {
+    hipStream_t s;
+    HIPCK(hipStreamCreate(&s));
+    *stream = (void *)s;
+    return 0;
+}
+extern "C" int hq_stream_destroy(void *stream) {
+    HIPCK(hipStreamDestroy(S(stream)));
+    return 0;
+}
+extern "C" int hq_stream_synchronize(void *stream) {
+    HIPCK(hipStreamSynchronize(S(stream)));
+    return 0;
+}
+extern "C" int hq_device_synchronize(void) {
+    HIPCK(hipDeviceSynchronize());
+    return 0;
+}
+
+extern "C" void hq_gemm_tiles(int M, int N, int *rows_per_tile, int *cols_per_tile) {
+    int mb, nb;
+    hq_gemm_config(M, N, &mb, &nb);
+    if (rows_per_tile) *rows_per_tile = M == 1 ? 1 : 16 * mb;
+    if (cols_per_tile) *cols_per_tile = M == 1 ? 16 : 64 * nb;
+}
+
+// ------------------------------------------------------------------------------------ timing
+namespace {
+template <typename F>
+int time_graph(int iters, int reps, void *stream, float *ms, F launch) {
+    if (iters < 1 || reps < 1) return fail("hq_time: iters = %d, reps = %d", iters, reps);
+    if (!stream) return fail("hq_time: needs a created stream (graph capture)");
+    hipStream_t st = S(stream);
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    HIPCK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    int rc = 0;
+    for (int i = 0; i < iters && !rc; i++) rc = launch(i);
+    hipError_t e = hipStreamEndCapture(st, &g);
+    if (rc) {
+        if (g) (void)hipGraphDestroy(g);
+        return -1;
+    }
+    if (e != hipSuccess) return fail("hipStreamEndCapture: %s", hipGetErrorString(e));
+    e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return fail("hipGraphInstantiate: %s", hipGetErrorString(e));
+    }
+    hipEvent_t e0, e1;
+    HIPCK(hipEventCreate(&e0));
+    HIPCK(hipEventCreate(&e1));
+    HIPCK(hipGraphLaunch(ge, st));  // warm-up
+    HIPCK(hipEventRecord(e0, st));
+    for (int r = 0; r < reps; r++) HIPCK(hipGraphLaunch(ge, st));
+    HIPCK(hipEventRecord(e1, st));
+    HIPCK(hipEventSynchronize(e1));
+    float total = 0.f;
+    HIPCK(hipEventElapsedTime(&total, e0, e1));
+    *ms = total / (float)(iters * reps);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    (void)hipGraphExecDestroy(ge);
+    (void)hipGraphDestroy(g);
+    return 0;
+}
+}  // namespace
+
+extern "C" int hq_time_gemm(hq_mat *const *Ws, int n_w, const uint16_t *A, int M, void *C, int c_is_f32, int iters,
+                            int reps, void *stream, float *ms) {
+    if (!Ws || n_w < 1) return fail("hq_time_gemm: no matrices");
+    for (int i = 0; i < n_w; i++)
+        if (!Ws[i] || Ws[i]->m.rows != Ws[0]->m.rows || Ws[i]->m.cols != Ws[0]->m.cols || Ws[i]->m.type != Ws[0]->m.type)
+            return fail("hq_time_gemm: matrices differ in shape or type");
+    return time_graph(iters, reps, stream, ms,
+                      [&](int i) { return hq_gemm(Ws[i % n_w], A, M, C, c_is_f32, 0, stream); });
+}
+
+extern "C" int hq_time_gather(hq_mat *const *Ws, int n_w, const uint16_t *H, const uint32_t *ids_dev, int n_sets,
+                              int B, int k, float *out, int iters, int reps, void *stream, float *ms) {
+    if (!Ws || n_w < 1) return fail("hq_time_gather: no matrices");
+    if (n_sets < 1) return fail("hq_time_gather: n_sets = %d", n_sets);
+    for (int i = 0; i < n_w; i++)
+        if (!Ws[i] || Ws[i]->m.rows != Ws[0]->m.rows || Ws[i]->m.cols != Ws[0]->m.cols || Ws[i]->m.type != Ws[0]->m.type)
+            return fail("hq_time_gather: matrices differ in shape or type");
+    return time_graph(iters, reps, stream, ms,
+                      [&](int i) {
+                          return hq_gather_dot_dev(Ws[i % n_w], H, ids_dev + (size_t)(i % n_sets) * B * k, B, k, out,
+                                                   stream);
+                      });
+}

@@ -1,0 +1,32 @@
+// hq_kernels.h - internal interface between the C-ABI layer (hq_api.hip) and the gfx950 kernels.
+#ifndef HQ_KERNELS_H
+#define HQ_KERNELS_H
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+enum { HQ_TYPE_Q8_0 = 8, HQ_TYPE_Q4_K = 12 };
+
+// A weight matrix resident in HBM, rows in Hugging Face order (see hq_kernels.hip for layouts).
+typedef struct {
+    int type;
+    uint32_t rows, cols;
+    const uint8_t *qs;   // Q8_0: biased quant plane [rows][cols]; Q4_K: super-blocks [rows][row_bytes]
+    const uint16_t *d;   // Q8_0: fp16 scale plane [rows][ldd]; Q4_K: unused
+    int ldd;             // Q8_0 scale-plane row stride in halves (cols/32 rounded up to 8)
+    size_t row_bytes;    // GGUF bytes per row
+} hq_dev_mat;
+
+// rows row0 .. row0 + nrows - 1, or rows ids[0 .. nrows - 1] when ids (device) is not null
+hipError_t hq_launch_dequant(const hq_dev_mat *W, uint32_t row0, const uint32_t *ids, uint32_t nrows, float *out,
+                             hipStream_t st);
+hipError_t hq_launch_gemv(const hq_dev_mat *W, const uint16_t *a, void *C, int c_f32, int accumulate, hipStream_t st);
+hipError_t hq_launch_gemm(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
+                          hipStream_t st);
+hipError_t hq_launch_gather(const hq_dev_mat *W, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
+                            hipStream_t st);
+hipError_t hq_launch_f32_to_f16(const float *in, uint16_t *out, size_t n, hipStream_t st);
+void hq_gemm_config(int M, int N, int *mb, int *nb);
+
+#endif

@@ -1,0 +1,350 @@
+"""ctypes binding of libhq.so, the gfx950 quantized matmul path (C ABI: include/hq.h, hq_llama.h).
+
+Python is plumbing here: it moves numpy arrays in and out of device buffers and calls the C ABI.
+There is no fallback: if libhq.so is not built, or a call fails, an exception is raised.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libhq.so")
+
+Q8_0, Q4_K = 8, 12
+DT_GGML = 3
+BLOCK_VALUES = {Q8_0: 32, Q4_K: 256}
+BLOCK_BYTES = {Q8_0: 34, Q4_K: 144}
+
+# Every function declared in include/hq.h and include/hq_llama.h.
+EXPORTS = (
+    "hq_last_error", "hq_device_init", "hq_device_count", "hq_device_name", "hq_mat_upload", "hq_mat_free",
+    "hq_mat_shape", "hq_mat_device_bytes", "hq_mat_download", "hq_dequant_f32", "hq_gemm", "hq_gemv",
+    "hq_gather_dot", "hq_gather_dot_dev", "hq_matmul_host", "hq_malloc", "hq_free", "hq_memcpy_h2d",
+    "hq_memcpy_d2h", "hq_memset", "hq_stream_create", "hq_stream_destroy", "hq_stream_synchronize",
+    "hq_device_synchronize", "hq_time_gemm", "hq_time_gather", "hq_gemm_tiles", "hq_llama_forward",
+    "hq_embed_f32",
+)
+
+
+class WMat(C.Structure):
+    """hq_wmat_t: field for field the reference wmat_t (cleanroom-transformer/src/transformer.h:293-300)."""
+    _fields_ = [("dtype", C.c_int), ("rows", C.c_uint32), ("cols", C.c_uint32), ("data", C.c_void_p),
+                ("ggml_type", C.c_int), ("perm_heads", C.c_uint32)]
+
+
+class LlamaLayer(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("q", "k", "v", "o", "gate", "up", "down")] + [
+        ("in_norm", C.c_void_p), ("post_norm", C.c_void_p)]
+
+
+class Llama(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("hidden", "n_layers", "intermediate", "vocab", "n_heads", "n_kv_heads",
+                                          "head_dim", "rot_dim")] + [
+        ("eps", C.c_float), ("rope_theta", C.c_float), ("embed", C.c_void_p), ("lm_head", C.c_void_p),
+        ("final_norm", C.c_void_p), ("layers", C.c_void_p)]
+
+
+class HQError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def load(path=LIB_PATH):
+    """Load libhq.so once; raise if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise HQError(f"{path} is not built: run __graft_entry__.build() (make -C hilbert-pruned-8b_amd/csrc)")
+    L = C.CDLL(path)
+    vp, i, sz, u32 = C.c_void_p, C.c_int, C.c_size_t, C.c_uint32
+    sig = {
+        "hq_last_error": (C.c_char_p, []),
+        "hq_device_init": (i, [i]),
+        "hq_device_count": (i, [C.POINTER(i)]),
+        "hq_device_name": (i, [i, C.c_char_p, sz, C.c_char_p, sz]),
+        "hq_mat_upload": (i, [C.POINTER(WMat), i, C.POINTER(vp)]),
+        "hq_mat_free": (None, [vp]),
+        "hq_mat_shape": (i, [vp, C.POINTER(u32), C.POINTER(u32), C.POINTER(i)]),
+        "hq_mat_device_bytes": (sz, [vp]),
+        "hq_mat_download": (i, [vp, vp, sz]),
+        "hq_dequant_f32": (i, [vp, u32, u32, vp, vp]),
+        "hq_gemm": (i, [vp, vp, i, vp, i, i, vp]),
+        "hq_gemv": (i, [vp, vp, vp, i, i, vp]),
+        "hq_gather_dot": (i, [vp, vp, vp, i, i, vp, vp]),
+        "hq_gather_dot_dev": (i, [vp, vp, vp, i, i, vp, vp]),
+        "hq_matmul_host": (i, [vp, vp, sz, vp, C.c_bool]),
+        "hq_malloc": (i, [C.POINTER(vp), sz]),
+        "hq_free": (i, [vp]),
+        "hq_memcpy_h2d": (i, [vp, vp, sz, vp]),
+        "hq_memcpy_d2h": (i, [vp, vp, sz, vp]),
+        "hq_memset": (i, [vp, i, sz, vp]),
+        "hq_stream_create": (i, [C.POINTER(vp)]),
+        "hq_stream_destroy": (i, [vp]),
+        "hq_stream_synchronize": (i, [vp]),
+        "hq_device_synchronize": (i, []),
+        "hq_time_gemm": (i, [C.POINTER(vp), i, vp, i, vp, i, i, i, vp, C.POINTER(C.c_float)]),
+        "hq_time_gather": (i, [C.POINTER(vp), i, vp, vp, i, i, i, vp, i, i, vp, C.POINTER(C.c_float)]),
+        "hq_gemm_tiles": (None, [i, i, C.POINTER(i), C.POINTER(i)]),
+        "hq_llama_forward": (i, [C.POINTER(Llama), vp, sz, vp, u32, vp]),
+        "hq_embed_f32": (i, [vp, vp, i, vp, vp]),
+    }
+    for name in EXPORTS:
+        fn = getattr(L, name)
+        fn.restype, fn.argtypes = sig[name]
+    _lib = L
+    return L
+
+
+def _check(rc):
+    if rc != 0:
+        raise HQError(load().hq_last_error().decode(errors="replace"))
+
+
+def last_error():
+    return load().hq_last_error().decode(errors="replace")
+
+
+def row_bytes(gtype, cols):
+    return cols // BLOCK_VALUES[gtype] * BLOCK_BYTES[gtype]
+
+
+def _ptr(a):
+    return C.c_void_p(a.ctypes.data)
+
+
+class DevBuf:
+    """A device allocation (hq_malloc) with numpy copy helpers."""
+
+    def __init__(self, nbytes):
+        load()
+        p = C.c_void_p()
+        _check(_lib.hq_malloc(C.byref(p), max(int(nbytes), 16)))
+        self.ptr, self.nbytes = p.value, int(nbytes)
+
+    @classmethod
+    def from_array(cls, a):
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a, stream=None):
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        _check(_lib.hq_memcpy_h2d(self.ptr, _ptr(a), a.nbytes, stream))
+
+    def download(self, shape, dtype, stream=None):
+        out = np.empty(shape, dtype=dtype)
+        assert out.nbytes <= self.nbytes
+        _check(_lib.hq_memcpy_d2h(_ptr(out), self.ptr, out.nbytes, stream))
+        return out
+
+    def zero(self, stream=None):
+        _check(_lib.hq_memset(self.ptr, 0, self.nbytes, stream))
+
+    def free(self):
+        if self.ptr:
+            _check(_lib.hq_free(self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Mat:
+    """A weight matrix resident in HBM (hq_mat_upload)."""
+
+    def __init__(self, blocks, gtype, rows, cols, perm_heads=0, device=0):
+        load()
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        if blocks.nbytes != rows * row_bytes(gtype, cols):
+            raise HQError(f"blocks hold {blocks.nbytes} bytes, expected {rows * row_bytes(gtype, cols)}")
+        w = WMat(DT_GGML, rows, cols, blocks.ctypes.data, gtype, perm_heads)
+        h = C.c_void_p()
+        _check(_lib.hq_mat_upload(C.byref(w), device, C.byref(h)))
+        self.h, self.gtype, self.rows, self.cols = h.value, gtype, rows, cols
+
+    @property
+    def device_bytes(self):
+        return _lib.hq_mat_device_bytes(self.h)
+
+    def download(self):
+        out = np.empty((self.rows, row_bytes(self.gtype, self.cols)), dtype=np.uint8)
+        _check(_lib.hq_mat_download(self.h, _ptr(out), out.nbytes))
+        return out
+
+    def free(self):
+        if self.h:
+            _lib.hq_mat_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def device_init(device=0):
+    _check(load().hq_device_init(device))
+
+
+def device_name(device=0):
+    n, a = C.create_string_buffer(256), C.create_string_buffer(64)
+    _check(load().hq_device_name(device, n, 256, a, 64))
+    return n.value.decode(), a.value.decode()
+
+
+def synchronize():
+    _check(load().hq_device_synchronize())
+
+
+def dequant(W, row0=0, nrows=None, stream=None):
+    nrows = W.rows - row0 if nrows is None else nrows
+    out = DevBuf(nrows * W.cols * 4)
+    _check(_lib.hq_dequant_f32(W.h, row0, nrows, out.ptr, stream))
+    return out.download((nrows, W.cols), np.float32)
+
+
+def gemm(W, A, M, C_buf, c_f32=True, accumulate=False, stream=None):
+    """Device-pointer GEMM: A, C_buf are DevBuf (or raw pointers)."""
+    a = A.ptr if isinstance(A, DevBuf) else A
+    c = C_buf.ptr if isinstance(C_buf, DevBuf) else C_buf
+    _check(_lib.hq_gemm(W.h, a, M, c, int(c_f32), int(accumulate), stream))
+
+
+def gemm_np(W, a_f16_bits, c_f32=True, c_init=None):
+    """Convenience: numpy fp16 bits [M, K] in, numpy fp32 / fp16-bits [M, N] out (accumulate into c_init)."""
+    a = np.ascontiguousarray(a_f16_bits, dtype=np.uint16)
+    M = a.shape[0]
+    dA = DevBuf.from_array(a)
+    esize = 4 if c_f32 else 2
+    dC = DevBuf(M * W.rows * esize)
+    if c_init is not None:
+        dC.upload(np.ascontiguousarray(c_init))
+    gemm(W, dA, M, dC, c_f32, c_init is not None)
+    synchronize()
+    out = dC.download((M, W.rows), np.float32 if c_f32 else np.uint16)
+    dA.free(), dC.free()
+    return out
+
+
+def gather_dot_np(W, h_f16_bits, ids, device_ids=False):
+    h = np.ascontiguousarray(h_f16_bits, dtype=np.uint16)
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    B, k = ids.shape
+    dH = DevBuf.from_array(h)
+    dO = DevBuf(B * k * 4)
+    if device_ids:
+        dI = DevBuf.from_array(ids)
+        _check(_lib.hq_gather_dot_dev(W.h, dH.ptr, dI.ptr, B, k, dO.ptr, None))
+    else:
+        _check(_lib.hq_gather_dot(W.h, dH.ptr, _ptr(ids), B, k, dO.ptr, None))
+    synchronize()
+    return dO.download((B, k), np.float32)
+
+
+def matmul_host(W, x, y=None, accumulate=False):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T = x.shape[0]
+    if y is None:
+        y = np.zeros((T, W.rows), dtype=np.float32)
+    _check(_lib.hq_matmul_host(W.h, _ptr(x), T, _ptr(y), bool(accumulate)))
+    return y
+
+
+def embed(W, ids):
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    out = DevBuf(len(ids) * W.cols * 4)
+    _check(_lib.hq_embed_f32(W.h, _ptr(ids), len(ids), out.ptr, None))
+    synchronize()
+    return out.download((len(ids), W.cols), np.float32)
+
+
+def gemm_tiles(M, N):
+    r, c = C.c_int(), C.c_int()
+    load().hq_gemm_tiles(M, N, C.byref(r), C.byref(c))
+    return r.value, c.value
+
+
+class Stream:
+    def __init__(self):
+        p = C.c_void_p()
+        _check(load().hq_stream_create(C.byref(p)))
+        self.ptr = p.value
+
+    def sync(self):
+        _check(_lib.hq_stream_synchronize(self.ptr))
+
+    def destroy(self):
+        if self.ptr:
+            _check(_lib.hq_stream_destroy(self.ptr))
+            self.ptr = None
+
+
+def time_gemm(mats, A, M, C_buf, c_f32, iters, reps, stream):
+    arr = (C.c_void_p * len(mats))(*[m.h for m in mats])
+    ms = C.c_float()
+    _check(_lib.hq_time_gemm(arr, len(mats), A.ptr, M, C_buf.ptr, int(c_f32), iters, reps, stream.ptr, C.byref(ms)))
+    return ms.value
+
+
+def time_gather(mats, H, ids_dev, n_sets, B, k, out, iters, reps, stream):
+    arr = (C.c_void_p * len(mats))(*[m.h for m in mats])
+    ms = C.c_float()
+    _check(_lib.hq_time_gather(arr, len(mats), H.ptr, ids_dev.ptr, n_sets, B, k, out.ptr, iters, reps, stream.ptr,
+                               C.byref(ms)))
+    return ms.value
+
+
+class LlamaModel:
+    """Config-1 model resident on the GPU, from a synth.tiny_llama()-style dict (llama.cpp storage
+    order for q/k rows; perm_heads un-permutes them at upload, as the reference's model.c:382)."""
+
+    def __init__(self, model, device=0):
+        c = model["cfg"]
+        self.cfg = c
+        H, I, V = c["hidden"], c["intermediate"], c["vocab"]
+        qw, kvw = c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
+        self.mats = []
+
+        def up(blocks, rows, cols, perm=0):
+            m = Mat(blocks, Q8_0, rows, cols, perm, device)
+            self.mats.append(m)
+            return m.h
+
+        self.norms = [np.ascontiguousarray(model["final_norm"], np.float32)]
+        self.layers = (LlamaLayer * c["n_layers"])()
+        shapes = {"q": (qw, H, c["n_heads"]), "k": (kvw, H, c["n_kv_heads"]), "v": (kvw, H, 0), "o": (H, qw, 0),
+                  "gate": (I, H, 0), "up": (I, H, 0), "down": (H, I, 0)}
+        for li, L in enumerate(model["layers"]):
+            for name, (r, k, perm) in shapes.items():
+                setattr(self.layers[li], name, up(L[name], r, k, perm))
+            n_in = np.ascontiguousarray(L["in_norm"], np.float32)
+            n_post = np.ascontiguousarray(L["post_norm"], np.float32)
+            self.norms += [n_in, n_post]
+            self.layers[li].in_norm = n_in.ctypes.data
+            self.layers[li].post_norm = n_post.ctypes.data
+        self.st = Llama(H, c["n_layers"], I, V, c["n_heads"], c["n_kv_heads"], c["head_dim"], c["rot_dim"], c["eps"],
+                        c["rope_theta"], up(model["embed"], V, H), up(model["lm_head"], V, H),
+                        self.norms[0].ctypes.data, C.cast(self.layers, C.c_void_p).value)
+
+    def forward(self, tokens, ids):
+        tokens = np.ascontiguousarray(tokens, np.uint32)
+        ids = np.ascontiguousarray(ids, np.uint32)
+        logits = np.empty(len(ids), np.float32)
+        _check(_lib.hq_llama_forward(C.byref(self.st), _ptr(tokens), len(tokens), _ptr(ids), len(ids),
+                                     _ptr(logits)))
+        return logits
+
+    def free(self):
+        for m in self.mats:
+            m.free()
+        self.mats = []

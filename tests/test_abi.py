@@ -1,0 +1,89 @@
+"""CPU checks of the C ABI: libhq.so is built, loads, and exports every function the headers
+declare; host-side argument validation and tile selection work without a GPU."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+import hq
+import synth
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADERS = [os.path.join(ROOT, "include", f) for f in sorted(os.listdir(os.path.join(ROOT, "include"))) if f.endswith(".h")]
+
+
+def declared_functions():
+    names = set()
+    for path in HEADERS:
+        text = open(path).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"^[A-Za-z_][\w\s\*]*?\b(hq_\w+)\s*\(", text, flags=re.M):
+            names.add(m.group(1))
+    return names
+
+
+def test_library_built_and_exports_every_declared_function():
+    assert os.path.exists(hq.LIB_PATH), "libhq.so not built: run __graft_entry__.build()"
+    lib = C.CDLL(hq.LIB_PATH)
+    declared = declared_functions()
+    assert len(declared) >= 25
+    missing = [n for n in sorted(declared) if not hasattr(lib, n)]
+    assert not missing, missing
+    assert declared == set(hq.EXPORTS), declared ^ set(hq.EXPORTS)
+
+
+def test_binding_signatures_load():
+    lib = hq.load()
+    for name in hq.EXPORTS:
+        assert getattr(lib, name).argtypes is not None
+
+
+def test_wmat_layout_matches_reference_struct():
+    # reference wmat_t: {dtype_t dtype; uint32_t rows, cols; const void *data; int ggml_type; uint32_t perm_heads}
+    assert C.sizeof(hq.WMat) == 32
+    assert [hq.WMat.__dict__[f].offset for f in ("dtype", "rows", "cols", "data", "ggml_type", "perm_heads")] == \
+        [0, 4, 8, 16, 24, 28]
+
+
+@pytest.mark.parametrize("dtype,gtype,rows,cols,perm,msg", [
+    (0, 8, 4, 64, 0, "not a GGUF block type"),
+    (3, 2, 4, 64, 0, "not supported"),
+    (3, 8, 4, 48, 0, "whole number"),
+    (3, 12, 4, 512 + 32, 0, "whole number"),
+    (3, 8, 0, 64, 0, "whole number"),
+    (3, 8, 6, 64, 4, "heads of even size"),
+])
+def test_upload_rejects_bad_descriptors_before_touching_a_device(dtype, gtype, rows, cols, perm, msg):
+    lib = hq.load()
+    buf = np.zeros(1 << 16, np.uint8)
+    w = hq.WMat(dtype, rows, cols, buf.ctypes.data, gtype, perm)
+    h = C.c_void_p()
+    assert lib.hq_mat_upload(C.byref(w), 0, C.byref(h)) == -1
+    assert msg in hq.last_error()
+    assert h.value is None
+
+
+def test_gemm_tile_selection():
+    # every M from 1 to 4096 gets a tile; M = 1 is the GEMV
+    assert hq.gemm_tiles(1, 9728) == (1, 16)
+    for M in (2, 16, 17, 33, 64, 65, 512, 4096):
+        r, c = hq.gemm_tiles(M, 9728)
+        assert r in (16, 32, 64, 128) and c in (64, 128, 192, 256)
+        assert r >= min(M, 128) or r == 128
+    # wave quantization over 256 CUs: M=512, N=9728 takes 128 x 192 tiles (4 x 51 = 204 tiles, one
+    # round) rather than 128 x 128 (304 tiles, two rounds)
+    assert hq.gemm_tiles(512, 9728) == (128, 192)
+
+
+def test_synth_is_deterministic():
+    a = synth.q4_k_blocks(synth.Rng(9), 4, 512)
+    b = synth.q4_k_blocks(synth.Rng(9), 4, 512)
+    assert np.array_equal(a, b)
+    x = synth.activations_f16(synth.Rng(3), 2, 64)
+    assert x.dtype == np.uint16 and np.isfinite(x.view(np.float16)).all()
+    # fp16 scales |N(0,1)| * 2e-4 are non-negative and finite
+    q = synth.q8_0_blocks(synth.Rng(4), 8, 256)
+    d = q.reshape(-1, 34)[:, :2].copy().view(np.float16)
+    assert (d >= 0).all() and np.isfinite(d).all()
