@@ -218,7 +218,7 @@ extern "C" int hq_dequant_f32(const hq_mat *W, uint32_t row0, uint32_t nrows, fl
 
 extern "C" int hq_gemm(const hq_mat *W, const uint16_t *A, int M, void *C, int c_is_f32, int accumulate, void *stream) {
     if (!W || !A || !C) return fail("hq_gemm: null argument");
-    if (M < 1) return fail("hq_gemm: M = %d", M);
+    if (M < 1 || M > (1 << 23)) return fail("hq_gemm: M = %d (1 .. 8388608)", M);
     if (!aligned(A, 16)) return fail("hq_gemm: A must be 16-byte aligned");
     if (!aligned(C, c_is_f32 ? 4 : 2)) return fail("hq_gemm: C is misaligned");
     if (use_device(W->device)) return -1;
@@ -244,9 +244,9 @@ extern "C" int hq_gather_dot_dev(const hq_mat *head, const uint16_t *H, const ui
 
 // Library-owned staging buffers for host-pointer entry points, per device.
 namespace {
-struct Staging {  // slots: 0 ids / x fp32, 1 x fp16, 2 y fp32, 3 embedding ids
-    void *buf[4] = {nullptr, nullptr, nullptr, nullptr};
-    size_t cap[4] = {0, 0, 0, 0};
+struct Staging {  // slots: 0 x fp32, 1 x fp16, 2 y fp32 (hq_matmul_host), 3 embedding ids, 4 readout ids
+    void *buf[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
+    size_t cap[5] = {0, 0, 0, 0, 0};
 };
 std::mutex g_staging_mu;
 std::vector<Staging> g_staging;
@@ -277,7 +277,7 @@ extern "C" int hq_gather_dot(const hq_mat *head, const uint16_t *H, const uint32
     if (n == 0) return 0;
     if (use_device(head->device)) return -1;
     void *d_ids;
-    if (staging(head->device, 0, n * sizeof(uint32_t), &d_ids)) return -1;
+    if (staging(head->device, 4, n * sizeof(uint32_t), &d_ids)) return -1;
     HIPCK(hipMemcpyAsync(d_ids, ids, n * sizeof(uint32_t), hipMemcpyHostToDevice, S(stream)));
     return hq_gather_dot_dev(head, H, (const uint32_t *)d_ids, B, k, out, stream);
 }
