@@ -205,48 +205,15 @@ static hipStream_t S(void *s) { return (hipStream_t)s; }
 
 static int aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
-extern "C" int hq_dequant_f32(const hq_mat *W, uint32_t row0, uint32_t nrows, float *out, void *stream) {
-    if (!W || !out) return fail("hq_dequant_f32: null argument");
-    if (row0 > W->m.rows || nrows > W->m.rows - row0)
-        return fail("hq_dequant_f32: rows [%u, %u) outside [0, %u)", row0, row0 + nrows, W->m.rows);
-    if (!aligned(out, 16)) return fail("hq_dequant_f32: output must be 16-byte aligned");
-    if (nrows == 0) return 0;
-    if (use_device(W->device)) return -1;
-    HIPCK(hq_launch_dequant(&W->m, row0, nullptr, nrows, out, S(stream)));
-    return 0;
-}
-
-extern "C" int hq_gemm(const hq_mat *W, const uint16_t *A, int M, void *C, int c_is_f32, int accumulate, void *stream) {
-    if (!W || !A || !C) return fail("hq_gemm: null argument");
-    if (M < 1 || M > (1 << 23)) return fail("hq_gemm: M = %d (1 .. 8388608)", M);
-    if (!aligned(A, 16)) return fail("hq_gemm: A must be 16-byte aligned");
-    if (!aligned(C, c_is_f32 ? 4 : 2)) return fail("hq_gemm: C is misaligned");
-    if (use_device(W->device)) return -1;
-    if (M == 1) HIPCK(hq_launch_gemv(&W->m, A, C, c_is_f32, accumulate, S(stream)));
-    else HIPCK(hq_launch_gemm(&W->m, A, M, C, c_is_f32, accumulate, S(stream)));
-    return 0;
-}
-
-extern "C" int hq_gemv(const hq_mat *W, const uint16_t *a, void *c, int c_is_f32, int accumulate, void *stream) {
-    return hq_gemm(W, a, 1, c, c_is_f32, accumulate, stream);
-}
-
-extern "C" int hq_gather_dot_dev(const hq_mat *head, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
-                                 void *stream) {
-    if (!head || !H || !ids || !out) return fail("hq_gather_dot: null argument");
-    if (B < 0 || k < 0 || (long)B * k > (1l << 30)) return fail("hq_gather_dot: B = %d, k = %d", B, k);
-    if (!aligned(H, 16)) return fail("hq_gather_dot: H must be 16-byte aligned");
-    if ((long)B * k == 0) return 0;
-    if (use_device(head->device)) return -1;
-    HIPCK(hq_launch_gather(&head->m, H, ids, B, k, out, S(stream)));
-    return 0;
-}
-
-// Library-owned staging buffers for host-pointer entry points, per device.
+// Library-owned device buffers, per device: staging for host-pointer entry points and the GEMM
+// workspace. Grown on demand (hipMalloc), so the first call of a larger shape allocates: capture a
+// call into a HIP graph only after an eager call of the same shape.
 namespace {
-struct Staging {  // slots: 0 x fp32, 1 x fp16, 2 y fp32 (hq_matmul_host), 3 embedding ids, 4 readout ids
-    void *buf[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
-    size_t cap[5] = {0, 0, 0, 0, 0};
+struct Staging {  // slots: 0 x fp32, 1 x fp16, 2 y fp32 (hq_matmul_host), 3 embedding ids, 4 readout ids,
+                  // 5 GEMM partial tiles, 6 GEMM tile counters (kept zero)
+    void *buf[7] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    size_t cap[7] = {0, 0, 0, 0, 0, 0, 0};
+    int n_cu = 0;
 };
 std::mutex g_staging_mu;
 std::vector<Staging> g_staging;
@@ -265,7 +232,85 @@ int staging(int device, int slot, size_t bytes, void **p) {
     *p = s.buf[slot];
     return 0;
 }
+
+// Stream-K workspace for hq_gemm on W's device. A counter array that grows is zeroed once here,
+// synchronously; the kernels leave every counter back at zero.
+int gemm_work(const hq_mat *W, int M, HqGemmWork *wk) {
+    int n_cu;
+    {
+        std::lock_guard<std::mutex> lk(g_staging_mu);
+        if ((int)g_staging.size() <= W->device) g_staging.resize(W->device + 1);
+        if (!g_staging[W->device].n_cu) {
+            int v = 0;
+            HIPCK(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, W->device));
+            g_staging[W->device].n_cu = v > 0 ? v : 1;
+        }
+        n_cu = g_staging[W->device].n_cu;
+    }
+    size_t pb, cb;
+    hq_gemm_work_bytes(&W->m, M, n_cu, &pb, &cb);
+    void *part, *cnt;
+    size_t old_cap;
+    {
+        std::lock_guard<std::mutex> lk(g_staging_mu);
+        old_cap = g_staging[W->device].cap[6];
+    }
+    if (staging(W->device, 5, pb, &part) || staging(W->device, 6, cb, &cnt)) return -1;
+    size_t new_cap;
+    {
+        std::lock_guard<std::mutex> lk(g_staging_mu);
+        new_cap = g_staging[W->device].cap[6];
+    }
+    if (new_cap != old_cap) HIPCK(hipMemset(cnt, 0, new_cap));
+    wk->partials = (float *)part;
+    wk->counters = (int *)cnt;
+    wk->n_cu = n_cu;
+    return 0;
+}
 }  // namespace
+
+extern "C" int hq_dequant_f32(const hq_mat *W, uint32_t row0, uint32_t nrows, float *out, void *stream) {
+    if (!W || !out) return fail("hq_dequant_f32: null argument");
+    if (row0 > W->m.rows || nrows > W->m.rows - row0)
+        return fail("hq_dequant_f32: rows [%u, %u) outside [0, %u)", row0, row0 + nrows, W->m.rows);
+    if (!aligned(out, 16)) return fail("hq_dequant_f32: output must be 16-byte aligned");
+    if (nrows == 0) return 0;
+    if (use_device(W->device)) return -1;
+    HIPCK(hq_launch_dequant(&W->m, row0, nullptr, nrows, out, S(stream)));
+    return 0;
+}
+
+extern "C" int hq_gemm(const hq_mat *W, const uint16_t *A, int M, void *C, int c_is_f32, int accumulate, void *stream) {
+    if (!W || !A || !C) return fail("hq_gemm: null argument");
+    if (M < 1 || M > (1 << 23)) return fail("hq_gemm: M = %d (1 .. 8388608)", M);
+    if (!aligned(A, 16)) return fail("hq_gemm: A must be 16-byte aligned");
+    if (!aligned(C, c_is_f32 ? 4 : 2)) return fail("hq_gemm: C is misaligned");
+    if (use_device(W->device)) return -1;
+    if (M == 1) {
+        HIPCK(hq_launch_gemv(&W->m, A, C, c_is_f32, accumulate, S(stream)));
+        return 0;
+    }
+    HqGemmWork wk;
+    if (gemm_work(W, M, &wk)) return -1;
+    HIPCK(hq_launch_gemm(&W->m, A, M, C, c_is_f32, accumulate, wk, S(stream)));
+    return 0;
+}
+
+extern "C" int hq_gemv(const hq_mat *W, const uint16_t *a, void *c, int c_is_f32, int accumulate, void *stream) {
+    return hq_gemm(W, a, 1, c, c_is_f32, accumulate, stream);
+}
+
+extern "C" int hq_gather_dot_dev(const hq_mat *head, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
+                                 void *stream) {
+    if (!head || !H || !ids || !out) return fail("hq_gather_dot: null argument");
+    if (B < 0 || k < 0 || (long)B * k > (1l << 30)) return fail("hq_gather_dot: B = %d, k = %d", B, k);
+    if (!aligned(H, 16)) return fail("hq_gather_dot: H must be 16-byte aligned");
+    if ((long)B * k == 0) return 0;
+    if (use_device(head->device)) return -1;
+    HIPCK(hq_launch_gather(&head->m, H, ids, B, k, out, S(stream)));
+    return 0;
+}
+
 
 extern "C" int hq_gather_dot(const hq_mat *head, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
                              void *stream) {
@@ -412,6 +457,8 @@ extern "C" int hq_time_gemm(hq_mat *const *Ws, int n_w, const uint16_t *A, int M
     for (int i = 0; i < n_w; i++)
         if (!Ws[i] || Ws[i]->m.rows != Ws[0]->m.rows || Ws[i]->m.cols != Ws[0]->m.cols || Ws[i]->m.type != Ws[0]->m.type)
             return fail("hq_time_gemm: matrices differ in shape or type");
+    if (hq_gemm(Ws[0], A, M, C, c_is_f32, 0, stream)) return -1;  // sizes the workspace outside the capture
+    HIPCK(hipStreamSynchronize(S(stream)));
     return time_graph(iters, reps, stream, ms,
                       [&](int i) { return hq_gemm(Ws[i % n_w], A, M, C, c_is_f32, 0, stream); });
 }

@@ -235,59 +235,92 @@ __global__ void __launch_bounds__(256) k_gather_q4_k(const uint8_t *__restrict__
 }
 
 // ============================================================================ MFMA GEMM
-// Tile: BM = 16*MB rows of A (M) by BN = 64*NB columns (N, weight rows); 4 waves, wave w owns
-// columns [16*NB*w, 16*NB*(w+1)) of the tile and all BM rows. K advances in chunks of KC = 256
-// activations staged in LDS (row stride LDA halves, padded against bank conflicts).
+// Work decomposition (Stream-K): the output is cut into tiles of BM = 16*MB rows (M) by
+// BN = 64*NB columns (N, weight rows), and each tile into K-units of KC = 256 activations (one
+// Q4_K super-block, eight Q8_0 blocks). The tile-major list of (tile, unit) pairs is split into G
+// equal contiguous ranges, one per persistent workgroup (G = number of CUs), so every CU gets the
+// same MFMA work whatever the shape (no wave quantization). A tile cut between workgroups is
+// combined through a workspace: each contributor stores its fp32 partial tile, then increments the
+// tile's counter; the contributor that brings the counter to its final value adds the others'
+// partials and writes C, then resets the counter. No workgroup ever waits on another.
+//
+// Inside a workgroup: 4 waves, wave w owns columns [16*NB*w, 16*NB*(w+1)) of the tile and all BM
+// rows. Pipeline per unit: the next unit's activation tile is streamed global -> LDS by
+// global_load_lds_dwordx4 (no registers) into the other half of a double buffer, and each wave
+// prefetches the next unit's weight bytes into registers, while the current unit is decoded and
+// multiplied. One barrier per unit.
+//
+// LDS tile layout: row r holds 32 slots of 16 bytes; slot p holds activation chunk p ^ (r & 15)
+// (XOR swizzle), so the 16 lanes of an MFMA operand read (16 rows, same chunk) hit 16 distinct
+// 4-bank groups and the DMA writes stay contiguous (two rows per 64-lane instruction).
 //
 // v_mfma_f32_16x16x32_f16 operands (per lane l: ln = l % 16, lg = l / 16): A holds row ln,
 // 8 k-slots of group lg; B holds column ln, the same 8 k-slots; D holds column ln, rows 4*lg..4*lg+3.
 // The k-slot -> k mapping inside one MFMA is free as long as A and B agree; it is chosen so each
-// lane's 8 weights come from one 16-byte load and each lane's 8 activations are 16 contiguous bytes.
+// lane's 8 weights come from one 16-byte load and each lane's 8 activations are one 16-byte slot.
+//
+// Q4_K: the B operand is the exact integer s*q; the per-unit fp32 accumulator is folded with d.
+// The min term dmin * sum_sub m_sub * S_sub (S = fp32 sum of the sub-block's 32 activations, from
+// v_dot2_f32_f16 over the LDS tile, split hi + lo fp16) is one MFMA per unit with the integer m as
+// B operand, folded with dmin. S of unit u is complete only after the next barrier, so the min
+// term of unit u is applied in unit u + 1 (or right before a tile is finished).
 namespace {
 constexpr int KC = 256;
-constexpr int LDA = KC + 8;
 
-template <int MB>
-struct Smem {
-    _Float16 a[16 * MB * LDA];
-    _Float16 s[16 * MB * 16];  // Q4_K: per row, fp16 hi[8] then lo[8] of the 8 sub-block sums
+typedef __attribute__((address_space(3))) void lds_void;
+
+DEV lds_void *lds_ptr(const void *p) { return (lds_void *)(uintptr_t)p; }
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Raw buffer over `bytes` bytes: loads at offsets >= bytes return zero.
+DEV rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, 0x00020000);
+}
+
+DEV u4v buf_load16(rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+// Activation tile DMA: instruction qq of wave w moves rows r = 8qq + 2w + (lane >> 5) (two 256-half
+// rows per 64-lane instruction) into LDS slots (r, lane & 31). The per-lane byte offset is
+// a_base[qq & 1] (row and swizzled chunk) plus the uniform qq * 16 * K + 2 * k0 in soffset.
+struct ADma {
+    uint32_t base[2];
 };
 
 template <int MB>
-DEV void stage_a(Smem<MB> &sm, const uint16_t *__restrict__ A, int M, int K, int m0, int k0, int kc) {
-    constexpr int BM = 16 * MB;
-    for (int i = threadIdx.x; i < BM * (KC / 8); i += 256) {
-        const int r = i / (KC / 8), kk = (i % (KC / 8)) * 8, m = m0 + r;
-        u4v v = {0u, 0u, 0u, 0u};
-        if (m < M && kk < kc) v = *(const u4v *)(A + (size_t)m * K + k0 + kk);
-        *(u4v *)(&sm.a[r * LDA + kk]) = v;
+DEV ADma adma_setup(int K, int m0) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, p = lane & 31;
+    const int r0 = 2 * wave + (lane >> 5);
+    ADma d;
+#pragma unroll
+    for (int x = 0; x < 2; x++) {
+        const int c = p ^ ((8 * x + r0) & 15);
+        d.base[x] = (uint32_t)((m0 + r0) * K + 8 * c) * 2u;
+    }
+    return d;
+}
+
+template <int MB>
+DEV void dma_a(_Float16 *buf, rsrc_t ra, const ADma &d, int K, int k0) {
+    constexpr int INSTR = 16 * MB / 2;
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int qq = 0; qq < (INSTR + 3) / 4; qq++) {
+        const int q = 4 * qq + wave;
+        if (INSTR % 4 == 0 || q < INSTR)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, lds_ptr(buf + q * 512), 16, d.base[qq & 1],
+                                                     (uint32_t)(qq * 16 * K + 2 * k0), 0, 0);
     }
 }
 
-// Q4_K: S[r][sub] = fp32 sum of the 32 staged activations of sub-block sub, split hi + lo fp16.
-template <int MB>
-DEV void stage_sums(Smem<MB> &sm) {
-    constexpr int BM = 16 * MB;
-    for (int i = threadIdx.x; i < BM * 8; i += 256) {
-        const int r = i >> 3, sub = i & 7;
-        const h8 *p = (const h8 *)&sm.a[r * LDA + 32 * sub];
-        float s = 0.f;
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const h8 x = p[v];
-#pragma unroll
-            for (int e = 0; e < 8; e++) s += (float)x[e];
-        }
-        const _Float16 hi = (_Float16)s;
-        const _Float16 lo = (_Float16)(s - (float)hi);
-        sm.s[r * 16 + sub] = hi;
-        sm.s[r * 16 + 8 + sub] = lo;
-    }
-}
+// A fragment: row r (= 16*i + ln), activation chunk c (8 halves).
+DEV h8 a_frag(const _Float16 *buf, int r, int c) { return *(const h8 *)(buf + r * KC + 8 * (c ^ (r & 15))); }
 
 DEV f4 mfma(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
 
-// B fragment from 4 bytes (u = q+128 biased int8) x 2 words -> fp16(q*d), 8 values.
+// B fragment from 8 bytes u = q + 128 (two words) -> fp16(q * d): one rounding of the exact product.
 DEV h8 frag_q8_0(uint32_t w0, uint32_t w1, h2 d2) {
     const h2 bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
     const uint32_t w[2] = {w0, w1};
@@ -304,8 +337,8 @@ DEV h8 frag_q8_0(uint32_t w0, uint32_t w1, h2 d2) {
     return out;
 }
 
-// B fragment of exact integers s*q from the low (hi_nib = false) or high nibbles of 8 bytes.
-// fp16(1024 + q) * s - 1024*s, or fp16(1024 + 16q) * (s/16) - 64*s: one fused rounding of an
+// B fragment of exact integers s*q from the low (HI_NIB = false) or high nibbles of 8 bytes:
+// fp16(1024 + q) * s - 1024*s, or fp16(1024 + 16q) * (s/16) - 64*s, one fused rounding of an
 // exact integer <= 945, hence exact.
 template <bool HI_NIB>
 DEV h8 frag_q4_k(uint32_t w0, uint32_t w1, h2 mul, h2 add) {
@@ -324,67 +357,27 @@ DEV h8 frag_q4_k(uint32_t w0, uint32_t w1, h2 mul, h2 add) {
     return out;
 }
 
-DEV h8 lds_frag(const _Float16 *p) { return *(const h8 *)p; }
+// fp16 pair (1024 + b0, 1024 + b1) minus 1024: the bytes as exact fp16 integers.
+DEV h2 bytes_f16(uint32_t w, bool hi_pair) {
+    const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    return as_h2(hi_pair ? perm_hi(w) : perm_lo(w)) - k1024;
+}
 
-}  // namespace
+struct SkPlan {
+    int tm, tiles, upt;  // M-tiles, tiles, K-units per tile
+    int base, extra;     // workgroup w owns units [w*base + min(w, extra), (w+1)*base + min(w+1, extra))
+    int G;               // workgroups
+};
+
+DEV int sk_start(const SkPlan &p, int w) { return w * p.base + (w < p.extra ? w : p.extra); }
+DEV int sk_owner(const SkPlan &p, int u) {
+    const int big = p.extra * (p.base + 1);
+    return u < big ? u / (p.base + 1) : p.extra + (u - big) / p.base;
+}
 
 template <int MB, int NB>
-__global__ void __launch_bounds__(256) k_gemm_q8_0(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ dpl,
-                                                   int ldd, const uint16_t *__restrict__ A, int M, int N, int K,
-                                                   void *C, int c_f32, int accumulate) {
-    __shared__ Smem<MB> sm;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, ln = lane & 15, lg = lane >> 4;
-    const int m0 = blockIdx.y * 16 * MB, nw = blockIdx.x * 64 * NB + wave * 16 * NB;
-    f4 acc[MB][NB];
-#pragma unroll
-    for (int i = 0; i < MB; i++)
-#pragma unroll
-        for (int j = 0; j < NB; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
-
-    const uint8_t *wrow[NB];
-    const uint16_t *drow[NB];
-#pragma unroll
-    for (int j = 0; j < NB; j++) {
-        int n = nw + 16 * j + ln;
-        n = n < N ? n : N - 1;
-        wrow[j] = qs + (size_t)n * K;
-        drow[j] = dpl + (size_t)n * ldd;
-    }
-    for (int k0 = 0; k0 < K; k0 += KC) {
-        const int kc = K - k0 < KC ? K - k0 : KC;
-        __syncthreads();
-        stage_a<MB>(sm, A, M, K, m0, k0, kc);
-        __syncthreads();
-        // 64-value steps: lane (ln, lg) loads weights [kk + 16*lg, +16) of its row (one block);
-        // MFMA t in {0, 1} takes bytes 8t..8t+7 of that load.
-        for (int kk = 0; kk < kc; kk += 64) {
-            const bool full = kk + 64 <= kc;  // a 32-value tail leaves lanes lg >= 2 without data
-            h8 bf[NB][2];
-#pragma unroll
-            for (int j = 0; j < NB; j++) {
-                u4v q = {0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
-                uint16_t dv = 0;
-                if (full || lg < 2) {
-                    q = *(const u4v *)(wrow[j] + k0 + kk + 16 * lg);
-                    dv = drow[j][(k0 + kk) / 32 + (lg >> 1)];
-                }
-                const _Float16 dh = __builtin_bit_cast(_Float16, dv);
-                const h2 d2 = {dh, dh};
-                bf[j][0] = frag_q8_0(q.x, q.y, d2);
-                bf[j][1] = frag_q8_0(q.z, q.w, d2);
-            }
-#pragma unroll
-            for (int t = 0; t < 2; t++) {
-#pragma unroll
-                for (int i = 0; i < MB; i++) {
-                    const h8 af = lds_frag(&sm.a[(16 * i + ln) * LDA + kk + 16 * lg + 8 * t]);
-#pragma unroll
-                    for (int j = 0; j < NB; j++) acc[i][j] = mfma(af, bf[j][t], acc[i][j]);
-                }
-            }
-        }
-    }
-    // D layout: lane holds column ln, rows 4*lg + e
+DEV void store_tile(void *C, const f4 (&acc)[MB][NB], int M, int N, int m0, int nw, int ln, int lg, int c_f32,
+                    int accumulate) {
 #pragma unroll
     for (int j = 0; j < NB; j++) {
         const int n = nw + 16 * j + ln;
@@ -399,47 +392,301 @@ __global__ void __launch_bounds__(256) k_gemm_q8_0(const uint8_t *__restrict__ q
     }
 }
 
+// Tile finished by this workgroup: store it, or run the partial-tile protocol.
 template <int MB, int NB>
-__global__ void __launch_bounds__(256) k_gemm_q4_k(const uint8_t *__restrict__ W, size_t row_bytes,
-                                                   const uint16_t *__restrict__ A, int M, int N, int K, void *C,
-                                                   int c_f32, int accumulate) {
-    __shared__ Smem<MB> sm;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, ln = lane & 15, lg = lane >> 4;
-    const int m0 = blockIdx.y * 16 * MB, nw = blockIdx.x * 64 * NB + wave * 16 * NB;
-    f4 acc[MB][NB];
+DEV void finish_tile(f4 (&acc)[MB][NB], const SkPlan &p, int w, int u0, int u1, int tile, int *s_flag,
+                     float *__restrict__ partials, int *__restrict__ counters, void *C, int M, int N, int m0, int nw,
+                     int ln, int lg, int c_f32, int accumulate) {
+    const int t0 = tile * p.upt, t1 = t0 + p.upt;
+    if (t0 >= u0 && t1 <= u1) {
+        store_tile<MB, NB>(C, acc, M, N, m0, nw, ln, lg, c_f32, accumulate);
+        return;
+    }
+    constexpr int PER = 256 * MB * NB * 4;  // floats per partial tile
+    const int tid = threadIdx.x;
+    // slot 2w: the tile this workgroup starts in; 2w + 1: the tile it ends in. Partials are written
+    // and read with agent-scope (cross-XCD coherent) accesses, which bypass the non-coherent L2, so
+    // no L2 write-back or invalidation is needed; the counter update is ordered after the stores
+    // by waiting for them (stores count in vmcnt) before the barrier.
+    const int slot = tile == u0 / p.upt ? 2 * w : 2 * w + 1;
+    float *mine = partials + (size_t)slot * PER;
 #pragma unroll
     for (int i = 0; i < MB; i++)
 #pragma unroll
-        for (int j = 0; j < NB; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
-
-    const uint8_t *wrow[NB];
+        for (int j = 0; j < NB; j++)
 #pragma unroll
-    for (int j = 0; j < NB; j++) {
-        int n = nw + 16 * j + ln;
-        n = n < N ? n : N - 1;
-        wrow[j] = W + (size_t)n * row_bytes;
+            for (int e = 0; e < 4; e++)
+                __hip_atomic_store(mine + ((i * NB + j) * 4 + e) * 256 + tid, acc[i][j][e], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    const int wf = sk_owner(p, t0), wl = sk_owner(p, t1 - 1);
+    if (tid == 0) {
+        const int prev = atomicAdd(&counters[tile], 1);
+        const int last = prev == wl - wf;
+        if (last) atomicExch(&counters[tile], 0);
+        *s_flag = last;
     }
-    // Lane (ln, lg) loads chunk c = 4L + lg (L = 0, 1) of the 128 quant bytes: p = 2L + lg/2,
-    // h = lg%2. MFMA i = 4L + t: t = 0/1 low nibbles of bytes 0-7 / 8-15, t = 2/3 high nibbles;
-    // its activations start at k = 64p + 16h + 8(t&1) + 32(t>>1); its sub-block is 2p + (t>>1).
-    const int pA = lg >> 1, hA = lg & 1;
-    for (int k0 = 0; k0 < K; k0 += KC) {
-        __syncthreads();
-        stage_a<MB>(sm, A, M, K, m0, k0, KC);
-        __syncthreads();
-        stage_sums<MB>(sm);
-        __syncthreads();
-        const int sb = k0 / 256;
+    __syncthreads();
+    if (!*s_flag) return;
+    for (int o = wf; o <= wl; o++) {
+        if (o == w) continue;
+        const int os = tile == sk_start(p, o) / p.upt ? 2 * o : 2 * o + 1;
+        float *src = partials + (size_t)os * PER;
+#pragma unroll
+        for (int i = 0; i < MB; i++)
+#pragma unroll
+            for (int j = 0; j < NB; j++)
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    acc[i][j][e] += __hip_atomic_load(src + ((i * NB + j) * 4 + e) * 256 + tid, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+    }
+    store_tile<MB, NB>(C, acc, M, N, m0, nw, ln, lg, c_f32, accumulate);
+}
+}  // namespace
+
+struct GemmArgs {
+    const uint8_t *qs;    // Q8_0 quant plane / Q4_K blocks
+    const uint16_t *d;    // Q8_0 scale plane
+    int ldd;
+    size_t row_bytes;
+    const uint16_t *A;
+    int M, N, K;
+    void *C;
+    int c_f32, accumulate;
+    SkPlan plan;
+    float *partials;
+    int *counters;
+};
+
+DEV int sk_worker(int G) {
+    // consecutive ranges (which share tiles and weight slabs) on the same XCD: workgroups are dealt
+    // round-robin to the 8 XCDs
+    const int bid = blockIdx.x;
+    return G % 8 == 0 ? (bid % 8) * (G / 8) + bid / 8 : bid;
+}
+
+template <int MB, int NB>
+__global__ void __launch_bounds__(256) k_gemm_q8_0(GemmArgs g) {
+    __shared__ __attribute__((aligned(16))) _Float16 sa[2][16 * MB * KC];
+    __shared__ int s_flag;
+    const SkPlan &p = g.plan;
+    const int w = sk_worker(p.G), u0 = sk_start(p, w), u1 = sk_start(p, w + 1);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, ln = lane & 15, lg = lane >> 4;
+    const int M = g.M, N = g.N, K = g.K;
+    const rsrc_t ra = make_rsrc(g.A, (uint32_t)((size_t)M * K * 2));
+    const rsrc_t rq = make_rsrc(g.qs, (uint32_t)((size_t)N * K));
+    const rsrc_t rd = make_rsrc(g.d, (uint32_t)((size_t)N * g.ldd * 2));
+    // per-tile lane offsets: rows beyond N read zero weights
+    ADma adma;
+    uint32_t vq[NB], vd[NB];
+    auto tile_setup = [&](int tile) {
+        const int m0 = (tile % p.tm) * 16 * MB, nw = (tile / p.tm) * 64 * NB + wave * 16 * NB;
+        adma = adma_setup<MB>(K, m0);
 #pragma unroll
         for (int j = 0; j < NB; j++) {
-            const uint8_t *b = wrow[j] + (size_t)sb * 144;
-            const u4v hdr = *(const u4v *)b;
-            const u4v q0 = *(const u4v *)(b + 16 + 16 * lg);
-            const u4v q1 = *(const u4v *)(b + 16 + 64 + 16 * lg);
+            const uint32_t n = (uint32_t)(nw + 16 * j + ln);
+            vq[j] = n * (uint32_t)K + 16u * lg;
+            vd[j] = n * (uint32_t)g.ldd * 2u;
+        }
+    };
+    // lane (ln, lg) holds weights [64s + 16lg, +16) of the unit for s = 0..3 and its 8 block scales
+    auto load_w = [&](int k0, u4v (&q)[NB][4], u4v (&d)[NB]) {
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            d[j] = buf_load16(rd, vd[j], (uint32_t)(k0 / 16));
+#pragma unroll
+            for (int s = 0; s < 4; s++) q[j][s] = buf_load16(rq, vq[j] + 64u * s, (uint32_t)k0);
+        }
+    };
+    f4 acc[MB][NB];
+    u4v qc[NB][4], dc[NB];
+    int cur_tile = u0 / p.upt;
+    tile_setup(cur_tile);
+    dma_a<MB>(sa[0], ra, adma, K, (u0 % p.upt) * KC);
+    load_w((u0 % p.upt) * KC, qc, dc);
+    for (int u = u0; u < u1; u++) {
+        const int cb = (u - u0) & 1, tile = u / p.upt, ku = u % p.upt;
+        const int m0 = (tile % p.tm) * 16 * MB, nw = (tile / p.tm) * 64 * NB + wave * 16 * NB;
+        const int k0 = ku * KC, kc = K - k0 < KC ? K - k0 : KC;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        u4v qn[NB][4], dn[NB];
+        if (u + 1 < u1) {
+            const int t1 = (u + 1) / p.upt;
+            if (t1 != cur_tile) {
+                cur_tile = t1;
+                tile_setup(t1);
+            }
+            const int k1 = ((u + 1) % p.upt) * KC;
+            dma_a<MB>(sa[cb ^ 1], ra, adma, K, k1);
+            load_w(k1, qn, dn);
+        }
+        if (u == u0 || ku == 0) {
+#pragma unroll
+            for (int i = 0; i < MB; i++)
+#pragma unroll
+                for (int j = 0; j < NB; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+        }
+        // decode: bf[j][2s + t] covers activations 64s + 16lg + 8t .. +8 (chunk index 8s + 2lg + t);
+        // pieces past the end of K (last unit of a row only) get a zero scale
+        h8 bf[NB][8];
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            const uint32_t dw[4] = {dc[j].x, dc[j].y, dc[j].z, dc[j].w};
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const int blk = 2 * s + (lg >> 1);  // block of this lane's 16 weights
+                const uint32_t dd = dw[blk >> 1] >> (16 * (blk & 1));
+                const int valid = 64 * s + 16 * lg < kc;
+                const _Float16 dh = __builtin_bit_cast(_Float16, (uint16_t)(valid ? dd : 0u));
+                const h2 d2 = {dh, dh};
+                bf[j][2 * s] = frag_q8_0(qc[j][s].x, qc[j][s].y, d2);
+                bf[j][2 * s + 1] = frag_q8_0(qc[j][s].z, qc[j][s].w, d2);
+            }
+        }
+        const _Float16 *buf = sa[cb];
+#pragma unroll
+        for (int i = 0; i < MB; i++) {
+            const int r = 16 * i + ln;
+#pragma unroll
+            for (int f = 0; f < 8; f++) {
+                const h8 af = a_frag(buf, r, 8 * (f >> 1) + 2 * lg + (f & 1));
+#pragma unroll
+                for (int j = 0; j < NB; j++) acc[i][j] = mfma(af, bf[j][f], acc[i][j]);
+            }
+        }
+        if (ku == p.upt - 1 || u == u1 - 1)
+            finish_tile<MB, NB>(acc, p, w, u0, u1, tile, &s_flag, g.partials, g.counters, g.C, M, N, m0, nw, ln, lg,
+                                g.c_f32, g.accumulate);
+        if (u + 1 < u1) {
+#pragma unroll
+            for (int j = 0; j < NB; j++) {
+                dc[j] = dn[j];
+#pragma unroll
+                for (int s = 0; s < 4; s++) qc[j][s] = qn[j][s];
+            }
+        }
+    }
+}
+
+template <int MB, int NB>
+__global__ void __launch_bounds__(256) k_gemm_q4_k(GemmArgs g) {
+    constexpr int BM = 16 * MB;
+    __shared__ __attribute__((aligned(16))) _Float16 sa[2][BM * KC];
+    __shared__ __attribute__((aligned(16))) _Float16 ss[2][BM * 16];  // per row: sums hi[8], lo[8]
+    __shared__ int s_flag;
+    const SkPlan &p = g.plan;
+    const int w = sk_worker(p.G), u0 = sk_start(p, w), u1 = sk_start(p, w + 1);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
+    const int M = g.M, N = g.N, K = g.K;
+    const rsrc_t ra = make_rsrc(g.A, (uint32_t)((size_t)M * K * 2));
+    const rsrc_t rw = make_rsrc(g.qs, (uint32_t)((size_t)N * g.row_bytes));
+    ADma adma;
+    uint32_t vh[NB], vq[NB];
+    // Lane (ln, lg) loads chunk c = 4L + lg (L = 0, 1) of the 128 quant bytes: p = 2L + lg/2,
+    // h = lg%2. MFMA 4L + t: t = 0/1 low nibbles of bytes 0-7 / 8-15, t = 2/3 high nibbles; its
+    // activations start at k = 64p + 16h + 8(t&1) + 32(t>>1) (chunk k/8); sub-block 2p + (t>>1).
+    auto tile_setup = [&](int tile) {
+        const int m0 = (tile % p.tm) * BM, nw = (tile / p.tm) * 64 * NB + wave * 16 * NB;
+        adma = adma_setup<MB>(K, m0);
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            const uint32_t n = (uint32_t)(nw + 16 * j + ln);
+            vh[j] = n * (uint32_t)g.row_bytes;
+            vq[j] = vh[j] + 16u + 16u * lg;
+        }
+    };
+    auto load_w = [&](int sb, u4v (&h)[NB], u4v (&q0)[NB], u4v (&q1)[NB]) {
+        const uint32_t so = (uint32_t)sb * 144u;
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            h[j] = buf_load16(rw, vh[j], so);
+            q0[j] = buf_load16(rw, vq[j], so);
+            q1[j] = buf_load16(rw, vq[j] + 64u, so);
+        }
+    };
+    const int pA = lg >> 1, hA = lg & 1;
+    f4 acc[MB][NB];
+    u4v hc[NB], q0c[NB], q1c[NB];
+    // min term deferred from the previous unit: integer m operand and -dmin per column block
+    h8 bm_prev[NB];
+    float ndmin_prev[NB];
+    bool min_pending = false;
+    int cur_tile = u0 / p.upt;
+    tile_setup(cur_tile);
+    dma_a<MB>(sa[0], ra, adma, K, (u0 % p.upt) * KC);
+    load_w(u0 % p.upt, hc, q0c, q1c);
+    auto apply_min = [&](const _Float16 *sbuf) {
+#pragma unroll
+        for (int i = 0; i < MB; i++) {
+            // lanes lg even: sums hi, odd: lo (lanes lg >= 2 meet a zero B operand)
+            const h8 as = *(const h8 *)(sbuf + (16 * i + ln) * 16 + 8 * (lg & 1));
+#pragma unroll
+            for (int j = 0; j < NB; j++) {
+                const f4 mp = mfma(as, bm_prev[j], f4{0.f, 0.f, 0.f, 0.f});
+                acc[i][j] += mp * ndmin_prev[j];
+            }
+        }
+    };
+    for (int u = u0; u < u1; u++) {
+        const int cb = (u - u0) & 1, tile = u / p.upt, sb = u % p.upt;
+        const int m0 = (tile % p.tm) * BM, nw = (tile / p.tm) * 64 * NB + wave * 16 * NB;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (min_pending) {  // the previous unit of this tile: its sums are complete now
+            apply_min(ss[cb ^ 1]);
+            min_pending = false;
+        }
+        u4v hn[NB], q0n[NB], q1n[NB];
+        if (u + 1 < u1) {
+            const int t1 = (u + 1) / p.upt;
+            if (t1 != cur_tile) {
+                cur_tile = t1;
+                tile_setup(t1);
+            }
+            const int sb1 = (u + 1) % p.upt;
+            dma_a<MB>(sa[cb ^ 1], ra, adma, K, sb1 * KC);
+            load_w(sb1, hn, q0n, q1n);
+        }
+        if (u == u0 || sb == 0) {
+#pragma unroll
+            for (int i = 0; i < MB; i++)
+#pragma unroll
+                for (int j = 0; j < NB; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+        }
+        const _Float16 *buf = sa[cb];
+        // sub-block sums of this unit: thread -> (row, sub) pairs, rows fastest (conflict-free reads)
+        {
+            const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+            for (int q = 0; q < (BM * 8 + 255) / 256; q++) {
+                const int pr = tid + 256 * q;
+                if ((BM * 8) % 256 == 0 || pr < BM * 8) {
+                    const int r = pr % BM, sub = pr / BM;
+                    float s = 0.f;
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        const u4v x = *(const u4v *)(buf + r * KC + 8 * ((4 * sub + v) ^ (r & 15)));
+                        s = __builtin_amdgcn_fdot2(as_h2(x.x), one, s, false);
+                        s = __builtin_amdgcn_fdot2(as_h2(x.y), one, s, false);
+                        s = __builtin_amdgcn_fdot2(as_h2(x.z), one, s, false);
+                        s = __builtin_amdgcn_fdot2(as_h2(x.w), one, s, false);
+                    }
+                    const _Float16 hi = (_Float16)s;
+                    ss[cb][r * 16 + sub] = hi;
+                    ss[cb][r * 16 + 8 + sub] = (_Float16)(s - (float)hi);
+                }
+            }
+        }
+        h8 bf[NB][8];
+        float dsc[NB];
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
             uint32_t sw0, sw1, mw0, mw1;
-            q4k_scale_words(hdr.y, hdr.z, hdr.w, sw0, sw1, mw0, mw1);
-            // scales of this lane's sub-blocks: L=0 -> subs 2pA, 2pA+1 (sw0); L=1 -> 4+2pA, 5+2pA (sw1)
-            h2 mulL[2][2], addL[2][2];  // [L][nibble half]
+            q4k_scale_words(hc[j].y, hc[j].z, hc[j].w, sw0, sw1, mw0, mw1);
+            h2 mulL[2][2], addL[2][2];
 #pragma unroll
             for (int L = 0; L < 2; L++) {
                 const uint32_t sw = L ? sw1 : sw0;
@@ -452,54 +699,51 @@ __global__ void __launch_bounds__(256) k_gemm_q4_k(const uint8_t *__restrict__ W
                     addL[L][hi] = h2{add, add};
                 }
             }
-            h8 bf[8];
-            bf[0] = frag_q4_k<false>(q0.x, q0.y, mulL[0][0], addL[0][0]);
-            bf[1] = frag_q4_k<false>(q0.z, q0.w, mulL[0][0], addL[0][0]);
-            bf[2] = frag_q4_k<true>(q0.x, q0.y, mulL[0][1], addL[0][1]);
-            bf[3] = frag_q4_k<true>(q0.z, q0.w, mulL[0][1], addL[0][1]);
-            bf[4] = frag_q4_k<false>(q1.x, q1.y, mulL[1][0], addL[1][0]);
-            bf[5] = frag_q4_k<false>(q1.z, q1.w, mulL[1][0], addL[1][0]);
-            bf[6] = frag_q4_k<true>(q1.x, q1.y, mulL[1][1], addL[1][1]);
-            bf[7] = frag_q4_k<true>(q1.z, q1.w, mulL[1][1], addL[1][1]);
-            // min-term operand: lanes lg 0,1 -> -(dmin*m) hi, lanes 2,3 -> lo; k-slot e = sub-block e
-            const float dmin = h2f((uint16_t)(hdr.x >> 16));
-            h8 bmin;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float v = dmin * (float)byte_of(e < 4 ? mw0 : mw1, e & 3);
-                const _Float16 vh = (_Float16)v;
-                bmin[e] = lg < 2 ? -vh : -(_Float16)(v - (float)vh);
-            }
-            const float d = h2f((uint16_t)hdr.x);
-#pragma unroll
-            for (int i = 0; i < MB; i++) {
-                const _Float16 *arow = &sm.a[(16 * i + ln) * LDA];
-                f4 part = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int L = 0; L < 2; L++)
-#pragma unroll
-                    for (int t = 0; t < 4; t++) {
-                        const int kA = 64 * (2 * L + pA) + 16 * hA + 8 * (t & 1) + 32 * (t >> 1);
-                        part = mfma(lds_frag(arow + kA), bf[4 * L + t], part);
-                    }
-                acc[i][j] += part * d;
-                // A side of the min term: lanes lg 0,2 -> S hi, lanes 1,3 -> S lo
-                const h8 as = lds_frag(&sm.s[(16 * i + ln) * 16 + 8 * (lg & 1)]);
-                acc[i][j] = mfma(as, bmin, acc[i][j]);
-            }
+            bf[j][0] = frag_q4_k<false>(q0c[j].x, q0c[j].y, mulL[0][0], addL[0][0]);
+            bf[j][1] = frag_q4_k<false>(q0c[j].z, q0c[j].w, mulL[0][0], addL[0][0]);
+            bf[j][2] = frag_q4_k<true>(q0c[j].x, q0c[j].y, mulL[0][1], addL[0][1]);
+            bf[j][3] = frag_q4_k<true>(q0c[j].z, q0c[j].w, mulL[0][1], addL[0][1]);
+            bf[j][4] = frag_q4_k<false>(q1c[j].x, q1c[j].y, mulL[1][0], addL[1][0]);
+            bf[j][5] = frag_q4_k<false>(q1c[j].z, q1c[j].w, mulL[1][0], addL[1][0]);
+            bf[j][6] = frag_q4_k<true>(q1c[j].x, q1c[j].y, mulL[1][1], addL[1][1]);
+            bf[j][7] = frag_q4_k<true>(q1c[j].z, q1c[j].w, mulL[1][1], addL[1][1]);
+            // min operand for the next barrier: lanes lg 0, 1 carry m_0..m_7 (k-slot e = sub-block e)
+            const h2 m01 = bytes_f16(mw0, false), m23 = bytes_f16(mw0, true);
+            const h2 m45 = bytes_f16(mw1, false), m67 = bytes_f16(mw1, true);
+            const h8 mv = {m01.x, m01.y, m23.x, m23.y, m45.x, m45.y, m67.x, m67.y};
+            bm_prev[j] = lg < 2 ? mv : h8{0, 0, 0, 0, 0, 0, 0, 0};
+            ndmin_prev[j] = -h2f((uint16_t)(hc[j].x >> 16));
+            dsc[j] = h2f((uint16_t)hc[j].x);
         }
-    }
 #pragma unroll
-    for (int j = 0; j < NB; j++) {
-        const int n = nw + 16 * j + ln;
-        if (n >= N) continue;
+        for (int i = 0; i < MB; i++) {
+            const int r = 16 * i + ln;
+            f4 part[NB];
 #pragma unroll
-        for (int i = 0; i < MB; i++)
+            for (int j = 0; j < NB; j++) part[j] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int m = m0 + 16 * i + 4 * lg + e;
-                if (m < M) store_out(C, (size_t)m * N + n, acc[i][j][e], c_f32, accumulate);
-            }
+            for (int L = 0; L < 2; L++)
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const h8 af = a_frag(buf, r, 8 * (2 * L + pA) + 2 * hA + (t & 1) + 4 * (t >> 1));
+#pragma unroll
+                    for (int j = 0; j < NB; j++) part[j] = mfma(af, bf[j][4 * L + t], part[j]);
+                }
+#pragma unroll
+            for (int j = 0; j < NB; j++) acc[i][j] += part[j] * dsc[j];
+        }
+        min_pending = true;
+        if (sb == p.upt - 1 || u == u1 - 1) {
+            __syncthreads();  // this unit's sums, written by other waves
+            apply_min(ss[cb]);
+            min_pending = false;
+            finish_tile<MB, NB>(acc, p, w, u0, u1, tile, &s_flag, g.partials, g.counters, g.C, M, N, m0, nw, ln, lg,
+                                g.c_f32, g.accumulate);
+        }
+        if (u + 1 < u1) {
+#pragma unroll
+            for (int j = 0; j < NB; j++) hc[j] = hn[j], q0c[j] = q0n[j], q1c[j] = q1n[j];
+        }
     }
 }
 
@@ -549,43 +793,58 @@ hipError_t hq_launch_gather(const hq_dev_mat *W, const uint16_t *H, const uint32
     return hipGetLastError();
 }
 
-template <int MB, int NB>
-static void launch_gemm_t(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
-                          hipStream_t st) {
-    const int N = (int)W->rows, K = (int)W->cols;
-    dim3 grid((unsigned)((N + 64 * NB - 1) / (64 * NB)), (unsigned)((M + 16 * MB - 1) / (16 * MB)));
-    if (W->type == HQ_TYPE_Q8_0)
-        k_gemm_q8_0<MB, NB><<<grid, 256, 0, st>>>(W->qs, W->d, W->ldd, A, M, N, K, C, c_f32, accumulate);
-    else
-        k_gemm_q4_k<MB, NB><<<grid, 256, 0, st>>>(W->qs, W->row_bytes, A, M, N, K, C, c_f32, accumulate);
+static SkPlan hq_sk_plan(int M, int N, int K, int mb, int nb, int n_cu) {
+    SkPlan p;
+    p.tm = (M + 16 * mb - 1) / (16 * mb);
+    p.tiles = p.tm * ((N + 64 * nb - 1) / (64 * nb));
+    p.upt = (K + KC - 1) / KC;
+    const long units = (long)p.tiles * p.upt;
+    int G = (int)(units < n_cu ? units : n_cu);
+    if (G >= 8) G -= G % 8;
+    p.G = G;
+    p.base = (int)(units / G);
+    p.extra = (int)(units % G);
+    return p;
 }
 
-// Tile choice: MB (16-row blocks of M per tile) grows with M up to 8; NB (16-column blocks per
-// wave) is picked to minimise ceil(tiles / 256 CUs) * tile area, i.e. wave quantization.
+template <int MB, int NB>
+static void launch_gemm_t(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
+                          const HqGemmWork &wk, hipStream_t st) {
+    GemmArgs g;
+    g.qs = W->qs, g.d = W->d, g.ldd = W->ldd, g.row_bytes = W->row_bytes, g.A = A;
+    g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;
+    g.plan = hq_sk_plan(M, g.N, g.K, MB, NB, wk.n_cu);
+    g.partials = wk.partials, g.counters = wk.counters;
+    if (W->type == HQ_TYPE_Q8_0) k_gemm_q8_0<MB, NB><<<g.plan.G, 256, 0, st>>>(g);
+    else if constexpr (MB % 2 == 0) k_gemm_q4_k<MB, NB><<<g.plan.G, 256, 0, st>>>(g);
+}
+
+// Tile choice: MB (16-row blocks of M per tile) grows with M up to 8 (Q4_K: at least 2); NB = 2
+// (128 x 128 tiles at large M keep the accumulators and the decoded weights in VGPRs). Stream-K
+// removes the wave-quantization cost, so the tile only sets the operand reuse.
 void hq_gemm_config(int M, int N, int *mb, int *nb) {
-    int m = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
-    const int mt = (M + 16 * m - 1) / (16 * m);
-    int best = 1;
-    double best_cost = 1e300;
-    for (int n = 1; n <= 4; n++) {
-        const long tiles = (long)mt * ((N + 64 * n - 1) / (64 * n));
-        const long rounds = (tiles + 255) / 256;
-        const double cost = (double)rounds * (16.0 * m) * (64.0 * n) * (1.0 + 0.08 / n);
-        if (cost < best_cost - 1e-9) best_cost = cost, best = n;
-    }
-    *mb = m;
-    *nb = best;
+    (void)N;
+    *mb = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
+    *nb = 2;
+}
+
+void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_bytes, size_t *counter_bytes) {
+    int mb, nb;
+    hq_gemm_config(M, (int)W->rows, &mb, &nb);
+    if (W->type == HQ_TYPE_Q4_K && mb == 1) mb = 2;
+    const SkPlan p = hq_sk_plan(M, (int)W->rows, (int)W->cols, mb, nb, n_cu);
+    *partial_bytes = (size_t)2 * p.G * 256 * mb * nb * 4 * sizeof(float);
+    *counter_bytes = (size_t)p.tiles * sizeof(int);
 }
 
 hipError_t hq_launch_gemm(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
-                          hipStream_t st) {
+                          const HqGemmWork &wk, hipStream_t st) {
     int mb, nb;
     hq_gemm_config(M, (int)W->rows, &mb, &nb);
+    if (W->type == HQ_TYPE_Q4_K && mb == 1) mb = 2;
 #define CASE(a, b) \
-    if (mb == a && nb == b) return launch_gemm_t<a, b>(W, A, M, C, c_f32, accumulate, st), hipGetLastError();
-#define ROW(a) CASE(a, 1) CASE(a, 2) CASE(a, 3) CASE(a, 4)
-    ROW(1) ROW(2) ROW(4) ROW(8)
-#undef ROW
+    if (mb == a && nb == b) return launch_gemm_t<a, b>(W, A, M, C, c_f32, accumulate, wk, st), hipGetLastError();
+    CASE(1, 2) CASE(2, 2) CASE(4, 2) CASE(8, 2)
 #undef CASE
     return hipErrorInvalidValue;
 }
