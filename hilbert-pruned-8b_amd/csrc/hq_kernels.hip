@@ -105,78 +105,128 @@ __global__ void __launch_bounds__(256) k_dequant_q4_k(const uint8_t *__restrict_
 }
 
 // ============================================================================ GEMV (M = 1) / gather
-// 16 lanes per row; 4 rows per wave. Lane j of a row walks 16-byte chunks j, j+16, ... of the
-// row's quant bytes and keeps an fp32 partial; a 16-lane butterfly reduces it.
-DEV float sum16(float v) {
-    v += __shfl_xor(v, 8, 16);
-    v += __shfl_xor(v, 4, 16);
-    v += __shfl_xor(v, 2, 16);
-    v += __shfl_xor(v, 1, 16);
+// LPR lanes per weight row (16, 32 or 64: chosen so the grid covers every CU), 256 / LPR rows per
+// workgroup. Lane j of a row walks 16-byte chunks j, j + LPR, ... of the row's quant bytes, four
+// chunks per batch with all loads issued before any use (memory-level parallelism), and keeps an
+// fp32 partial; an LPR-lane butterfly reduces it. Quants become exact fp16 integers (v_perm_b32 under
+// 0x64, then subtract the 1024 / 1152 bias) and meet the fp16 activations in v_dot2_f32_f16, so
+// every product is exact and every sum is fp32.
+template <int LPR>
+DEV float row_sum(float v) {
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, LPR);
     return v;
 }
 
-// 16 fp16 activations starting at a (32-byte aligned) as fp32.
-DEV void load_a16(const uint16_t *__restrict__ a, float *x) {
-    const u4v v0 = *(const u4v *)a, v1 = *(const u4v *)(a + 8);
-    const uint32_t w[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const h2 p = as_h2(w[i]);
-        x[2 * i] = (float)p.x;
-        x[2 * i + 1] = (float)p.y;
-    }
+DEV u4v load16(const void *p) { return *(const u4v *)p; }
+
+// sum of 8 products q*a: q from a word of 4 exact fp16 pairs builder, a from 4 words of fp16 pairs
+DEV float dot8(const h2 (&q)[4], const u4v a, float s) {
+    s = __builtin_amdgcn_fdot2(q[0], as_h2(a.x), s, false);
+    s = __builtin_amdgcn_fdot2(q[1], as_h2(a.y), s, false);
+    s = __builtin_amdgcn_fdot2(q[2], as_h2(a.z), s, false);
+    s = __builtin_amdgcn_fdot2(q[3], as_h2(a.w), s, false);
+    return s;
 }
 
-// Q8_0 row dot: sum over the row of q*d*a. Chunk c = 16 values of block c/2.
+DEV float sum8(const u4v a, float s) {
+    const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    s = __builtin_amdgcn_fdot2(as_h2(a.x), one, s, false);
+    s = __builtin_amdgcn_fdot2(as_h2(a.y), one, s, false);
+    s = __builtin_amdgcn_fdot2(as_h2(a.z), one, s, false);
+    s = __builtin_amdgcn_fdot2(as_h2(a.w), one, s, false);
+    return s;
+}
+
+// Q8_0 row dot: chunk c = 16 values of block c/2 (biased bytes u = q + 128, d plane).
+template <int LPR>
 DEV float dot_row_q8_0(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ d, const uint16_t *__restrict__ a,
                        int K, int j) {
+    const int nch = K / 16;
+    const h2 bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
     float acc = 0.f;
-    for (int c = j; c < K / 16; c += 16) {
-        const u4v q = *(const u4v *)(qs + 16 * c);
-        const float dv = h2f(d[c >> 1]);
-        float x[16];
-        load_a16(a + 16 * c, x);
-        const uint32_t w[4] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u, q.w ^ 0x80808080u};
-        float p = 0.f;
+    for (int c0 = j; c0 < nch; c0 += 4 * LPR) {
+        u4v q[4], a0[4], a1[4];
+        float dv[4];
 #pragma unroll
-        for (int i = 0; i < 16; i++) p += (float)(int8_t)byte_of(w[i >> 2], i & 3) * x[i];
-        acc += p * dv;
+        for (int b = 0; b < 4; b++) {
+            const int c = c0 + b * LPR, cc = c < nch ? c : nch - 1;
+            q[b] = load16(qs + 16 * cc);
+            a0[b] = load16(a + 16 * cc);
+            a1[b] = load16(a + 16 * cc + 8);
+            dv[b] = c < nch ? h2f(d[cc >> 1]) : 0.f;
+        }
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const uint32_t w[4] = {q[b].x, q[b].y, q[b].z, q[b].w};
+            h2 lo[4], hi[4];
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                lo[2 * i] = as_h2(perm_lo(w[i])) + bias;
+                lo[2 * i + 1] = as_h2(perm_hi(w[i])) + bias;
+                hi[2 * i] = as_h2(perm_lo(w[2 + i])) + bias;
+                hi[2 * i + 1] = as_h2(perm_hi(w[2 + i])) + bias;
+            }
+            const float s = dot8(hi, a1[b], dot8(lo, a0[b], 0.f));
+            acc += s * dv[b];
+        }
     }
     return acc;
 }
 
 // Q4_K row dot. Chunk c = 16 bytes of qs of super-block c/8: part t = c%8 -> p = t/2, h = t%2;
 // low nibbles are values 64p+16h+i (sub 2p), high nibbles 64p+32+16h+i (sub 2p+1).
+template <int LPR>
 DEV float dot_row_q4_k(const uint8_t *__restrict__ row, const uint16_t *__restrict__ a, int K, int j) {
+    const int nch = K / 32;
+    const h2 k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const h2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f}, k64 = {(_Float16)-64.0f, (_Float16)-64.0f};
     float acc = 0.f;
-    for (int c = j; c < K / 32; c += 16) {
-        const uint8_t *b = row + (size_t)(c >> 3) * 144;
-        const int t = c & 7, p = t >> 1, h = t & 1;
-        const u4v hdr = *(const u4v *)b;
-        const u4v q = *(const u4v *)(b + 16 + 16 * t);
-        uint32_t sw0, sw1, mw0, mw1;
-        q4k_scale_words(hdr.y, hdr.z, hdr.w, sw0, sw1, mw0, mw1);
-        const int s0 = 2 * p, s1 = 2 * p + 1;
-        const float d = h2f((uint16_t)hdr.x), dmin = h2f((uint16_t)(hdr.x >> 16));
-        const float ds0 = d * (float)byte_of(s0 < 4 ? sw0 : sw1, s0 & 3);
-        const float ds1 = d * (float)byte_of(s1 < 4 ? sw0 : sw1, s1 & 3);
-        const float dm0 = dmin * (float)byte_of(s0 < 4 ? mw0 : mw1, s0 & 3);
-        const float dm1 = dmin * (float)byte_of(s1 < 4 ? mw0 : mw1, s1 & 3);
-        const int kb = (c >> 3) * 256 + 64 * p + 16 * h;
-        float xl[16], xh[16];
-        load_a16(a + kb, xl);
-        load_a16(a + kb + 32, xh);
-        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-        float ql = 0.f, qh = 0.f, sl = 0.f, sh = 0.f;
+    for (int c0 = j; c0 < nch; c0 += 4 * LPR) {
+        u4v hd[4], q[4], al0[4], al1[4], ah0[4], ah1[4];
+        bool ok[4];
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const uint32_t by = byte_of(w[i >> 2], i & 3);
-            ql += (float)(by & 0xfu) * xl[i];
-            qh += (float)(by >> 4) * xh[i];
-            sl += xl[i];
-            sh += xh[i];
+        for (int b = 0; b < 4; b++) {
+            const int c = c0 + b * LPR, cc = c < nch ? c : nch - 1;
+            ok[b] = c < nch;
+            const uint8_t *blk = row + (size_t)(cc >> 3) * 144;
+            const int t = cc & 7;
+            hd[b] = load16(blk);
+            q[b] = load16(blk + 16 + 16 * t);
+            const int kb = (cc >> 3) * 256 + 64 * (t >> 1) + 16 * (t & 1);
+            al0[b] = load16(a + kb);
+            al1[b] = load16(a + kb + 8);
+            ah0[b] = load16(a + kb + 32);
+            ah1[b] = load16(a + kb + 40);
         }
-        acc += (ds0 * ql - dm0 * sl) + (ds1 * qh - dm1 * sh);
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int t = ((c0 + b * LPR) & 7), p = t >> 1;
+            uint32_t sw0, sw1, mw0, mw1;
+            q4k_scale_words(hd[b].y, hd[b].z, hd[b].w, sw0, sw1, mw0, mw1);
+            const int s0 = 2 * p, s1 = 2 * p + 1;
+            const float d = h2f((uint16_t)hd[b].x), dmin = h2f((uint16_t)(hd[b].x >> 16));
+            const float ds0 = d * (float)byte_of(s0 < 4 ? sw0 : sw1, s0 & 3);
+            const float ds1 = d * (float)byte_of(s1 < 4 ? sw0 : sw1, s1 & 3);
+            const float dm0 = dmin * (float)byte_of(s0 < 4 ? mw0 : mw1, s0 & 3);
+            const float dm1 = dmin * (float)byte_of(s1 < 4 ? mw0 : mw1, s1 & 3);
+            const uint32_t w[4] = {q[b].x, q[b].y, q[b].z, q[b].w};
+            h2 l0[4], l1[4], g0[4], g1[4];  // low nibbles of bytes 0-7 / 8-15, high nibbles of bytes 0-7 / 8-15
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t x = (i & 1) ? perm_hi(w[i >> 1]) : perm_lo(w[i >> 1]);
+                const uint32_t y = (i & 1) ? perm_hi(w[2 + (i >> 1)]) : perm_lo(w[2 + (i >> 1)]);
+                l0[i] = as_h2(x & 0xff0fff0fu) + k1024;
+                l1[i] = as_h2(y & 0xff0fff0fu) + k1024;
+                g0[i] = __builtin_elementwise_fma(as_h2(x & 0xfff0fff0u), s16, k64);
+                g1[i] = __builtin_elementwise_fma(as_h2(y & 0xfff0fff0u), s16, k64);
+            }
+            const float ql = dot8(l1, al1[b], dot8(l0, al0[b], 0.f));
+            const float qh = dot8(g1, ah1[b], dot8(g0, ah0[b], 0.f));
+            const float sl = sum8(al1[b], sum8(al0[b], 0.f)), sh = sum8(ah1[b], sum8(ah0[b], 0.f));
+            const float v = (ds0 * ql - dm0 * sl) + (ds1 * qh - dm1 * sh);
+            acc += ok[b] ? v : 0.f;
+        }
     }
     return acc;
 }
@@ -191,46 +241,169 @@ DEV void store_out(void *C, size_t idx, float v, int c_f32, int accumulate) {
     }
 }
 
+// ---- row-group GEMV: one wave per R weight rows (64 lanes per row), activations loaded once per
+// slice into registers and reused by the R rows, all R x TS weight loads of a slice in flight together.
+constexpr int GV_TS = 2;  // 16-byte chunks per lane per K slice
+
+// Q8_0: R rows n0 .. n0+R-1 (clamped) against activation vector a; returns the lane's partials.
+template <int R>
+DEV void rows_q8_0(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ d, int ldd,
+                   const uint16_t *__restrict__ a, int K, const int (&n)[R], int j, float (&acc)[R]) {
+    const int nch = K / 16;
+    const h2 bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.f;
+    for (int c0 = j; c0 < nch; c0 += 64 * GV_TS) {
+        u4v a0[GV_TS], a1[GV_TS], q[R][GV_TS];
+        float dv[R][GV_TS];
+#pragma unroll
+        for (int t = 0; t < GV_TS; t++) {
+            const int c = c0 + 64 * t, cc = c < nch ? c : nch - 1;
+            a0[t] = load16(a + 16 * cc);
+            a1[t] = load16(a + 16 * cc + 8);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                q[r][t] = load16(qs + (size_t)n[r] * K + 16 * cc);
+                dv[r][t] = c < nch ? h2f(d[(size_t)n[r] * ldd + (cc >> 1)]) : 0.f;
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < GV_TS; t++)
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint32_t w[4] = {q[r][t].x, q[r][t].y, q[r][t].z, q[r][t].w};
+                h2 lo[4], hi[4];
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    lo[2 * i] = as_h2(perm_lo(w[i])) + bias;
+                    lo[2 * i + 1] = as_h2(perm_hi(w[i])) + bias;
+                    hi[2 * i] = as_h2(perm_lo(w[2 + i])) + bias;
+                    hi[2 * i + 1] = as_h2(perm_hi(w[2 + i])) + bias;
+                }
+                acc[r] += dot8(hi, a1[t], dot8(lo, a0[t], 0.f)) * dv[r][t];
+            }
+    }
+}
+
+// Q4_K: chunk c = 16 bytes of qs of super-block c/8 (32 values, see dot_row_q4_k).
+template <int R>
+DEV void rows_q4_k(const uint8_t *__restrict__ W, size_t row_bytes, const uint16_t *__restrict__ a, int K,
+                   const int (&n)[R], int j, float (&acc)[R]) {
+    const int nch = K / 32;
+    const h2 k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const h2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f}, k64 = {(_Float16)-64.0f, (_Float16)-64.0f};
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.f;
+    for (int c0 = j; c0 < nch; c0 += 64 * GV_TS) {
+        u4v al0[GV_TS], al1[GV_TS], ah0[GV_TS], ah1[GV_TS], hd[R][GV_TS], q[R][GV_TS];
+#pragma unroll
+        for (int t = 0; t < GV_TS; t++) {
+            const int c = c0 + 64 * t, cc = c < nch ? c : nch - 1, tt = cc & 7;
+            const int kb = (cc >> 3) * 256 + 64 * (tt >> 1) + 16 * (tt & 1);
+            al0[t] = load16(a + kb);
+            al1[t] = load16(a + kb + 8);
+            ah0[t] = load16(a + kb + 32);
+            ah1[t] = load16(a + kb + 40);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint8_t *blk = W + (size_t)n[r] * row_bytes + (size_t)(cc >> 3) * 144;
+                hd[r][t] = load16(blk);
+                q[r][t] = load16(blk + 16 + 16 * tt);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < GV_TS; t++) {
+            const int c = c0 + 64 * t, tt = c & 7, p = tt >> 1;
+            const float sl = sum8(al1[t], sum8(al0[t], 0.f)), sh = sum8(ah1[t], sum8(ah0[t], 0.f));
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                uint32_t sw0, sw1, mw0, mw1;
+                q4k_scale_words(hd[r][t].y, hd[r][t].z, hd[r][t].w, sw0, sw1, mw0, mw1);
+                const int s0 = 2 * p, s1 = 2 * p + 1;
+                const float dd = h2f((uint16_t)hd[r][t].x), dmin = h2f((uint16_t)(hd[r][t].x >> 16));
+                const float ds0 = dd * (float)byte_of(s0 < 4 ? sw0 : sw1, s0 & 3);
+                const float ds1 = dd * (float)byte_of(s1 < 4 ? sw0 : sw1, s1 & 3);
+                const float dm0 = dmin * (float)byte_of(s0 < 4 ? mw0 : mw1, s0 & 3);
+                const float dm1 = dmin * (float)byte_of(s1 < 4 ? mw0 : mw1, s1 & 3);
+                const uint32_t w[4] = {q[r][t].x, q[r][t].y, q[r][t].z, q[r][t].w};
+                h2 l0[4], l1[4], g0[4], g1[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t x = (i & 1) ? perm_hi(w[i >> 1]) : perm_lo(w[i >> 1]);
+                    const uint32_t y = (i & 1) ? perm_hi(w[2 + (i >> 1)]) : perm_lo(w[2 + (i >> 1)]);
+                    l0[i] = as_h2(x & 0xff0fff0fu) + k1024;
+                    l1[i] = as_h2(y & 0xff0fff0fu) + k1024;
+                    g0[i] = __builtin_elementwise_fma(as_h2(x & 0xfff0fff0u), s16, k64);
+                    g1[i] = __builtin_elementwise_fma(as_h2(y & 0xfff0fff0u), s16, k64);
+                }
+                const float ql = dot8(l1, al1[t], dot8(l0, al0[t], 0.f));
+                const float qh = dot8(g1, ah1[t], dot8(g0, ah0[t], 0.f));
+                const float v = (ds0 * ql - dm0 * sl) + (ds1 * qh - dm1 * sh);
+                acc[r] += c < nch ? v : 0.f;
+            }
+        }
+    }
+}
+
+// out row n (wave-uniform) of the R rows of this wave.
+template <int R>
 __global__ void __launch_bounds__(256) k_gemv_q8_0(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ d,
                                                    int ldd, const uint16_t *__restrict__ a, int N, int K, void *C,
                                                    int c_f32, int accumulate) {
-    const int n = blockIdx.x * 16 + (threadIdx.x >> 4), j = threadIdx.x & 15;
-    const int nr = n < N ? n : N - 1;
-    const float v = sum16(dot_row_q8_0(qs + (size_t)nr * K, d + (size_t)nr * ldd, a, K, j));
-    if (j == 0 && n < N) store_out(C, n, v, c_f32, accumulate);
+    const int j = threadIdx.x & 63, n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+    int n[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) n[r] = n0 + r < N ? n0 + r : N - 1;
+    float acc[R];
+    rows_q8_0<R>(qs, d, ldd, a, K, n, j, acc);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const float v = row_sum<64>(acc[r]);
+        if (j == 0 && n0 + r < N) store_out(C, n0 + r, v, c_f32, accumulate);
+    }
 }
 
+template <int R>
 __global__ void __launch_bounds__(256) k_gemv_q4_k(const uint8_t *__restrict__ W, size_t row_bytes,
                                                    const uint16_t *__restrict__ a, int N, int K, void *C, int c_f32,
                                                    int accumulate) {
-    const int n = blockIdx.x * 16 + (threadIdx.x >> 4), j = threadIdx.x & 15;
-    const int nr = n < N ? n : N - 1;
-    const float v = sum16(dot_row_q4_k(W + (size_t)nr * row_bytes, a, K, j));
-    if (j == 0 && n < N) store_out(C, n, v, c_f32, accumulate);
+    const int j = threadIdx.x & 63, n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+    int n[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) n[r] = n0 + r < N ? n0 + r : N - 1;
+    float acc[R];
+    rows_q4_k<R>(W, row_bytes, a, K, n, j, acc);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const float v = row_sum<64>(acc[r]);
+        if (j == 0 && n0 + r < N) store_out(C, n0 + r, v, c_f32, accumulate);
+    }
 }
 
 // out[i] = dot(H[i / k], W[ids[i]]) for i < pairs. An id >= rows reads row 0 and stores NaN, so a
 // bad id can never move a load outside the matrix.
+template <int LPR>
 __global__ void __launch_bounds__(256) k_gather_q8_0(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ d,
                                                      int ldd, const uint16_t *__restrict__ H,
                                                      const uint32_t *__restrict__ ids, int pairs, int k, int K,
                                                      uint32_t rows, float *__restrict__ out) {
-    const int i = blockIdx.x * 16 + (threadIdx.x >> 4), j = threadIdx.x & 15;
+    const int i = blockIdx.x * (256 / LPR) + (int)threadIdx.x / LPR, j = threadIdx.x % LPR;
     const int ic = i < pairs ? i : pairs - 1;
     const uint32_t id = ids[ic];
     const size_t r = id < rows ? id : 0;
-    const float v = sum16(dot_row_q8_0(qs + r * K, d + r * ldd, H + (size_t)(ic / k) * K, K, j));
+    const float v = row_sum<LPR>(dot_row_q8_0<LPR>(qs + r * K, d + r * ldd, H + (size_t)(ic / k) * K, K, j));
     if (j == 0 && i < pairs) out[i] = id < rows ? v : __builtin_nanf("");
 }
 
+template <int LPR>
 __global__ void __launch_bounds__(256) k_gather_q4_k(const uint8_t *__restrict__ W, size_t row_bytes,
                                                      const uint16_t *__restrict__ H, const uint32_t *__restrict__ ids,
                                                      int pairs, int k, int K, uint32_t rows, float *__restrict__ out) {
-    const int i = blockIdx.x * 16 + (threadIdx.x >> 4), j = threadIdx.x & 15;
+    const int i = blockIdx.x * (256 / LPR) + (int)threadIdx.x / LPR, j = threadIdx.x % LPR;
     const int ic = i < pairs ? i : pairs - 1;
     const uint32_t id = ids[ic];
     const size_t r = id < rows ? id : 0;
-    const float v = sum16(dot_row_q4_k(W + r * row_bytes, H + (size_t)(ic / k) * K, K, j));
+    const float v = row_sum<LPR>(dot_row_q4_k<LPR>(W + r * row_bytes, H + (size_t)(ic / k) * K, K, j));
     if (j == 0 && i < pairs) out[i] = id < rows ? v : __builtin_nanf("");
 }
 
@@ -772,24 +945,47 @@ hipError_t hq_launch_dequant(const hq_dev_mat *W, uint32_t row0, const uint32_t 
     return hipGetLastError();
 }
 
-hipError_t hq_launch_gemv(const hq_dev_mat *W, const uint16_t *a, void *C, int c_f32, int accumulate, hipStream_t st) {
+// Lanes per row. HBM latency is hidden by the number of loads in flight, so rows are spread over
+// a whole wave (one load round per lane at K = 2560) unless there are rows enough for several
+// waves per SIMD at fewer lanes.
+static int lanes_per_row(long rows) { return rows >= 65536 ? 16 : rows >= 32768 ? 32 : 64; }
+
+template <int R>
+static void launch_gemv_t(const hq_dev_mat *W, const uint16_t *a, void *C, int c_f32, int accumulate, hipStream_t st) {
     const int N = (int)W->rows, K = (int)W->cols;
-    const unsigned g = (unsigned)((N + 15) / 16);
+    const unsigned g = (unsigned)((N + 4 * R - 1) / (4 * R));
     if (W->type == HQ_TYPE_Q8_0)
-        k_gemv_q8_0<<<g, 256, 0, st>>>(W->qs, W->d, W->ldd, a, N, K, C, c_f32, accumulate);
+        k_gemv_q8_0<R><<<g, 256, 0, st>>>(W->qs, W->d, W->ldd, a, N, K, C, c_f32, accumulate);
     else
-        k_gemv_q4_k<<<g, 256, 0, st>>>(W->qs, W->row_bytes, a, N, K, C, c_f32, accumulate);
+        k_gemv_q4_k<R><<<g, 256, 0, st>>>(W->qs, W->row_bytes, a, N, K, C, c_f32, accumulate);
+}
+
+// Rows per wave: 2 (activations reused twice; measured best of 1, 2, 4 at N = 9728), 1 when that
+// would leave the grid short of about two workgroups per CU.
+hipError_t hq_launch_gemv(const hq_dev_mat *W, const uint16_t *a, void *C, int c_f32, int accumulate, hipStream_t st) {
+    if (W->rows >= 4096) launch_gemv_t<2>(W, a, C, c_f32, accumulate, st);
+    else launch_gemv_t<1>(W, a, C, c_f32, accumulate, st);
     return hipGetLastError();
+}
+
+template <int LPR>
+static void launch_gather_t(const hq_dev_mat *W, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
+                            hipStream_t st) {
+    const int pairs = B * k, K = (int)W->cols;
+    const unsigned g = (unsigned)((pairs + 256 / LPR - 1) / (256 / LPR));
+    if (W->type == HQ_TYPE_Q8_0)
+        k_gather_q8_0<LPR><<<g, 256, 0, st>>>(W->qs, W->d, W->ldd, H, ids, pairs, k, K, W->rows, out);
+    else
+        k_gather_q4_k<LPR><<<g, 256, 0, st>>>(W->qs, W->row_bytes, H, ids, pairs, k, K, W->rows, out);
 }
 
 hipError_t hq_launch_gather(const hq_dev_mat *W, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
                             hipStream_t st) {
-    const int pairs = B * k, K = (int)W->cols;
-    const unsigned g = (unsigned)((pairs + 15) / 16);
-    if (W->type == HQ_TYPE_Q8_0)
-        k_gather_q8_0<<<g, 256, 0, st>>>(W->qs, W->d, W->ldd, H, ids, pairs, k, K, W->rows, out);
-    else
-        k_gather_q4_k<<<g, 256, 0, st>>>(W->qs, W->row_bytes, H, ids, pairs, k, K, W->rows, out);
+    switch (lanes_per_row((long)B * k)) {
+    case 16: launch_gather_t<16>(W, H, ids, B, k, out, st); break;
+    case 32: launch_gather_t<32>(W, H, ids, B, k, out, st); break;
+    default: launch_gather_t<64>(W, H, ids, B, k, out, st); break;
+    }
     return hipGetLastError();
 }
 
