@@ -210,9 +210,9 @@ static int aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 // call into a HIP graph only after an eager call of the same shape.
 namespace {
 struct Staging {  // slots: 0 x fp32, 1 x fp16, 2 y fp32 (hq_matmul_host), 3 embedding ids, 4 readout ids,
-                  // 5 GEMM partial tiles, 6 GEMM tile counters (kept zero)
-    void *buf[7] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
-    size_t cap[7] = {0, 0, 0, 0, 0, 0, 0};
+                  // 5 GEMM partial tiles, 6 GEMM tile counters (kept zero), 7 activation sub-block sums
+    void *buf[8] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    size_t cap[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     int n_cu = 0;
 };
 std::mutex g_staging_mu;
@@ -247,15 +247,16 @@ int gemm_work(const hq_mat *W, int M, HqGemmWork *wk) {
         }
         n_cu = g_staging[W->device].n_cu;
     }
-    size_t pb, cb;
-    hq_gemm_work_bytes(&W->m, M, n_cu, &pb, &cb);
-    void *part, *cnt;
+    size_t pb, cb, sb;
+    hq_gemm_work_bytes(&W->m, M, n_cu, &pb, &cb, &sb);
+    void *part, *cnt, *sums = nullptr;
     size_t old_cap;
     {
         std::lock_guard<std::mutex> lk(g_staging_mu);
         old_cap = g_staging[W->device].cap[6];
     }
     if (staging(W->device, 5, pb, &part) || staging(W->device, 6, cb, &cnt)) return -1;
+    if (sb && staging(W->device, 7, sb, &sums)) return -1;
     size_t new_cap;
     {
         std::lock_guard<std::mutex> lk(g_staging_mu);
@@ -264,6 +265,7 @@ int gemm_work(const hq_mat *W, int M, HqGemmWork *wk) {
     if (new_cap != old_cap) HIPCK(hipMemset(cnt, 0, new_cap));
     wk->partials = (float *)part;
     wk->counters = (int *)cnt;
+    wk->sums = (uint16_t *)sums;
     wk->n_cu = n_cu;
     return 0;
 }
@@ -402,11 +404,12 @@ extern "C" int hq_device_synchronize(void) {
     return 0;
 }
 
-extern "C" void hq_gemm_tiles(int M, int N, int *rows_per_tile, int *cols_per_tile) {
-    int mb, nb;
-    hq_gemm_config(M, N, &mb, &nb);
-    if (rows_per_tile) *rows_per_tile = M == 1 ? 1 : 16 * mb;
-    if (cols_per_tile) *cols_per_tile = M == 1 ? 16 : 64 * nb;
+extern "C" void hq_gemm_tiles(int ggml_type, int M, int N, int *rows_per_tile, int *cols_per_tile) {
+    (void)N;
+    int r = 1, c = 16;
+    if (M > 1) hq_gemm_tile_shape(ggml_type, M, &r, &c);
+    if (rows_per_tile) *rows_per_tile = r;
+    if (cols_per_tile) *cols_per_tile = c;
 }
 
 // ------------------------------------------------------------------------------------ timing

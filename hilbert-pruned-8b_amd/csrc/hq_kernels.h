@@ -23,19 +23,23 @@ hipError_t hq_launch_dequant(const hq_dev_mat *W, uint32_t row0, const uint32_t 
                              hipStream_t st);
 hipError_t hq_launch_gemv(const hq_dev_mat *W, const uint16_t *a, void *C, int c_f32, int accumulate, hipStream_t st);
 // Stream-K workspace: fp32 partial tiles and per-tile counters (zero when idle; each launch leaves
-// them zero), and the number of CUs the persistent grid is sized for.
+// them zero), the activation sub-block sums of the wide Q4_K kernel, and the number of CUs the
+// persistent grid is sized for.
 struct HqGemmWork {
     float *partials;
     int *counters;
+    uint16_t *sums;
     int n_cu;
 };
-void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_bytes, size_t *counter_bytes);
+void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_bytes, size_t *counter_bytes,
+                        size_t *sums_bytes);
 // M >= 2.
 hipError_t hq_launch_gemm(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
                           const HqGemmWork &wk, hipStream_t st);
 hipError_t hq_launch_gather(const hq_dev_mat *W, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
                             hipStream_t st);
 hipError_t hq_launch_f32_to_f16(const float *in, uint16_t *out, size_t n, hipStream_t st);
-void hq_gemm_config(int M, int N, int *mb, int *nb);
+// rows x columns of one GEMM output tile (M >= 2)
+void hq_gemm_tile_shape(int type, int M, int *rows, int *cols);
 
 #endif

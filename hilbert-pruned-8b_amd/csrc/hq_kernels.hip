@@ -565,32 +565,39 @@ DEV void store_tile(void *C, const f4 (&acc)[MB][NB], int M, int N, int m0, int 
     }
 }
 
-// Tile finished by this workgroup: store it, or run the partial-tile protocol.
-template <int MB, int NB>
+// Partial tiles are written and read with device-scope (sc1) buffer accesses: they go to the
+// cross-XCD coherent level, so no L2 write-back or invalidation is needed, and unlike atomics they
+// are not serialized, so a 16-byte access per (row block, column block) is in flight at once.
+constexpr int CPOL_SC1 = 16;
+
+DEV void buf_store16(rsrc_t r, f4 v, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, v), r, voff, soff, CPOL_SC1);
+}
+
+DEV f4 buf_load16_sc1(rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, CPOL_SC1));
+}
+
+// Tile finished by this workgroup (NT threads): store it, or run the partial-tile protocol. Partial
+// slot layout: (row block i, column block j) of thread tid at 16 * ((i * NB + j) * NT + tid).
+template <int MB, int NB, int NT>
 DEV void finish_tile(f4 (&acc)[MB][NB], const SkPlan &p, int w, int u0, int u1, int tile, int *s_flag,
-                     float *__restrict__ partials, int *__restrict__ counters, void *C, int M, int N, int m0, int nw,
-                     int ln, int lg, int c_f32, int accumulate) {
+                     rsrc_t rpart, int *__restrict__ counters, void *C, int M, int N, int m0, int nw, int ln, int lg,
+                     int c_f32, int accumulate) {
     const int t0 = tile * p.upt, t1 = t0 + p.upt;
     if (t0 >= u0 && t1 <= u1) {
         store_tile<MB, NB>(C, acc, M, N, m0, nw, ln, lg, c_f32, accumulate);
         return;
     }
-    constexpr int PER = 256 * MB * NB * 4;  // floats per partial tile
+    constexpr uint32_t PER = NT * MB * NB * 16;  // bytes per partial tile
     const int tid = threadIdx.x;
-    // slot 2w: the tile this workgroup starts in; 2w + 1: the tile it ends in. Partials are written
-    // and read with agent-scope (cross-XCD coherent) accesses, which bypass the non-coherent L2, so
-    // no L2 write-back or invalidation is needed; the counter update is ordered after the stores
-    // by waiting for them (stores count in vmcnt) before the barrier.
+    // slot 2w: the tile this workgroup starts in; 2w + 1: the tile it ends in. The counter update
+    // is ordered after the stores by waiting for them (stores count in vmcnt) before the barrier.
     const int slot = tile == u0 / p.upt ? 2 * w : 2 * w + 1;
-    float *mine = partials + (size_t)slot * PER;
 #pragma unroll
     for (int i = 0; i < MB; i++)
 #pragma unroll
-        for (int j = 0; j < NB; j++)
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-                __hip_atomic_store(mine + ((i * NB + j) * 4 + e) * 256 + tid, acc[i][j][e], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+        for (int j = 0; j < NB; j++) buf_store16(rpart, acc[i][j], (uint32_t)tid * 16u, slot * PER + (i * NB + j) * NT * 16);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     const int wf = sk_owner(p, t0), wl = sk_owner(p, t1 - 1);
@@ -604,16 +611,21 @@ DEV void finish_tile(f4 (&acc)[MB][NB], const SkPlan &p, int w, int u0, int u1, 
     if (!*s_flag) return;
     for (int o = wf; o <= wl; o++) {
         if (o == w) continue;
-        const int os = tile == sk_start(p, o) / p.upt ? 2 * o : 2 * o + 1;
-        float *src = partials + (size_t)os * PER;
+        const uint32_t os = (uint32_t)(tile == sk_start(p, o) / p.upt ? 2 * o : 2 * o + 1) * PER;
+        constexpr int IG = MB < 4 ? MB : 4;  // row blocks per batch of loads (bounds the registers)
 #pragma unroll
-        for (int i = 0; i < MB; i++)
+        for (int i0 = 0; i0 < MB; i0 += IG) {
+            f4 v[IG][NB];
 #pragma unroll
-            for (int j = 0; j < NB; j++)
+            for (int i = 0; i < IG; i++)
 #pragma unroll
-                for (int e = 0; e < 4; e++)
-                    acc[i][j][e] += __hip_atomic_load(src + ((i * NB + j) * 4 + e) * 256 + tid, __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
+                for (int j = 0; j < NB; j++)
+                    v[i][j] = buf_load16_sc1(rpart, (uint32_t)tid * 16u, os + ((i0 + i) * NB + j) * NT * 16);
+#pragma unroll
+            for (int i = 0; i < IG; i++)
+#pragma unroll
+                for (int j = 0; j < NB; j++) acc[i0 + i][j] += v[i][j];
+        }
     }
     store_tile<MB, NB>(C, acc, M, N, m0, nw, ln, lg, c_f32, accumulate);
 }
@@ -630,7 +642,9 @@ struct GemmArgs {
     int c_f32, accumulate;
     SkPlan plan;
     float *partials;
+    uint32_t partial_bytes;
     int *counters;
+    const uint16_t *sums;  // wide Q4_K kernel: activation sub-block sums (k_asums)
 };
 
 DEV int sk_worker(int G) {
@@ -646,6 +660,7 @@ __global__ void __launch_bounds__(256) k_gemm_q8_0(GemmArgs g) {
     __shared__ int s_flag;
     const SkPlan &p = g.plan;
     const int w = sk_worker(p.G), u0 = sk_start(p, w), u1 = sk_start(p, w + 1);
+    const rsrc_t rpart = make_rsrc(g.partials, g.partial_bytes);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, ln = lane & 15, lg = lane >> 4;
     const int M = g.M, N = g.N, K = g.K;
     const rsrc_t ra = make_rsrc(g.A, (uint32_t)((size_t)M * K * 2));
@@ -731,7 +746,7 @@ __global__ void __launch_bounds__(256) k_gemm_q8_0(GemmArgs g) {
             }
         }
         if (ku == p.upt - 1 || u == u1 - 1)
-            finish_tile<MB, NB>(acc, p, w, u0, u1, tile, &s_flag, g.partials, g.counters, g.C, M, N, m0, nw, ln, lg,
+            finish_tile<MB, NB, 256>(acc, p, w, u0, u1, tile, &s_flag, rpart, g.counters, g.C, M, N, m0, nw, ln, lg,
                                 g.c_f32, g.accumulate);
         if (u + 1 < u1) {
 #pragma unroll
@@ -752,6 +767,7 @@ __global__ void __launch_bounds__(256) k_gemm_q4_k(GemmArgs g) {
     __shared__ int s_flag;
     const SkPlan &p = g.plan;
     const int w = sk_worker(p.G), u0 = sk_start(p, w), u1 = sk_start(p, w + 1);
+    const rsrc_t rpart = make_rsrc(g.partials, g.partial_bytes);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
     const int M = g.M, N = g.N, K = g.K;
     const rsrc_t ra = make_rsrc(g.A, (uint32_t)((size_t)M * K * 2));
@@ -910,13 +926,233 @@ __global__ void __launch_bounds__(256) k_gemm_q4_k(GemmArgs g) {
             __syncthreads();  // this unit's sums, written by other waves
             apply_min(ss[cb]);
             min_pending = false;
-            finish_tile<MB, NB>(acc, p, w, u0, u1, tile, &s_flag, g.partials, g.counters, g.C, M, N, m0, nw, ln, lg,
+            finish_tile<MB, NB, 256>(acc, p, w, u0, u1, tile, &s_flag, rpart, g.counters, g.C, M, N, m0, nw, ln, lg,
                                 g.c_f32, g.accumulate);
         }
         if (u + 1 < u1) {
 #pragma unroll
             for (int j = 0; j < NB; j++) hc[j] = hn[j], q0c[j] = q0n[j], q1c[j] = q1n[j];
         }
+    }
+}
+
+// ---------------------------------------------------------------------------- wide Q4_K GEMM (M > 64)
+// 8 waves, two per SIMD (one wave's LDS and memory waits are covered by the other's MFMAs); tile
+// 128 (M) x 256 (N): wave w owns columns [32w, 32w + 32) and all 128 rows, decoded as in
+// k_gemm_q4_k. The activation sub-block sums come from k_asums (one pass over A per GEMM instead of
+// one per N tile): plane S[m][u][16] fp16 = {hi(S_0..S_7), lo(S_0..S_7)} of unit u, staged in LDS
+// next to the activation tile. The min term is one MFMA per (16-row block, 16-column block, unit)
+// accumulating straight into the output: A operand lanes lg = 0..3 hold S_hi, S_lo, S_hi, S_lo of
+// sub-blocks 0..7, B operand lanes hold Bh, Bh, Bl, Bl with Bh = fp16(-dmin*m) and
+// Bl = fp16(-dmin*m - Bh), exact because -dmin*m has at most 17 significant bits; the four products
+// sum to S*(-dmin*m) to about 2^-22 relative, so no fp32 fold is needed for it.
+constexpr int WNW = 8;  // waves per workgroup
+
+// A tile DMA: instruction q = w + 8qq (rows 2q, 2q + 1) of wave w; r & 15 = (2w + (lane >> 5)) & 15
+// is the same for every qq, so one per-lane base serves all of them.
+DEV uint32_t adma_w_base(int K, int m0) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, p = lane & 31;
+    const int r0 = 2 * wave + (lane >> 5);
+    return (uint32_t)((m0 + r0) * K + 8 * (p ^ (r0 & 15))) * 2u;
+}
+
+template <int MB>
+DEV void dma_a_w(_Float16 *buf, rsrc_t ra, uint32_t base, int K, int k0) {
+    constexpr int PER_WAVE = 16 * MB / 2 / WNW;
+    static_assert(PER_WAVE * WNW * 2 == 16 * MB, "tile rows must split evenly over the waves");
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int qq = 0; qq < PER_WAVE; qq++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, lds_ptr(buf + (wave + WNW * qq) * 512), 16, base,
+                                                 (uint32_t)(qq * 16 * K * 2 + 2 * k0), 0, 0);
+}
+
+// S tile of unit u: 16*MB rows x 32 bytes, one 1 KB instruction (32 rows) per wave w < 16*MB/32.
+// Per-lane base: row 32w + lane/2, half lane % 2.
+template <int MB>
+DEV void dma_s_w(uint16_t *buf, rsrc_t rs, uint32_t base, int u) {
+    constexpr int INSTR = 16 * MB / 32;
+    const int wave = threadIdx.x >> 6;
+    if (wave < INSTR)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, lds_ptr(buf + wave * 512), 16, base, (uint32_t)(u * 32), 0, 0);
+}
+
+template <int MB>
+__global__ void __launch_bounds__(512) k_gemm_q4_k_w(GemmArgs g) {
+    constexpr int BM = 16 * MB, NB = 2, NT = 64 * WNW;
+    static_assert(BM / 32 <= WNW, "S tile DMA needs one wave per 32 rows");
+    __shared__ __attribute__((aligned(16))) _Float16 sa[2][BM * KC];
+    __shared__ __attribute__((aligned(16))) uint16_t ssum[2][BM * 16];
+    __shared__ int s_flag;
+    const SkPlan &p = g.plan;
+    const int w = sk_worker(p.G), u0 = sk_start(p, w), u1 = sk_start(p, w + 1);
+    const rsrc_t rpart = make_rsrc(g.partials, g.partial_bytes);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
+    const int M = g.M, N = g.N, K = g.K, U = K / KC;
+    const rsrc_t ra = make_rsrc(g.A, (uint32_t)((size_t)M * K * 2));
+    const rsrc_t rw = make_rsrc(g.qs, (uint32_t)((size_t)N * g.row_bytes));
+    const rsrc_t rs = make_rsrc(g.sums, (uint32_t)((size_t)M * U * 32));
+    uint32_t abase = 0, sbase = 0, vh[NB], vq[NB];
+    auto tile_setup = [&](int tile) {
+        const int m0 = (tile % p.tm) * BM, nw = (tile / p.tm) * 16 * NB * WNW + wave * 16 * NB;
+        abase = adma_w_base(K, m0);
+        sbase = (uint32_t)((m0 + 32 * wave + (lane >> 1)) * U * 32 + 16 * (lane & 1));
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            const uint32_t n = (uint32_t)(nw + 16 * j + ln);
+            vh[j] = n * (uint32_t)g.row_bytes;
+            vq[j] = vh[j] + 16u + 16u * lg;
+        }
+    };
+    auto load_w = [&](int sb, u4v (&h)[NB], u4v (&q0)[NB], u4v (&q1)[NB]) {
+        const uint32_t so = (uint32_t)sb * 144u;
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            h[j] = buf_load16(rw, vh[j], so);
+            q0[j] = buf_load16(rw, vq[j], so);
+            q1[j] = buf_load16(rw, vq[j] + 64u, so);
+        }
+    };
+    const int pA = lg >> 1, hA = lg & 1;
+    // byte offset of this lane's A fragment (L, t) in row block 0 of a tile buffer: row ln, chunk
+    // c = 8(2L + pA) + 2hA + (t & 1) + 4(t >> 1) stored at slot c ^ ln; row block i adds 16*KC*2*i
+    uint32_t aoff[8];
+#pragma unroll
+    for (int f = 0; f < 8; f++) {
+        const int L = f >> 2, t = f & 3;
+        const int c = 8 * (2 * L + pA) + 2 * hA + (t & 1) + 4 * (t >> 1);
+        aoff[f] = (uint32_t)(ln * KC + 8 * (c ^ ln)) * 2u;
+    }
+    const uint32_t soff = (uint32_t)(ln * 16 + 8 * (lg & 1)) * 2u;
+    f4 acc[MB][NB];
+    int cur_tile = u0 / p.upt;
+    tile_setup(cur_tile);
+    dma_a_w<MB>(sa[0], ra, abase, K, (u0 % p.upt) * KC);
+    dma_s_w<MB>(ssum[0], rs, sbase, u0 % p.upt);
+    // one unit: wait for its operands, start the next unit's, multiply, finish the tile if it ends
+    auto unit = [&](int u, const u4v (&hc)[NB], const u4v (&q0c)[NB], const u4v (&q1c)[NB], u4v (&hn)[NB],
+                    u4v (&q0n)[NB], u4v (&q1n)[NB]) {
+        const int cb = (u - u0) & 1, tile = u / p.upt, sb = u % p.upt;
+        const int m0 = (tile % p.tm) * BM, nw = (tile / p.tm) * 16 * NB * WNW + wave * 16 * NB;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (u + 1 < u1) {
+            const int t1 = (u + 1) / p.upt;
+            if (t1 != cur_tile) {
+                cur_tile = t1;
+                tile_setup(t1);
+            }
+            const int sb1 = (u + 1) % p.upt;
+            dma_a_w<MB>(sa[cb ^ 1], ra, abase, K, sb1 * KC);
+            dma_s_w<MB>(ssum[cb ^ 1], rs, sbase, sb1);
+            load_w(sb1, hn, q0n, q1n);
+        }
+        if (u == u0 || sb == 0) {
+#pragma unroll
+            for (int i = 0; i < MB; i++)
+#pragma unroll
+                for (int j = 0; j < NB; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+        }
+        h8 bf[NB][8], bmin[NB];
+        float dsc[NB];
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            uint32_t sw0, sw1, mw0, mw1;
+            q4k_scale_words(hc[j].y, hc[j].z, hc[j].w, sw0, sw1, mw0, mw1);
+            h2 mulL[2][2], addL[2][2];
+#pragma unroll
+            for (int L = 0; L < 2; L++) {
+                const uint32_t sw = L ? sw1 : sw0;
+#pragma unroll
+                for (int hi = 0; hi < 2; hi++) {
+                    const float s = (float)byte_of(sw, 2 * pA + hi);
+                    const _Float16 mul = (_Float16)(hi ? s * 0.0625f : s);
+                    const _Float16 add = (_Float16)(hi ? -64.0f * s : -1024.0f * s);
+                    mulL[L][hi] = h2{mul, mul};
+                    addL[L][hi] = h2{add, add};
+                }
+            }
+            bf[j][0] = frag_q4_k<false>(q0c[j].x, q0c[j].y, mulL[0][0], addL[0][0]);
+            bf[j][1] = frag_q4_k<false>(q0c[j].z, q0c[j].w, mulL[0][0], addL[0][0]);
+            bf[j][2] = frag_q4_k<true>(q0c[j].x, q0c[j].y, mulL[0][1], addL[0][1]);
+            bf[j][3] = frag_q4_k<true>(q0c[j].z, q0c[j].w, mulL[0][1], addL[0][1]);
+            bf[j][4] = frag_q4_k<false>(q1c[j].x, q1c[j].y, mulL[1][0], addL[1][0]);
+            bf[j][5] = frag_q4_k<false>(q1c[j].z, q1c[j].w, mulL[1][0], addL[1][0]);
+            bf[j][6] = frag_q4_k<true>(q1c[j].x, q1c[j].y, mulL[1][1], addL[1][1]);
+            bf[j][7] = frag_q4_k<true>(q1c[j].z, q1c[j].w, mulL[1][1], addL[1][1]);
+            // min operand: k-slot e = sub-block e
+            const _Float16 ndm = -__builtin_bit_cast(_Float16, (uint16_t)(hc[j].x >> 16));
+            const h2 nd2 = {ndm, ndm};
+            const h2 mv[4] = {bytes_f16(mw0, false), bytes_f16(mw0, true), bytes_f16(mw1, false),
+                              bytes_f16(mw1, true)};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const h2 bh = mv[q] * nd2;
+                const h2 bl = __builtin_elementwise_fma(mv[q], nd2, -bh);
+                const h2 v = lg < 2 ? bh : bl;
+                bmin[j][2 * q] = v.x;
+                bmin[j][2 * q + 1] = v.y;
+            }
+            dsc[j] = h2f((uint16_t)hc[j].x);
+        }
+        const char *abuf = (const char *)sa[cb];
+        const char *sbuf = (const char *)ssum[cb] + soff;
+        uint32_t ad[8];
+#pragma unroll
+        for (int f = 0; f < 8; f++) ad[f] = (uint32_t)(uintptr_t)abuf + aoff[f];
+#pragma unroll
+        for (int i = 0; i < MB; i++) {
+            const h8 as = *(const h8 *)(sbuf + i * 16 * 32);
+#pragma unroll
+            for (int j = 0; j < NB; j++) acc[i][j] = mfma(as, bmin[j], acc[i][j]);
+            f4 part[NB];
+#pragma unroll
+            for (int j = 0; j < NB; j++) part[j] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int f = 0; f < 8; f++) {
+                const h8 af = *(const h8 *)(lds_void *)(uintptr_t)(ad[f] + i * 16 * KC * 2);
+#pragma unroll
+                for (int j = 0; j < NB; j++) part[j] = mfma(af, bf[j][f], part[j]);
+            }
+#pragma unroll
+            for (int j = 0; j < NB; j++) acc[i][j] += part[j] * dsc[j];
+        }
+        if (sb == p.upt - 1 || u == u1 - 1)
+            finish_tile<MB, NB, NT>(acc, p, w, u0, u1, tile, &s_flag, rpart, g.counters, g.C, M, N, m0, nw, ln, lg,
+                                    g.c_f32, g.accumulate);
+    };
+    u4v hA0[NB], qA0[NB], qA1[NB], hB0[NB], qB0[NB], qB1[NB];
+    load_w(u0 % p.upt, hA0, qA0, qA1);
+    for (int u = u0; u < u1; u += 2) {  // two units per trip: the weight registers alternate roles
+        unit(u, hA0, qA0, qA1, hB0, qB0, qB1);
+        if (u + 1 < u1) unit(u + 1, hB0, qB0, qB1, hA0, qA0, qA1);
+    }
+}
+
+// Activation sub-block sums for the wide Q4_K GEMM: S[m][u][s] = fp16 hi and S[m][u][8 + s] = fp16
+// lo of the fp32 sum of activations 256u + 32s .. +32 of row m (hi + lo = the fp32 sum).
+__global__ void __launch_bounds__(256) k_asums(const uint16_t *__restrict__ A, int M, int K,
+                                               uint16_t *__restrict__ S) {
+    const int nsub = K / 32;
+    const size_t n = (size_t)M * nsub;
+    const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    for (size_t t = blockIdx.x * (size_t)256 + threadIdx.x; t < n; t += (size_t)gridDim.x * 256) {
+        const size_t m = t / nsub;
+        const int b = (int)(t % nsub);
+        const u4v *src = (const u4v *)(A + m * K + 32 * b);
+        float s = 0.f;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const u4v x = src[v];
+            s = __builtin_amdgcn_fdot2(as_h2(x.x), one, s, false);
+            s = __builtin_amdgcn_fdot2(as_h2(x.y), one, s, false);
+            s = __builtin_amdgcn_fdot2(as_h2(x.z), one, s, false);
+            s = __builtin_amdgcn_fdot2(as_h2(x.w), one, s, false);
+        }
+        const _Float16 hi = (_Float16)s;
+        uint16_t *dst = S + (m * (size_t)(K / 256) + b / 8) * 16 + (b % 8);
+        dst[0] = __builtin_bit_cast(uint16_t, hi);
+        dst[8] = __builtin_bit_cast(uint16_t, (_Float16)(s - (float)hi));
     }
 }
 
@@ -989,10 +1225,10 @@ hipError_t hq_launch_gather(const hq_dev_mat *W, const uint16_t *H, const uint32
     return hipGetLastError();
 }
 
-static SkPlan hq_sk_plan(int M, int N, int K, int mb, int nb, int n_cu) {
+static SkPlan hq_sk_plan(int M, int N, int K, int bm, int bn, int n_cu) {
     SkPlan p;
-    p.tm = (M + 16 * mb - 1) / (16 * mb);
-    p.tiles = p.tm * ((N + 64 * nb - 1) / (64 * nb));
+    p.tm = (M + bm - 1) / bm;
+    p.tiles = p.tm * ((N + bn - 1) / bn);
     p.upt = (K + KC - 1) / KC;
     const long units = (long)p.tiles * p.upt;
     int G = (int)(units < n_cu ? units : n_cu);
@@ -1003,44 +1239,74 @@ static SkPlan hq_sk_plan(int M, int N, int K, int mb, int nb, int n_cu) {
     return p;
 }
 
-template <int MB, int NB>
-static void launch_gemm_t(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
-                          const HqGemmWork &wk, hipStream_t st) {
-    GemmArgs g;
-    g.qs = W->qs, g.d = W->d, g.ldd = W->ldd, g.row_bytes = W->row_bytes, g.A = A;
-    g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;
-    g.plan = hq_sk_plan(M, g.N, g.K, MB, NB, wk.n_cu);
-    g.partials = wk.partials, g.counters = wk.counters;
-    if (W->type == HQ_TYPE_Q8_0) k_gemm_q8_0<MB, NB><<<g.plan.G, 256, 0, st>>>(g);
-    else if constexpr (MB % 2 == 0) k_gemm_q4_k<MB, NB><<<g.plan.G, 256, 0, st>>>(g);
+namespace {
+// Kernel choice for M >= 2: MB (16-row blocks of M per tile) grows with M up to 8 (Q4_K: at least 2);
+// NB = 2 16-column blocks per wave. Q4_K with M > 64 uses the wide 8-wave kernel (tile 128 x 256).
+// Stream-K removes the wave-quantization cost, so the tile only sets the operand reuse.
+struct GemmCfg {
+    int mb, nb, waves;
+    bool wide;
+};
+
+GemmCfg gemm_cfg(const hq_dev_mat *W, int M) {
+    GemmCfg c;
+    c.mb = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
+    c.nb = 2;
+    if (W->type == HQ_TYPE_Q4_K && c.mb == 1) c.mb = 2;
+    c.wide = W->type == HQ_TYPE_Q4_K && M > 64;
+    c.waves = c.wide ? WNW : 4;
+    return c;
 }
 
-// Tile choice: MB (16-row blocks of M per tile) grows with M up to 8 (Q4_K: at least 2); NB = 2
-// (128 x 128 tiles at large M keep the accumulators and the decoded weights in VGPRs). Stream-K
-// removes the wave-quantization cost, so the tile only sets the operand reuse.
-void hq_gemm_config(int M, int N, int *mb, int *nb) {
-    (void)N;
-    *mb = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
-    *nb = 2;
+SkPlan gemm_plan(const hq_dev_mat *W, int M, const GemmCfg &c, int n_cu) {
+    return hq_sk_plan(M, (int)W->rows, (int)W->cols, 16 * c.mb, 16 * c.nb * c.waves, n_cu);
+}
+}  // namespace
+
+void hq_gemm_tile_shape(int type, int M, int *rows, int *cols) {
+    hq_dev_mat W = {};
+    W.type = type;
+    const GemmCfg c = gemm_cfg(&W, M);
+    *rows = 16 * c.mb;
+    *cols = 16 * c.nb * c.waves;
 }
 
-void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_bytes, size_t *counter_bytes) {
-    int mb, nb;
-    hq_gemm_config(M, (int)W->rows, &mb, &nb);
-    if (W->type == HQ_TYPE_Q4_K && mb == 1) mb = 2;
-    const SkPlan p = hq_sk_plan(M, (int)W->rows, (int)W->cols, mb, nb, n_cu);
-    *partial_bytes = (size_t)2 * p.G * 256 * mb * nb * 4 * sizeof(float);
+void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_bytes, size_t *counter_bytes,
+                        size_t *sums_bytes) {
+    const GemmCfg c = gemm_cfg(W, M);
+    const SkPlan p = gemm_plan(W, M, c, n_cu);
+    *partial_bytes = (size_t)2 * p.G * 64 * c.waves * c.mb * c.nb * 4 * sizeof(float);
     *counter_bytes = (size_t)p.tiles * sizeof(int);
+    *sums_bytes = c.wide ? (size_t)M * (W->cols / KC) * 32 : 0;
 }
 
 hipError_t hq_launch_gemm(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
                           const HqGemmWork &wk, hipStream_t st) {
-    int mb, nb;
-    hq_gemm_config(M, (int)W->rows, &mb, &nb);
-    if (W->type == HQ_TYPE_Q4_K && mb == 1) mb = 2;
-#define CASE(a, b) \
-    if (mb == a && nb == b) return launch_gemm_t<a, b>(W, A, M, C, c_f32, accumulate, wk, st), hipGetLastError();
-    CASE(1, 2) CASE(2, 2) CASE(4, 2) CASE(8, 2)
+    const GemmCfg c = gemm_cfg(W, M);
+    GemmArgs g;
+    g.qs = W->qs, g.d = W->d, g.ldd = W->ldd, g.row_bytes = W->row_bytes, g.A = A;
+    g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;
+    g.plan = gemm_plan(W, M, c, wk.n_cu);
+    g.partials = wk.partials, g.counters = wk.counters, g.sums = wk.sums;
+    {
+        size_t pb, cb, sb;
+        hq_gemm_work_bytes(W, M, wk.n_cu, &pb, &cb, &sb);
+        if (pb > 0xffffffffu) return hipErrorInvalidValue;
+        g.partial_bytes = (uint32_t)pb;
+    }
+    if (c.wide) {
+        const size_t nsub = (size_t)M * (W->cols / 32);
+        k_asums<<<grid_for(nsub, 256, 8192), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
+        k_gemm_q4_k_w<8><<<g.plan.G, 64 * WNW, 0, st>>>(g);
+        return hipGetLastError();
+    }
+#define CASE(a)                                                                                 \
+    if (c.mb == a) {                                                                            \
+        if (W->type == HQ_TYPE_Q8_0) k_gemm_q8_0<a, 2><<<g.plan.G, 256, 0, st>>>(g);            \
+        else if constexpr (a % 2 == 0) k_gemm_q4_k<a, 2><<<g.plan.G, 256, 0, st>>>(g);          \
+        return hipGetLastError();                                                               \
+    }
+    CASE(1) CASE(2) CASE(4) CASE(8)
 #undef CASE
     return hipErrorInvalidValue;
 }

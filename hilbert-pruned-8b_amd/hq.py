@@ -88,7 +88,7 @@ def load(path=LIB_PATH):
         "hq_device_synchronize": (i, []),
         "hq_time_gemm": (i, [C.POINTER(vp), i, vp, i, vp, i, i, i, vp, C.POINTER(C.c_float)]),
         "hq_time_gather": (i, [C.POINTER(vp), i, vp, vp, i, i, i, vp, i, i, vp, C.POINTER(C.c_float)]),
-        "hq_gemm_tiles": (None, [i, i, C.POINTER(i), C.POINTER(i)]),
+        "hq_gemm_tiles": (None, [i, i, i, C.POINTER(i), C.POINTER(i)]),
         "hq_llama_forward": (i, [C.POINTER(Llama), vp, sz, vp, u32, vp]),
         "hq_embed_f32": (i, [vp, vp, i, vp, vp]),
     }
@@ -268,9 +268,9 @@ def embed(W, ids):
     return out.download((len(ids), W.cols), np.float32)
 
 
-def gemm_tiles(M, N):
+def gemm_tiles(gtype, M, N):
     r, c = C.c_int(), C.c_int()
-    load().hq_gemm_tiles(M, N, C.byref(r), C.byref(c))
+    load().hq_gemm_tiles(gtype, M, N, C.byref(r), C.byref(c))
     return r.value, c.value
 
 

@@ -111,8 +111,8 @@ int hq_time_gemm(hq_mat *const *Ws, int n_w, const uint16_t *A, int M, void *C, 
 int hq_time_gather(hq_mat *const *Ws, int n_w, const uint16_t *H, const uint32_t *ids_dev, int n_sets, int B, int k,
                    float *out, int iters, int reps, void *stream, float *ms);
 
-/* The tile configuration hq_gemm uses for an M x N problem (diagnostics). */
-void hq_gemm_tiles(int M, int N, int *rows_per_tile, int *cols_per_tile);
+/* The output tile hq_gemm uses for an M x N problem of the given ggml type (diagnostics). */
+void hq_gemm_tiles(int ggml_type, int M, int N, int *rows_per_tile, int *cols_per_tile);
 
 #ifdef __cplusplus
 }

@@ -67,13 +67,18 @@ def test_upload_rejects_bad_descriptors_before_touching_a_device(dtype, gtype, r
 
 def test_gemm_tile_selection():
     # every M from 1 to 4096 gets a tile; M = 1 is the GEMV
-    assert hq.gemm_tiles(1, 9728) == (1, 16)
-    for M in (2, 16, 17, 33, 64, 65, 512, 4096):
-        r, c = hq.gemm_tiles(M, 9728)
-        assert r in (16, 32, 64, 128) and c == 128
-        assert r >= min(M, 128) or r == 128
-    # Stream-K balances any tile count over the CUs; large M uses 128 x 128 tiles
-    assert hq.gemm_tiles(512, 9728) == (128, 128)
+    for gtype in (synth.Q8_0, synth.Q4_K):
+        assert hq.gemm_tiles(gtype, 1, 9728) == (1, 16)
+        for M in (2, 16, 17, 33, 64, 65, 512, 4096):
+            r, c = hq.gemm_tiles(gtype, M, 9728)
+            assert r in (16, 32, 64, 128)
+            assert r >= min(M, 128) or r == 128
+            # Q4_K above M = 64: the 8-wave kernel, 256 columns per tile
+            assert c == (256 if gtype == synth.Q4_K and M > 64 else 128)
+    # Stream-K balances any tile count over the CUs
+    assert hq.gemm_tiles(synth.Q8_0, 512, 9728) == (128, 128)
+    assert hq.gemm_tiles(synth.Q4_K, 512, 9728) == (128, 256)
+    assert hq.gemm_tiles(synth.Q4_K, 2, 9728) == (32, 128)
 
 
 def test_synth_is_deterministic():

@@ -118,7 +118,7 @@ RAGGED = [(synth.Q8_0, 100, 512, M) for M in (1, 2, 5, 17, 33, 65, 200)] + \
 
 @pytest.mark.parametrize("gtype,N,K,M", FULL + RAGGED)
 def test_gemm_parity(hqlib, oracle, gtype, N, K, M):
-    say(f"gemm type={gtype} M={M} N={N} K={K} tiles={hqlib.gemm_tiles(M, N)}")
+    say(f"gemm type={gtype} M={M} N={N} K={K} tiles={hqlib.gemm_tiles(gtype, M, N)}")
     blocks = weights(gtype, N, K, 100 + gtype)
     rng = synth.Rng(1000 + M + N + K)
     a = synth.activations_f16(rng, M, K)
@@ -162,7 +162,7 @@ def test_gemm_large_m_row_sample(hqlib, oracle):
         blocks = weights(gtype, N, K, 100 + gtype)
         a = synth.activations_f16(synth.Rng(M), M, K)
         W = hqlib.Mat(blocks, gtype, N, K)
-        say(f"gemm large type={gtype} M={M} tiles={hqlib.gemm_tiles(M, N)}")
+        say(f"gemm large type={gtype} M={M} tiles={hqlib.gemm_tiles(gtype, M, N)}")
         got = hqlib.gemm_np(W, a)
         cols = np.unique(np.concatenate([np.arange(0, 256), np.arange(N - 256, N),
                                          synth.Rng(3).choice_without_replacement(N, 256)])).astype(np.int64)
