@@ -967,6 +967,13 @@ DEV void dma_a_w(_Float16 *buf, rsrc_t ra, uint32_t base, int K, int k0) {
                                                  (uint32_t)(qq * 16 * K * 2 + 2 * k0), 0, 0);
 }
 
+// Instruction qq of dma_a_w alone (the wide kernel spreads them over a unit's k-steps).
+DEV void dma_a_w1(_Float16 *buf, rsrc_t ra, uint32_t base, int K, int k0, int qq) {
+    const int wave = threadIdx.x >> 6;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, lds_ptr(buf + (wave + WNW * qq) * 512), 16, base,
+                                             (uint32_t)(qq * 16 * K * 2 + 2 * k0), 0, 0);
+}
+
 // S tile of unit u: 16*MB rows x 32 bytes, one 1 KB instruction (32 rows) per wave w < 16*MB/32.
 // Per-lane base: row 32w + lane/2, half lane % 2.
 template <int MB>
@@ -979,73 +986,84 @@ DEV void dma_s_w(uint16_t *buf, rsrc_t rs, uint32_t base, int u) {
 
 template <int MB>
 __global__ void __launch_bounds__(512) k_gemm_q4_k_w(GemmArgs g) {
-    constexpr int BM = 16 * MB, NB = 2, NT = 64 * WNW;
+    constexpr int BM = 16 * MB, NB = 2, NT = 64 * WNW, BN = 16 * NB * WNW;
     static_assert(BM / 32 <= WNW, "S tile DMA needs one wave per 32 rows");
     __shared__ __attribute__((aligned(16))) _Float16 sa[2][BM * KC];
     __shared__ __attribute__((aligned(16))) uint16_t ssum[2][BM * 16];
+    __shared__ uint32_t s_sink[64];  // target of the L2 warm-up loads (never read)
     __shared__ int s_flag;
     const SkPlan &p = g.plan;
     const int w = sk_worker(p.G), u0 = sk_start(p, w), u1 = sk_start(p, w + 1);
     const rsrc_t rpart = make_rsrc(g.partials, g.partial_bytes);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, ln = lane & 15, lg = lane >> 4;
     const int M = g.M, N = g.N, K = g.K, U = K / KC;
+    const uint32_t rb = (uint32_t)g.row_bytes;
     const rsrc_t ra = make_rsrc(g.A, (uint32_t)((size_t)M * K * 2));
     const rsrc_t rw = make_rsrc(g.qs, (uint32_t)((size_t)N * g.row_bytes));
     const rsrc_t rs = make_rsrc(g.sums, (uint32_t)((size_t)M * U * 32));
-    uint32_t abase = 0, sbase = 0, vh[NB], vq[NB];
+    uint32_t abase = 0, sbase = 0, vh[NB];
+    const uint32_t vqo = 16u + 16u * lg;  // quant chunk lg of this lane, after the 16-byte header
     auto tile_setup = [&](int tile) {
-        const int m0 = (tile % p.tm) * BM, nw = (tile / p.tm) * 16 * NB * WNW + wave * 16 * NB;
+        const int m0 = (tile % p.tm) * BM, nw = (tile / p.tm) * BN + wave * 16 * NB;
         abase = adma_w_base(K, m0);
         sbase = (uint32_t)((m0 + 32 * wave + (lane >> 1)) * U * 32 + 16 * (lane & 1));
 #pragma unroll
-        for (int j = 0; j < NB; j++) {
-            const uint32_t n = (uint32_t)(nw + 16 * j + ln);
-            vh[j] = n * (uint32_t)g.row_bytes;
-            vq[j] = vh[j] + 16u + 16u * lg;
-        }
+        for (int j = 0; j < NB; j++) vh[j] = (uint32_t)(nw + 16 * j + ln) * rb;
     };
-    auto load_w = [&](int sb, u4v (&h)[NB], u4v (&q0)[NB], u4v (&q1)[NB]) {
-        const uint32_t so = (uint32_t)sb * 144u;
-#pragma unroll
-        for (int j = 0; j < NB; j++) {
-            h[j] = buf_load16(rw, vh[j], so);
-            q0[j] = buf_load16(rw, vq[j], so);
-            q1[j] = buf_load16(rw, vq[j] + 64u, so);
-        }
+    // Pull unit u's weight lines (BN columns x 144 bytes) into L2 ahead of the register loads:
+    // thread pair (2c, 2c + 1) touches bytes {0, 143} and {72} of column c's super-block, which
+    // covers every 128-byte line it spans. The bytes land in a scratch LDS word, not in registers.
+    auto touch_w = [&](int u) {
+        const int t = u / p.upt, sb = u % p.upt;
+        const uint32_t off = (uint32_t)((t / p.tm) * BN + (tid >> 1)) * rb + (uint32_t)sb * 144u;
+        const uint32_t o2 = (tid & 1) ? 72u : 0u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, lds_ptr(s_sink), 4, off + o2, 0, 0, 0);
+        if (!(tid & 1)) __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, lds_ptr(s_sink), 4, off + 140u, 0, 0, 0);
     };
     const int pA = lg >> 1, hA = lg & 1;
-    // byte offset of this lane's A fragment (L, t) in row block 0 of a tile buffer: row ln, chunk
-    // c = 8(2L + pA) + 2hA + (t & 1) + 4(t >> 1) stored at slot c ^ ln; row block i adds 16*KC*2*i
-    uint32_t aoff[8];
-#pragma unroll
-    for (int f = 0; f < 8; f++) {
-        const int L = f >> 2, t = f & 3;
-        const int c = 8 * (2 * L + pA) + 2 * hA + (t & 1) + 4 * (t >> 1);
-        aoff[f] = (uint32_t)(ln * KC + 8 * (c ^ ln)) * 2u;
-    }
+    const uint32_t ssel = pA ? 0x04030402u : 0x04010400u;  // scale bytes (2pA, 2pA + 1) as fp16 1024 + s
+    // A fragment (L, t) of this lane in row block 0 of a tile buffer: row ln, chunk
+    // c = 8(2L + pA) + 2hA + (t & 1) + 4(t >> 1) at slot c ^ ln. The step bits (bits 0, 2, 4 of c)
+    // are disjoint from the lane bits (8pA + 2hA), so slot = (8pA + 2hA) ^ ln ^ step bits and the
+    // byte offset is arow + (xs ^ 16 * step bits); row block i adds 16*KC*2*i.
+    const uint32_t arow = (uint32_t)(ln * KC * 2), xs = (uint32_t)(((8 * pA + 2 * hA) ^ ln) * 16);
     const uint32_t soff = (uint32_t)(ln * 16 + 8 * (lg & 1)) * 2u;
     f4 acc[MB][NB];
+    // one register set of weights: the header, quant half 0 and quant half 1 of the next unit are
+    // loaded into it as soon as the current unit has consumed each part
+    u4v hc[NB], q0c[NB], q1c[NB];
     int cur_tile = u0 / p.upt;
     tile_setup(cur_tile);
-    dma_a_w<MB>(sa[0], ra, abase, K, (u0 % p.upt) * KC);
-    dma_s_w<MB>(ssum[0], rs, sbase, u0 % p.upt);
-    // one unit: wait for its operands, start the next unit's, multiply, finish the tile if it ends
-    auto unit = [&](int u, const u4v (&hc)[NB], const u4v (&q0c)[NB], const u4v (&q1c)[NB], u4v (&hn)[NB],
-                    u4v (&q0n)[NB], u4v (&q1n)[NB]) {
+    {
+        const int sb = u0 % p.upt;
+        dma_a_w<MB>(sa[0], ra, abase, K, sb * KC);
+        dma_s_w<MB>(ssum[0], rs, sbase, sb);
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            hc[j] = buf_load16(rw, vh[j], (uint32_t)sb * 144u);
+            q0c[j] = buf_load16(rw, vh[j] + vqo, (uint32_t)sb * 144u);
+            q1c[j] = buf_load16(rw, vh[j] + vqo + 64u, (uint32_t)sb * 144u);
+        }
+        if (u0 + 1 < u1) touch_w(u0 + 1);
+    }
+    for (int u = u0; u < u1; u++) {
         const int cb = (u - u0) & 1, tile = u / p.upt, sb = u % p.upt;
-        const int m0 = (tile % p.tm) * BM, nw = (tile / p.tm) * 16 * NB * WNW + wave * 16 * NB;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const int m0 = (tile % p.tm) * BM, nw = (tile / p.tm) * BN + wave * 16 * NB;
+        // everything but the last NB loads (quant half 1 of this unit, waited for where it is
+        // used) has arrived: this unit's activation and sum tiles are in LDS for all waves after
+        // the barrier
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NB) : "memory");
         __syncthreads();
-        if (u + 1 < u1) {
+        const bool more = u + 1 < u1;
+        const int sb1 = (u + 1) % p.upt;
+        const uint32_t so1 = (uint32_t)sb1 * 144u;
+        if (more) {
             const int t1 = (u + 1) / p.upt;
             if (t1 != cur_tile) {
                 cur_tile = t1;
                 tile_setup(t1);
             }
-            const int sb1 = (u + 1) % p.upt;
-            dma_a_w<MB>(sa[cb ^ 1], ra, abase, K, sb1 * KC);
             dma_s_w<MB>(ssum[cb ^ 1], rs, sbase, sb1);
-            load_w(sb1, hn, q0n, q1n);
         }
         if (u == u0 || sb == 0) {
 #pragma unroll
@@ -1053,34 +1071,24 @@ __global__ void __launch_bounds__(512) k_gemm_q4_k_w(GemmArgs g) {
 #pragma unroll
                 for (int j = 0; j < NB; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
         }
-        h8 bf[NB][8], bmin[NB];
+        // per-unit constants. (x, y) = (low-nibble sub-block 4L + 2pA, high-nibble sub-block
+        // 4L + 2pA + 1): the B fragment is fma(fp16(1024 + q), mul, add) with mul = (s, s/16) and
+        // add = (-1024 s, -64 s); bmin is the min operand (k-slot e = sub-block e); dsc = d.
+        h2 mulL[NB][2], addL[NB][2];
+        h8 bmin[NB];
         float dsc[NB];
+        const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const h2 kmul = {(_Float16)1.0f, (_Float16)0.0625f}, kadd = {(_Float16)-1024.0f, (_Float16)-64.0f};
 #pragma unroll
         for (int j = 0; j < NB; j++) {
             uint32_t sw0, sw1, mw0, mw1;
             q4k_scale_words(hc[j].y, hc[j].z, hc[j].w, sw0, sw1, mw0, mw1);
-            h2 mulL[2][2], addL[2][2];
 #pragma unroll
             for (int L = 0; L < 2; L++) {
-                const uint32_t sw = L ? sw1 : sw0;
-#pragma unroll
-                for (int hi = 0; hi < 2; hi++) {
-                    const float s = (float)byte_of(sw, 2 * pA + hi);
-                    const _Float16 mul = (_Float16)(hi ? s * 0.0625f : s);
-                    const _Float16 add = (_Float16)(hi ? -64.0f * s : -1024.0f * s);
-                    mulL[L][hi] = h2{mul, mul};
-                    addL[L][hi] = h2{add, add};
-                }
+                const h2 sp = as_h2(__builtin_amdgcn_perm(0x64646464u, L ? sw1 : sw0, ssel)) - k1024;
+                mulL[j][L] = sp * kmul;
+                addL[j][L] = sp * kadd;
             }
-            bf[j][0] = frag_q4_k<false>(q0c[j].x, q0c[j].y, mulL[0][0], addL[0][0]);
-            bf[j][1] = frag_q4_k<false>(q0c[j].z, q0c[j].w, mulL[0][0], addL[0][0]);
-            bf[j][2] = frag_q4_k<true>(q0c[j].x, q0c[j].y, mulL[0][1], addL[0][1]);
-            bf[j][3] = frag_q4_k<true>(q0c[j].z, q0c[j].w, mulL[0][1], addL[0][1]);
-            bf[j][4] = frag_q4_k<false>(q1c[j].x, q1c[j].y, mulL[1][0], addL[1][0]);
-            bf[j][5] = frag_q4_k<false>(q1c[j].z, q1c[j].w, mulL[1][0], addL[1][0]);
-            bf[j][6] = frag_q4_k<true>(q1c[j].x, q1c[j].y, mulL[1][1], addL[1][1]);
-            bf[j][7] = frag_q4_k<true>(q1c[j].z, q1c[j].w, mulL[1][1], addL[1][1]);
-            // min operand: k-slot e = sub-block e
             const _Float16 ndm = -__builtin_bit_cast(_Float16, (uint16_t)(hc[j].x >> 16));
             const h2 nd2 = {ndm, ndm};
             const h2 mv[4] = {bytes_f16(mw0, false), bytes_f16(mw0, true), bytes_f16(mw1, false),
@@ -1095,37 +1103,63 @@ __global__ void __launch_bounds__(512) k_gemm_q4_k_w(GemmArgs g) {
             }
             dsc[j] = h2f((uint16_t)hc[j].x);
         }
-        const char *abuf = (const char *)sa[cb];
-        const char *sbuf = (const char *)ssum[cb] + soff;
-        uint32_t ad[8];
+        // Loads for the unit after this one are issued unconditionally (no branch inside the
+        // unit): past the workgroup's last unit they read in-bounds rows (or out-of-range zeros)
+        // into registers and an LDS buffer that nothing reads again.
 #pragma unroll
-        for (int f = 0; f < 8; f++) ad[f] = (uint32_t)(uintptr_t)abuf + aoff[f];
+        for (int j = 0; j < NB; j++) hc[j] = buf_load16(rw, vh[j], so1);
+        const uint32_t abuf = (uint32_t)(uintptr_t)sa[cb];
+        const char *sbuf = (const char *)ssum[cb] + soff;
+        // k-step outermost: step f's A fragments are read together, its two B fragments decoded,
+        // then its 2*MB MFMAs issued
+        f4 part[MB][NB];
+#pragma unroll
+        for (int f = 0; f < 8; f++) {
+            const int L = f >> 2, t = f & 3;
+            const uint32_t ad = abuf + arow + (xs ^ (uint32_t)(16 * ((t & 1) + 4 * (t >> 1) + 16 * L)));
+            h8 af[MB];
+#pragma unroll
+            for (int i = 0; i < MB; i++) af[i] = *(const h8 *)(lds_void *)(uintptr_t)(ad + i * 16 * KC * 2);
+            h8 bf[NB];
+#pragma unroll
+            for (int j = 0; j < NB; j++) {
+                const u4v &q = L ? q1c[j] : q0c[j];
+                const uint32_t w0 = (t & 1) ? q.z : q.x, w1 = (t & 1) ? q.w : q.y;
+                const h2 mu = mulL[j][L], ad2 = addL[j][L];
+                bf[j] = (t >> 1) ? frag_q4_k<true>(w0, w1, h2{mu.y, mu.y}, h2{ad2.y, ad2.y})
+                                 : frag_q4_k<false>(w0, w1, h2{mu.x, mu.x}, h2{ad2.x, ad2.x});
+            }
+#pragma unroll
+            for (int i = 0; i < MB; i++)
+#pragma unroll
+                for (int j = 0; j < NB; j++)
+                    part[i][j] = mfma(af[i], bf[j], f == 0 ? f4{0.f, 0.f, 0.f, 0.f} : part[i][j]);
+            // the next unit's activation tile streams in one instruction per step, so the memory
+            // pipeline is not flooded right after the barrier
+            static_assert(16 * MB / 2 / WNW == 8, "one DMA instruction per k-step");
+            dma_a_w1(sa[cb ^ 1], ra, abase, K, sb1 * KC, f);
+            if (f == 4) touch_w(u + 2);
+            if (f == 3) {  // quant half 0 consumed: load the next unit's
+#pragma unroll
+                for (int j = 0; j < NB; j++) q0c[j] = buf_load16(rw, vh[j] + vqo, so1);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int j = 0; j < NB; j++) q1c[j] = buf_load16(rw, vh[j] + vqo + 64u, so1);
 #pragma unroll
         for (int i = 0; i < MB; i++) {
             const h8 as = *(const h8 *)(sbuf + i * 16 * 32);
 #pragma unroll
             for (int j = 0; j < NB; j++) acc[i][j] = mfma(as, bmin[j], acc[i][j]);
-            f4 part[NB];
-#pragma unroll
-            for (int j = 0; j < NB; j++) part[j] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int f = 0; f < 8; f++) {
-                const h8 af = *(const h8 *)(lds_void *)(uintptr_t)(ad[f] + i * 16 * KC * 2);
-#pragma unroll
-                for (int j = 0; j < NB; j++) part[j] = mfma(af, bf[j][f], part[j]);
-            }
-#pragma unroll
-            for (int j = 0; j < NB; j++) acc[i][j] += part[j] * dsc[j];
         }
+#pragma unroll
+        for (int i = 0; i < MB; i++)
+#pragma unroll
+            for (int j = 0; j < NB; j++) acc[i][j] += part[i][j] * dsc[j];
         if (sb == p.upt - 1 || u == u1 - 1)
             finish_tile<MB, NB, NT>(acc, p, w, u0, u1, tile, &s_flag, rpart, g.counters, g.C, M, N, m0, nw, ln, lg,
                                     g.c_f32, g.accumulate);
-    };
-    u4v hA0[NB], qA0[NB], qA1[NB], hB0[NB], qB0[NB], qB1[NB];
-    load_w(u0 % p.upt, hA0, qA0, qA1);
-    for (int u = u0; u < u1; u += 2) {  // two units per trip: the weight registers alternate roles
-        unit(u, hA0, qA0, qA1, hB0, qB0, qB1);
-        if (u + 1 < u1) unit(u + 1, hB0, qB0, qB1, hA0, qA0, qA1);
     }
 }
 
