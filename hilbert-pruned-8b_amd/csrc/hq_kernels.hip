@@ -548,21 +548,73 @@ DEV int sk_owner(const SkPlan &p, int u) {
     return u < big ? u / (p.base + 1) : p.extra + (u - big) / p.base;
 }
 
+// Quad permutes of one VGPR by DPP, written as inline assembly: this compiler merges
+// __builtin_amdgcn_mov_dpp / update_dpp calls that share a DPP control but read different
+// registers into one move of the first register (observed on gfx950, ROCm 7.2). The s_nop gives
+// the source's producer 5 wait states (a plain VALU write needs 2 before a DPP read; a
+// v_dot2c_f32_f16 result needs more).
+DEV float dpp_quad_1032(float v) {
+    float r;
+    asm volatile("s_nop 4\n\tv_mov_b32_dpp %0, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf" : "=v"(r) : "v"(v));
+    return r;
+}
+DEV float dpp_quad_2301(float v) {
+    float r;
+    asm volatile("s_nop 4\n\tv_mov_b32_dpp %0, %1 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf" : "=v"(r) : "v"(v));
+    return r;
+}
+
+// 4 x 4 transpose inside each quad of lanes: on entry lane k of a quad holds x[e] = X[e][k], on
+// return x[e] = X[k][e]. Two rounds, each swapping the (register bit, lane bit) off-diagonal pairs:
+// bit 0 through quad_perm [1,0,3,2], bit 1 through quad_perm [2,3,0,1].
+DEV f4 quad_transpose(f4 x) {
+    const int k = threadIdx.x & 3;
+    f4 y, z;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float t = dpp_quad_1032(x[e ^ 1]);
+        y[e] = ((e ^ k) & 1) ? t : x[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float t = dpp_quad_2301(y[e ^ 2]);
+        z[e] = ((e ^ k) & 2) ? t : y[e];
+    }
+    return z;
+}
+
+// Output tile of one wave: block (i, j) holds rows m0 + 16i + 4lg + e, column nw + 16j + ln in
+// register e of lane (ln, lg). A quad transpose gives lane (4c + k, lg) row 4lg + k, columns
+// 4c .. 4c + 3, stored as one 8-byte (fp16) or 16-byte (fp32) access when N % 4 == 0, else
+// element by element (the same values and roundings either way).
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 template <int MB, int NB>
 DEV void store_tile(void *C, const f4 (&acc)[MB][NB], int M, int N, int m0, int nw, int ln, int lg, int c_f32,
                     int accumulate) {
+    const int k = ln & 3, c4 = ln & ~3;
+    const bool wide = (N & 3) == 0;
 #pragma unroll
-    for (int j = 0; j < NB; j++) {
-        const int n = nw + 16 * j + ln;
-        if (n >= N) continue;
+    for (int j = 0; j < NB; j++)
 #pragma unroll
-        for (int i = 0; i < MB; i++)
+        for (int i = 0; i < MB; i++) {
+            const f4 y = quad_transpose(acc[i][j]);
+            const int m = m0 + 16 * i + 4 * lg + k, n = nw + 16 * j + c4;
+            if (m >= M || n >= N) continue;
+            const size_t idx = (size_t)m * N + n;
+            if (wide) {
+                if (c_f32) {
+                    f4 *c = (f4 *)((float *)C + idx);
+                    *c = accumulate ? *c + y : y;
+                } else {
+                    h4 *c = (h4 *)((_Float16 *)C + idx);
+                    *c = __builtin_convertvector(accumulate ? __builtin_convertvector(*c, f4) + y : y, h4);
+                }
+            } else {
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int m = m0 + 16 * i + 4 * lg + e;
-                if (m < M) store_out(C, (size_t)m * N + n, acc[i][j][e], c_f32, accumulate);
+                for (int e = 0; e < 4; e++)
+                    if (n + e < N) store_out(C, idx + e, y[e], c_f32, accumulate);
             }
-    }
+        }
 }
 
 // Partial tiles are written and read with device-scope (sc1) buffer accesses: they go to the
@@ -1164,29 +1216,31 @@ __global__ void __launch_bounds__(512) k_gemm_q4_k_w(GemmArgs g) {
 }
 
 // Activation sub-block sums for the wide Q4_K GEMM: S[m][u][s] = fp16 hi and S[m][u][8 + s] = fp16
-// lo of the fp32 sum of activations 256u + 32s .. +32 of row m (hi + lo = the fp32 sum).
+// lo of the fp32 sum of activations 256u + 32s .. +32 of row m (hi + lo = the fp32 sum). One
+// 16-byte chunk per thread; the four chunks of a sub-block sit in one quad of lanes and are added
+// by two DPP rounds ((c0 + c1) + (c2 + c3) in every lane), then lanes 0 and 1 of the quad write hi
+// and lo. M*K/8 is a multiple of 4, so a quad is always entirely inside or outside the range.
 __global__ void __launch_bounds__(256) k_asums(const uint16_t *__restrict__ A, int M, int K,
                                                uint16_t *__restrict__ S) {
-    const int nsub = K / 32;
-    const size_t n = (size_t)M * nsub;
+    const size_t n = (size_t)M * K / 8;
     const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
     for (size_t t = blockIdx.x * (size_t)256 + threadIdx.x; t < n; t += (size_t)gridDim.x * 256) {
-        const size_t m = t / nsub;
-        const int b = (int)(t % nsub);
-        const u4v *src = (const u4v *)(A + m * K + 32 * b);
-        float s = 0.f;
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const u4v x = src[v];
-            s = __builtin_amdgcn_fdot2(as_h2(x.x), one, s, false);
-            s = __builtin_amdgcn_fdot2(as_h2(x.y), one, s, false);
-            s = __builtin_amdgcn_fdot2(as_h2(x.z), one, s, false);
-            s = __builtin_amdgcn_fdot2(as_h2(x.w), one, s, false);
+        const u4v x = *(const u4v *)(A + 8 * t);
+        float v = __builtin_amdgcn_fdot2(as_h2(x.x), one, 0.f, false);
+        v = __builtin_amdgcn_fdot2(as_h2(x.y), one, v, false);
+        v = __builtin_amdgcn_fdot2(as_h2(x.z), one, v, false);
+        v = __builtin_amdgcn_fdot2(as_h2(x.w), one, v, false);
+        v += dpp_quad_1032(v);
+        v += dpp_quad_2301(v);
+        const int part = (int)(t & 3);
+        if (part < 2) {
+            const size_t b = t >> 2;  // sub-block index m * (K / 32) + k / 32
+            const size_t m = b / (size_t)(K / 32);
+            const int kb = (int)(b % (size_t)(K / 32));
+            const _Float16 hi = (_Float16)v;
+            S[(m * (size_t)(K / 256) + kb / 8) * 16 + 8 * part + (kb % 8)] =
+                __builtin_bit_cast(uint16_t, part ? (_Float16)(v - (float)hi) : hi);
         }
-        const _Float16 hi = (_Float16)s;
-        uint16_t *dst = S + (m * (size_t)(K / 256) + b / 8) * 16 + (b % 8);
-        dst[0] = __builtin_bit_cast(uint16_t, hi);
-        dst[8] = __builtin_bit_cast(uint16_t, (_Float16)(s - (float)hi));
     }
 }
 
@@ -1329,8 +1383,8 @@ hipError_t hq_launch_gemm(const hq_dev_mat *W, const uint16_t *A, int M, void *C
         g.partial_bytes = (uint32_t)pb;
     }
     if (c.wide) {
-        const size_t nsub = (size_t)M * (W->cols / 32);
-        k_asums<<<grid_for(nsub, 256, 8192), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
+        const size_t n16 = (size_t)M * (W->cols / 8);
+        k_asums<<<grid_for(n16, 256, 16384), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
         k_gemm_q4_k_w<8><<<g.plan.G, 64 * WNW, 0, st>>>(g);
         return hipGetLastError();
     }
