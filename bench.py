@@ -134,6 +134,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
+                    help="only run 20 device-to-device copies of BYTES bytes (the known-size kernel the "
+                         "FETCH_SIZE / WRITE_SIZE counters are scaled by) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); the quantized matmul "
@@ -143,6 +146,15 @@ def main():
     import synth
     hq.load()
     hq.device_init(0)
+    if args.calibrate_copy:
+        n = args.calibrate_copy
+        src, dst = hq.DevBuf(n), hq.DevBuf(n)
+        hq._check(hq.load().hq_memset(src.ptr, 1, n, None))
+        for _ in range(20):
+            hq._check(hq.load().hq_memcpy_d2d(dst.ptr, src.ptr, n, None))
+        hq.synchronize()
+        log(f"calibration: 20 device copies of {n} bytes")
+        return
     name, arch = hq.device_name(0)
     log("device", name, arch)
     stream = hq.Stream()

@@ -376,6 +376,11 @@ extern "C" int hq_memcpy_h2d(void *dst, const void *src, size_t n, void *stream)
     HIPCK(hipStreamSynchronize(S(stream)));
     return 0;
 }
+extern "C" int hq_memcpy_d2d(void *dst, const void *src, size_t n, void *stream) {
+    HIPCK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, S(stream)));
+    return 0;
+}
+
 extern "C" int hq_memcpy_d2h(void *dst, const void *src, size_t n, void *stream) {
     HIPCK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, S(stream)));
     HIPCK(hipStreamSynchronize(S(stream)));

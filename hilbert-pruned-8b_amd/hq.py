@@ -21,7 +21,7 @@ EXPORTS = (
     "hq_last_error", "hq_device_init", "hq_device_count", "hq_device_name", "hq_mat_upload", "hq_mat_free",
     "hq_mat_shape", "hq_mat_device_bytes", "hq_mat_download", "hq_dequant_f32", "hq_gemm", "hq_gemv",
     "hq_gather_dot", "hq_gather_dot_dev", "hq_matmul_host", "hq_malloc", "hq_free", "hq_memcpy_h2d",
-    "hq_memcpy_d2h", "hq_memset", "hq_stream_create", "hq_stream_destroy", "hq_stream_synchronize",
+    "hq_memcpy_d2h", "hq_memcpy_d2d", "hq_memset", "hq_stream_create", "hq_stream_destroy", "hq_stream_synchronize",
     "hq_device_synchronize", "hq_time_gemm", "hq_time_gather", "hq_gemm_tiles", "hq_llama_forward",
     "hq_embed_f32",
 )
@@ -81,6 +81,7 @@ def load(path=LIB_PATH):
         "hq_free": (i, [vp]),
         "hq_memcpy_h2d": (i, [vp, vp, sz, vp]),
         "hq_memcpy_d2h": (i, [vp, vp, sz, vp]),
+        "hq_memcpy_d2d": (i, [vp, vp, sz, vp]),
         "hq_memset": (i, [vp, i, sz, vp]),
         "hq_stream_create": (i, [C.POINTER(vp)]),
         "hq_stream_destroy": (i, [vp]),

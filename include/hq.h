@@ -96,6 +96,9 @@ int hq_malloc(void **p, size_t n);
 int hq_free(void *p);
 int hq_memcpy_h2d(void *dst, const void *src, size_t n, void *stream);
 int hq_memcpy_d2h(void *dst, const void *src, size_t n, void *stream);
+/* device to device, asynchronous on `stream` (also the copy kernel the HBM-traffic counters are
+ * calibrated against) */
+int hq_memcpy_d2d(void *dst, const void *src, size_t n, void *stream);
 int hq_memset(void *dst, int value, size_t n, void *stream);
 int hq_stream_create(void **stream);
 int hq_stream_destroy(void *stream);
