@@ -8,7 +8,14 @@ HIP-graph replay of exactly `steps` launches, timed with HIP events on the launc
 `warmup` eager launches and one untimed replay of the same graph.
 
 Also reported (key "sweep"): the config 2 / 3 M sweeps and the config 5 option readout, each as
-achieved TFLOP/s and GB/s of algorithmic bytes (W blocks once + A + C) and their roofline fractions.
+achieved TFLOP/s and GB/s of algorithmic bytes (W blocks once + A + C) and their roofline fractions,
+and config 4 (the 4B-class hybrid's 32-layer projection sequence at M = 16384, BASELINE's literal
+widths: each distinct projection shape timed, weighted by its count in the sequence).
+
+roofline: the headline GEMM's main kernel, timed alone (hq_time_gemm_kernel; the Q4_K activation
+pre-pass runs once outside the timed graph) with HIP events on its stream; `traffic` is its HBM
+bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (calibrated against a
+device copy of known size).
 
 cpu_baseline: the CPU oracle (a restatement of the reference's cpu_backend.c matmul, compiled with
 the reference's flags, OpenMP) on the headline GEMM, timed on this host's cores.
@@ -41,23 +48,26 @@ def gemm_bytes(gtype, M, N, K, c_bytes):
 
 
 def read_traffic(name):
-    """HBM bytes per launch of the headline kernel from the committed PMC summary, or None."""
-    path = os.path.join(ROOT, "profiles", "pmc_traffic.txt")
+    """HBM bytes per launch of the headline kernel from the committed rocprofv3 counter summary
+    (line `traffic_bytes_per_launch <workload> <bytes>`), or None."""
+    path = os.path.join(ROOT, "profiles", "q4k_gemm_m512_k2560_n9728_hbm_traffic.md")
     if not os.path.exists(path):
         return None
     for line in open(path):
-        if line.startswith(name + " "):
+        f = line.split()
+        if len(f) == 3 and f[0] == "traffic_bytes_per_launch" and f[1] == name:
             try:
-                return float(line.split()[1])
-            except (IndexError, ValueError):
+                return float(f[2])
+            except ValueError:
                 return None
     return None
 
 
-def bench_gemm(hq, synth, gtype, N, K, M, c_f32, steps, warmup, stream, eager_warmup=True):
+def bench_gemm(hq, synth, gtype, N, K, M, c_f32, steps, warmup, stream, eager_warmup=True, kernel_time=False,
+               rotate=True, settle_s=0.0):
     rb = synth.row_bytes(gtype, K)
     blocks = synth.random_blocks(gtype, synth.Rng(4242 + gtype + N), N, K)
-    copies = max(2, -(-ROTATE_BYTES // (N * rb)))
+    copies = max(2, -(-ROTATE_BYTES // (N * rb))) if rotate else 2
     mats = [hq.Mat(blocks, gtype, N, K) for _ in range(copies)]
     A = hq.DevBuf.from_array(synth.activations_f16(synth.Rng(99 + M), M, K))
     C = hq.DevBuf(M * N * (4 if c_f32 else 2))
@@ -65,17 +75,46 @@ def bench_gemm(hq, synth, gtype, N, K, M, c_f32, steps, warmup, stream, eager_wa
         for i in range(warmup):
             hq.gemm(mats[i % copies], A, M, C, c_f32, False, stream.ptr)
         stream.sync()
+        # untimed: keep the GPU busy for settle_s so its clocks are at their loaded level
+        t_end, i = time.perf_counter() + settle_s, 0
+        while time.perf_counter() < t_end:
+            for _ in range(20):
+                hq.gemm(mats[i % copies], A, M, C, c_f32, False, stream.ptr)
+                i += 1
+            stream.sync()
     t0 = time.perf_counter()
     ms = hq.time_gemm(mats, A, M, C, c_f32, steps, 1, stream)
     wall = time.perf_counter() - t0
+    ms_kernel = hq.time_gemm_kernel(mats, A, M, C, c_f32, steps, 1, stream) if (kernel_time and M > 1) else None
     for m in mats:
         m.free()
     A.free(), C.free()
     flop = 2.0 * M * N * K
     nbytes = gemm_bytes(gtype, M, N, K, 4 if c_f32 else 2)
-    return dict(type="q8_0" if gtype == synth.Q8_0 else "q4_k", M=M, N=N, K=K, us=ms * 1e3,
-                tflops=flop / (ms * 1e-3) / 1e12, gbs=nbytes / (ms * 1e-3) / 1e9, copies=copies,
-                wall_s=wall)
+    r = dict(type="q8_0" if gtype == synth.Q8_0 else "q4_k", M=M, N=N, K=K, us=ms * 1e3,
+             tflops=flop / (ms * 1e-3) / 1e12, gbs=nbytes / (ms * 1e-3) / 1e9, copies=copies, wall_s=wall)
+    if ms_kernel is not None:
+        r["kernel_us"] = ms_kernel * 1e3
+        r["kernel_tflops"] = flop / (ms_kernel * 1e-3) / 1e12
+    return r
+
+
+def bench_config4(hq, synth, stream, M=16384):
+    """Config 4: the hybrid 4B projection sequence (32 layers) at M = 16384; each distinct shape timed
+    once (3 launches), total = sum over the sequence."""
+    counts = {}
+    for layer in synth.hybrid_4b_projections():
+        for _, n, k in layer:
+            counts[(n, k)] = counts.get((n, k), 0) + 1
+    total_us, flop, shapes = 0.0, 0.0, []
+    for (n, k), cnt in sorted(counts.items()):
+        r = bench_gemm(hq, synth, synth.Q4_K, n, k, M, False, 3, 1, stream, rotate=False)
+        total_us += cnt * r["us"]
+        flop += cnt * 2.0 * M * n * k
+        shapes.append({"N": n, "K": k, "count": cnt, "us": round(r["us"], 2), "tflops": round(r["tflops"], 1)})
+    return dict(type="config4_hybrid_4b_q4_k", M=M, projections=sum(counts.values()), total_ms=round(total_us / 1e3, 3),
+                tflop=round(flop / 1e12, 2), tflops=round(flop / (total_us * 1e-6) / 1e12, 1),
+                frac=round(flop / (total_us * 1e-6) / 1e12 / PEAK_TFLOPS, 4), bound="mfma", shapes=shapes)
 
 
 def bench_gather(hq, synth, k, stream, reps=3):
@@ -160,7 +199,8 @@ def main():
     stream = hq.Stream()
 
     gtype, N, K, M = synth.Q4_K, 9728, 2560, 512
-    head = bench_gemm(hq, synth, gtype, N, K, M, False, args.steps, args.warmup, stream)
+    head = bench_gemm(hq, synth, gtype, N, K, M, False, args.steps, args.warmup, stream, kernel_time=True,
+                      settle_s=0.3)
     log("headline", head)
     value = head["tflops"]
 
@@ -181,9 +221,14 @@ def main():
             r["bound"], r["frac"] = "hbm", round(r["gbs"] / PEAK_GBS, 4)
             log("sweep", r)
             sweep.append({key: (round(v, 4) if isinstance(v, float) else v) for key, v in r.items()})
+        r = bench_config4(hq, synth, stream)
+        log("sweep", r)
+        sweep.append(r)
 
-    roofline = dict(bound="mfma", achieved=round(value, 3), peak=PEAK_TFLOPS, unit="TFLOP/s",
-                    frac=round(value / PEAK_TFLOPS, 4), traffic=read_traffic("q4_k_gemm_m512_k2560_n9728"))
+    kt = head["kernel_tflops"]
+    roofline = dict(bound="mfma", achieved=round(kt, 3), peak=PEAK_TFLOPS, unit="TFLOP/s",
+                    frac=round(kt / PEAK_TFLOPS, 4), traffic=read_traffic("q4_k_gemm_m512_k2560_n9728"),
+                    kernel="k_gemm_q4_k_w<8>", kernel_us=round(head["kernel_us"], 3))
     cpu = None if args.no_cpu else cpu_baseline(synth, gtype, N, K, M)
     line = {
         "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,

@@ -471,6 +471,27 @@ extern "C" int hq_time_gemm(hq_mat *const *Ws, int n_w, const uint16_t *A, int M
                       [&](int i) { return hq_gemm(Ws[i % n_w], A, M, C, c_is_f32, 0, stream); });
 }
 
+extern "C" int hq_time_gemm_kernel(hq_mat *const *Ws, int n_w, const uint16_t *A, int M, void *C, int c_is_f32,
+                                   int iters, int reps, void *stream, float *ms) {
+    if (!Ws || n_w < 1) return fail("hq_time_gemm_kernel: no matrices");
+    if (M < 2) return fail("hq_time_gemm_kernel: M = %d (the GEMM kernels run for M >= 2)", M);
+    for (int i = 0; i < n_w; i++)
+        if (!Ws[i] || Ws[i]->m.rows != Ws[0]->m.rows || Ws[i]->m.cols != Ws[0]->m.cols || Ws[i]->m.type != Ws[0]->m.type)
+            return fail("hq_time_gemm_kernel: matrices differ in shape or type");
+    if (!aligned(A, 16)) return fail("hq_time_gemm_kernel: A must be 16-byte aligned");
+    if (use_device(Ws[0]->device)) return -1;
+    HqGemmWork wk;
+    if (gemm_work(Ws[0], M, &wk)) return -1;
+    // the pre-pass depends on A only: run it once, then time the main kernel alone
+    HIPCK(hq_launch_gemm_pre(&Ws[0]->m, A, M, wk, S(stream)));
+    HIPCK(hq_launch_gemm_main(&Ws[0]->m, A, M, C, c_is_f32, 0, wk, S(stream)));
+    HIPCK(hipStreamSynchronize(S(stream)));
+    return time_graph(iters, reps, stream, ms, [&](int i) {
+        HIPCK(hq_launch_gemm_main(&Ws[i % n_w]->m, A, M, C, c_is_f32, 0, wk, S(stream)));
+        return 0;
+    });
+}
+
 extern "C" int hq_time_gather(hq_mat *const *Ws, int n_w, const uint16_t *H, const uint32_t *ids_dev, int n_sets,
                               int B, int k, float *out, int iters, int reps, void *stream, float *ms) {
     if (!Ws || n_w < 1) return fail("hq_time_gather: no matrices");

@@ -33,7 +33,11 @@ struct HqGemmWork {
 };
 void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_bytes, size_t *counter_bytes,
                         size_t *sums_bytes);
-// M >= 2.
+// M >= 2: hq_launch_gemm = hq_launch_gemm_pre (activation pre-pass, if the kernel needs one) then
+// hq_launch_gemm_main.
+hipError_t hq_launch_gemm_pre(const hq_dev_mat *W, const uint16_t *A, int M, const HqGemmWork &wk, hipStream_t st);
+hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
+                               const HqGemmWork &wk, hipStream_t st);
 hipError_t hq_launch_gemm(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
                           const HqGemmWork &wk, hipStream_t st);
 hipError_t hq_launch_gather(const hq_dev_mat *W, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,

@@ -1368,8 +1368,19 @@ void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_by
     *sums_bytes = c.wide ? (size_t)M * (W->cols / KC) * 32 : 0;
 }
 
-hipError_t hq_launch_gemm(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
-                          const HqGemmWork &wk, hipStream_t st) {
+// Pre-pass of a GEMM (the wide Q4_K kernel's activation sub-block sums; nothing otherwise).
+hipError_t hq_launch_gemm_pre(const hq_dev_mat *W, const uint16_t *A, int M, const HqGemmWork &wk, hipStream_t st) {
+    const GemmCfg c = gemm_cfg(W, M);
+    if (c.wide) {
+        const size_t n16 = (size_t)M * (W->cols / 8);
+        k_asums<<<grid_for(n16, 256, 16384), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
+    }
+    return hipGetLastError();
+}
+
+// Main kernel of a GEMM (needs hq_launch_gemm_pre's output for the same A).
+hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
+                               const HqGemmWork &wk, hipStream_t st) {
     const GemmCfg c = gemm_cfg(W, M);
     GemmArgs g;
     g.qs = W->qs, g.d = W->d, g.ldd = W->ldd, g.row_bytes = W->row_bytes, g.A = A;
@@ -1383,8 +1394,6 @@ hipError_t hq_launch_gemm(const hq_dev_mat *W, const uint16_t *A, int M, void *C
         g.partial_bytes = (uint32_t)pb;
     }
     if (c.wide) {
-        const size_t n16 = (size_t)M * (W->cols / 8);
-        k_asums<<<grid_for(n16, 256, 16384), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
         k_gemm_q4_k_w<8><<<g.plan.G, 64 * WNW, 0, st>>>(g);
         return hipGetLastError();
     }
@@ -1397,6 +1406,12 @@ hipError_t hq_launch_gemm(const hq_dev_mat *W, const uint16_t *A, int M, void *C
     CASE(1) CASE(2) CASE(4) CASE(8)
 #undef CASE
     return hipErrorInvalidValue;
+}
+
+hipError_t hq_launch_gemm(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
+                          const HqGemmWork &wk, hipStream_t st) {
+    const hipError_t e = hq_launch_gemm_pre(W, A, M, wk, st);
+    return e != hipSuccess ? e : hq_launch_gemm_main(W, A, M, C, c_f32, accumulate, wk, st);
 }
 
 hipError_t hq_launch_f32_to_f16(const float *in, uint16_t *out, size_t n, hipStream_t st) {

@@ -22,7 +22,7 @@ EXPORTS = (
     "hq_mat_shape", "hq_mat_device_bytes", "hq_mat_download", "hq_dequant_f32", "hq_gemm", "hq_gemv",
     "hq_gather_dot", "hq_gather_dot_dev", "hq_matmul_host", "hq_malloc", "hq_free", "hq_memcpy_h2d",
     "hq_memcpy_d2h", "hq_memcpy_d2d", "hq_memset", "hq_stream_create", "hq_stream_destroy", "hq_stream_synchronize",
-    "hq_device_synchronize", "hq_time_gemm", "hq_time_gather", "hq_gemm_tiles", "hq_llama_forward",
+    "hq_device_synchronize", "hq_time_gemm", "hq_time_gemm_kernel", "hq_time_gather", "hq_gemm_tiles", "hq_llama_forward",
     "hq_embed_f32",
 )
 
@@ -88,6 +88,7 @@ def load(path=LIB_PATH):
         "hq_stream_synchronize": (i, [vp]),
         "hq_device_synchronize": (i, []),
         "hq_time_gemm": (i, [C.POINTER(vp), i, vp, i, vp, i, i, i, vp, C.POINTER(C.c_float)]),
+        "hq_time_gemm_kernel": (i, [C.POINTER(vp), i, vp, i, vp, i, i, i, vp, C.POINTER(C.c_float)]),
         "hq_time_gather": (i, [C.POINTER(vp), i, vp, vp, i, i, i, vp, i, i, vp, C.POINTER(C.c_float)]),
         "hq_gemm_tiles": (None, [i, i, i, C.POINTER(i), C.POINTER(i)]),
         "hq_llama_forward": (i, [C.POINTER(Llama), vp, sz, vp, u32, vp]),
@@ -294,6 +295,15 @@ def time_gemm(mats, A, M, C_buf, c_f32, iters, reps, stream):
     arr = (C.c_void_p * len(mats))(*[m.h for m in mats])
     ms = C.c_float()
     _check(_lib.hq_time_gemm(arr, len(mats), A.ptr, M, C_buf.ptr, int(c_f32), iters, reps, stream.ptr, C.byref(ms)))
+    return ms.value
+
+
+def time_gemm_kernel(mats, A, M, C_buf, c_f32, iters, reps, stream):
+    """Average duration (ms) of the GEMM's main kernel alone (see hq_time_gemm_kernel)."""
+    arr = (C.c_void_p * len(mats))(*[m.h for m in mats])
+    ms = C.c_float()
+    _check(_lib.hq_time_gemm_kernel(arr, len(mats), A.ptr, M, C_buf.ptr, int(c_f32), iters, reps, stream.ptr,
+                                    C.byref(ms)))
     return ms.value
 
 

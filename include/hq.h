@@ -111,6 +111,10 @@ int hq_device_synchronize(void);
  * replay; *ms = mean milliseconds per launch measured with HIP events on `stream`. */
 int hq_time_gemm(hq_mat *const *Ws, int n_w, const uint16_t *A, int M, void *C, int c_is_f32, int iters, int reps,
                  void *stream, float *ms);
+/* As hq_time_gemm, timing only the GEMM's main kernel (M >= 2): an activation pre-pass the
+ * kernel needs (it depends on A alone) runs once before the capture. */
+int hq_time_gemm_kernel(hq_mat *const *Ws, int n_w, const uint16_t *A, int M, void *C, int c_is_f32, int iters,
+                        int reps, void *stream, float *ms);
 int hq_time_gather(hq_mat *const *Ws, int n_w, const uint16_t *H, const uint32_t *ids_dev, int n_sets, int B, int k,
                    float *out, int iters, int reps, void *stream, float *ms);
 
