@@ -12,10 +12,11 @@ achieved TFLOP/s and GB/s of algorithmic bytes (W blocks once + A + C) and their
 and config 4 (the 4B-class hybrid's 32-layer projection sequence at M = 16384, BASELINE's literal
 widths: each distinct projection shape timed, weighted by its count in the sequence).
 
-roofline: the headline GEMM's main kernel, timed alone (hq_time_gemm_kernel; the Q4_K activation
-pre-pass runs once outside the timed graph) with HIP events on its stream; `traffic` is its HBM
-bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (calibrated against a
-device copy of known size).
+roofline: the headline GEMM's main kernel (k_gemm_q4_k_ws<5>: full-K 128 x 160 tiles), timed alone
+(hq_time_gemm_kernel; the Q4_K activation pre-pass runs once outside the timed graph) with HIP
+events on its stream; `traffic` is its HBM bytes per launch from the committed rocprofv3
+FETCH_SIZE / WRITE_SIZE summary (calibrated against a device copy of known size), null when that
+summary was taken for a different kernel.
 
 cpu_baseline: the CPU oracle (a restatement of the reference's cpu_backend.c matmul, compiled with
 the reference's flags, OpenMP) on the headline GEMM, timed on this host's cores.
@@ -47,20 +48,31 @@ def gemm_bytes(gtype, M, N, K, c_bytes):
     return N * synth.row_bytes(gtype, K) + M * K * 2 + M * N * c_bytes
 
 
-def read_traffic(name):
+def read_traffic(name, kernel):
     """HBM bytes per launch of the headline kernel from the committed rocprofv3 counter summary
-    (line `traffic_bytes_per_launch <workload> <bytes>`), or None."""
+    (line `traffic_bytes_per_launch <workload> <kernel> <bytes>`), or None when the summary is for
+    another kernel."""
     path = os.path.join(ROOT, "profiles", "q4k_gemm_m512_k2560_n9728_hbm_traffic.md")
     if not os.path.exists(path):
         return None
     for line in open(path):
         f = line.split()
-        if len(f) == 3 and f[0] == "traffic_bytes_per_launch" and f[1] == name:
+        if len(f) == 4 and f[0] == "traffic_bytes_per_launch" and f[1] == name and f[2] == kernel:
             try:
-                return float(f[2])
+                return float(f[3])
             except ValueError:
                 return None
     return None
+
+
+def main_kernel_name(hq, gtype, M, N):
+    """Name of the GEMM main kernel hq_gemm dispatches for this shape (as rocprofv3 lists it)."""
+    import synth
+    rows, cols = hq.gemm_tiles(gtype, M, N)
+    if gtype == synth.Q4_K and M > 64:
+        return "k_gemm_q4_k_w<8>" if cols == 256 else f"k_gemm_q4_k_ws<{cols // 32}>"
+    mb = rows // 16
+    return f"k_gemm_q8_0<{mb}, 2>" if gtype == synth.Q8_0 else f"k_gemm_q4_k<{mb}, 2>"
 
 
 def bench_gemm(hq, synth, gtype, N, K, M, c_f32, steps, warmup, stream, eager_warmup=True, kernel_time=False,
@@ -226,9 +238,10 @@ def main():
         sweep.append(r)
 
     kt = head["kernel_tflops"]
+    kname = main_kernel_name(hq, gtype, M, N)
     roofline = dict(bound="mfma", achieved=round(kt, 3), peak=PEAK_TFLOPS, unit="TFLOP/s",
-                    frac=round(kt / PEAK_TFLOPS, 4), traffic=read_traffic("q4_k_gemm_m512_k2560_n9728"),
-                    kernel="k_gemm_q4_k_w<8>", kernel_us=round(head["kernel_us"], 3))
+                    frac=round(kt / PEAK_TFLOPS, 4), traffic=read_traffic("q4_k_gemm_m512_k2560_n9728", kname),
+                    kernel=kname, kernel_us=round(head["kernel_us"], 3))
     cpu = None if args.no_cpu else cpu_baseline(synth, gtype, N, K, M)
     line = {
         "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,

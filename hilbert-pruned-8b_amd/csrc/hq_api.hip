@@ -412,7 +412,7 @@ extern "C" int hq_device_synchronize(void) {
 extern "C" void hq_gemm_tiles(int ggml_type, int M, int N, int *rows_per_tile, int *cols_per_tile) {
     (void)N;
     int r = 1, c = 16;
-    if (M > 1) hq_gemm_tile_shape(ggml_type, M, &r, &c);
+    if (M > 1) hq_gemm_tile_shape(ggml_type, M, N, 256, 256, &r, &c);
     if (rows_per_tile) *rows_per_tile = r;
     if (cols_per_tile) *cols_per_tile = c;
 }

@@ -1,0 +1,140 @@
+// hq_device.h - device helpers shared by the gfx950 kernel sources (hq_kernels.hip, hq_gemm_ws.hip).
+#ifndef HQ_DEVICE_H
+#define HQ_DEVICE_H
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+
+#define DEV static __device__ __forceinline__
+
+DEV float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+DEV h2 as_h2(uint32_t x) { return __builtin_bit_cast(h2, x); }
+
+// Bytes 4-7 of the v_perm_b32 source pair {S0, S1} come from S0 = 0x64646464 (the high byte of
+// fp16 1024.0); bytes 0-3 from S1 = w. Result: [w.byte(i), 0x64, w.byte(j), 0x64].
+DEV uint32_t perm_lo(uint32_t w) { return __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u); }  // bytes 0,1
+DEV uint32_t perm_hi(uint32_t w) { return __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u); }  // bytes 2,3
+
+// Q4_K scales/mins (ggml_quant.h:51-59) as four words of bytes: sw0 = s0..s3, sw1 = s4..s7,
+// mw0 = m0..m3, mw1 = m4..m7, from the 12 scale bytes held in words q0 (bytes 0-3), q1 (4-7), q2 (8-11).
+DEV void q4k_scale_words(uint32_t q0, uint32_t q1, uint32_t q2, uint32_t &sw0, uint32_t &sw1, uint32_t &mw0,
+                         uint32_t &mw1) {
+    sw0 = q0 & 0x3f3f3f3fu;
+    mw0 = q1 & 0x3f3f3f3fu;
+    sw1 = (q2 & 0x0f0f0f0fu) | ((q0 >> 2) & 0x30303030u);
+    mw1 = ((q2 >> 4) & 0x0f0f0f0fu) | ((q1 >> 2) & 0x30303030u);
+}
+
+DEV uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
+
+DEV void store_out(void *C, size_t idx, float v, int c_f32, int accumulate) {
+    if (c_f32) {
+        float *c = (float *)C + idx;
+        *c = accumulate ? *c + v : v;
+    } else {
+        _Float16 *c = (_Float16 *)C + idx;
+        *c = (_Float16)(accumulate ? (float)*c + v : v);
+    }
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+DEV lds_void *lds_ptr(const void *p) { return (lds_void *)(uintptr_t)p; }
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Raw buffer over `bytes` bytes: loads at offsets >= bytes return zero.
+DEV rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, 0x00020000);
+}
+
+DEV u4v buf_load16(rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+DEV f4 mfma(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+
+// fp16 pair (1024 + b0, 1024 + b1) minus 1024: the bytes as exact fp16 integers.
+DEV h2 bytes_f16(uint32_t w, bool hi_pair) {
+    const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    return as_h2(hi_pair ? perm_hi(w) : perm_lo(w)) - k1024;
+}
+
+// Quad permutes of one VGPR by DPP, written as inline assembly: this compiler merges
+// __builtin_amdgcn_mov_dpp / update_dpp calls that share a DPP control but read different
+// registers into one move of the first register (observed on gfx950, ROCm 7.2). The s_nop gives
+// the source's producer 5 wait states (a plain VALU write needs 2 before a DPP read; a
+// v_dot2c_f32_f16 result needs more).
+DEV float dpp_quad_1032(float v) {
+    float r;
+    asm volatile("s_nop 4\n\tv_mov_b32_dpp %0, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf" : "=v"(r) : "v"(v));
+    return r;
+}
+DEV float dpp_quad_2301(float v) {
+    float r;
+    asm volatile("s_nop 4\n\tv_mov_b32_dpp %0, %1 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf" : "=v"(r) : "v"(v));
+    return r;
+}
+
+// 4 x 4 transpose inside each quad of lanes: on entry lane k of a quad holds x[e] = X[e][k], on
+// return x[e] = X[k][e]. Two rounds, each swapping the (register bit, lane bit) off-diagonal pairs:
+// bit 0 through quad_perm [1,0,3,2], bit 1 through quad_perm [2,3,0,1].
+DEV f4 quad_transpose(f4 x) {
+    const int k = threadIdx.x & 3;
+    f4 y, z;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float t = dpp_quad_1032(x[e ^ 1]);
+        y[e] = ((e ^ k) & 1) ? t : x[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float t = dpp_quad_2301(y[e ^ 2]);
+        z[e] = ((e ^ k) & 2) ? t : y[e];
+    }
+    return z;
+}
+
+// Output tile of one wave: block (i, j) holds rows m0 + 16i + 4lg + e, column nw + 16j + ln in
+// register e of lane (ln, lg). A quad transpose gives lane (4c + k, lg) row 4lg + k, columns
+// 4c .. 4c + 3, stored as one 8-byte (fp16) or 16-byte (fp32) access when N % 4 == 0, else
+// element by element (the same values and roundings either way).
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+template <int MB, int NB>
+DEV void store_tile(void *C, const f4 (&acc)[MB][NB], int M, int N, int m0, int nw, int ln, int lg, int c_f32,
+                    int accumulate) {
+    const int k = ln & 3, c4 = ln & ~3;
+    const bool wide = (N & 3) == 0;
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int i = 0; i < MB; i++) {
+            const f4 y = quad_transpose(acc[i][j]);
+            const int m = m0 + 16 * i + 4 * lg + k, n = nw + 16 * j + c4;
+            if (m >= M || n >= N) continue;
+            const size_t idx = (size_t)m * N + n;
+            if (wide) {
+                if (c_f32) {
+                    f4 *c = (f4 *)((float *)C + idx);
+                    *c = accumulate ? *c + y : y;
+                } else {
+                    h4 *c = (h4 *)((_Float16 *)C + idx);
+                    *c = __builtin_convertvector(accumulate ? __builtin_convertvector(*c, f4) + y : y, h4);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (n + e < N) store_out(C, idx + e, y[e], c_f32, accumulate);
+            }
+        }
+}
+
+#endif

@@ -25,36 +25,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "hq_device.h"
 #include "hq_kernels.h"
 
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef float f4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u2v __attribute__((ext_vector_type(2)));
-typedef uint32_t u4v __attribute__((ext_vector_type(4)));
-
-#define DEV static __device__ __forceinline__
-
-DEV float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
-
-DEV h2 as_h2(uint32_t x) { return __builtin_bit_cast(h2, x); }
-
-// Bytes 4-7 of the v_perm_b32 source pair {S0, S1} come from S0 = 0x64646464 (the high byte of
-// fp16 1024.0); bytes 0-3 from S1 = w. Result: [w.byte(i), 0x64, w.byte(j), 0x64].
-DEV uint32_t perm_lo(uint32_t w) { return __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u); }  // bytes 0,1
-DEV uint32_t perm_hi(uint32_t w) { return __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u); }  // bytes 2,3
-
-// Q4_K scales/mins (ggml_quant.h:51-59) as four words of bytes: sw0 = s0..s3, sw1 = s4..s7,
-// mw0 = m0..m3, mw1 = m4..m7, from the 12 scale bytes held in words q0 (bytes 0-3), q1 (4-7), q2 (8-11).
-DEV void q4k_scale_words(uint32_t q0, uint32_t q1, uint32_t q2, uint32_t &sw0, uint32_t &sw1, uint32_t &mw0,
-                         uint32_t &mw1) {
-    sw0 = q0 & 0x3f3f3f3fu;
-    mw0 = q1 & 0x3f3f3f3fu;
-    sw1 = (q2 & 0x0f0f0f0fu) | ((q0 >> 2) & 0x30303030u);
-    mw1 = ((q2 >> 4) & 0x0f0f0f0fu) | ((q1 >> 2) & 0x30303030u);
-}
-
-DEV uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
 
 // ============================================================================ dequantize
 // Output row r is matrix row ids[r] when ids is given (embedding gather), else row0 + r.
@@ -231,15 +204,6 @@ DEV float dot_row_q4_k(const uint8_t *__restrict__ row, const uint16_t *__restri
     return acc;
 }
 
-DEV void store_out(void *C, size_t idx, float v, int c_f32, int accumulate) {
-    if (c_f32) {
-        float *c = (float *)C + idx;
-        *c = accumulate ? *c + v : v;
-    } else {
-        _Float16 *c = (_Float16 *)C + idx;
-        *c = (_Float16)(accumulate ? (float)*c + v : v);
-    }
-}
 
 // ---- row-group GEMV: one wave per R weight rows (64 lanes per row), activations loaded once per
 // slice into registers and reused by the R rows, all R x TS weight loads of a slice in flight together.
@@ -440,20 +404,6 @@ __global__ void __launch_bounds__(256) k_gather_q4_k(const uint8_t *__restrict__
 namespace {
 constexpr int KC = 256;
 
-typedef __attribute__((address_space(3))) void lds_void;
-
-DEV lds_void *lds_ptr(const void *p) { return (lds_void *)(uintptr_t)p; }
-
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-
-// Raw buffer over `bytes` bytes: loads at offsets >= bytes return zero.
-DEV rsrc_t make_rsrc(const void *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, 0x00020000);
-}
-
-DEV u4v buf_load16(rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-}
 
 // Activation tile DMA: instruction qq of wave w moves rows r = 8qq + 2w + (lane >> 5) (two 256-half
 // rows per 64-lane instruction) into LDS slots (r, lane & 31). The per-lane byte offset is
@@ -491,7 +441,6 @@ DEV void dma_a(_Float16 *buf, rsrc_t ra, const ADma &d, int K, int k0) {
 // A fragment: row r (= 16*i + ln), activation chunk c (8 halves).
 DEV h8 a_frag(const _Float16 *buf, int r, int c) { return *(const h8 *)(buf + r * KC + 8 * (c ^ (r & 15))); }
 
-DEV f4 mfma(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
 
 // B fragment from 8 bytes u = q + 128 (two words) -> fp16(q * d): one rounding of the exact product.
 DEV h8 frag_q8_0(uint32_t w0, uint32_t w1, h2 d2) {
@@ -530,11 +479,6 @@ DEV h8 frag_q4_k(uint32_t w0, uint32_t w1, h2 mul, h2 add) {
     return out;
 }
 
-// fp16 pair (1024 + b0, 1024 + b1) minus 1024: the bytes as exact fp16 integers.
-DEV h2 bytes_f16(uint32_t w, bool hi_pair) {
-    const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-    return as_h2(hi_pair ? perm_hi(w) : perm_lo(w)) - k1024;
-}
 
 struct SkPlan {
     int tm, tiles, upt;  // M-tiles, tiles, K-units per tile
@@ -548,74 +492,6 @@ DEV int sk_owner(const SkPlan &p, int u) {
     return u < big ? u / (p.base + 1) : p.extra + (u - big) / p.base;
 }
 
-// Quad permutes of one VGPR by DPP, written as inline assembly: this compiler merges
-// __builtin_amdgcn_mov_dpp / update_dpp calls that share a DPP control but read different
-// registers into one move of the first register (observed on gfx950, ROCm 7.2). The s_nop gives
-// the source's producer 5 wait states (a plain VALU write needs 2 before a DPP read; a
-// v_dot2c_f32_f16 result needs more).
-DEV float dpp_quad_1032(float v) {
-    float r;
-    asm volatile("s_nop 4\n\tv_mov_b32_dpp %0, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf" : "=v"(r) : "v"(v));
-    return r;
-}
-DEV float dpp_quad_2301(float v) {
-    float r;
-    asm volatile("s_nop 4\n\tv_mov_b32_dpp %0, %1 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf" : "=v"(r) : "v"(v));
-    return r;
-}
-
-// 4 x 4 transpose inside each quad of lanes: on entry lane k of a quad holds x[e] = X[e][k], on
-// return x[e] = X[k][e]. Two rounds, each swapping the (register bit, lane bit) off-diagonal pairs:
-// bit 0 through quad_perm [1,0,3,2], bit 1 through quad_perm [2,3,0,1].
-DEV f4 quad_transpose(f4 x) {
-    const int k = threadIdx.x & 3;
-    f4 y, z;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const float t = dpp_quad_1032(x[e ^ 1]);
-        y[e] = ((e ^ k) & 1) ? t : x[e];
-    }
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const float t = dpp_quad_2301(y[e ^ 2]);
-        z[e] = ((e ^ k) & 2) ? t : y[e];
-    }
-    return z;
-}
-
-// Output tile of one wave: block (i, j) holds rows m0 + 16i + 4lg + e, column nw + 16j + ln in
-// register e of lane (ln, lg). A quad transpose gives lane (4c + k, lg) row 4lg + k, columns
-// 4c .. 4c + 3, stored as one 8-byte (fp16) or 16-byte (fp32) access when N % 4 == 0, else
-// element by element (the same values and roundings either way).
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-template <int MB, int NB>
-DEV void store_tile(void *C, const f4 (&acc)[MB][NB], int M, int N, int m0, int nw, int ln, int lg, int c_f32,
-                    int accumulate) {
-    const int k = ln & 3, c4 = ln & ~3;
-    const bool wide = (N & 3) == 0;
-#pragma unroll
-    for (int j = 0; j < NB; j++)
-#pragma unroll
-        for (int i = 0; i < MB; i++) {
-            const f4 y = quad_transpose(acc[i][j]);
-            const int m = m0 + 16 * i + 4 * lg + k, n = nw + 16 * j + c4;
-            if (m >= M || n >= N) continue;
-            const size_t idx = (size_t)m * N + n;
-            if (wide) {
-                if (c_f32) {
-                    f4 *c = (f4 *)((float *)C + idx);
-                    *c = accumulate ? *c + y : y;
-                } else {
-                    h4 *c = (h4 *)((_Float16 *)C + idx);
-                    *c = __builtin_convertvector(accumulate ? __builtin_convertvector(*c, f4) + y : y, h4);
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    if (n + e < N) store_out(C, idx + e, y[e], c_f32, accumulate);
-            }
-        }
-}
 
 // Partial tiles are written and read with device-scope (sc1) buffer accesses: they go to the
 // cross-XCD coherent level, so no L2 write-back or invalidation is needed, and unlike atomics they
@@ -1334,15 +1210,27 @@ namespace {
 struct GemmCfg {
     int mb, nb, waves;
     bool wide;
+    int ws_nb;  // > 0: the full-K tile kernel k_gemm_q4_k_ws with 32 * ws_nb columns per tile
 };
 
-GemmCfg gemm_cfg(const hq_dev_mat *W, int M) {
+// Q4_K with M > 64 runs the full-K tile kernel when its tiles fit in one round on the CUs and fill
+// at least 70 % of them (e.g. M = 512, N = 9728: 244 tiles of 128 x 160 on 256 CUs); otherwise the
+// Stream-K wide kernel (few long tiles, such as N = 2560 at M = 512, or many tiles at large M, where
+// its split-tile overhead is amortised: measured faster at M = 4096 and 16384).
+GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
     GemmCfg c;
     c.mb = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
     c.nb = 2;
     if (W->type == HQ_TYPE_Q4_K && c.mb == 1) c.mb = 2;
     c.wide = W->type == HQ_TYPE_Q4_K && M > 64;
     c.waves = c.wide ? WNW : 4;
+    c.ws_nb = 0;
+    if (c.wide && (size_t)M * W->cols * 2 < ((size_t)1 << 32)) {
+        float eff = 0.f;
+        const int nb = hq_ws_choose(M, (int)W->rows, n_cu, &eff);
+        const long tiles = (long)((M + 127) / 128) * (((int)W->rows + 32 * nb - 1) / (32 * nb));
+        if (eff >= 0.7f && tiles <= n_cu) c.ws_nb = nb;
+    }
     return c;
 }
 
@@ -1351,26 +1239,28 @@ SkPlan gemm_plan(const hq_dev_mat *W, int M, const GemmCfg &c, int n_cu) {
 }
 }  // namespace
 
-void hq_gemm_tile_shape(int type, int M, int *rows, int *cols) {
+void hq_gemm_tile_shape(int type, int M, int N, int K, int n_cu, int *rows, int *cols) {
     hq_dev_mat W = {};
     W.type = type;
-    const GemmCfg c = gemm_cfg(&W, M);
-    *rows = 16 * c.mb;
-    *cols = 16 * c.nb * c.waves;
+    W.rows = (uint32_t)N;
+    W.cols = (uint32_t)K;
+    const GemmCfg c = gemm_cfg(&W, M, n_cu);
+    *rows = c.ws_nb ? 128 : 16 * c.mb;
+    *cols = c.ws_nb ? 32 * c.ws_nb : 16 * c.nb * c.waves;
 }
 
 void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_bytes, size_t *counter_bytes,
                         size_t *sums_bytes) {
-    const GemmCfg c = gemm_cfg(W, M);
+    const GemmCfg c = gemm_cfg(W, M, n_cu);
     const SkPlan p = gemm_plan(W, M, c, n_cu);
-    *partial_bytes = (size_t)2 * p.G * 64 * c.waves * c.mb * c.nb * 4 * sizeof(float);
-    *counter_bytes = (size_t)p.tiles * sizeof(int);
+    *partial_bytes = c.ws_nb ? 0 : (size_t)2 * p.G * 64 * c.waves * c.mb * c.nb * 4 * sizeof(float);
+    *counter_bytes = c.ws_nb ? 0 : (size_t)p.tiles * sizeof(int);
     *sums_bytes = c.wide ? (size_t)M * (W->cols / KC) * 32 : 0;
 }
 
 // Pre-pass of a GEMM (the wide Q4_K kernel's activation sub-block sums; nothing otherwise).
 hipError_t hq_launch_gemm_pre(const hq_dev_mat *W, const uint16_t *A, int M, const HqGemmWork &wk, hipStream_t st) {
-    const GemmCfg c = gemm_cfg(W, M);
+    const GemmCfg c = gemm_cfg(W, M, wk.n_cu);
     if (c.wide) {
         const size_t n16 = (size_t)M * (W->cols / 8);
         k_asums<<<grid_for(n16, 256, 16384), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
@@ -1381,7 +1271,8 @@ hipError_t hq_launch_gemm_pre(const hq_dev_mat *W, const uint16_t *A, int M, con
 // Main kernel of a GEMM (needs hq_launch_gemm_pre's output for the same A).
 hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
                                const HqGemmWork &wk, hipStream_t st) {
-    const GemmCfg c = gemm_cfg(W, M);
+    const GemmCfg c = gemm_cfg(W, M, wk.n_cu);
+    if (c.ws_nb) return hq_launch_gemm_ws(W, A, wk.sums, M, C, c_f32, accumulate, c.ws_nb, st);
     GemmArgs g;
     g.qs = W->qs, g.d = W->d, g.ldd = W->ldd, g.row_bytes = W->row_bytes, g.A = A;
     g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;

@@ -118,7 +118,8 @@ int hq_time_gemm_kernel(hq_mat *const *Ws, int n_w, const uint16_t *A, int M, vo
 int hq_time_gather(hq_mat *const *Ws, int n_w, const uint16_t *H, const uint32_t *ids_dev, int n_sets, int B, int k,
                    float *out, int iters, int reps, void *stream, float *ms);
 
-/* The output tile hq_gemm uses for an M x N problem of the given ggml type (diagnostics). */
+/* The output tile hq_gemm uses for an M x N problem of the given ggml type on a 256-CU MI355X
+ * (diagnostics; the launch itself sizes for the device's CU count). */
 void hq_gemm_tiles(int ggml_type, int M, int N, int *rows_per_tile, int *cols_per_tile);
 
 #ifdef __cplusplus

@@ -73,12 +73,19 @@ def test_gemm_tile_selection():
             r, c = hq.gemm_tiles(gtype, M, 9728)
             assert r in (16, 32, 64, 128)
             assert r >= min(M, 128) or r == 128
-            # Q4_K above M = 64: the 8-wave kernel, 256 columns per tile
-            assert c == (256 if gtype == synth.Q4_K and M > 64 else 128)
-    # Stream-K balances any tile count over the CUs
+            if gtype == synth.Q4_K and M > 64:
+                # Q4_K above M = 64: full-K tiles of 128 x 32NB when they fill the CUs, else the
+                # 8-wave Stream-K kernel (128 x 256)
+                assert (r, c) == (128, 256) or (r == 128 and c in (64, 96, 128, 160))
+            else:
+                assert c == 128
+    # Stream-K balances any tile count over the CUs (Q8_0, narrow Q4_K, few Q4_K tiles)
     assert hq.gemm_tiles(synth.Q8_0, 512, 9728) == (128, 128)
-    assert hq.gemm_tiles(synth.Q4_K, 512, 9728) == (128, 256)
     assert hq.gemm_tiles(synth.Q4_K, 2, 9728) == (32, 128)
+    assert hq.gemm_tiles(synth.Q4_K, 65, 9728) == (128, 256)
+    # full-K tiles: 4 x 61 tiles of 128 x 160 on 256 CUs; more tiles than CUs: Stream-K
+    assert hq.gemm_tiles(synth.Q4_K, 512, 9728) == (128, 160)
+    assert hq.gemm_tiles(synth.Q4_K, 4096, 9728) == (128, 256)
 
 
 def test_synth_is_deterministic():

@@ -113,7 +113,9 @@ RAGGED = [(synth.Q8_0, 100, 512, M) for M in (1, 2, 5, 17, 33, 65, 200)] + \
          [(synth.Q4_K, 100, 512, M) for M in (1, 2, 5, 17, 33, 65, 200)] + \
          [(synth.Q8_0, 40, 512, 5), (synth.Q8_0, 40, 512, 40), (synth.Q4_K, 40, 512, 5), (synth.Q4_K, 40, 512, 40),
           (synth.Q8_0, 1408, 512, 128), (synth.Q8_0, 512, 1408, 128), (synth.Q8_0, 72, 96, 3), (synth.Q8_0, 72, 96, 40),
-          (synth.Q4_K, 130, 2560, 31), (synth.Q4_K, 33, 256, 1), (synth.Q4_K, 33, 256, 20)]
+          (synth.Q4_K, 130, 2560, 31), (synth.Q4_K, 33, 256, 1), (synth.Q4_K, 33, 256, 20)] + \
+         [(synth.Q4_K, 9500, 768, 500), (synth.Q4_K, 9728, 512, 350), (synth.Q4_K, 9728, 256, 350),
+          (synth.Q4_K, 9000, 768, 1000)]  # full-K tiles (the last: Stream-K, more tiles than CUs)
 
 
 @pytest.mark.parametrize("gtype,N,K,M", FULL + RAGGED)
@@ -129,17 +131,17 @@ def test_gemm_parity(hqlib, oracle, gtype, N, K, M):
     W.free()
 
 
-@pytest.mark.parametrize("gtype", [synth.Q8_0, synth.Q4_K])
-@pytest.mark.parametrize("M", [1, 48])
-def test_gemm_accumulate_and_fp16_output(hqlib, oracle, gtype, M):
-    N, K = 320, 1024
+@pytest.mark.parametrize("gtype,M,N,K", [(synth.Q8_0, 1, 320, 1024), (synth.Q8_0, 48, 320, 1024),
+                                         (synth.Q4_K, 1, 320, 1024), (synth.Q4_K, 48, 320, 1024),
+                                         (synth.Q4_K, 350, 9728, 256)])
+def test_gemm_accumulate_and_fp16_output(hqlib, oracle, gtype, M, N, K):
     blocks = weights(gtype, N, K, 7)
     rng = synth.Rng(77 + M)
     a = synth.activations_f16(rng, M, K)
     c0 = rng.normal(M * N).astype(np.float32).reshape(M, N)
     W = hqlib.Mat(blocks, gtype, N, K)
     ref = oracle.matmul(blocks, gtype, N, K, oracle.f16_to_f32(a), c0.copy(), True)
-    say(f"gemm accumulate fp32 type={gtype} M={M}")
+    say(f"gemm accumulate fp32 type={gtype} M={M} N={N} K={K} tiles={hqlib.gemm_tiles(gtype, M, N)}")
     check(hqlib.gemm_np(W, a, c_f32=True, c_init=c0), ref, gtype, "accumulate fp32")
     say(f"gemm fp16 out type={gtype} M={M}")
     got16 = hqlib.gemm_np(W, a, c_f32=False).view(np.float16).astype(np.float32)
