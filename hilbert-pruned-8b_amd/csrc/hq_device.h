@@ -61,6 +61,11 @@ DEV u4v buf_load16(rsrc_t r, uint32_t voff, uint32_t soff) {
 }
 
 DEV f4 mfma(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+// bf16 MFMA on operands held as 16-bit patterns (loaded through the same h8 path as fp16 ones)
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+DEV f4 mfma_bf16(h8 a, h8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8, a), __builtin_bit_cast(bf8, b), c, 0, 0, 0);
+}
 
 // fp16 pair (1024 + b0, 1024 + b1) minus 1024: the bytes as exact fp16 integers.
 DEV h2 bytes_f16(uint32_t w, bool hi_pair) {

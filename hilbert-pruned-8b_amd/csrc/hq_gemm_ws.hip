@@ -19,21 +19,24 @@
 // K is walked in stages of 128 (half a super-block); LDS holds two stages (double buffering) and one
 // s_barrier per stage hands a stage from producers to consumers.
 //
-// Exactness (no weight is ever rounded to 16 bits). The B operand is the integer s*q (<= 945, exact
-// in fp16). A super-block's products accumulate in fp32 (part), which is folded into the output
-// accumulator as acc += d * part once per super-block. The min term -dmin * sum_sub m_sub * S_sub
-// (S_sub = fp32 sum of the sub-block's 32 activations, from k_asums as fp16 hi + lo) is one MFMA per
-// (row block, column block, super-block) accumulating into acc: A slots hold S_hi, S_lo, S_hi, S_lo
-// of the 8 sub-blocks, B slots Bh, Bh, Bl, Bl with Bh = fp16(-dmin*m), Bl = fp16(-dmin*m - Bh)
-// (exact: -dmin*m has at most 17 significant bits), so the four products sum to S * (-dmin*m) to
-// about 2^-22 relative.
+// Arithmetic (no weight is ever rounded to 16 bits). Column n's accumulators hold its dot products
+// in units of c_u = d_u (the super-block scale; 1 where d_u = 0) during super-block u: the main B
+// operand is then the integer s*q (<= 945, exact in fp16; 0 where d_u = 0), where a super-block
+// begins the accumulators are multiplied by c_{u-1} / c_u (fp32), and at the end by c_{U-1}. The min
+// term -dmin * sum_sub m_sub * S_sub (S_sub = fp32 sum of the sub-block's 32 activations, from
+// k_asums as bf16 hi + lo) is one bf16 MFMA per (row block, column block, super-block): A slots hold
+// S_hi, S_lo, S_hi, S_lo of the 8 sub-blocks, B slots Bh, Bh, Bl, Bl with x = -dmin * m / c_u
+// (fp32), Bh = bf16(x), Bl = bf16(x - Bh); the four products sum to S * x to about 2^-16 relative
+// (bf16 keeps fp32's exponent range, so no S or x overflows).
 //
 // LDS layouts (16-byte slots; a stage row is 128 k = 16 slots):
 //   A tile [128 rows][16 slots], slot p of row r at p ^ (r & 15);
 //   B tile [BN columns][16 slots], slot p of column c at p ^ (c & 15);
 //   (the XOR swizzle makes the 16 lanes of an MFMA operand read hit 16 distinct slots: such reads run
 //   at the full 256 bytes per clock)
-//   S [128 rows][16 halves] = hi[8], lo[8]; Bmin [BN][16 halves] = Bh[8], Bl[8]; D [BN] fp16 d.
+//   S [128 rows][16 bf16] = hi[8], lo[8]; Bmin [BN][16 bf16] = Bh[8], Bl[8]; R [BN] fp32
+//   c_{u-1} / c_u; CL [BN] fp32 c_u of the latest super-block staged; scale words [2][BN][2] (two
+//   super-blocks: 6-bit scales of sub-blocks 0-3 and 4-7, zero where d = 0).
 #include <type_traits>
 
 #include "hq_device.h"
@@ -66,6 +69,19 @@ DEV u2v buf_load8(rsrc_t r, uint32_t voff, uint32_t soff) {
 
 DEV void dma16(rsrc_t r, void *lds, uint32_t voff, uint32_t soff) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_ptr(lds), 16, voff, soff, 0, 0);
+}
+
+// L2 prefetch: a 4-byte-per-lane LDS DMA of the bytes at voff into a scratch LDS slot that is never
+// read (256 bytes at lds_addr). Written as assembly: the compiler waits for every LDS DMA it knows
+// of before any later LDS access, which would put the fetch's latency in front of the next LDS
+// read. The issuing wave waits for it (s_waitcnt vmcnt) before it ends. M0 is restored.
+DEV void l2_touch(rsrc_t r, uint32_t voff, uint32_t lds_addr) {
+    uint32_t save;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 1\n\tbuffer_load_dword %2, %3, 0 offen lds\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(save)
+                 : "s"(lds_addr), "v"(voff), "s"(r)
+                 : "memory");
 }
 
 // Eight fp16 B values s*q for 8 consecutive k from the low (HI = false) or high nibbles of 8 bytes:
@@ -117,7 +133,7 @@ DEV void store_rows4(void *C, const f4 (&acc)[MB][NB], int M, int N, int r0, int
     }
 }
 
-// LDS arena (bytes): A stages, B stages, S, Bmin, D.
+// LDS arena (bytes): A stages, B stages, S, Bmin, R, CL, scale words, prefetch scratch.
 template <int NB>
 struct WsLds {
     static constexpr int BN = 32 * NB;
@@ -125,21 +141,35 @@ struct WsLds {
     static constexpr int B = 2 * A_BYTES, B_BYTES = BN * WS_KS * 2;
     static constexpr int S = B + 2 * B_BYTES;
     static constexpr int BM = S + WS_BM * 32;
-    static constexpr int D = BM + BN * 32;
-    static constexpr int TOTAL = D + BN * 2;
+    static constexpr int R = BM + BN * 32;
+    static constexpr int CL = R + BN * 4;
+    static constexpr int H = CL + BN * 4;
+    static constexpr int PF = H + 2 * BN * 8;  // prefetch scratch, 4 x 256 bytes (never read)
+    static constexpr int TOTAL = PF + 1024;
     static_assert(TOTAL <= 160 * 1024, "LDS budget");
+};
+
+// One consumer k-step (compile-time): A register set P (main k-steps); operand source SRC (0 / 1 =
+// stage buffer, 2 = min-term tiles) at k-step F of the stage; BAR = last k-step of a stage (holds
+// the stage barrier); NSRC / NF = the next k-step's source and k-step.
+template <int P_, int SRC_, int F_, bool BAR_, int NSRC_, int NF_>
+struct WsStep {
+    static constexpr int P = P_, SRC = SRC_, F = F_, NSRC = NSRC_, NF = NF_;
+    static constexpr bool BAR = BAR_;
 };
 
 template <int NB>
 __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
     constexpr int BN = 32 * NB;
     using L = WsLds<NB>;
-    __shared__ __attribute__((aligned(16))) char lds[L::TOTAL];
+    __shared__ __attribute__((aligned(256))) char lds[L::TOTAL];  // fragment addresses XOR bits 6-7
     _Float16 *const sA0 = (_Float16 *)(lds + L::A);
     _Float16 *const sB0 = (_Float16 *)(lds + L::B);
     uint16_t *const sS = (uint16_t *)(lds + L::S);
     uint16_t *const sBm = (uint16_t *)(lds + L::BM);
-    uint16_t *const sD = (uint16_t *)(lds + L::D);
+    uint32_t *const sH = (uint32_t *)(lds + L::H);
+    float *const sR = (float *)(lds + L::R);
+    float *const sCL = (float *)(lds + L::CL);
     auto sA = [&](int h) { return sA0 + h * (L::A_BYTES / 2); };
     auto sB = [&](int h) { return sB0 + h * (L::B_BYTES / 2); };
 
@@ -156,216 +186,325 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
 
     if (wave >= 4) {
         // ------------------------------------------------------------------ producers
-        const int pt = tid - 256, pw = wave - 4, xi = pt & 7;
+        // Stage s's work, done in stage s - 1: its activation tile (LDS DMA), its decoded B tile, and
+        // in an odd stage the next super-block's S tile and min-term operands. Vector-memory
+        // instructions are spread over the decode of the thread's columns (the texture path takes
+        // ~20 clocks per instruction per CU, so a burst of them would stall the wave for the whole
+        // burst); the end-of-stage wait covers the DMAs only (loads issued after them retire later).
+        const int pw = __builtin_amdgcn_readfirstlane(wave - 4);  // wave-uniform LDS targets
+        const int pt = tid - 256, xi = pt & 7;
         const rsrc_t rs = make_rsrc(g.S, (uint32_t)((size_t)M * U * 32));
         // activation DMA: instruction qq of wave pw fills rows 4(pw + 4qq) .. +4 (1 KB); lane l takes
         // row 4(pw + 4qq) + l/16, LDS slot l % 16, global chunk (l % 16) ^ (row & 15)
         const int arow = 4 * pw + (lane >> 4);
         const uint32_t a_voff = (uint32_t)(((m0 + arow) * K + 8 * ((lane & 15) ^ (arow & 15))) * 2);
-        auto dma_a = [&](int s) {
-            _Float16 *dst = sA(s & 1);
-#pragma unroll
-            for (int qq = 0; qq < 8; qq++)
-                dma16(ra, dst + (pw + 4 * qq) * 512, a_voff, (uint32_t)(qq * 16 * K * 2 + s * WS_KS * 2));
+        auto dma_a = [&](int s, int qq) {
+            dma16(ra, sA(s & 1) + (pw + 4 * qq) * 512, a_voff, (uint32_t)(qq * 16 * K * 2 + s * WS_KS * 2));
         };
         // S tile of unit u: 32 rows (1 KB) per wave; lane l: row 32pw + l/2, half l % 2
         const uint32_t s_voff = (uint32_t)(((m0 + 32 * pw + (lane >> 1)) * U) * 32 + 16 * (lane & 1));
         auto dma_s = [&](int u) { dma16(rs, sS + pw * 512, s_voff, (uint32_t)(u * 32)); };
-        // weight bytes: this thread's columns c_i = pt/8 + 32i (i < NB), half-chunk xi of each stage
+        // quant bytes: this thread's columns c_i = pt/8 + 32i (i < NB), half-chunk xi of each stage
+        // (bytes 16 + 8(8(s % 2) + xi) of super-block s/2). Four register sets: stage s's go to
+        // Q[s % 4], three stages before its decode.
         uint32_t w_voff[NB];
 #pragma unroll
-        for (int i = 0; i < NB; i++) w_voff[i] = (uint32_t)(n0 + (pt >> 3) + 32 * i) * g.row_bytes;
-        // Register sets with compile-time roles (no dynamic indexing): Hc = header of the current unit,
-        // Hn = header of the next; Q0 / Q1 = quant half-chunks of the unit's even / odd stage.
-        u4v Hc[NB], Hn[NB];
-        u2v Q0[NB], Q1[NB];
-        // header of column pt (pt < BN) for the min-term operands: current / next unit
-        const uint32_t m_voff = (uint32_t)(n0 + (pt < BN ? pt : 0)) * g.row_bytes;
-        u4v Mc, Mn;
-        auto load_h = [&](u4v (&h)[NB], int u) {
-#pragma unroll
-            for (int i = 0; i < NB; i++) h[i] = buf_load16(rw, w_voff[i], (uint32_t)(u * 144));
+        for (int i = 0; i < NB; i++) w_voff[i] = (uint32_t)(n0 + (pt >> 3) + 32 * i) * g.row_bytes + 16u + 8u * (uint32_t)xi;
+        u2v Q[4][NB];
+        auto load_q = [&](u2v (&q)[NB], int s, int i) {
+            q[i] = buf_load8(rw, w_voff[i], (uint32_t)((s >> 1) * 144 + 64 * (s & 1)));
         };
-        // half-chunk xi of stage s: bytes 16 + 8(8(s % 2) + xi) of super-block s/2 (the lane part in
-        // the vector offset, the stage part in the uniform one)
-        const uint32_t q_voff = 16u + 8u * (uint32_t)xi;
-        auto load_q = [&](u2v (&q)[NB], int s) {
-            const uint32_t so = (uint32_t)((s >> 1) * 144 + 64 * (s & 1));
-#pragma unroll
-            for (int i = 0; i < NB; i++) q[i] = buf_load8(rw, w_voff[i] + q_voff, so);
+        // super-block headers, one column per thread (pt < BN; the other threads load column 0's
+        // and drop it, so that every wave issues the same loads): H[u % 2] holds unit u's
+        const bool colt = pt < BN;
+        const uint32_t m_voff = (uint32_t)(n0 + (colt ? pt : 0)) * g.row_bytes;
+        u4v H[2];
+        auto load_hdr = [&](u4v &h, int u) { h = buf_load16(rw, m_voff, (uint32_t)(u * 144)); };
+        // a unit's scale words for the decode (sub-blocks 0-3 / 4-7; zero where d = 0, so that B = 0
+        // there) -> sH[u % 2][pt]
+        auto write_scales = [&](const u4v hm, int buf) {
+            if (!colt) return;
+            uint32_t sw0, sw1, mw0, mw1;
+            q4k_scale_words(hm.y, hm.z, hm.w, sw0, sw1, mw0, mw1);
+            const uint32_t nz = (hm.x & 0x7fffu) ? 0xffffffffu : 0u;
+            *(u2v *)(sH + (buf * BN + pt) * 2) = u2v{sw0 & nz, sw1 & nz};
         };
-        // decode a stage into sB(h) (h = stage parity): half-chunk X = 8h + xi covers sub-blocks 2p
-        // (low nibbles) and 2p + 1 (high) with p = 2h + xi/4; its 8 + 8 values sit at stage slots
-        // 8(xi/4) + (xi % 4) and that + 4
+        // min-term operands, rescale ratio and unit of a super-block (header hm of column pt;
+        // c_prev = the column's previous unit, 1 before the first)
+        float c_prev = 1.0f;
+        auto write_min = [&](const u4v hm) {
+            if (!colt) return;
+            uint32_t sw0, sw1, mw0, mw1;
+            q4k_scale_words(hm.y, hm.z, hm.w, sw0, sw1, mw0, mw1);
+            const float d = h2f((uint16_t)hm.x), dmin = h2f((uint16_t)(hm.x >> 16));
+            const float c = d != 0.0f ? d : 1.0f, inv = 1.0f / c;
+            u4v bh, bl;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint32_t w = q < 2 ? mw0 : mw1;
+                const float x0 = (-dmin * (float)byte_of(w, 2 * (q & 1))) * inv;  // -dmin * m is exact
+                const float x1 = (-dmin * (float)byte_of(w, 2 * (q & 1) + 1)) * inv;
+                const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
+                const __bf16 l0 = (__bf16)(x0 - (float)h0), l1 = (__bf16)(x1 - (float)h1);
+                bh[q] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+                bl[q] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+            }
+            *(u4v *)(sBm + pt * 16) = bh;
+            *(u4v *)(sBm + pt * 16 + 8) = bl;
+            sR[pt] = c_prev * inv;
+            sCL[pt] = c;
+            c_prev = c;
+        };
+        // The vector-memory items of a stage: 8 activation DMAs, the S DMA, a header load (into hd),
+        // NB quant loads (into qd; s_* / u_* < 0: item absent); item k is issued before column
+        // k * NB / (10 + NB) of the decode. Whatever is issued after the DMAs may still be in flight
+        // at the end of the stage: a load has until the end of the next stage.
+        auto issue = [&](int i, int s_dma, int u_s, int u_h, u4v &hd, int s_q, u2v (&qd)[NB]) {
+#pragma unroll
+            for (int k = 0; k < 10 + NB; k++) {
+                if (k * NB / (10 + NB) != i) continue;
+                if (k < 8) {
+                    if (s_dma >= 0) dma_a(s_dma, k);
+                } else if (k == 8) {
+                    if (u_s >= 0) dma_s(u_s);
+                } else if (k == 9) {
+                    if (u_h >= 0) load_hdr(hd, u_h);
+                } else if (s_q >= 0) {
+                    load_q(qd, s_q, k - 10);
+                }
+            }
+        };
+        // decode stage s (H = s % 2) into sB(H): column c_i's half-chunk X = 8H + xi covers
+        // sub-blocks 2p (low nibbles) and 2p + 1 (high) with p = 2H + xi/4; its 8 + 8 values sit at
+        // stage slots 8(xi/4) + (xi % 4) and that + 4. The scale words of a unit are read from sH
+        // once, at the start of its even stage's decode (both words: Sw1 keeps the odd stage's).
         const int slot_lo = 8 * (xi >> 2) + (xi & 3);
         const uint32_t ssel = (xi >> 2) ? 0x04030402u : 0x04010400u;  // scale bytes 2(p%2), 2(p%2)+1
-        auto decode = [&](const u4v (&hd_)[NB], const u2v (&q)[NB], int h) {
-            _Float16 *dst = sB(h);
+        uint32_t Sw1[NB];
+        auto decode = [&](auto hc, auto sbc, const u2v (&q)[NB], int s_dma, int u_s, int u_h, u4v &hd, int s_q,
+                          u2v (&qd)[NB]) {
+            constexpr int HS = decltype(hc)::value, SB = decltype(sbc)::value;
+            _Float16 *dst = sB(HS);
             const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
             const h2 kmul = {(_Float16)1.0f, (_Float16)0.0625f}, kadd = {(_Float16)-1024.0f, (_Float16)-64.0f};
+            uint32_t Sw0[NB];
+            if constexpr (HS == 0) {
+#pragma unroll
+                for (int i = 0; i < NB; i++) {
+                    const u2v w = *(const u2v *)(sH + (SB * BN + (pt >> 3) + 32 * i) * 2);
+                    Sw0[i] = w.x;
+                    Sw1[i] = w.y;
+                }
+            }
 #pragma unroll
             for (int i = 0; i < NB; i++) {
-                const u4v hd = hd_[i];
-                uint32_t sw0, sw1, mw0, mw1;
-                q4k_scale_words(hd.y, hd.z, hd.w, sw0, sw1, mw0, mw1);
-                // sub-block pair p = 2h + xi/4: scales in sw0 (p < 2) or sw1
-                const h2 sp = as_h2(__builtin_amdgcn_perm(0x64646464u, h ? sw1 : sw0, ssel)) - k1024;
+                issue(i, s_dma, u_s, u_h, hd, s_q, qd);
+                const uint32_t c = (uint32_t)((pt >> 3) + 32 * i), sg = c & 15u;
+                const uint32_t sw = HS ? Sw1[i] : Sw0[i];
+                const h2 sp = as_h2(__builtin_amdgcn_perm(0x64646464u, sw, ssel)) - k1024;
                 const h2 mu = sp * kmul, ad = sp * kadd;
                 const h8 lo = decode8<false>(q[i], h2{mu.x, mu.x}, h2{ad.x, ad.x});
                 const h8 hi = decode8<true>(q[i], h2{mu.y, mu.y}, h2{ad.y, ad.y});
-                const uint32_t c = (uint32_t)((pt >> 3) + 32 * i), sg = c & 15u;
                 *(h8 *)(dst + c * WS_KS + 8 * ((uint32_t)slot_lo ^ sg)) = lo;
                 *(h8 *)(dst + c * WS_KS + 8 * ((uint32_t)(slot_lo + 4) ^ sg)) = hi;
             }
         };
-        // min-term operands and d of a unit, one thread per column (pt < BN, header hm of column pt):
-        // Bh = fp16(-dmin * m), Bl = fp16(-dmin * m - Bh) for the 8 sub-blocks, in fp16 pairs
-        auto write_min = [&](const u4v hm) {
-            if (pt >= BN) return;
-            uint32_t sw0, sw1, mw0, mw1;
-            q4k_scale_words(hm.y, hm.z, hm.w, sw0, sw1, mw0, mw1);
-            const _Float16 ndm = -__builtin_bit_cast(_Float16, (uint16_t)(hm.x >> 16));
-            const h2 nd2 = {ndm, ndm};
-            const h2 mv[4] = {bytes_f16(mw0, false), bytes_f16(mw0, true), bytes_f16(mw1, false), bytes_f16(mw1, true)};
-            h8 bh, bl;
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const h2 h = mv[q] * nd2;                                  // one rounding of the exact product
-                const h2 l = __builtin_elementwise_fma(mv[q], nd2, -h);    // the remainder
-                bh[2 * q] = h.x, bh[2 * q + 1] = h.y;
-                bl[2 * q] = l.x, bl[2 * q + 1] = l.y;
-            }
-            *(h8 *)(sBm + pt * 16) = bh;
-            *(h8 *)(sBm + pt * 16 + 8) = bl;
-            sD[pt] = (uint16_t)hm.x;
-        };
-        // A stage ends when this wave's LDS writes are done and the loads the next stage reads from
-        // LDS (the activation tile, the S tile) have landed. Vector-memory loads retire in issue
-        // order, so those are issued first in every stage and the weight loads for later stages
-        // after them; the end-of-stage wait leaves the latter in flight (vmcnt(n) = n newest loads
-        // may be outstanding). A weight load issued in stage s is read by the decode in stage s + 1
-        // and is waited for by the end of stage s + 1 at the latest: about two stages of latency.
-        auto end_stage = [&](auto n_in_flight) {
-            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(decltype(n_in_flight)::value) : "memory");
+        // end of a stage: this wave's LDS writes done, and every load issued before the last
+        // n_in_flight ones (the DMAs among them) landed; then the barrier
+        auto end_stage = [&](int n_in_flight) {
+            if (n_in_flight == 2 * NB + 1) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(2 * NB + 1) : "memory");
+            else if (n_in_flight == NB + 1) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(NB + 1) : "memory");
+            else if (n_in_flight == NB) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(NB) : "memory");
+            else if (n_in_flight == 1) asm volatile("s_waitcnt vmcnt(1) lgkmcnt(0)" ::: "memory");
+            else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
             wg_barrier();
         };
-        using keep0 = std::integral_constant<int, 0>;
-        using keepq = std::integral_constant<int, NB>;
-        using keephq = std::integral_constant<int, 2 * NB + 1>;
-        // prologue: stage 0 decoded and its activation tile in LDS before the first barrier
-        load_h(Hc, 0);
-        load_q(Q0, 0);
-        Mc = buf_load16(rw, m_voff, 0);
-        dma_a(0);
-        load_q(Q1, 1);
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NB + 8) : "memory");  // Hc, Q0, Mc
-        decode(Hc, Q0, 0);
-        end_stage(keepq{});  // Q1 may still be in flight
-        for (int u = 0; u < U; u++) {
-            const bool last = u + 1 == U;
-            // stage 2u: activation tile 2u + 1, then the next headers and quants 2u + 2; decode
-            // stage 2u + 1
-            dma_a(2 * u + 1);
-            if (!last) {
-                load_h(Hn, u + 1);
-                Mn = buf_load16(rw, m_voff, (uint32_t)((u + 1) * 144));
-                load_q(Q0, 2 * u + 2);
-            }
-            decode(Hc, Q1, 1);
-            if (!last) end_stage(keephq{});
-            else end_stage(keep0{});
-            // stage 2u + 1: activation tile 2u + 2 and the S tile of unit u, then quants 2u + 3;
-            // decode stage 2u + 2 (next unit), min-term operands of unit u
-            if (!last) dma_a(2 * u + 2);
-            dma_s(u);
-            if (!last) load_q(Q1, 2 * u + 3);
-            if (!last) decode(Hn, Q0, 0);
-            write_min(Mc);
-            if (!last) end_stage(keepq{});
-            else end_stage(keep0{});
+        using i0 = std::integral_constant<int, 0>;
+        using i1 = std::integral_constant<int, 1>;
+        const int S2 = 2 * U;  // stages
+        // prologue, phase 1: headers of units 0 and 1 and stage 0's quants; unit 0's scale words and
+        // min-term operands (written before any LDS DMA is in flight: the compiler waits for all
+        // outstanding DMAs before an LDS access); stage 0's activation tile, unit 0's S tile, the
+        // quants of stages 1 and 2, the header of unit 2
+        load_hdr(H[0], 0);
+        load_hdr(H[1], U > 1 ? 1 : 0);
 #pragma unroll
-            for (int i = 0; i < NB; i++) Hc[i] = Hn[i];
-            Mc = Mn;
+        for (int i = 0; i < NB; i++) load_q(Q[0], 0, i);
+        write_scales(H[0], 0);
+        write_min(H[0]);
+#pragma unroll
+        for (int k = 0; k < 8; k++) dma_a(0, k);
+        dma_s(0);
+#pragma unroll
+        for (int i = 0; i < NB; i++) load_q(Q[1], 1, i);
+#pragma unroll
+        for (int i = 0; i < NB; i++) load_q(Q[2], S2 > 2 ? 2 : 0, i);
+        load_hdr(H[0], U > 2 ? 2 : 0);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        wg_barrier();  // unit 0's scale words are visible
+        // phase 2: decode stage 0; the stage-0 barrier
+        decode(i0{}, i0{}, Q[0], -1, -1, -1, H[1], -1, Q[3]);
+        end_stage(2 * NB + 1);  // DMAs of phase 1 landed (Q[1], Q[2], H[0] may be in flight)
+        // Super-block u, in stages 2u (P = u % 2 picks the register sets) and 2u + 1.
+        auto unit = [&](auto par, int u) {
+            constexpr int P = decltype(par)::value;
+            const int t = 2 * u;
+            const bool q3 = t + 3 < S2, q4 = t + 4 < S2, nx = u + 1 < U, h3 = u + 3 < U;
+            // stage 2u: decode stage 2u + 1 (this unit, odd half); activation tile 2u + 1; quants
+            // of stage 2u + 3; the next unit's scale words
+            decode(i1{}, std::integral_constant<int, P>{}, Q[(2 * P + 1) & 3], t + 1, -1, -1, H[P], q3 ? t + 3 : -1,
+                   Q[(2 * P + 3) & 3]);
+            if (nx) write_scales(H[P ^ 1], P ^ 1);
+            end_stage(q3 ? NB : 0);
+            if (!nx) return;  // the last stage has nothing to stage
+            // stage 2u + 1: the next unit's min-term operands (its header's last use: the register then
+            // takes the header of unit u + 3); decode stage 2u + 2 (next unit, even half); activation
+            // tile 2u + 2, the next unit's S tile, header u + 3, quants of stage 2u + 4
+            write_min(H[P ^ 1]);
+            decode(i0{}, std::integral_constant<int, P ^ 1>{}, Q[(2 * P + 2) & 3], t + 2, u + 1, h3 ? u + 3 : -1,
+                   H[P ^ 1], q4 ? t + 4 : -1, Q[(2 * P) & 3]);
+            end_stage((q4 ? NB : 0) + (h3 ? 1 : 0));
+        };
+        int u = 0;
+        for (; u + 1 < U; u += 2) {
+            unit(i0{}, u);
+            unit(i1{}, u + 1);
         }
+        if (u < U) unit(i0{}, u);
+        wg_barrier();  // the last stage's barrier
         return;
     }
 
     // ---------------------------------------------------------------------- consumers
+    // A consumer wave's work is a stream of k-steps of 4 x NB MFMAs into acc: per super-block one min
+    // k-step (S x Bmin, bf16; its MFMA groups first rescale the blocks they update by c_{u-1} / c_u)
+    // and 8 main k-steps (32 k of a stage buffer). Every k-step reads the operands of the next one
+    // while its own MFMAs run: the next A fragments first (into the other A register set; after the
+    // second group in a min k-step), the next B fragment j right after the MFMAs that used B fragment
+    // j. The last k-step of a stage passes the stage barrier after its first MFMA groups (its own
+    // operands are in registers by then) and reads the next stage's operands after it. Scheduling
+    // barriers keep that order: left alone, the compiler sinks every LDS read next to its first
+    // use, and the MFMAs wait for LDS latency at every group.
     const int wm = wave & 1, wn = wave >> 1, ln = lane & 15, lg = lane >> 4;
-    // byte offsets inside a stage buffer: A row 64wm + 16i + ln, B column (BN/2)wn + 16j + ln
-    const uint32_t a_row = (uint32_t)((64 * wm + ln) * WS_KS * 2);
-    const uint32_t b_col = (uint32_t)(((BN / 2) * wn + ln) * WS_KS * 2);
-    auto a_frag = [&](int buf, int i, int f) {
-        const char *base = (const char *)sA(buf) + a_row + i * 16 * WS_KS * 2;
-        return *(const h8 *)(base + 16 * ((uint32_t)(4 * f + lg) ^ (uint32_t)ln));
+    // slot (4f + lg) ^ ln of row ln: bits 4-5 of the byte offset from (lg ^ ln) & 3, bits 6-7 from
+    // f ^ (ln >> 2), so the k-step-f address is the k-step-0 address with 64 f XORed in (rows are
+    // 256-byte aligned)
+    const uint32_t sw0 = 16u * ((uint32_t)lg ^ (uint32_t)ln);
+    const uint32_t a_lane = (uint32_t)(uintptr_t)sA(0) + (uint32_t)((64 * wm + ln) * WS_KS * 2) + sw0;
+    const uint32_t b_lane = (uint32_t)(uintptr_t)sB(0) + (uint32_t)(((BN / 2) * wn + ln) * WS_KS * 2) + sw0;
+    using lds_h8 = const __attribute__((address_space(3))) h8;
+    using lds_f4 = const __attribute__((address_space(3))) f4;
+    auto lds_at = [](uint32_t byte) { return *(lds_h8 *)(uintptr_t)byte; };
+    const uint32_t s_base = (uint32_t)(uintptr_t)(sS + (64 * wm + ln) * 16 + 8 * (lg & 1));
+    const uint32_t m_base = (uint32_t)(uintptr_t)(sBm + ((BN / 2) * wn + ln) * 16 + 8 * (lg >> 1));
+    // per-column fp32 factors of lane (ln, lg) in block j: columns 16j + 4lg .. + 3
+    const uint32_t r_base = (uint32_t)(uintptr_t)(sR + (BN / 2) * wn + 4 * lg);
+    const uint32_t cl_base = (uint32_t)(uintptr_t)(sCL + (BN / 2) * wn + 4 * lg);
+    // operand sources: 0 / 1 = stage buffer, 2 = min-term tiles; A fragment i rows 16i.., B fragment
+    // j columns 16j.. of the wave's block
+    auto ldA = [&](int src, int i, int f) -> h8 {
+        return src == 2 ? lds_at(s_base + i * 16 * 32)
+                        : lds_at((a_lane ^ (64u * f)) + src * L::A_BYTES + i * 16 * WS_KS * 2);
     };
-    auto b_frag = [&](int buf, int j, int f) {
-        const char *base = (const char *)sB(buf) + b_col + j * 16 * WS_KS * 2;
-        return *(const h8 *)(base + 16 * ((uint32_t)(4 * f + lg) ^ (uint32_t)ln));
+    auto ldB = [&](int src, int j, int f) -> h8 {
+        return src == 2 ? lds_at(m_base + j * 16 * 32)
+                        : lds_at((b_lane ^ (64u * f)) + src * L::B_BYTES + j * 16 * WS_KS * 2);
     };
-    f4 acc[4][NB], part[4][NB];
+    auto ldR = [&](int j) { return *(lds_f4 *)(uintptr_t)(r_base + j * 16 * 4); };
+    f4 acc[4][NB];
+    h8 fa[2][4], am[4], fb[NB];  // A fragments: main k-steps alternate fa[0] / fa[1]; min k-step am
+    f4 rr[2];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < NB; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
-    // Fold of the super-block just completed: acc += d * part, then its min-term MFMA. With the
-    // weight fragment as the MFMA's first operand, lane (ln, lg) of block (i, j) holds row 16i + ln,
-    // columns 16j + 4lg .. + 3 of the wave's tile, so it needs the 4 d values of those columns.
-    auto fold = [&]() {
-        h8 am[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) am[i] = *(const h8 *)(sS + (64 * wm + 16 * i + ln) * 16 + 8 * (lg & 1));
-#pragma unroll
-        for (int j = 0; j < NB; j++) {
-            const int c = (BN / 2) * wn + 16 * j;
-            const h8 bm = *(const h8 *)(sBm + (c + ln) * 16 + 8 * (lg >> 1));
-            const h4 d4 = *(const h4 *)(sD + c + 4 * lg);
-            const f4 dv = __builtin_convertvector(d4, f4);
+    constexpr int JB = NB >= 3 ? 2 : 1;  // MFMA groups of a stage's last k-step before its barrier
+    auto kstep = [&](auto cfg) {
+        using C = decltype(cfg);
+        constexpr int P = C::P;
+        auto read_next_a = [&]() {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                acc[i][j] += part[i][j] * dv;
-                acc[i][j] = mfma(bm, am[i], acc[i][j]);
+                if constexpr (C::NSRC == 2) am[i] = ldA(2, i, 0);
+                else fa[P ^ 1][i] = ldA(C::NSRC, i, C::NF);
             }
+            if constexpr (C::NSRC == 2) rr[0] = ldR(0);
+        };
+        // the next k-step's A fragments: at the start, or (min k-step) after group JA
+        constexpr int JA = C::SRC == 2 ? JB : 0;
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            if (!C::BAR && j == JA) read_next_a();
+            if (C::BAR && j == JB) {
+                // every read of this stage's buffers has been issued: wait for them, hand the
+                // buffers back, then read the next stage's first operands
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                wg_barrier();
+                read_next_a();
+#pragma unroll
+                for (int jj = 0; jj < JB; jj++) fb[jj] = ldB(C::NSRC, jj, C::NF);
+            }
+            if constexpr (C::SRC == 2) {
+                if (j + 1 < NB) rr[(j + 1) & 1] = ldR(j + 1);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[i][j] *= rr[j & 1];
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[i][j] = mfma_bf16(fb[j], am[i], acc[i][j]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[i][j] = mfma(fb[j], fa[P][i], acc[i][j]);
+            }
+            if (!(C::BAR && j < JB)) fb[j] = ldB(C::NSRC, j, C::NF);
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
-    // One stage: 4 k-steps of 32. A fragments of k-step f + 1 are read (into the other register set)
-    // before the MFMAs of k-step f; a B fragment is re-read for k-step f + 1 right after its 4 MFMAs
-    // of k-step f are issued. The scheduling barriers keep this order (the compiler would otherwise
-    // sink each read next to its first use and stall on it). An even stage (the first of a
-    // super-block) starts with the previous super-block's fold.
-    auto stage = [&](int buf, bool first, bool do_fold) {
-        if (do_fold) fold();
-        h8 fa[2][4], fb[NB];
+    wg_barrier();  // the producers' prologue, phase 1
+    wg_barrier();  // stage 0 and unit 0's min-term tiles are in LDS
 #pragma unroll
-        for (int i = 0; i < 4; i++) fa[0][i] = a_frag(buf, i, 0);
+    for (int i = 0; i < 4; i++) am[i] = ldA(2, i, 0);
 #pragma unroll
-        for (int j = 0; j < NB; j++) fb[j] = b_frag(buf, j, 0);
-#pragma unroll
-        for (int f = 0; f < 4; f++) {
-            const int cur = f & 1;
-
-            if (f < 3) {
-#pragma unroll
-                for (int i = 0; i < 4; i++) fa[cur ^ 1][i] = a_frag(buf, i, f + 1);
-            }
-    #pragma unroll
-            for (int j = 0; j < NB; j++) {
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    part[i][j] = mfma(fb[j], fa[cur][i], (f == 0 && first) ? f4{0.f, 0.f, 0.f, 0.f} : part[i][j]);
-                if (f < 3) fb[j] = b_frag(buf, j, f + 1);
-            }
-
+    for (int j = 0; j < NB; j++) fb[j] = ldB(2, j, 0);
+    rr[0] = ldR(0);
+    // Weight prefetch: the producers' loads retire in issue order, so a load that misses L2 would
+    // hold up the end-of-stage wait for the activation DMA issued after it. The consumers (whose
+    // own waits cover only LDS reads) touch every cache line of super-block u + 3 of the tile's
+    // columns at the start of super-block u; the mt workgroups that share an N-tile (same XCD, same
+    // L2) split the columns. Lane e of the four consumer waves (and of e + 256, ...) touches bytes
+    // {0, 72, 143} (e % 3) of column mt_i + mt (e / 3).
+    const int pf_cols = (BN - mt_i + g.mt - 1) / g.mt, pf_lanes = 3 * pf_cols;
+    const rsrc_t rw_pf = make_rsrc(g.W, (uint32_t)((size_t)N * g.row_bytes));
+    const uint32_t pf_lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds + L::PF) + 256u * (uint32_t)wave);
+    auto prefetch = [&](int v) {
+        for (int e0 = 64 * wave; e0 < pf_lanes; e0 += 256) {
+            const int e = e0 + lane, jc = e / 3, t = e - 3 * jc;
+            const int c = mt_i + g.mt * (e < pf_lanes ? jc : 0);
+            const uint32_t voff = (uint32_t)(n0 + c) * g.row_bytes + 144u * (uint32_t)v + (t == 0 ? 0u : t == 1 ? 72u : 143u);
+            l2_touch(rw_pf, voff, pf_lds);
         }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        wg_barrier();
     };
-    wg_barrier();
+    // per super-block: its min k-step, 4 k-steps of the even stage (buffer 0), 4 of the odd stage
+    // (buffer 1). The last k-step also reads the next super-block's min operands; after the last
+    // super-block those reads return stale LDS contents that are never used.
     for (int u = 0; u < U; u++) {
-        stage(0, true, u > 0);
-        stage(1, false, false);
+        if (u + 3 < U) prefetch(u + 3);
+        kstep(WsStep<1, 2, 0, false, 0, 0>{});  // P = 1: E0's A fragments go to fa[0]
+        kstep(WsStep<0, 0, 0, false, 0, 1>{});
+        kstep(WsStep<1, 0, 1, false, 0, 2>{});
+        kstep(WsStep<0, 0, 2, false, 0, 3>{});
+        kstep(WsStep<1, 0, 3, true, 1, 0>{});
+        kstep(WsStep<0, 1, 0, false, 1, 1>{});
+        kstep(WsStep<1, 1, 1, false, 1, 2>{});
+        kstep(WsStep<0, 1, 2, false, 1, 3>{});
+        kstep(WsStep<1, 1, 3, true, 2, 0>{});
     }
-    fold();  // last super-block
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the prefetches
+    // back to true units: multiply by the last super-block's c (written with its min-term tiles)
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+        const f4 cl = *(lds_f4 *)(uintptr_t)(cl_base + j * 16 * 4);
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i][j] *= cl;
+    }
     // Output: lane (ln, lg) of block (i, j) holds row 16i + ln, 4 consecutive columns: one 8-byte
     // (fp16) or 16-byte (fp32) store per block when the 4 columns are inside C and aligned.
     store_rows4<4, NB>(g.C, acc, M, N, m0 + 64 * wm, n0 + (BN / 2) * wn, ln, lg, g.c_f32, g.accumulate);

@@ -1091,11 +1091,13 @@ __global__ void __launch_bounds__(512) k_gemm_q4_k_w(GemmArgs g) {
     }
 }
 
-// Activation sub-block sums for the wide Q4_K GEMM: S[m][u][s] = fp16 hi and S[m][u][8 + s] = fp16
-// lo of the fp32 sum of activations 256u + 32s .. +32 of row m (hi + lo = the fp32 sum). One
-// 16-byte chunk per thread; the four chunks of a sub-block sit in one quad of lanes and are added
-// by two DPP rounds ((c0 + c1) + (c2 + c3) in every lane), then lanes 0 and 1 of the quad write hi
-// and lo. M*K/8 is a multiple of 4, so a quad is always entirely inside or outside the range.
+// Activation sub-block sums for the wide Q4_K GEMMs: S[m][u][s] = hi and S[m][u][8 + s] = lo of the
+// fp32 sum of activations 256u + 32s .. +32 of row m, in fp16 (BF16 = false: the Stream-K kernel)
+// or bf16 (the full-K tile kernel). One 16-byte chunk per thread; the four chunks of a sub-block sit
+// in one quad of lanes and are added by two DPP rounds ((c0 + c1) + (c2 + c3) in every lane), then
+// lanes 0 and 1 of the quad write hi and lo. M*K/8 is a multiple of 4, so a quad is always entirely
+// inside or outside the range.
+template <bool BF16>
 __global__ void __launch_bounds__(256) k_asums(const uint16_t *__restrict__ A, int M, int K,
                                                uint16_t *__restrict__ S) {
     const size_t n = (size_t)M * K / 8;
@@ -1113,9 +1115,15 @@ __global__ void __launch_bounds__(256) k_asums(const uint16_t *__restrict__ A, i
             const size_t b = t >> 2;  // sub-block index m * (K / 32) + k / 32
             const size_t m = b / (size_t)(K / 32);
             const int kb = (int)(b % (size_t)(K / 32));
-            const _Float16 hi = (_Float16)v;
-            S[(m * (size_t)(K / 256) + kb / 8) * 16 + 8 * part + (kb % 8)] =
-                __builtin_bit_cast(uint16_t, part ? (_Float16)(v - (float)hi) : hi);
+            uint16_t bits;
+            if constexpr (BF16) {
+                const __bf16 hi = (__bf16)v;
+                bits = __builtin_bit_cast(uint16_t, part ? (__bf16)(v - (float)hi) : hi);
+            } else {
+                const _Float16 hi = (_Float16)v;
+                bits = __builtin_bit_cast(uint16_t, part ? (_Float16)(v - (float)hi) : hi);
+            }
+            S[(m * (size_t)(K / 256) + kb / 8) * 16 + 8 * part + (kb % 8)] = bits;
         }
     }
 }
@@ -1263,7 +1271,8 @@ hipError_t hq_launch_gemm_pre(const hq_dev_mat *W, const uint16_t *A, int M, con
     const GemmCfg c = gemm_cfg(W, M, wk.n_cu);
     if (c.wide) {
         const size_t n16 = (size_t)M * (W->cols / 8);
-        k_asums<<<grid_for(n16, 256, 16384), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
+        if (c.ws_nb) k_asums<true><<<grid_for(n16, 256, 16384), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
+        else k_asums<false><<<grid_for(n16, 256, 16384), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
     }
     return hipGetLastError();
 }
