@@ -309,6 +309,84 @@ DEV void rows_q4_k(const uint8_t *__restrict__ W, size_t row_bytes, const uint16
     }
 }
 
+// ---- Q4_K GEMV (M = 1), LPR lanes per row (16 or 64; 256 / LPR rows per workgroup). Lane j of a row
+// takes the quant chunks j, j + LPR, ... (chunk c = 16 quant bytes of super-block c/8, part
+// t = c % 8, p = t/2, h = t % 2: low nibbles are the values 64p + 16h + i of sub-block 2p, high
+// nibbles 64p + 32 + 16h + i of sub-block 2p + 1) in batches of CB chunks, two batches in flight: a
+// batch's loads (quant bytes and super-block header) are issued before the previous batch is
+// decoded, and the first batch before the activation vector and its 16-value group sums are staged
+// in LDS. Decode: the masked nibbles under exponent 0x64 are the fp16 values 1024 + q (low) and
+// 1024 + 16q (high), dotted with the activations by v_dot2_f32_f16 (exact products, fp32 sums);
+// the 1024 bias comes off in fp32 through the group sums (dot(q, a) = dot(1024 + q, a) - 1024 sum(a),
+// ~1e-5 relative error from the larger partial sums).
+template <int LPR, int CB>
+__global__ void __launch_bounds__(256) k_gemv_q4_k_p(const uint8_t *__restrict__ W, size_t row_bytes,
+                                                     const uint16_t *__restrict__ a, int N, int K, void *C, int c_f32,
+                                                     int accumulate) {
+    extern __shared__ __attribute__((aligned(16))) char gv_lds[];
+    uint16_t *const sa = (uint16_t *)gv_lds;            // K activations
+    float *const sg = (float *)(gv_lds + 2 * (size_t)K);  // K / 16 group sums
+    const int tid = threadIdx.x, j = tid % LPR, n = blockIdx.x * (256 / LPR) + tid / LPR;
+    const uint8_t *row = W + (size_t)(n < N ? n : N - 1) * row_bytes;
+    const int nc = K / 32, nb = (nc + LPR * CB - 1) / (LPR * CB);
+    u4v hd0[CB], q0[CB], hd1[CB], q1[CB];
+    auto load = [&](u4v (&hd)[CB], u4v (&q)[CB], int bt) {
+#pragma unroll
+        for (int b = 0; b < CB; b++) {
+            const int c = j + LPR * (CB * bt + b), cc = c < nc ? c : nc - 1;
+            const uint8_t *blk = row + (size_t)(cc >> 3) * 144;
+            hd[b] = load16(blk);
+            q[b] = load16(blk + 16 + 16 * (cc & 7));
+        }
+    };
+    float acc = 0.f;
+    auto compute = [&](const u4v (&hd)[CB], const u4v (&q)[CB], int bt) {
+#pragma unroll
+        for (int b = 0; b < CB; b++) {
+            const int c = j + LPR * (CB * bt + b);
+            if (c >= nc) break;
+            const int t = c & 7, p = t >> 1;
+            const int kb = (c >> 3) * 256 + 64 * p + 16 * (t & 1);
+            uint32_t sw0, sw1, mw0, mw1;
+            q4k_scale_words(hd[b].y, hd[b].z, hd[b].w, sw0, sw1, mw0, mw1);
+            const uint32_t sh = 16u * (uint32_t)(p & 1);
+            const uint32_t sw = (p < 2 ? sw0 : sw1) >> sh, mw = (p < 2 ? mw0 : mw1) >> sh;
+            const float d = h2f((uint16_t)hd[b].x), dmin = h2f((uint16_t)(hd[b].x >> 16));
+            const float ds0 = d * (float)(sw & 0xffu), ds1 = d * (float)((sw >> 8) & 0xffu);
+            const float dm0 = dmin * (float)(mw & 0xffu), dm1 = dmin * (float)((mw >> 8) & 0xffu);
+            const u4v al0 = *(const u4v *)(sa + kb), al1 = *(const u4v *)(sa + kb + 8);
+            const u4v ah0 = *(const u4v *)(sa + kb + 32), ah1 = *(const u4v *)(sa + kb + 40);
+            const uint32_t wl[4] = {q[b].x & 0x0f0f0f0fu, q[b].y & 0x0f0f0f0fu, q[b].z & 0x0f0f0f0fu,
+                                    q[b].w & 0x0f0f0f0fu};
+            const uint32_t wh[4] = {q[b].x & 0xf0f0f0f0u, q[b].y & 0xf0f0f0f0u, q[b].z & 0xf0f0f0f0u,
+                                    q[b].w & 0xf0f0f0f0u};
+            const h2 l0[4] = {as_h2(perm_lo(wl[0])), as_h2(perm_hi(wl[0])), as_h2(perm_lo(wl[1])), as_h2(perm_hi(wl[1]))};
+            const h2 l1[4] = {as_h2(perm_lo(wl[2])), as_h2(perm_hi(wl[2])), as_h2(perm_lo(wl[3])), as_h2(perm_hi(wl[3]))};
+            const h2 g0[4] = {as_h2(perm_lo(wh[0])), as_h2(perm_hi(wh[0])), as_h2(perm_lo(wh[1])), as_h2(perm_hi(wh[1]))};
+            const h2 g1[4] = {as_h2(perm_lo(wh[2])), as_h2(perm_hi(wh[2])), as_h2(perm_lo(wh[3])), as_h2(perm_hi(wh[3]))};
+            const float sl = sg[kb >> 4], shi = sg[(kb >> 4) + 2];
+            const float ql = dot8(l1, al1, dot8(l0, al0, 0.f)) - 1024.0f * sl;   // dot(q, a), low nibbles
+            const float qh = dot8(g1, ah1, dot8(g0, ah0, 0.f)) - 1024.0f * shi;  // 16 dot(q, a), high
+            acc += (ds0 * ql - dm0 * sl) + (0.0625f * ds1 * qh - dm1 * shi);
+        }
+    };
+    load(hd0, q0, 0);
+    for (int i = tid; i < K / 8; i += 256) *(u4v *)(sa + 8 * i) = load16(a + 8 * i);
+    __syncthreads();
+    for (int i = tid; i < K / 16; i += 256) sg[i] = sum8(*(const u4v *)(sa + 16 * i + 8), sum8(*(const u4v *)(sa + 16 * i), 0.f));
+    __syncthreads();
+    for (int bt = 0;; bt += 2) {
+        if (bt + 1 < nb) load(hd1, q1, bt + 1);
+        compute(hd0, q0, bt);
+        if (bt + 1 >= nb) break;
+        if (bt + 2 < nb) load(hd0, q0, bt + 2);
+        compute(hd1, q1, bt + 1);
+        if (bt + 2 >= nb) break;
+    }
+    const float v = row_sum<LPR>(acc);
+    if (j == 0 && n < N) store_out(C, n, v, c_f32, accumulate);
+}
+
 // out row n (wave-uniform) of the R rows of this wave.
 template <int R>
 __global__ void __launch_bounds__(256) k_gemv_q8_0(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ d,
@@ -1171,6 +1249,24 @@ static void launch_gemv_t(const hq_dev_mat *W, const uint16_t *a, void *C, int c
 // Rows per wave: 2 (activations reused twice; measured best of 1, 2, 4 at N = 9728), 1 when that
 // would leave the grid short of about two workgroups per CU.
 hipError_t hq_launch_gemv(const hq_dev_mat *W, const uint16_t *a, void *C, int c_f32, int accumulate, hipStream_t st) {
+    if (W->type == HQ_TYPE_Q4_K) {
+        // 16 lanes per row when that still gives every CU several workgroups, else 64; two batches
+        // of CB chunks per lane in flight
+        const int N = (int)W->rows, K = (int)W->cols, nc = K / 32;
+        const int lpr = N >= 16 * 256 * 2 ? 16 : 64;
+        const int cpl = (nc + lpr - 1) / lpr, cb = cpl <= 2 ? 1 : cpl <= 4 ? 2 : cpl <= 6 ? 3 : 4;
+        const unsigned g = (unsigned)((N + 256 / lpr - 1) / (256 / lpr));
+        const size_t lds = (size_t)K * 2 + (size_t)K / 16 * 4;
+        if (lds > 64 * 1024) return hipErrorInvalidValue;
+#define GVP(l, c) k_gemv_q4_k_p<l, c><<<g, 256, lds, st>>>(W->qs, W->row_bytes, a, N, K, C, c_f32, accumulate)
+        if (lpr == 16) {
+            if (cb == 1) GVP(16, 1); else if (cb == 2) GVP(16, 2); else if (cb == 3) GVP(16, 3); else GVP(16, 4);
+        } else {
+            if (cb == 1) GVP(64, 1); else if (cb == 2) GVP(64, 2); else if (cb == 3) GVP(64, 3); else GVP(64, 4);
+        }
+#undef GVP
+        return hipGetLastError();
+    }
     if (W->rows >= 4096) launch_gemv_t<2>(W, a, C, c_f32, accumulate, st);
     else launch_gemv_t<1>(W, a, C, c_f32, accumulate, st);
     return hipGetLastError();
