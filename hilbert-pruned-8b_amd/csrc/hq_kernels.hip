@@ -1171,38 +1171,30 @@ __global__ void __launch_bounds__(512) k_gemm_q4_k_w(GemmArgs g) {
 
 // Activation sub-block sums for the wide Q4_K GEMMs: S[m][u][s] = hi and S[m][u][8 + s] = lo of the
 // fp32 sum of activations 256u + 32s .. +32 of row m, in fp16 (BF16 = false: the Stream-K kernel)
-// or bf16 (the full-K tile kernel). One 16-byte chunk per thread; the four chunks of a sub-block sit
-// in one quad of lanes and are added by two DPP rounds ((c0 + c1) + (c2 + c3) in every lane), then
-// lanes 0 and 1 of the quad write hi and lo. M*K/8 is a multiple of 4, so a quad is always entirely
-// inside or outside the range.
+// or bf16 (the full-K tile kernel). One thread per sub-block (four 16-byte loads, 32-bit index math;
+// M * K / 32 < 2^31 is checked by the launcher).
 template <bool BF16>
 __global__ void __launch_bounds__(256) k_asums(const uint16_t *__restrict__ A, int M, int K,
                                                uint16_t *__restrict__ S) {
-    const size_t n = (size_t)M * K / 8;
-    const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
-    for (size_t t = blockIdx.x * (size_t)256 + threadIdx.x; t < n; t += (size_t)gridDim.x * 256) {
-        const u4v x = *(const u4v *)(A + 8 * t);
-        float v = __builtin_amdgcn_fdot2(as_h2(x.x), one, 0.f, false);
-        v = __builtin_amdgcn_fdot2(as_h2(x.y), one, v, false);
-        v = __builtin_amdgcn_fdot2(as_h2(x.z), one, v, false);
-        v = __builtin_amdgcn_fdot2(as_h2(x.w), one, v, false);
-        v += dpp_quad_1032(v);
-        v += dpp_quad_2301(v);
-        const int part = (int)(t & 3);
-        if (part < 2) {
-            const size_t b = t >> 2;  // sub-block index m * (K / 32) + k / 32
-            const size_t m = b / (size_t)(K / 32);
-            const int kb = (int)(b % (size_t)(K / 32));
-            uint16_t bits;
-            if constexpr (BF16) {
-                const __bf16 hi = (__bf16)v;
-                bits = __builtin_bit_cast(uint16_t, part ? (__bf16)(v - (float)hi) : hi);
-            } else {
-                const _Float16 hi = (_Float16)v;
-                bits = __builtin_bit_cast(uint16_t, part ? (_Float16)(v - (float)hi) : hi);
-            }
-            S[(m * (size_t)(K / 256) + kb / 8) * 16 + 8 * part + (kb % 8)] = bits;
+    const uint32_t kb = (uint32_t)K / 32u, n = (uint32_t)M * kb;
+    for (uint32_t t = blockIdx.x * 256u + threadIdx.x; t < n; t += gridDim.x * 256u) {
+        const uint16_t *src = A + (size_t)t * 32;
+        const u4v x0 = load16(src), x1 = load16(src + 8), x2 = load16(src + 16), x3 = load16(src + 24);
+        const float v = sum8(x3, sum8(x2, sum8(x1, sum8(x0, 0.f))));
+        const uint32_t m = t / kb, s = t - m * kb;
+        uint16_t hb, lb;
+        if constexpr (BF16) {
+            const __bf16 hi = (__bf16)v;
+            hb = __builtin_bit_cast(uint16_t, hi);
+            lb = __builtin_bit_cast(uint16_t, (__bf16)(v - (float)hi));
+        } else {
+            const _Float16 hi = (_Float16)v;
+            hb = __builtin_bit_cast(uint16_t, hi);
+            lb = __builtin_bit_cast(uint16_t, (_Float16)(v - (float)hi));
         }
+        uint16_t *dst = S + ((size_t)m * (kb / 8) + s / 8) * 16 + (s % 8);
+        dst[0] = hb;
+        dst[8] = lb;
     }
 }
 
@@ -1366,9 +1358,10 @@ void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_by
 hipError_t hq_launch_gemm_pre(const hq_dev_mat *W, const uint16_t *A, int M, const HqGemmWork &wk, hipStream_t st) {
     const GemmCfg c = gemm_cfg(W, M, wk.n_cu);
     if (c.wide) {
-        const size_t n16 = (size_t)M * (W->cols / 8);
-        if (c.ws_nb) k_asums<true><<<grid_for(n16, 256, 16384), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
-        else k_asums<false><<<grid_for(n16, 256, 16384), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
+        const size_t nsub = (size_t)M * (W->cols / 32);
+        if (nsub >= ((size_t)1 << 31)) return hipErrorInvalidValue;
+        if (c.ws_nb) k_asums<true><<<grid_for(nsub, 256, 16384), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
+        else k_asums<false><<<grid_for(nsub, 256, 16384), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
     }
     return hipGetLastError();
 }
