@@ -615,12 +615,25 @@ DEV void finish_tile(f4 (&acc)[MB][NB], const SkPlan &p, int w, int u0, int u1, 
     }
     __syncthreads();
     if (!*s_flag) return;
-    for (int o = wf; o <= wl; o++) {
-        if (o == w) continue;
-        const uint32_t os = (uint32_t)(tile == sk_start(p, o) / p.upt ? 2 * o : 2 * o + 1) * PER;
-        constexpr int IG = MB < 4 ? MB : 4;  // row blocks per batch of loads (bounds the registers)
+    // The partials are summed in owner order wf .. wl (this workgroup's own in its place), so the
+    // result is the same whichever contributor arrives last.
+    constexpr int IG = MB < 4 ? MB : 4;  // row blocks per batch of loads (bounds the registers)
 #pragma unroll
-        for (int i0 = 0; i0 < MB; i0 += IG) {
+    for (int i0 = 0; i0 < MB; i0 += IG) {
+        f4 s[IG][NB];
+#pragma unroll
+        for (int i = 0; i < IG; i++)
+#pragma unroll
+            for (int j = 0; j < NB; j++) s[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+        for (int o = wf; o <= wl; o++) {
+            if (o == w) {
+#pragma unroll
+                for (int i = 0; i < IG; i++)
+#pragma unroll
+                    for (int j = 0; j < NB; j++) s[i][j] += acc[i0 + i][j];
+                continue;
+            }
+            const uint32_t os = (uint32_t)(tile == sk_start(p, o) / p.upt ? 2 * o : 2 * o + 1) * PER;
             f4 v[IG][NB];
 #pragma unroll
             for (int i = 0; i < IG; i++)
@@ -630,8 +643,12 @@ DEV void finish_tile(f4 (&acc)[MB][NB], const SkPlan &p, int w, int u0, int u1, 
 #pragma unroll
             for (int i = 0; i < IG; i++)
 #pragma unroll
-                for (int j = 0; j < NB; j++) acc[i0 + i][j] += v[i][j];
+                for (int j = 0; j < NB; j++) s[i][j] += v[i][j];
         }
+#pragma unroll
+        for (int i = 0; i < IG; i++)
+#pragma unroll
+            for (int j = 0; j < NB; j++) acc[i0 + i][j] = s[i][j];
     }
     store_tile<MB, NB>(C, acc, M, N, m0, nw, ln, lg, c_f32, accumulate);
 }

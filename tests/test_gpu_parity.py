@@ -174,6 +174,117 @@ def test_gemm_large_m_row_sample(hqlib, oracle):
         W.free()
 
 
+def special_q4_k_weights(seed, rows, cols):
+    """Q4_K weights whose super-block scales take the values the kernels treat specially: d = 0
+    with dmin kept (the tile kernel then works in units of 1 and zeroes that super-block's
+    quants), dmin = 0, negative d or dmin, subnormal d or dmin, and d 30x larger than its
+    neighbours (so consecutive super-blocks differ in scale by up to ~2^30); plus one row with
+    d = dmin = 0 everywhere (exact zeros) and one with d = 0 everywhere (min term only)."""
+    rng = synth.Rng(seed)
+    blk = synth.q4_k_blocks(rng, rows, cols)
+    nb = rows * (cols // 256)
+    v = blk.reshape(nb, 144)
+    d = v[:, 0:2].copy().view(np.uint16).ravel()
+    dm = v[:, 2:4].copy().view(np.uint16).ravel()
+    kind = rng.bytes(nb) % 16
+    sub = (rng.bytes(nb * 2).view(np.uint16) & 0x3FF) | 1
+    big = synth.f16_bits(np.abs(rng.normal(nb)) * 3e-2)
+    d = np.where(kind < 2, 0, d)
+    dm = np.where(kind == 2, 0, dm)
+    d = np.where(kind == 3, d | 0x8000, d)
+    dm = np.where(kind == 4, dm | 0x8000, dm)
+    d = np.where(kind == 5, sub, d)
+    dm = np.where(kind == 6, sub, dm)
+    d = np.where(kind == 7, big, d).astype(np.uint16)
+    dm = dm.astype(np.uint16)
+    spb = cols // 256
+    d.reshape(rows, spb)[rows // 7] = 0
+    dm.reshape(rows, spb)[rows // 7] = 0
+    d.reshape(rows, spb)[2 * (rows // 7)] = 0
+    v[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    v[:, 2:4] = dm.view(np.uint8).reshape(nb, 2)
+    return blk
+
+
+def f64_reference(oracle, blocks, gtype, N, K, a16):
+    """float64 product of the oracle's (bit-exact) dequantised weights and the fp16 activations,
+    and the row-wise |W| @ |a| that bounds any fp32 summation order's error."""
+    a = oracle.f16_to_f32(a16).astype(np.float64)
+    w = oracle.dequantize(blocks, gtype, N, K).astype(np.float64)
+    return a @ w.T, np.abs(a) @ np.abs(w).T
+
+
+# the tile kernel (M = 350, 512 at N = 9728), Stream-K wide (N = 2560), the narrow M <= 64 kernel
+# and the GEMV (M = 1)
+SPECIAL = [(9728, 512, 350), (9728, 2560, 512), (2560, 9728, 512), (9728, 2560, 48), (9728, 2560, 1),
+           (2560, 9728, 1)]
+
+
+@pytest.mark.parametrize("N,K,M", SPECIAL)
+def test_gemm_special_scales(hqlib, oracle, N, K, M):
+    """Q4_K GEMM/GEMV on weights with zero, negative, subnormal and widely varying super-block
+    scales, at the north-star bar against the oracle; the float64 product bounds the error by
+    2^-13 |W| @ |a| per output (the oracle's own fp32 error stays below 1e-6 of it)."""
+    blocks = special_q4_k_weights(31 + M, N, K)
+    a = synth.activations_f16(synth.Rng(400 + M), M, K)
+    W = hqlib.Mat(blocks, synth.Q4_K, N, K)
+    say(f"gemm special scales M={M} N={N} K={K} tiles={hqlib.gemm_tiles(synth.Q4_K, M, N)}")
+    got = hqlib.gemm_np(W, a)
+    W.free()
+    ref = oracle.matmul(blocks, synth.Q4_K, N, K, oracle.f16_to_f32(a))
+    r, m = rel_l2(got, ref), max_abs(got, ref)
+    say(f"special scales: rel_l2 {r:.2e} max_abs {m:.2e} max|ref| {np.abs(ref).max():.1f}")
+    assert r <= REL_L2 and m <= MAX_ABS
+    r64, bound = f64_reference(oracle, blocks, synth.Q4_K, N, K, a)
+    assert np.all(np.abs(got - r64) <= 2.0 ** -13 * bound)
+    assert np.all(got[:, N // 7] == 0.0)
+
+
+@pytest.mark.parametrize("gtype,N,K,M", [(synth.Q4_K, n, k, m) for n, k, m in SPECIAL] +
+                         [(synth.Q8_0, 9728, 2560, 1), (synth.Q8_0, 9728, 2560, 128)])
+def test_gemm_positive_activations(hqlib, oracle, gtype, N, K, M):
+    """Non-negative activations of magnitude up to ~16 (|N(0,1)| * 4): the Q4_K min term no longer
+    cancels across a sub-block, so the kernels' reassociated bias terms (the GEMV's 1024 + q
+    decode, the tile kernel's bf16 hi/lo sub-block sums) carry their largest error here. Outputs
+    reach ~3e4, where the oracle's own fp32 summation is off by ~5e-3, so the bar is rel-L2 <= 1e-3
+    against the oracle and 2^-13 |W| @ |a| against the float64 product. The same call with the
+    activations scaled by 2^6 must give the outputs scaled by 2^6 bit for bit (every step is exact
+    under a power-of-two scale)."""
+    blocks = weights(gtype, N, K, 100 + gtype)
+    rng = synth.Rng(500 + M + N)
+    a = synth.f16_bits(np.abs(rng.normal(M * K)) * 4).reshape(M, K)
+    W = hqlib.Mat(blocks, gtype, N, K)
+    say(f"gemm positive activations type={gtype} M={M} N={N} K={K} tiles={hqlib.gemm_tiles(gtype, M, N)}")
+    got = hqlib.gemm_np(W, a)
+    a64 = synth.f16_bits(oracle.f16_to_f32(a) * 64).reshape(M, K)
+    say("scaled by 2^6")
+    got64 = hqlib.gemm_np(W, a64)
+    W.free()
+    ref = oracle.matmul(blocks, gtype, N, K, oracle.f16_to_f32(a))
+    r = rel_l2(got, ref)
+    say(f"positive activations: rel_l2 {r:.2e} max_abs {max_abs(got, ref):.2e} max|ref| {np.abs(ref).max():.1f}")
+    assert r <= REL_L2
+    r64, bound = f64_reference(oracle, blocks, gtype, N, K, a)
+    assert np.all(np.abs(got - r64) <= 2.0 ** -13 * bound)
+    assert np.array_equal(got64, got * 64)
+
+
+def test_gather_special_scales(hqlib, oracle):
+    V, K, B, k = 4096, 2560, 64, 5
+    blocks = special_q4_k_weights(61, V, K)
+    rng = synth.Rng(62)
+    H = synth.activations_f16(rng, B, K)
+    ids = np.stack([rng.choice_without_replacement(V, k) for _ in range(B)]).astype(np.uint32)
+    ids[0, 0], ids[1, 0] = V // 7, 2 * (V // 7)
+    W = hqlib.Mat(blocks, synth.Q4_K, V, K)
+    say("gather special scales")
+    got = hqlib.gather_dot_np(W, H, ids)
+    W.free()
+    ref = oracle.gather_dot(blocks, synth.Q4_K, V, K, oracle.f16_to_f32(H), ids)
+    assert rel_l2(got, ref) <= REL_L2 and max_abs(got, ref) <= MAX_ABS
+    assert got[0, 0] == 0.0
+
+
 def test_matmul_host_drop_in(hqlib, oracle):
     """hq_matmul_host: fp32 host x in, fp32 host y out, accumulate, as cpu_backend.c's matmul; x is
     rounded to fp16 on the device, so it matches the oracle on fp16-rounded x."""
