@@ -188,6 +188,8 @@ def main():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run 20 device-to-device copies of BYTES bytes (the known-size kernel the "
                          "FETCH_SIZE / WRITE_SIZE counters are scaled by) and exit")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="only time the three M = 1 GEMV shapes of the sweep (for profiling) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); the quantized matmul "
@@ -209,6 +211,12 @@ def main():
     name, arch = hq.device_name(0)
     log("device", name, arch)
     stream = hq.Stream()
+    if args.gemv_only:
+        for g, n, k in [(synth.Q8_0, 9728, 2560), (synth.Q4_K, 9728, 2560), (synth.Q4_K, 2560, 9728)]:
+            r = bench_gemm(hq, synth, g, n, k, 1, False, args.steps, args.warmup, stream, settle_s=0.2)
+            r["frac_hbm"] = round(r["gbs"] / PEAK_GBS, 4)
+            log("gemv", r)
+        return
 
     gtype, N, K, M = synth.Q4_K, 9728, 2560, 512
     head = bench_gemm(hq, synth, gtype, N, K, M, False, args.steps, args.warmup, stream, kernel_time=True,

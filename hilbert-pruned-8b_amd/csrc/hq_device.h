@@ -56,6 +56,36 @@ DEV rsrc_t make_rsrc(const void *base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, 0x00020000);
 }
 
+// LDS DMA: lane i's 16 bytes at voff + soff land at lds + 16 i (lds is wave-uniform).
+DEV void dma16(rsrc_t r, void *lds, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_ptr(lds), 16, voff, soff, 0, 0);
+}
+
+// The same 16-byte LDS DMA written as assembly, so the compiler does not track it: it would
+// otherwise wait for every earlier LDS DMA before each later LDS read. The caller waits for it
+// with an explicit s_waitcnt vmcnt. lds_addr is the wave-uniform LDS byte address; M0 is restored.
+DEV void dma16_untracked(rsrc_t r, uint32_t lds_addr, uint32_t voff) {
+    uint32_t save;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 1\n\tbuffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(save)
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(r)
+                 : "memory");
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform n in 0 .. 31 (the count is an immediate of the instruction).
+DEV void wait_vmcnt(int n) {
+    switch (n) {
+#define HQ_VMW(i) case i: asm volatile("s_waitcnt vmcnt(" #i ")" ::: "memory"); break;
+        HQ_VMW(0) HQ_VMW(1) HQ_VMW(2) HQ_VMW(3) HQ_VMW(4) HQ_VMW(5) HQ_VMW(6) HQ_VMW(7)
+        HQ_VMW(8) HQ_VMW(9) HQ_VMW(10) HQ_VMW(11) HQ_VMW(12) HQ_VMW(13) HQ_VMW(14) HQ_VMW(15)
+        HQ_VMW(16) HQ_VMW(17) HQ_VMW(18) HQ_VMW(19) HQ_VMW(20) HQ_VMW(21) HQ_VMW(22) HQ_VMW(23)
+        HQ_VMW(24) HQ_VMW(25) HQ_VMW(26) HQ_VMW(27) HQ_VMW(28) HQ_VMW(29) HQ_VMW(30) HQ_VMW(31)
+#undef HQ_VMW
+    default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    }
+}
+
 DEV u4v buf_load16(rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }

@@ -67,10 +67,6 @@ DEV u2v buf_load8(rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
 }
 
-DEV void dma16(rsrc_t r, void *lds, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_ptr(lds), 16, voff, soff, 0, 0);
-}
-
 // L2 prefetch: a 4-byte-per-lane LDS DMA of the bytes at voff into a scratch LDS slot that is never
 // read (256 bytes at lds_addr). Written as assembly: the compiler waits for every LDS DMA it knows
 // of before any later LDS access, which would put the fetch's latency in front of the next LDS

@@ -309,82 +309,173 @@ DEV void rows_q4_k(const uint8_t *__restrict__ W, size_t row_bytes, const uint16
     }
 }
 
-// ---- Q4_K GEMV (M = 1), LPR lanes per row (16 or 64; 256 / LPR rows per workgroup). Lane j of a row
-// takes the quant chunks j, j + LPR, ... (chunk c = 16 quant bytes of super-block c/8, part
-// t = c % 8, p = t/2, h = t % 2: low nibbles are the values 64p + 16h + i of sub-block 2p, high
-// nibbles 64p + 32 + 16h + i of sub-block 2p + 1) in batches of CB chunks, two batches in flight: a
-// batch's loads (quant bytes and super-block header) are issued before the previous batch is
-// decoded, and the first batch before the activation vector and its 16-value group sums are staged
-// in LDS. Decode: the masked nibbles under exponent 0x64 are the fp16 values 1024 + q (low) and
-// 1024 + 16q (high), dotted with the activations by v_dot2_f32_f16 (exact products, fp32 sums);
-// the 1024 bias comes off in fp32 through the group sums (dot(q, a) = dot(1024 + q, a) - 1024 sum(a),
-// ~1e-5 relative error from the larger partial sums).
-template <int LPR, int CB>
-__global__ void __launch_bounds__(256) k_gemv_q4_k_p(const uint8_t *__restrict__ W, size_t row_bytes,
+// One GEMV unit from LDS: 64 values of a weight row (32-byte quant group p of the super-block at
+// blk: low nibbles = sub-block 2p, high nibbles = sub-block 2p + 1) dotted with activations
+// [64 ku, 64 ku + 64) of sa, using the 32-value sums ss[2 ku], ss[2 ku + 1]. The quants become the
+// fp16 values 1024 + q (low) and 1024 + 16 q (high) under v_perm_b32, meet the activations in
+// v_dot2_f32_f16 (exact products, fp32 sums), and the 1024 bias comes off in fp32 through the sums:
+// d sc dot(q, a) - dmin m sum(a) per sub-block (ggml_quant.h:51-59 scale and min codes).
+DEV float gemv_unit_q4_k(const char *blk, int p, const char *sa, const float *ss, int ku) {
+    const u4v hd = *(const u4v *)blk;
+    const u4v q0 = *(const u4v *)(blk + 16 + 32 * p), q1 = *(const u4v *)(blk + 32 + 32 * p);
+    const u4v *const av = (const u4v *)(sa + 128 * ku);
+    const float s0 = ss[2 * ku], s1 = ss[2 * ku + 1];
+    uint32_t sw0, sw1, mw0, mw1;
+    q4k_scale_words(hd.y, hd.z, hd.w, sw0, sw1, mw0, mw1);
+    const uint32_t sh = 16u * (uint32_t)(p & 1);
+    const uint32_t sw = (p < 2 ? sw0 : sw1) >> sh, mw = (p < 2 ? mw0 : mw1) >> sh;
+    const float d = h2f((uint16_t)hd.x), dmin = h2f((uint16_t)(hd.x >> 16));
+    const float ds0 = d * (float)(sw & 0xffu), ds1 = d * (float)((sw >> 8) & 0xffu);
+    const float dm0 = dmin * (float)(mw & 0xffu), dm1 = dmin * (float)((mw >> 8) & 0xffu);
+    float part[4];
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        const u4v q = c ? q1 : q0;
+        const uint32_t wl[4] = {q.x & 0x0f0f0f0fu, q.y & 0x0f0f0f0fu, q.z & 0x0f0f0f0fu, q.w & 0x0f0f0f0fu};
+        const uint32_t wh[4] = {q.x & 0xf0f0f0f0u, q.y & 0xf0f0f0f0u, q.z & 0xf0f0f0f0u, q.w & 0xf0f0f0f0u};
+        const h2 l0[4] = {as_h2(perm_lo(wl[0])), as_h2(perm_hi(wl[0])), as_h2(perm_lo(wl[1])), as_h2(perm_hi(wl[1]))};
+        const h2 l1[4] = {as_h2(perm_lo(wl[2])), as_h2(perm_hi(wl[2])), as_h2(perm_lo(wl[3])), as_h2(perm_hi(wl[3]))};
+        const h2 g0[4] = {as_h2(perm_lo(wh[0])), as_h2(perm_hi(wh[0])), as_h2(perm_lo(wh[1])), as_h2(perm_hi(wh[1]))};
+        const h2 g1[4] = {as_h2(perm_lo(wh[2])), as_h2(perm_hi(wh[2])), as_h2(perm_lo(wh[3])), as_h2(perm_hi(wh[3]))};
+        part[c] = dot8(l1, av[2 * c + 1], dot8(l0, av[2 * c], 0.f));
+        part[2 + c] = dot8(g1, av[4 + 2 * c + 1], dot8(g0, av[4 + 2 * c], 0.f));
+    }
+    const float ql = (part[0] + part[1]) - 1024.0f * s0;  // dot(q, a), sub-block 2p
+    const float qh = (part[2] + part[3]) - 1024.0f * s1;  // 16 dot(q, a), sub-block 2p + 1
+    return (ds0 * ql - dm0 * s0) + (0.0625f * ds1 * qh - dm1 * s1);
+}
+
+// ---- Q4_K GEMV (M = 1) through LDS: a workgroup owns R consecutive weight rows, which are one
+// contiguous byte range of W. It copies that slab and the activation vector into LDS with 16-byte
+// LDS DMAs (1 KB per wave instruction, fully coalesced, no registers), forms the 32-value sub-block
+// sums of the activations, then every lane dots units of 64 values (one 32-byte quant group p of a
+// super-block: low nibbles = sub-block 2p, high nibbles = sub-block 2p + 1) from LDS. Lane tid
+// always works on row tid % R (R divides 256), so its partial sums stay in one register; the R
+// row totals are reduced across lanes and waves in a fixed order. Units: gemv_unit_q4_k (one
+// super-block header read and one scale decode per 64 values).
+template <int R>
+__global__ void __launch_bounds__(256) k_gemv_q4_k_s(const uint8_t *__restrict__ W, uint32_t row_bytes,
                                                      const uint16_t *__restrict__ a, int N, int K, void *C, int c_f32,
                                                      int accumulate) {
-    extern __shared__ __attribute__((aligned(16))) char gv_lds[];
-    uint16_t *const sa = (uint16_t *)gv_lds;            // K activations
-    float *const sg = (float *)(gv_lds + 2 * (size_t)K);  // K / 16 group sums
-    const int tid = threadIdx.x, j = tid % LPR, n = blockIdx.x * (256 / LPR) + tid / LPR;
-    const uint8_t *row = W + (size_t)(n < N ? n : N - 1) * row_bytes;
-    const int nc = K / 32, nb = (nc + LPR * CB - 1) / (LPR * CB);
-    u4v hd0[CB], q0[CB], hd1[CB], q1[CB];
-    auto load = [&](u4v (&hd)[CB], u4v (&q)[CB], int bt) {
-#pragma unroll
-        for (int b = 0; b < CB; b++) {
-            const int c = j + LPR * (CB * bt + b), cc = c < nc ? c : nc - 1;
-            const uint8_t *blk = row + (size_t)(cc >> 3) * 144;
-            hd[b] = load16(blk);
-            q[b] = load16(blk + 16 + 16 * (cc & 7));
-        }
-    };
-    float acc = 0.f;
-    auto compute = [&](const u4v (&hd)[CB], const u4v (&q)[CB], int bt) {
-#pragma unroll
-        for (int b = 0; b < CB; b++) {
-            const int c = j + LPR * (CB * bt + b);
-            if (c >= nc) break;
-            const int t = c & 7, p = t >> 1;
-            const int kb = (c >> 3) * 256 + 64 * p + 16 * (t & 1);
-            uint32_t sw0, sw1, mw0, mw1;
-            q4k_scale_words(hd[b].y, hd[b].z, hd[b].w, sw0, sw1, mw0, mw1);
-            const uint32_t sh = 16u * (uint32_t)(p & 1);
-            const uint32_t sw = (p < 2 ? sw0 : sw1) >> sh, mw = (p < 2 ? mw0 : mw1) >> sh;
-            const float d = h2f((uint16_t)hd[b].x), dmin = h2f((uint16_t)(hd[b].x >> 16));
-            const float ds0 = d * (float)(sw & 0xffu), ds1 = d * (float)((sw >> 8) & 0xffu);
-            const float dm0 = dmin * (float)(mw & 0xffu), dm1 = dmin * (float)((mw >> 8) & 0xffu);
-            const u4v al0 = *(const u4v *)(sa + kb), al1 = *(const u4v *)(sa + kb + 8);
-            const u4v ah0 = *(const u4v *)(sa + kb + 32), ah1 = *(const u4v *)(sa + kb + 40);
-            const uint32_t wl[4] = {q[b].x & 0x0f0f0f0fu, q[b].y & 0x0f0f0f0fu, q[b].z & 0x0f0f0f0fu,
-                                    q[b].w & 0x0f0f0f0fu};
-            const uint32_t wh[4] = {q[b].x & 0xf0f0f0f0u, q[b].y & 0xf0f0f0f0u, q[b].z & 0xf0f0f0f0u,
-                                    q[b].w & 0xf0f0f0f0u};
-            const h2 l0[4] = {as_h2(perm_lo(wl[0])), as_h2(perm_hi(wl[0])), as_h2(perm_lo(wl[1])), as_h2(perm_hi(wl[1]))};
-            const h2 l1[4] = {as_h2(perm_lo(wl[2])), as_h2(perm_hi(wl[2])), as_h2(perm_lo(wl[3])), as_h2(perm_hi(wl[3]))};
-            const h2 g0[4] = {as_h2(perm_lo(wh[0])), as_h2(perm_hi(wh[0])), as_h2(perm_lo(wh[1])), as_h2(perm_hi(wh[1]))};
-            const h2 g1[4] = {as_h2(perm_lo(wh[2])), as_h2(perm_hi(wh[2])), as_h2(perm_lo(wh[3])), as_h2(perm_hi(wh[3]))};
-            const float sl = sg[kb >> 4], shi = sg[(kb >> 4) + 2];
-            const float ql = dot8(l1, al1, dot8(l0, al0, 0.f)) - 1024.0f * sl;   // dot(q, a), low nibbles
-            const float qh = dot8(g1, ah1, dot8(g0, ah0, 0.f)) - 1024.0f * shi;  // 16 dot(q, a), high
-            acc += (ds0 * ql - dm0 * sl) + (0.0625f * ds1 * qh - dm1 * shi);
-        }
-    };
-    load(hd0, q0, 0);
-    for (int i = tid; i < K / 8; i += 256) *(u4v *)(sa + 8 * i) = load16(a + 8 * i);
+    extern __shared__ __attribute__((aligned(16))) char gs_lds[];
+    const uint32_t slab_bytes = (uint32_t)R * row_bytes, act_bytes = 2u * (uint32_t)K;
+    char *const slab = gs_lds;
+    char *const sa = gs_lds + slab_bytes;
+    float *const ss = (float *)(sa + act_bytes);  // K / 32 sub-block sums
+    float *const red = ss + K / 32;               // [4 waves][R] row partials
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const rsrc_t ra = make_rsrc(a, act_bytes);
+    const rsrc_t rw = make_rsrc(W, (uint32_t)N * row_bytes);  // rows >= N read as zero
+    for (uint32_t o = 1024u * wave; o < act_bytes; o += 4096u)
+        if (o + 16u * lane < act_bytes) dma16(ra, sa + o, o + 16u * lane, 0);
+    const uint32_t base = (uint32_t)blockIdx.x * slab_bytes;
+    for (uint32_t o = 1024u * wave; o < slab_bytes; o += 4096u)
+        if (o + 16u * lane < slab_bytes) dma16(rw, slab + o, base + o + 16u * lane, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    for (int i = tid; i < K / 16; i += 256) sg[i] = sum8(*(const u4v *)(sa + 16 * i + 8), sum8(*(const u4v *)(sa + 16 * i), 0.f));
-    __syncthreads();
-    for (int bt = 0;; bt += 2) {
-        if (bt + 1 < nb) load(hd1, q1, bt + 1);
-        compute(hd0, q0, bt);
-        if (bt + 1 >= nb) break;
-        if (bt + 2 < nb) load(hd0, q0, bt + 2);
-        compute(hd1, q1, bt + 1);
-        if (bt + 2 >= nb) break;
+    for (int i = tid; i < K / 32; i += 256) {
+        const u4v *p = (const u4v *)(sa + 64 * i);
+        ss[i] = sum8(p[3], sum8(p[2], sum8(p[1], sum8(p[0], 0.f))));
     }
-    const float v = row_sum<LPR>(acc);
-    if (j == 0 && n < N) store_out(C, n, v, c_f32, accumulate);
+    __syncthreads();
+    const int r = tid % R, units = R * (K / 64);
+    const char *const row = slab + r * row_bytes;
+    float acc = 0.f;
+    for (int u = tid; u < units; u += 256) {
+        const int ku = u / R;
+        acc += gemv_unit_q4_k(row + (ku >> 2) * 144, ku & 3, sa, ss, ku);
+    }
+#pragma unroll
+    for (int o = R; o < 64; o <<= 1) acc += __shfl_xor(acc, o, 64);
+    if (lane < R) red[wave * R + lane] = acc;
+    __syncthreads();
+    const int n = blockIdx.x * R + tid;
+    if (tid < R && n < N) store_out(C, n, ((red[tid] + red[R + tid]) + red[2 * R + tid]) + red[3 * R + tid], c_f32, accumulate);
+}
+
+// ---- Q4_K GEMV (M = 1), streamed: a workgroup owns 8 weight rows; its S waves split the row's
+// super-block pairs into S contiguous ranges. A wave streams its range through a ring of NS LDS
+// slots, one stage = one super-block pair of the 8 rows (8 x 288 bytes, three 1 KB LDS DMAs whose
+// lanes gather the 8 row pieces), NS stages in flight: it waits for the oldest stage with
+// s_waitcnt vmcnt, decodes it while the younger stages land, then refills the slot. In a stage,
+// lane (row = lane / 8, j = lane % 8) takes the unit j = 32-byte quant group j % 4 of super-block
+// j / 4 (64 values: low nibbles sub-block 2p, high nibbles 2p + 1), dotted by gemv_unit_q4_k.
+// The activations and their 32-value sub-block sums are staged once per workgroup. Row totals:
+// 8-lane butterfly, then the S wave partials in wave order. Needs an even number of super-blocks
+// per row.
+constexpr int GVR_SLOT = 8 * 288;
+
+template <int NS>
+__global__ void __launch_bounds__(256) k_gemv_q4_k_r(const uint8_t *__restrict__ W, uint32_t row_bytes,
+                                                     const uint16_t *__restrict__ a, int N, int K, void *C, int c_f32,
+                                                     int accumulate) {
+    extern __shared__ __attribute__((aligned(16))) char gr_lds[];
+    const int tid = threadIdx.x, lane = tid & 63, S = (int)blockDim.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar control flow
+    const uint32_t act_bytes = 2u * (uint32_t)K;
+    char *const sa = gr_lds;
+    float *const ss = (float *)(gr_lds + act_bytes);  // K / 32 sub-block sums
+    float *const red = ss + K / 32;                   // [S][8] wave partials
+    char *const ring = (char *)(red + 8 * S) + (size_t)wave * NS * GVR_SLOT;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)gr_lds;
+    const rsrc_t ra = make_rsrc(a, act_bytes);
+    const rsrc_t rw = make_rsrc(W, (uint32_t)N * row_bytes);  // rows >= N read as zero
+    const int n0 = blockIdx.x * 8, pairs = K / 512;
+    const int pr0 = wave * pairs / S, nst = (wave + 1) * pairs / S - pr0;
+    // this lane's gather offsets for the three DMA instructions of a stage (lane l = 64 q + lane of
+    // the stage: row l / 18, 16-byte piece l % 18)
+    uint32_t dvo[3];
+#pragma unroll
+    for (int q = 0; q < 3; q++) {
+        const int l = 64 * q + lane, row = l / 18, piece = l % 18;
+        dvo[q] = (uint32_t)(n0 + row) * row_bytes + 16u * (uint32_t)piece;
+    }
+    const uint32_t ring_addr = (uint32_t)(uintptr_t)ring;
+    auto issue = [&](int st) {
+        const uint32_t slot = ring_addr + (uint32_t)(st % NS) * GVR_SLOT, off = (uint32_t)(pr0 + st) * 288u;
+        dma16_untracked(rw, slot, dvo[0] + off);
+        dma16_untracked(rw, slot + 1024u, dvo[1] + off);
+        if (lane < 16) dma16_untracked(rw, slot + 2048u, dvo[2] + off);
+    };
+    // activations (this wave's share of the 1 KB pieces), then the first NS stages
+    int nact = 0;
+    for (uint32_t o = 1024u * wave; o < act_bytes; o += 1024u * S, nact++)
+        if (o + 16u * lane < act_bytes) dma16_untracked(ra, lds0 + o, o + 16u * lane);
+    const int pre = nst < NS ? nst : NS;
+    for (int st = 0; st < pre; st++) issue(st);
+    wait_vmcnt(3 * pre);
+    __syncthreads();
+    for (int i = tid; i < K / 32; i += 64 * S) {
+        const u4v *p = (const u4v *)(sa + 64 * i);
+        ss[i] = sum8(p[3], sum8(p[2], sum8(p[1], sum8(p[0], 0.f))));
+    }
+    __syncthreads();
+    const int row = lane >> 3, j = lane & 7, p = j & 3;
+    const uint32_t unit_off = (uint32_t)row * 288u + (uint32_t)(j >> 2) * 144u;
+    float acc = 0.f;
+    for (int st = 0; st < nst; st++) {
+        const int ahead = (nst - st - 1 < NS - 1) ? nst - st - 1 : NS - 1;
+        wait_vmcnt(3 * ahead);  // stage st has landed
+        acc += gemv_unit_q4_k(ring + (st % NS) * GVR_SLOT + unit_off, p, sa, ss, 4 * (2 * (pr0 + st) + (j >> 2)) + p);
+        if (st + NS < nst) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this slot's reads are done
+            issue(st + NS);
+        }
+    }
+    acc += __shfl_xor(acc, 1, 64);
+    acc += __shfl_xor(acc, 2, 64);
+    acc += __shfl_xor(acc, 4, 64);
+    if (S == 1) {
+        if (j == 0 && n0 + row < N) store_out(C, n0 + row, acc, c_f32, accumulate);
+        return;
+    }
+    if (j == 0) red[wave * 8 + row] = acc;
+    __syncthreads();
+    if (tid < 8 && n0 + tid < N) {
+        float v = red[tid];
+        for (int w = 1; w < S; w++) v += red[w * 8 + tid];
+        store_out(C, n0 + tid, v, c_f32, accumulate);
+    }
 }
 
 // out row n (wave-uniform) of the R rows of this wave.
@@ -1258,23 +1349,44 @@ static void launch_gemv_t(const hq_dev_mat *W, const uint16_t *a, void *C, int c
 // Rows per wave: 2 (activations reused twice; measured best of 1, 2, 4 at N = 9728), 1 when that
 // would leave the grid short of about two workgroups per CU.
 hipError_t hq_launch_gemv(const hq_dev_mat *W, const uint16_t *a, void *C, int c_f32, int accumulate, hipStream_t st) {
-    if (W->type == HQ_TYPE_Q4_K) {
-        // 16 lanes per row when that still gives every CU several workgroups, else 64; two batches
-        // of CB chunks per lane in flight
-        const int N = (int)W->rows, K = (int)W->cols, nc = K / 32;
-        const int lpr = N >= 16 * 256 * 2 ? 16 : 64;
-        const int cpl = (nc + lpr - 1) / lpr, cb = cpl <= 2 ? 1 : cpl <= 4 ? 2 : cpl <= 6 ? 3 : 4;
-        const unsigned g = (unsigned)((N + 256 / lpr - 1) / (256 / lpr));
-        const size_t lds = (size_t)K * 2 + (size_t)K / 16 * 4;
-        if (lds > 64 * 1024) return hipErrorInvalidValue;
-#define GVP(l, c) k_gemv_q4_k_p<l, c><<<g, 256, lds, st>>>(W->qs, W->row_bytes, a, N, K, C, c_f32, accumulate)
-        if (lpr == 16) {
-            if (cb == 1) GVP(16, 1); else if (cb == 2) GVP(16, 2); else if (cb == 3) GVP(16, 3); else GVP(16, 4);
-        } else {
-            if (cb == 1) GVP(64, 1); else if (cb == 2) GVP(64, 2); else if (cb == 3) GVP(64, 3); else GVP(64, 4);
+    if (W->type == HQ_TYPE_Q4_K && W->cols % 512 == 0 && W->rows >= 8 * 1024 &&
+        ((size_t)W->rows + 8) * W->row_bytes < ((size_t)1 << 32)) {
+        // streamed kernel when there are at least 1024 groups of 8 rows: two waves per group, each
+        // half of K (measured at N = 9728, K = 2560: 6.55 us against 6.8 for the slab kernel and
+        // 7.1 with one wave per group); fewer rows go to the slab kernel, whose 4-wave workgroups
+        // fill the CUs better there (N = 2560, K = 9728: 7.5 us against 8.3)
+        const int N = (int)W->rows, K = (int)W->cols, pairs = K / 512, S = pairs >= 2 ? 2 : 1;
+        constexpr int NS = 4;
+        const size_t lds = (size_t)K * 2 + (size_t)K / 32 * 4 + 32 * (size_t)S + (size_t)S * NS * GVR_SLOT;
+        if (lds <= 64 * 1024) {
+            k_gemv_q4_k_r<NS><<<(N + 7) / 8, 64 * S, lds, st>>>(W->qs, (uint32_t)W->row_bytes, a, N, K, C, c_f32,
+                                                                accumulate);
+            return hipGetLastError();
         }
-#undef GVP
-        return hipGetLastError();
+    }
+    if (W->type == HQ_TYPE_Q4_K && (size_t)W->rows * W->row_bytes < ((size_t)1 << 32)) {
+        // LDS-slab kernel: the most rows per workgroup (up to 32) that still give at least 512
+        // workgroups (two per CU) and fit the slab, activations and sums in 64 KB of LDS
+        const int N = (int)W->rows, K = (int)W->cols;
+        const size_t fixed = (size_t)K * 2 + (size_t)K / 32 * 4;
+        int R = 32;
+        while (R > 1 && ((N + R - 1) / R < 512 || fixed + (size_t)R * (W->row_bytes + 16) > 64 * 1024)) R >>= 1;
+        const size_t lds = fixed + (size_t)R * (W->row_bytes + 16);
+        if (lds <= 64 * 1024) {
+            const unsigned g = (unsigned)((N + R - 1) / R);
+            const uint32_t rb = (uint32_t)W->row_bytes;
+#define GVS(r) k_gemv_q4_k_s<r><<<g, 256, lds, st>>>(W->qs, rb, a, N, K, C, c_f32, accumulate)
+            switch (R) {
+            case 32: GVS(32); break;
+            case 16: GVS(16); break;
+            case 8: GVS(8); break;
+            case 4: GVS(4); break;
+            case 2: GVS(2); break;
+            default: GVS(1); break;
+            }
+#undef GVS
+            return hipGetLastError();
+        }
     }
     if (W->rows >= 4096) launch_gemv_t<2>(W, a, C, c_f32, accumulate, st);
     else launch_gemv_t<1>(W, a, C, c_f32, accumulate, st);

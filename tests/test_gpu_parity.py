@@ -115,7 +115,10 @@ RAGGED = [(synth.Q8_0, 100, 512, M) for M in (1, 2, 5, 17, 33, 65, 200)] + \
           (synth.Q8_0, 1408, 512, 128), (synth.Q8_0, 512, 1408, 128), (synth.Q8_0, 72, 96, 3), (synth.Q8_0, 72, 96, 40),
           (synth.Q4_K, 130, 2560, 31), (synth.Q4_K, 33, 256, 1), (synth.Q4_K, 33, 256, 20)] + \
          [(synth.Q4_K, 9500, 768, 500), (synth.Q4_K, 9728, 512, 350), (synth.Q4_K, 9728, 256, 350),
-          (synth.Q4_K, 9000, 768, 1000)]  # full-K tiles (the last: Stream-K, more tiles than CUs)
+          (synth.Q4_K, 9000, 768, 1000)] + \
+         [(synth.Q4_K, 8200, 1536, 1), (synth.Q4_K, 9728, 512, 1), (synth.Q4_K, 8192, 1024, 1)]
+# (the last: full-K tiles; Stream-K with more tiles than CUs; the streamed GEMV with a ragged last
+# row group and an odd K split, with one wave per row group, and with an even split)
 
 
 @pytest.mark.parametrize("gtype,N,K,M", FULL + RAGGED)
@@ -133,7 +136,7 @@ def test_gemm_parity(hqlib, oracle, gtype, N, K, M):
 
 @pytest.mark.parametrize("gtype,M,N,K", [(synth.Q8_0, 1, 320, 1024), (synth.Q8_0, 48, 320, 1024),
                                          (synth.Q4_K, 1, 320, 1024), (synth.Q4_K, 48, 320, 1024),
-                                         (synth.Q4_K, 350, 9728, 256)])
+                                         (synth.Q4_K, 350, 9728, 256), (synth.Q4_K, 1, 8192, 1024)])
 def test_gemm_accumulate_and_fp16_output(hqlib, oracle, gtype, M, N, K):
     blocks = weights(gtype, N, K, 7)
     rng = synth.Rng(77 + M)
