@@ -1364,8 +1364,8 @@ hipError_t hq_launch_gemv(const hq_dev_mat *W, const uint16_t *a, void *C, int c
             return hipGetLastError();
         }
     }
-    if (W->type == HQ_TYPE_Q4_K && (size_t)W->rows * W->row_bytes < ((size_t)1 << 32)) {
-        // LDS-slab kernel: the most rows per workgroup (up to 32) that still give at least 512
+    if (W->type == HQ_TYPE_Q4_K && ((size_t)W->rows + 32) * W->row_bytes < ((size_t)1 << 32)) {
+        // LDS-slab kernel (32-bit byte offsets up to the end of the last, possibly partial, slab): the most rows per workgroup (up to 32) that still give at least 512
         // workgroups (two per CU) and fit the slab, activations and sums in 64 KB of LDS
         const int N = (int)W->rows, K = (int)W->cols;
         const size_t fixed = (size_t)K * 2 + (size_t)K / 32 * 4;
