@@ -71,6 +71,8 @@ def main_kernel_name(hq, gtype, M, N):
     rows, cols = hq.gemm_tiles(gtype, M, N)
     if gtype == synth.Q4_K and M > 64:
         return "k_gemm_q4_k_w<8>" if cols == 256 else f"k_gemm_q4_k_ws<{cols // 32}>"
+    if gtype == synth.Q8_0 and rows == 128:
+        return f"k_gemm_q8_0_ws<{cols // 32}>"
     mb = rows // 16
     return f"k_gemm_q8_0<{mb}, 2>" if gtype == synth.Q8_0 else f"k_gemm_q4_k<{mb}, 2>"
 
@@ -190,6 +192,8 @@ def main():
                          "FETCH_SIZE / WRITE_SIZE counters are scaled by) and exit")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only time the three M = 1 GEMV shapes of the sweep (for profiling) and exit")
+    ap.add_argument("--shape", default="", metavar="TYPE:M:N:K",
+                    help="only time this one GEMM shape (TYPE q8_0 or q4_k; for profiling) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); the quantized matmul "
@@ -211,6 +215,12 @@ def main():
     name, arch = hq.device_name(0)
     log("device", name, arch)
     stream = hq.Stream()
+    if args.shape:
+        t, m, n, k = args.shape.split(":")
+        g = {"q8_0": synth.Q8_0, "q4_k": synth.Q4_K}[t]
+        r = bench_gemm(hq, synth, g, int(n), int(k), int(m), False, args.steps, args.warmup, stream, settle_s=0.2)
+        log("shape", main_kernel_name(hq, g, int(m), int(n)), r)
+        return
     if args.gemv_only:
         for g, n, k in [(synth.Q8_0, 9728, 2560), (synth.Q4_K, 9728, 2560), (synth.Q4_K, 2560, 9728)]:
             r = bench_gemm(hq, synth, g, n, k, 1, False, args.steps, args.warmup, stream, settle_s=0.2)

@@ -505,6 +505,236 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
     // (fp16) or 16-byte (fp32) store per block when the 4 columns are inside C and aligned.
     store_rows4<4, NB>(g.C, acc, M, N, m0 + 64 * wm, n0 + (BN / 2) * wn, ln, lg, g.c_f32, g.accumulate);
 }
+
+// ---------------------------------------------------------------------------------------------
+// Q8_0 tile kernel: the same decomposition, roles and consumer k-step stream as k_gemm_q4_k_ws,
+// without the min term and the rescale (a Q8_0 weight is q * d with one scale per 32 values, so the
+// B operand carries the scale: fp16(q * d), one rounding of the exact product, as in the other
+// Q8_0 kernels). Weights: the quant plane (bytes u = q + 128, row n at n * K) and the fp16 scale
+// plane (row n at n * ldd). Per 128-K stage, producer thread (column c = pt / 8 + 32 i, xi = pt % 8)
+// takes values 16 xi .. 16 xi + 15 of the stage: one 16-byte quant load and one 2-byte scale load
+// per column, three stages ahead (four register sets), decoded into B-tile slots 2 xi, 2 xi + 1.
+template <int NB>
+struct Ws8Lds {
+    static constexpr int BN = 32 * NB;
+    static constexpr int A = 0, A_BYTES = WS_BM * WS_KS * 2;
+    static constexpr int B = 2 * A_BYTES, B_BYTES = BN * WS_KS * 2;
+    static constexpr int PF = B + 2 * B_BYTES;  // prefetch scratch, 4 x 256 bytes (never read)
+    static constexpr int TOTAL = PF + 1024;
+    static_assert(TOTAL <= 160 * 1024, "LDS budget");
+};
+
+struct Ws8Args {
+    const uint8_t *Q;   // quant plane, bytes u = q + 128
+    const uint16_t *D;  // fp16 scale plane
+    int ldd;
+    const uint16_t *A;
+    int M, N, K;
+    void *C;
+    int c_f32, accumulate;
+    int mt, nt;
+};
+
+// 16 fp16 values fp16(q * d) from 16 stored bytes u = q + 128: fp16(1024 + u) - 1152 = q exactly,
+// then one rounding of q * d
+DEV void decode16_q8_0(const u4v q, h2 d2, h8 &lo, h8 &hi) {
+    const h2 bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    h2 v[8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        v[2 * i] = (as_h2(perm_lo(w[i])) + bias) * d2;
+        v[2 * i + 1] = (as_h2(perm_hi(w[i])) + bias) * d2;
+    }
+    lo = h8{v[0].x, v[0].y, v[1].x, v[1].y, v[2].x, v[2].y, v[3].x, v[3].y};
+    hi = h8{v[4].x, v[4].y, v[5].x, v[5].y, v[6].x, v[6].y, v[7].x, v[7].y};
+}
+
+template <int NB>
+__global__ void __launch_bounds__(WS_NT) k_gemm_q8_0_ws(Ws8Args g) {
+    constexpr int BN = 32 * NB;
+    using L = Ws8Lds<NB>;
+    __shared__ __attribute__((aligned(256))) char lds[L::TOTAL];
+    _Float16 *const sA0 = (_Float16 *)(lds + L::A);
+    _Float16 *const sB0 = (_Float16 *)(lds + L::B);
+    auto sA = [&](int h) { return sA0 + h * (L::A_BYTES / 2); };
+    auto sB = [&](int h) { return sB0 + h * (L::B_BYTES / 2); };
+    const int b = blockIdx.x, x = b & 7, j8 = b >> 3;
+    const int nt_i = x + 8 * (j8 / g.mt), mt_i = j8 % g.mt;
+    if (nt_i >= g.nt) return;
+    const int m0 = mt_i * WS_BM, n0 = nt_i * BN;
+    const int M = g.M, N = g.N, K = g.K, S2 = K / WS_KS;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const rsrc_t ra = make_rsrc(g.A, (uint32_t)((size_t)M * K * 2));
+    const rsrc_t rq = make_rsrc(g.Q, (uint32_t)((size_t)N * K));  // columns >= N read as zero
+
+    if (wave >= 4) {
+        // ------------------------------------------------------------------ producers
+        // Stage s's activation tile (LDS DMA) and decoded B tile are made in stage s - 1; the quant
+        // and scale loads of stage s + 3 are issued then too, one column's pair after each column's
+        // decode. The end-of-stage wait covers the DMAs (issued first) and everything older.
+        const int pw = __builtin_amdgcn_readfirstlane(wave - 4);
+        const int pt = tid - 256, xi = pt & 7;
+        const rsrc_t rd = make_rsrc(g.D, (uint32_t)((size_t)N * g.ldd * 2));
+        const int arow = 4 * pw + (lane >> 4);
+        const uint32_t a_voff = (uint32_t)(((m0 + arow) * K + 8 * ((lane & 15) ^ (arow & 15))) * 2);
+        auto dma_a = [&](int s, int qq) {
+            dma16(ra, sA(s & 1) + (pw + 4 * qq) * 512, a_voff, (uint32_t)(qq * 16 * K * 2 + s * WS_KS * 2));
+        };
+        uint32_t q_voff[NB], d_voff[NB];
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const uint32_t n = (uint32_t)(n0 + (pt >> 3) + 32 * i);
+            q_voff[i] = n * (uint32_t)K + 16u * (uint32_t)xi;
+            d_voff[i] = (n * (uint32_t)g.ldd + (uint32_t)(xi >> 1)) * 2u;
+        }
+        u4v Q[4][NB];
+        uint32_t D[4][NB];
+        auto load = [&](int set, int s, int i) {
+            Q[set][i] = buf_load16(rq, q_voff[i], (uint32_t)(s * WS_KS));
+            D[set][i] = __builtin_amdgcn_raw_buffer_load_b16(rd, d_voff[i], (uint32_t)(s * 8), 0);
+        };
+        const int slot0 = 2 * xi;
+        auto decode = [&](auto setc, int s) {
+            constexpr int SET = decltype(setc)::value;
+            _Float16 *dst = sB(s & 1);
+#pragma unroll
+            for (int i = 0; i < NB; i++) {
+                const uint32_t c = (uint32_t)((pt >> 3) + 32 * i), sg = c & 15u;
+                const _Float16 dh = __builtin_bit_cast(_Float16, (uint16_t)D[SET][i]);
+                h8 lo, hi;
+                decode16_q8_0(Q[SET][i], h2{dh, dh}, lo, hi);
+                *(h8 *)(dst + c * WS_KS + 8 * ((uint32_t)slot0 ^ sg)) = lo;
+                *(h8 *)(dst + c * WS_KS + 8 * ((uint32_t)(slot0 + 1) ^ sg)) = hi;
+                if (s + 3 < S2) load((SET + 3) & 3, s + 3, i);
+            }
+        };
+        auto end_stage = [&](bool loads_issued) {
+            if (loads_issued) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(2 * NB) : "memory");
+            else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+            wg_barrier();
+        };
+        using i0 = std::integral_constant<int, 0>;
+        using i1 = std::integral_constant<int, 1>;
+        using i2 = std::integral_constant<int, 2>;
+        using i3 = std::integral_constant<int, 3>;
+        // prologue: quants and scales of stages 0, 1, 2; stage 0's activation tile; decode stage 0
+#pragma unroll
+        for (int i = 0; i < NB; i++) load(0, 0, i);
+#pragma unroll
+        for (int i = 0; i < NB; i++) load(1, S2 > 1 ? 1 : 0, i);
+#pragma unroll
+        for (int i = 0; i < NB; i++) load(2, S2 > 2 ? 2 : 0, i);
+#pragma unroll
+        for (int k = 0; k < 8; k++) dma_a(0, k);
+        decode(i0{}, 0);
+        end_stage(3 < S2);
+        // stage t (consumers on stage t): make stage t + 1 (register set (t + 1) % 4)
+        auto step = [&](auto setc, int t) {
+            const int s = t + 1;
+            if (s < S2) {
+#pragma unroll
+                for (int k = 0; k < 8; k++) dma_a(s, k);
+                decode(setc, s);
+            }
+            end_stage(s + 3 < S2);
+        };
+        int t = 0;
+        for (; t + 4 <= S2; t += 4) {
+            step(i1{}, t);
+            step(i2{}, t + 1);
+            step(i3{}, t + 2);
+            step(i0{}, t + 3);
+        }
+        if (t < S2) step(i1{}, t++);
+        if (t < S2) step(i2{}, t++);
+        if (t < S2) step(i3{}, t++);
+        return;
+    }
+
+    // ---------------------------------------------------------------------- consumers
+    // k-step stream as in k_gemm_q4_k_ws: 4 main k-steps per stage, each reading the next k-step's
+    // operands while its MFMAs run; the stage barrier inside a stage's last k-step.
+    const int wm = wave & 1, wn = wave >> 1, ln = lane & 15, lg = lane >> 4;
+    const uint32_t sw0 = 16u * ((uint32_t)lg ^ (uint32_t)ln);
+    const uint32_t a_lane = (uint32_t)(uintptr_t)sA(0) + (uint32_t)((64 * wm + ln) * WS_KS * 2) + sw0;
+    const uint32_t b_lane = (uint32_t)(uintptr_t)sB(0) + (uint32_t)(((BN / 2) * wn + ln) * WS_KS * 2) + sw0;
+    using lds_h8 = const __attribute__((address_space(3))) h8;
+    auto lds_at = [](uint32_t byte) { return *(lds_h8 *)(uintptr_t)byte; };
+    auto ldA = [&](int src, int i, int f) -> h8 {
+        return lds_at((a_lane ^ (64u * f)) + src * L::A_BYTES + i * 16 * WS_KS * 2);
+    };
+    auto ldB = [&](int src, int j, int f) -> h8 {
+        return lds_at((b_lane ^ (64u * f)) + src * L::B_BYTES + j * 16 * WS_KS * 2);
+    };
+    f4 acc[4][NB];
+    h8 fa[2][4], fb[NB];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < NB; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+    constexpr int JB = NB >= 3 ? 2 : 1;
+    auto kstep = [&](auto cfg) {
+        using C = decltype(cfg);
+        constexpr int P = C::P;
+        auto read_next_a = [&]() {
+#pragma unroll
+            for (int i = 0; i < 4; i++) fa[P ^ 1][i] = ldA(C::NSRC, i, C::NF);
+        };
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            if (!C::BAR && j == 0) read_next_a();
+            if (C::BAR && j == JB) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                wg_barrier();
+                read_next_a();
+#pragma unroll
+                for (int jj = 0; jj < JB; jj++) fb[jj] = ldB(C::NSRC, jj, C::NF);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i][j] = mfma(fb[j], fa[P][i], acc[i][j]);
+            if (!(C::BAR && j < JB)) fb[j] = ldB(C::NSRC, j, C::NF);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    wg_barrier();  // stage 0 is in LDS
+#pragma unroll
+    for (int i = 0; i < 4; i++) fa[0][i] = ldA(0, i, 0);
+#pragma unroll
+    for (int j = 0; j < NB; j++) fb[j] = ldB(0, j, 0);
+    // L2 warm-up of the quants of stages t + 4, t + 5 at stage t (one 128-byte line per column and
+    // stage; the mt workgroups of an N-tile split the columns), as in k_gemm_q4_k_ws
+    const int pf_cols = (BN - mt_i + g.mt - 1) / g.mt, pf_lanes = 2 * pf_cols;
+    const uint32_t pf_lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds + L::PF) + 256u * (uint32_t)wave);
+    auto prefetch = [&](int s) {
+        for (int e0 = 64 * wave; e0 < pf_lanes; e0 += 256) {
+            const int e = e0 + lane, jc = e >> 1;
+            const int c = mt_i + g.mt * (e < pf_lanes ? jc : 0);
+            const uint32_t voff = (uint32_t)(n0 + c) * (uint32_t)K + (uint32_t)(s + (e & 1)) * WS_KS;
+            l2_touch(rq, voff, pf_lds);
+        }
+    };
+    int t = 0;
+    for (; t + 2 <= S2; t += 2) {
+        if (t + 5 < S2) prefetch(t + 4);
+        kstep(WsStep<0, 0, 0, false, 0, 1>{});
+        kstep(WsStep<1, 0, 1, false, 0, 2>{});
+        kstep(WsStep<0, 0, 2, false, 0, 3>{});
+        kstep(WsStep<1, 0, 3, true, 1, 0>{});
+        kstep(WsStep<0, 1, 0, false, 1, 1>{});
+        kstep(WsStep<1, 1, 1, false, 1, 2>{});
+        kstep(WsStep<0, 1, 2, false, 1, 3>{});
+        kstep(WsStep<1, 1, 3, true, 0, 0>{});
+    }
+    if (t < S2) {  // odd stage count: the last stage sits in buffer 0
+        kstep(WsStep<0, 0, 0, false, 0, 1>{});
+        kstep(WsStep<1, 0, 1, false, 0, 2>{});
+        kstep(WsStep<0, 0, 2, false, 0, 3>{});
+        kstep(WsStep<1, 0, 3, true, 1, 0>{});
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the prefetches
+    store_rows4<4, NB>(g.C, acc, M, N, m0 + 64 * wm, n0 + (BN / 2) * wn, ln, lg, g.c_f32, g.accumulate);
+}
 }  // namespace
 
 // Tile width for the shape: the NB (BN = 32 NB columns, NB <= 5 for the LDS budget) with the least
@@ -542,6 +772,25 @@ hipError_t hq_launch_gemm_ws(const hq_dev_mat *W, const uint16_t *A, const uint1
     case 3: k_gemm_q4_k_ws<3><<<grid, WS_NT, 0, st>>>(g); break;
     case 4: k_gemm_q4_k_ws<4><<<grid, WS_NT, 0, st>>>(g); break;
     case 5: k_gemm_q4_k_ws<5><<<grid, WS_NT, 0, st>>>(g); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t hq_launch_gemm_ws8(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
+                              int nb, hipStream_t st) {
+    if (W->cols % WS_KS) return hipErrorInvalidValue;
+    Ws8Args g;
+    g.Q = W->qs, g.D = W->d, g.ldd = W->ldd, g.A = A;
+    g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;
+    g.mt = (M + WS_BM - 1) / WS_BM;
+    g.nt = (g.N + 32 * nb - 1) / (32 * nb);
+    const unsigned grid = (unsigned)(8 * ((g.nt + 7) / 8) * g.mt);
+    switch (nb) {
+    case 2: k_gemm_q8_0_ws<2><<<grid, WS_NT, 0, st>>>(g); break;
+    case 3: k_gemm_q8_0_ws<3><<<grid, WS_NT, 0, st>>>(g); break;
+    case 4: k_gemm_q8_0_ws<4><<<grid, WS_NT, 0, st>>>(g); break;
+    case 5: k_gemm_q8_0_ws<5><<<grid, WS_NT, 0, st>>>(g); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -50,5 +50,7 @@ void hq_gemm_tile_shape(int type, int M, int N, int K, int n_cu, int *rows, int 
 int hq_ws_choose(int M, int N, int n_cu, float *eff);
 hipError_t hq_launch_gemm_ws(const hq_dev_mat *W, const uint16_t *A, const uint16_t *S, int M, void *C, int c_f32,
                              int accumulate, int nb, hipStream_t st);
+hipError_t hq_launch_gemm_ws8(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
+                              int nb, hipStream_t st);
 
 #endif

@@ -1435,7 +1435,8 @@ namespace {
 struct GemmCfg {
     int mb, nb, waves;
     bool wide;
-    int ws_nb;  // > 0: the full-K tile kernel k_gemm_q4_k_ws with 32 * ws_nb columns per tile
+    int ws_nb;   // > 0: the full-K tile kernel k_gemm_q4_k_ws with 32 * ws_nb columns per tile
+    int ws8_nb;  // > 0: the Q8_0 full-K tile kernel k_gemm_q8_0_ws, 32 * ws8_nb columns per tile
 };
 
 // Q4_K with M > 64 runs the full-K tile kernel when its tiles fit in one round on the CUs and fill
@@ -1456,6 +1457,15 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
         const long tiles = (long)((M + 127) / 128) * (((int)W->rows + 32 * nb - 1) / (32 * nb));
         if (eff >= 0.7f && tiles <= n_cu) c.ws_nb = nb;
     }
+    // Q8_0 with M > 64: the Q8_0 tile kernel when its tiles fill at least 70 % of the CU time
+    // (rounds of tiles included), K is whole 128-wide stages and the byte offsets fit 32 bits
+    c.ws8_nb = 0;
+    if (W->type == HQ_TYPE_Q8_0 && M > 64 && W->cols % 128 == 0 && (size_t)M * W->cols * 2 < ((size_t)1 << 32) &&
+        ((size_t)W->rows + 160) * W->cols < ((size_t)1 << 32)) {
+        float eff = 0.f;
+        const int nb = hq_ws_choose(M, (int)W->rows, n_cu, &eff);
+        if (eff >= 0.7f) c.ws8_nb = nb;
+    }
     return c;
 }
 
@@ -1470,16 +1480,17 @@ void hq_gemm_tile_shape(int type, int M, int N, int K, int n_cu, int *rows, int 
     W.rows = (uint32_t)N;
     W.cols = (uint32_t)K;
     const GemmCfg c = gemm_cfg(&W, M, n_cu);
-    *rows = c.ws_nb ? 128 : 16 * c.mb;
-    *cols = c.ws_nb ? 32 * c.ws_nb : 16 * c.nb * c.waves;
+    *rows = c.ws_nb || c.ws8_nb ? 128 : 16 * c.mb;
+    *cols = c.ws_nb ? 32 * c.ws_nb : c.ws8_nb ? 32 * c.ws8_nb : 16 * c.nb * c.waves;
 }
 
 void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_bytes, size_t *counter_bytes,
                         size_t *sums_bytes) {
     const GemmCfg c = gemm_cfg(W, M, n_cu);
     const SkPlan p = gemm_plan(W, M, c, n_cu);
-    *partial_bytes = c.ws_nb ? 0 : (size_t)2 * p.G * 64 * c.waves * c.mb * c.nb * 4 * sizeof(float);
-    *counter_bytes = c.ws_nb ? 0 : (size_t)p.tiles * sizeof(int);
+    const bool tile = c.ws_nb || c.ws8_nb;  // full-K tile kernels: no partial tiles
+    *partial_bytes = tile ? 0 : (size_t)2 * p.G * 64 * c.waves * c.mb * c.nb * 4 * sizeof(float);
+    *counter_bytes = tile ? 0 : (size_t)p.tiles * sizeof(int);
     *sums_bytes = c.wide ? (size_t)M * (W->cols / KC) * 32 : 0;
 }
 
@@ -1500,6 +1511,7 @@ hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, vo
                                const HqGemmWork &wk, hipStream_t st) {
     const GemmCfg c = gemm_cfg(W, M, wk.n_cu);
     if (c.ws_nb) return hq_launch_gemm_ws(W, A, wk.sums, M, C, c_f32, accumulate, c.ws_nb, st);
+    if (c.ws8_nb) return hq_launch_gemm_ws8(W, A, M, C, c_f32, accumulate, c.ws8_nb, st);
     GemmArgs g;
     g.qs = W->qs, g.d = W->d, g.ldd = W->ldd, g.row_bytes = W->row_bytes, g.A = A;
     g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;

@@ -116,9 +116,11 @@ RAGGED = [(synth.Q8_0, 100, 512, M) for M in (1, 2, 5, 17, 33, 65, 200)] + \
           (synth.Q4_K, 130, 2560, 31), (synth.Q4_K, 33, 256, 1), (synth.Q4_K, 33, 256, 20)] + \
          [(synth.Q4_K, 9500, 768, 500), (synth.Q4_K, 9728, 512, 350), (synth.Q4_K, 9728, 256, 350),
           (synth.Q4_K, 9000, 768, 1000)] + \
-         [(synth.Q4_K, 8200, 1536, 1), (synth.Q4_K, 9728, 512, 1), (synth.Q4_K, 8192, 1024, 1)]
+         [(synth.Q4_K, 8200, 1536, 1), (synth.Q4_K, 9728, 512, 1), (synth.Q4_K, 8192, 1024, 1)] + \
+         [(synth.Q8_0, 9500, 768, 500), (synth.Q8_0, 9728, 384, 512)]
 # (the last: full-K tiles; Stream-K with more tiles than CUs; the streamed GEMV with a ragged last
-# row group and an odd K split, with one wave per row group, and with an even split)
+# row group and an odd K split, with one wave per row group, and with an even split; the Q8_0 tile
+# kernel with ragged M and N, and with an odd number of 128-wide stages)
 
 
 @pytest.mark.parametrize("gtype,N,K,M", FULL + RAGGED)
@@ -136,7 +138,8 @@ def test_gemm_parity(hqlib, oracle, gtype, N, K, M):
 
 @pytest.mark.parametrize("gtype,M,N,K", [(synth.Q8_0, 1, 320, 1024), (synth.Q8_0, 48, 320, 1024),
                                          (synth.Q4_K, 1, 320, 1024), (synth.Q4_K, 48, 320, 1024),
-                                         (synth.Q4_K, 350, 9728, 256), (synth.Q4_K, 1, 8192, 1024)])
+                                         (synth.Q4_K, 350, 9728, 256), (synth.Q4_K, 1, 8192, 1024),
+                                         (synth.Q8_0, 512, 9728, 640)])
 def test_gemm_accumulate_and_fp16_output(hqlib, oracle, gtype, M, N, K):
     blocks = weights(gtype, N, K, 7)
     rng = synth.Rng(77 + M)
