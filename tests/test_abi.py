@@ -77,11 +77,18 @@ def test_gemm_tile_selection():
                 # Q4_K above M = 64: full-K tiles of 128 x 32NB when they fill the CUs, else the
                 # 8-wave Stream-K kernel (128 x 256)
                 assert (r, c) == (128, 256) or (r == 128 and c in (64, 96, 128, 160))
+            elif gtype == synth.Q8_0 and M > 64:
+                # Q8_0 above M = 64: full-K tiles of 128 x 32NB when they fill >= 70 % of the CU
+                # time (any number of rounds), else the narrow Stream-K kernel
+                assert c == 128 or (r == 128 and c in (64, 96, 128, 160))
             else:
                 assert c == 128
-    # Stream-K balances any tile count over the CUs (Q8_0, narrow Q4_K, few Q4_K tiles)
-    assert hq.gemm_tiles(synth.Q8_0, 512, 9728) == (128, 128)
+    # Stream-K balances any tile count over the CUs (narrow Q8_0 / Q4_K, few Q4_K tiles)
+    assert hq.gemm_tiles(synth.Q8_0, 128, 9728) == (128, 128)
     assert hq.gemm_tiles(synth.Q4_K, 2, 9728) == (32, 128)
+    # Q8_0 full-K tiles: 4 x 61 tiles of 128 x 160 at M = 512, 16 x 61 (four rounds) at M = 2048
+    assert hq.gemm_tiles(synth.Q8_0, 512, 9728) == (128, 160)
+    assert hq.gemm_tiles(synth.Q8_0, 2048, 9728) == (128, 160)
     assert hq.gemm_tiles(synth.Q4_K, 65, 9728) == (128, 256)
     # full-K tiles: 4 x 61 tiles of 128 x 160 on 256 CUs; more tiles than CUs: Stream-K
     assert hq.gemm_tiles(synth.Q4_K, 512, 9728) == (128, 160)
