@@ -65,16 +65,10 @@ def read_traffic(name, kernel):
     return None
 
 
-def main_kernel_name(hq, gtype, M, N):
-    """Name of the GEMM main kernel hq_gemm dispatches for this shape (as rocprofv3 lists it)."""
-    import synth
-    rows, cols = hq.gemm_tiles(gtype, M, N)
-    if gtype == synth.Q4_K and M > 64:
-        return "k_gemm_q4_k_w<8>" if cols == 256 else f"k_gemm_q4_k_ws<{cols // 32}>"
-    if gtype == synth.Q8_0 and rows == 128:
-        return f"k_gemm_q8_0_ws<{cols // 32}>"
-    mb = rows // 16
-    return f"k_gemm_q8_0<{mb}, 2>" if gtype == synth.Q8_0 else f"k_gemm_q4_k<{mb}, 2>"
+def main_kernel_name(hq, gtype, M, N, K):
+    """Name of the kernel hq_gemm dispatches for this shape (the main kernel where a pre-pass runs
+    first), as rocprofv3 lists it."""
+    return hq.gemm_kernel(gtype, M, N, K)
 
 
 def bench_gemm(hq, synth, gtype, N, K, M, c_f32, steps, warmup, stream, eager_warmup=True, kernel_time=False,
@@ -219,7 +213,7 @@ def main():
         t, m, n, k = args.shape.split(":")
         g = {"q8_0": synth.Q8_0, "q4_k": synth.Q4_K}[t]
         r = bench_gemm(hq, synth, g, int(n), int(k), int(m), False, args.steps, args.warmup, stream, settle_s=0.2)
-        log("shape", main_kernel_name(hq, g, int(m), int(n)), r)
+        log("shape", main_kernel_name(hq, g, int(m), int(n), int(k)), r)
         return
     if args.gemv_only:
         for g, n, k in [(synth.Q8_0, 9728, 2560), (synth.Q4_K, 9728, 2560), (synth.Q4_K, 2560, 9728)]:
@@ -256,7 +250,7 @@ def main():
         sweep.append(r)
 
     kt = head["kernel_tflops"]
-    kname = main_kernel_name(hq, gtype, M, N)
+    kname = main_kernel_name(hq, gtype, M, N, K)
     roofline = dict(bound="mfma", achieved=round(kt, 3), peak=PEAK_TFLOPS, unit="TFLOP/s",
                     frac=round(kt / PEAK_TFLOPS, 4), traffic=read_traffic("q4_k_gemm_m512_k2560_n9728", kname),
                     kernel=kname, kernel_us=round(head["kernel_us"], 3))

@@ -409,6 +409,11 @@ extern "C" int hq_device_synchronize(void) {
     return 0;
 }
 
+extern "C" void hq_gemm_kernel(int ggml_type, int M, int N, int K, char *name, int name_bytes) {
+    if (!name || name_bytes <= 0) return;
+    hq_gemm_kernel_name(ggml_type, M, N, K, 256, name, (size_t)name_bytes);
+}
+
 extern "C" void hq_gemm_tiles(int ggml_type, int M, int N, int *rows_per_tile, int *cols_per_tile) {
     (void)N;
     int r = 1, c = 16;

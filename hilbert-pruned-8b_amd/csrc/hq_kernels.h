@@ -45,6 +45,7 @@ hipError_t hq_launch_gather(const hq_dev_mat *W, const uint16_t *H, const uint32
 hipError_t hq_launch_f32_to_f16(const float *in, uint16_t *out, size_t n, hipStream_t st);
 // rows x columns of one GEMM output tile (M >= 2) on a device with n_cu CUs
 void hq_gemm_tile_shape(int type, int M, int N, int K, int n_cu, int *rows, int *cols);
+void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, size_t n);
 // Full-K tile Q4_K GEMM (hq_gemm_ws.hip): the tile width (32 * nb columns) for an M x N problem on
 // n_cu CUs and the fraction of CU time its tiles fill; the launch (S = k_asums output for A).
 int hq_ws_choose(int M, int N, int n_cu, float *eff);

@@ -24,6 +24,7 @@
 //       no weight value is ever rounded to 16 bits.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <cstdio>
 
 #include "hq_device.h"
 #include "hq_kernels.h"
@@ -1348,48 +1349,60 @@ static void launch_gemv_t(const hq_dev_mat *W, const uint16_t *a, void *C, int c
 
 // Rows per wave: 2 (activations reused twice; measured best of 1, 2, 4 at N = 9728), 1 when that
 // would leave the grid short of about two workgroups per CU.
-hipError_t hq_launch_gemv(const hq_dev_mat *W, const uint16_t *a, void *C, int c_f32, int accumulate, hipStream_t st) {
-    if (W->type == HQ_TYPE_Q4_K && W->cols % 512 == 0 && W->rows >= 8 * 1024 &&
-        ((size_t)W->rows + 8) * W->row_bytes < ((size_t)1 << 32)) {
-        // streamed kernel when there are at least 1024 groups of 8 rows: two waves per group, each
-        // half of K (measured at N = 9728, K = 2560: 6.55 us against 6.8 for the slab kernel and
-        // 7.1 with one wave per group); fewer rows go to the slab kernel, whose 4-wave workgroups
-        // fill the CUs better there (N = 2560, K = 9728: 7.5 us against 8.3)
-        const int N = (int)W->rows, K = (int)W->cols, pairs = K / 512, S = pairs >= 2 ? 2 : 1;
-        constexpr int NS = 4;
-        const size_t lds = (size_t)K * 2 + (size_t)K / 32 * 4 + 32 * (size_t)S + (size_t)S * NS * GVR_SLOT;
-        if (lds <= 64 * 1024) {
-            k_gemv_q4_k_r<NS><<<(N + 7) / 8, 64 * S, lds, st>>>(W->qs, (uint32_t)W->row_bytes, a, N, K, C, c_f32,
-                                                                accumulate);
-            return hipGetLastError();
-        }
+// GEMV kernel choice for a matrix (shared by the launcher and the diagnostics name).
+//   streamed Q4_K kernel when there are at least 1024 groups of 8 rows: two waves per group, each
+//   half of K (measured at N = 9728, K = 2560: 6.55 us against 6.8 for the slab kernel and 7.1 with
+//   one wave per group); fewer rows go to the slab kernel, whose 4-wave workgroups fill the CUs
+//   better there (N = 2560, K = 9728: 7.5 us against 8.3). Slab: the most rows per workgroup (up to
+//   32) that still give at least 512 workgroups (two per CU) and fit the slab, activations and sums
+//   in 64 KB of LDS. Byte offsets are 32-bit up to the end of the last, possibly partial, group.
+struct GemvPlan {
+    enum Kind { Q4K_STREAM, Q4K_SLAB, REG } kind;
+    int r;  // waves per group (stream), rows per workgroup (slab), rows per wave (register kernels)
+    size_t lds;
+};
+constexpr int GVR_NS = 4;  // stream ring depth
+
+static GemvPlan gemv_plan(const hq_dev_mat *W) {
+    const size_t N = W->rows, K = W->cols, rb = W->row_bytes;
+    if (W->type == HQ_TYPE_Q4_K && K % 512 == 0 && N >= 8 * 1024 && (N + 8) * rb < ((size_t)1 << 32)) {
+        const int S = K / 512 >= 2 ? 2 : 1;
+        const size_t lds = K * 2 + K / 32 * 4 + 32 * (size_t)S + (size_t)S * GVR_NS * GVR_SLOT;
+        if (lds <= 64 * 1024) return {GemvPlan::Q4K_STREAM, S, lds};
     }
-    if (W->type == HQ_TYPE_Q4_K && ((size_t)W->rows + 32) * W->row_bytes < ((size_t)1 << 32)) {
-        // LDS-slab kernel (32-bit byte offsets up to the end of the last, possibly partial, slab): the most rows per workgroup (up to 32) that still give at least 512
-        // workgroups (two per CU) and fit the slab, activations and sums in 64 KB of LDS
-        const int N = (int)W->rows, K = (int)W->cols;
-        const size_t fixed = (size_t)K * 2 + (size_t)K / 32 * 4;
+    if (W->type == HQ_TYPE_Q4_K && (N + 32) * rb < ((size_t)1 << 32)) {
+        const size_t fixed = K * 2 + K / 32 * 4;
         int R = 32;
-        while (R > 1 && ((N + R - 1) / R < 512 || fixed + (size_t)R * (W->row_bytes + 16) > 64 * 1024)) R >>= 1;
-        const size_t lds = fixed + (size_t)R * (W->row_bytes + 16);
-        if (lds <= 64 * 1024) {
-            const unsigned g = (unsigned)((N + R - 1) / R);
-            const uint32_t rb = (uint32_t)W->row_bytes;
-#define GVS(r) k_gemv_q4_k_s<r><<<g, 256, lds, st>>>(W->qs, rb, a, N, K, C, c_f32, accumulate)
-            switch (R) {
-            case 32: GVS(32); break;
-            case 16: GVS(16); break;
-            case 8: GVS(8); break;
-            case 4: GVS(4); break;
-            case 2: GVS(2); break;
-            default: GVS(1); break;
-            }
-#undef GVS
-            return hipGetLastError();
-        }
+        while (R > 1 && ((N + R - 1) / R < 512 || fixed + (size_t)R * (rb + 16) > 64 * 1024)) R >>= 1;
+        const size_t lds = fixed + (size_t)R * (rb + 16);
+        if (lds <= 64 * 1024) return {GemvPlan::Q4K_SLAB, R, lds};
     }
-    if (W->rows >= 4096) launch_gemv_t<2>(W, a, C, c_f32, accumulate, st);
-    else launch_gemv_t<1>(W, a, C, c_f32, accumulate, st);
+    return {GemvPlan::REG, N >= 4096 ? 2 : 1, 0};
+}
+
+hipError_t hq_launch_gemv(const hq_dev_mat *W, const uint16_t *a, void *C, int c_f32, int accumulate, hipStream_t st) {
+    const GemvPlan pl = gemv_plan(W);
+    const int N = (int)W->rows, K = (int)W->cols;
+    const uint32_t rb = (uint32_t)W->row_bytes;
+    if (pl.kind == GemvPlan::Q4K_STREAM) {
+        k_gemv_q4_k_r<GVR_NS><<<(N + 7) / 8, 64 * pl.r, pl.lds, st>>>(W->qs, rb, a, N, K, C, c_f32, accumulate);
+    } else if (pl.kind == GemvPlan::Q4K_SLAB) {
+        const unsigned g = (unsigned)((N + pl.r - 1) / pl.r);
+#define GVS(r) k_gemv_q4_k_s<r><<<g, 256, pl.lds, st>>>(W->qs, rb, a, N, K, C, c_f32, accumulate)
+        switch (pl.r) {
+        case 32: GVS(32); break;
+        case 16: GVS(16); break;
+        case 8: GVS(8); break;
+        case 4: GVS(4); break;
+        case 2: GVS(2); break;
+        default: GVS(1); break;
+        }
+#undef GVS
+    } else if (pl.r == 2) {
+        launch_gemv_t<2>(W, a, C, c_f32, accumulate, st);
+    } else {
+        launch_gemv_t<1>(W, a, C, c_f32, accumulate, st);
+    }
     return hipGetLastError();
 }
 
@@ -1482,6 +1495,28 @@ void hq_gemm_tile_shape(int type, int M, int N, int K, int n_cu, int *rows, int 
     const GemmCfg c = gemm_cfg(&W, M, n_cu);
     *rows = c.ws_nb || c.ws8_nb ? 128 : 16 * c.mb;
     *cols = c.ws_nb ? 32 * c.ws_nb : c.ws8_nb ? 32 * c.ws8_nb : 16 * c.nb * c.waves;
+}
+
+// Name of the kernel that does the work of an M x N x K hq_gemm call (the main kernel for GEMMs
+// with a pre-pass), as rocprofv3 lists it.
+void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, size_t n) {
+    hq_dev_mat W = {};
+    W.type = type;
+    W.rows = (uint32_t)N;
+    W.cols = (uint32_t)K;
+    W.row_bytes = type == HQ_TYPE_Q4_K ? (size_t)K / 256 * 144 : (size_t)K;
+    if (M == 1) {
+        const GemvPlan pl = gemv_plan(&W);
+        if (pl.kind == GemvPlan::Q4K_STREAM) snprintf(buf, n, "k_gemv_q4_k_r<%d>", GVR_NS);
+        else if (pl.kind == GemvPlan::Q4K_SLAB) snprintf(buf, n, "k_gemv_q4_k_s<%d>", pl.r);
+        else snprintf(buf, n, "%s<%d>", type == HQ_TYPE_Q4_K ? "k_gemv_q4_k" : "k_gemv_q8_0", pl.r);
+        return;
+    }
+    const GemmCfg c = gemm_cfg(&W, M, n_cu);
+    if (c.ws_nb) snprintf(buf, n, "k_gemm_q4_k_ws<%d>", c.ws_nb);
+    else if (c.ws8_nb) snprintf(buf, n, "k_gemm_q8_0_ws<%d>", c.ws8_nb);
+    else if (c.wide) snprintf(buf, n, "k_gemm_q4_k_w<%d>", WNW);
+    else snprintf(buf, n, "%s<%d, %d>", type == HQ_TYPE_Q4_K ? "k_gemm_q4_k" : "k_gemm_q8_0", c.mb, c.nb);
 }
 
 void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_bytes, size_t *counter_bytes,

@@ -23,7 +23,7 @@ EXPORTS = (
     "hq_gather_dot", "hq_gather_dot_dev", "hq_matmul_host", "hq_malloc", "hq_free", "hq_memcpy_h2d",
     "hq_memcpy_d2h", "hq_memcpy_d2d", "hq_memset", "hq_stream_create", "hq_stream_destroy", "hq_stream_synchronize",
     "hq_device_synchronize", "hq_time_gemm", "hq_time_gemm_kernel", "hq_time_gather", "hq_gemm_tiles", "hq_llama_forward",
-    "hq_embed_f32",
+    "hq_embed_f32", "hq_gemm_kernel",
 )
 
 
@@ -91,6 +91,7 @@ def load(path=LIB_PATH):
         "hq_time_gemm_kernel": (i, [C.POINTER(vp), i, vp, i, vp, i, i, i, vp, C.POINTER(C.c_float)]),
         "hq_time_gather": (i, [C.POINTER(vp), i, vp, vp, i, i, i, vp, i, i, vp, C.POINTER(C.c_float)]),
         "hq_gemm_tiles": (None, [i, i, i, C.POINTER(i), C.POINTER(i)]),
+        "hq_gemm_kernel": (None, [i, i, i, i, C.c_char_p, i]),
         "hq_llama_forward": (i, [C.POINTER(Llama), vp, sz, vp, u32, vp]),
         "hq_embed_f32": (i, [vp, vp, i, vp, vp]),
     }
@@ -274,6 +275,13 @@ def gemm_tiles(gtype, M, N):
     r, c = C.c_int(), C.c_int()
     load().hq_gemm_tiles(gtype, M, N, C.byref(r), C.byref(c))
     return r.value, c.value
+
+
+def gemm_kernel(gtype, M, N, K):
+    """Name of the kernel that does the work of an M x N x K hq_gemm (as rocprofv3 lists it)."""
+    buf = C.create_string_buffer(64)
+    load().hq_gemm_kernel(gtype, M, N, K, buf, 64)
+    return buf.value.decode()
 
 
 class Stream:

@@ -122,6 +122,11 @@ int hq_time_gather(hq_mat *const *Ws, int n_w, const uint16_t *H, const uint32_t
  * (diagnostics; the launch itself sizes for the device's CU count). */
 void hq_gemm_tiles(int ggml_type, int M, int N, int *rows_per_tile, int *cols_per_tile);
 
+/* Name of the kernel that does the work of an M x N x K hq_gemm call on a 256-CU MI355X (the main
+ * kernel where a pre-pass runs first), as rocprofv3 lists it; NUL-terminated, truncated to
+ * name_bytes (diagnostics for profiling). */
+void hq_gemm_kernel(int ggml_type, int M, int N, int K, char *name, int name_bytes);
+
 #ifdef __cplusplus
 }
 #endif
