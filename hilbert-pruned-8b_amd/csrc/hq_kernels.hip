@@ -1515,7 +1515,7 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
     const GemmCfg c = gemm_cfg(&W, M, n_cu);
     if (c.ws_nb) snprintf(buf, n, "k_gemm_q4_k_ws<%d>", c.ws_nb);
     else if (c.ws8_nb) snprintf(buf, n, "k_gemm_q8_0_ws<%d>", c.ws8_nb);
-    else if (c.wide) snprintf(buf, n, "k_gemm_q4_k_w<%d>", WNW);
+    else if (c.wide) snprintf(buf, n, "k_gemm_q4_k_w<%d>", c.mb);  // template argument: row blocks
     else snprintf(buf, n, "%s<%d, %d>", type == HQ_TYPE_Q4_K ? "k_gemm_q4_k" : "k_gemm_q8_0", c.mb, c.nb);
 }
 

@@ -65,6 +65,19 @@ def test_upload_rejects_bad_descriptors_before_touching_a_device(dtype, gtype, r
     assert h.value is None
 
 
+def test_gemm_kernel_names():
+    """hq_gemm_kernel names the kernel the launch plan picks (the names rocprofv3 lists)."""
+    cases = {(synth.Q4_K, 512, 9728, 2560): "k_gemm_q4_k_ws<5>", (synth.Q8_0, 512, 9728, 2560): "k_gemm_q8_0_ws<5>",
+             (synth.Q8_0, 2048, 9728, 2560): "k_gemm_q8_0_ws<5>", (synth.Q8_0, 128, 9728, 2560): "k_gemm_q8_0<8, 2>",
+             (synth.Q4_K, 4096, 9728, 2560): "k_gemm_q4_k_w<8>", (synth.Q4_K, 64, 9728, 2560): "k_gemm_q4_k<4, 2>",
+             (synth.Q8_0, 16, 9728, 2560): "k_gemm_q8_0<1, 2>", (synth.Q4_K, 1, 9728, 2560): "k_gemv_q4_k_r<4>",
+             (synth.Q4_K, 1, 2560, 9728): "k_gemv_q4_k_s<4>", (synth.Q4_K, 1, 100, 512): "k_gemv_q4_k_s<1>",
+             (synth.Q4_K, 1, 9728, 256): "k_gemv_q4_k_s<16>", (synth.Q8_0, 1, 9728, 2560): "k_gemv_q8_0<2>",
+             (synth.Q8_0, 1, 100, 512): "k_gemv_q8_0<1>"}
+    for (gtype, M, N, K), name in cases.items():
+        assert hq.gemm_kernel(gtype, M, N, K) == name, (gtype, M, N, K)
+
+
 def test_gemm_tile_selection():
     # every M from 1 to 4096 gets a tile; M = 1 is the GEMV
     for gtype in (synth.Q8_0, synth.Q4_K):
