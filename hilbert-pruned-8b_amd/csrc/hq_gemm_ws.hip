@@ -94,37 +94,51 @@ DEV h8 decode8(u2v q, h2 mul, h2 add) {
     return h8{v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
 }
 
-// Output block (i, j) of a consumer wave: lane (ln, lg) holds C[r0 + 16i + ln][c0 + 16j + 4lg + e]
-// in register e. Stored as one 8-byte (fp16) or 16-byte (fp32) access when the 4 columns lie inside
-// C and are aligned for it (N % 4 == 0 and C aligned to the access), else element by element (same
-// values and roundings either way).
-template <int MB, int NB>
-DEV void store_rows4(void *C, const f4 (&acc)[MB][NB], int M, int N, int r0, int c0, int ln, int lg, int c_f32,
-                     int accumulate) {
-    const bool wide = (N & 3) == 0 && ((uintptr_t)C & (c_f32 ? 15u : 7u)) == 0;
+// Epilogue through LDS. The output leaves the consumers' MFMA layout (lane (ln, lg) of block (i, j):
+// row 16i + ln, 4 consecutive columns) as 16-byte pieces of 16 rows, which the memory system writes
+// as partial lines; instead the consumers park the fp32 tile in LDS (rows padded by 4 floats against
+// bank conflicts; the stage buffers are free once the main loop is done) and all 512 threads store
+// it as whole row segments, 8 values per thread and access.
+template <int NB>
+DEV void ws_tile_to_lds(char *lds, const f4 (&acc)[4][NB], int wm, int wn, int ln, int lg) {
+    constexpr int BN = 32 * NB, LD = BN + 4;
 #pragma unroll
-    for (int i = 0; i < MB; i++) {
-        const int m = r0 + 16 * i + ln;
-        if (m >= M) continue;
+    for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < NB; j++) {
-            const int n = c0 + 16 * j + 4 * lg;
-            if (n >= N) continue;
-            const f4 y = acc[i][j];
-            const size_t idx = (size_t)m * N + n;
-            if (wide) {
-                if (c_f32) {
-                    f4 *c = (f4 *)((float *)C + idx);
-                    *c = accumulate ? *c + y : y;
-                } else {
-                    h4 *c = (h4 *)((_Float16 *)C + idx);
-                    *c = __builtin_convertvector(accumulate ? __builtin_convertvector(*c, f4) + y : y, h4);
-                }
+            const int r = 64 * wm + 16 * i + ln, c = (BN / 2) * wn + 16 * j + 4 * lg;
+            *(f4 *)(lds + (r * LD + c) * 4) = acc[i][j];
+        }
+}
+
+template <int NB>
+DEV void ws_lds_to_c(const char *lds, void *C, int M, int N, int m0, int n0, int c_f32, int accumulate) {
+    constexpr int BN = 32 * NB, LD = BN + 4, CH = BN / 8;
+    const bool wide = (N & 7) == 0 && ((uintptr_t)C & 15u) == 0;
+    for (int c = threadIdx.x; c < WS_BM * CH; c += WS_NT) {
+        const int row = c / CH, ch = c - row * CH, m = m0 + row, n = n0 + 8 * ch;
+        if (m >= M || n >= N) continue;
+        const f4 v0 = *(const f4 *)(lds + (row * LD + 8 * ch) * 4), v1 = *(const f4 *)(lds + (row * LD + 8 * ch + 4) * 4);
+        const size_t idx = (size_t)m * N + n;
+        if (wide && n + 8 <= N) {
+            if (c_f32) {
+                f4 *p = (f4 *)((float *)C + idx);
+                p[0] = accumulate ? p[0] + v0 : v0;
+                p[1] = accumulate ? p[1] + v1 : v1;
             } else {
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    if (n + e < N) store_out(C, idx + e, y[e], c_f32, accumulate);
+                h8 *p = (h8 *)((_Float16 *)C + idx);
+                f4 a0 = v0, a1 = v1;
+                if (accumulate) {
+                    const h8 o = *p;
+                    a0 += f4{(float)o[0], (float)o[1], (float)o[2], (float)o[3]};
+                    a1 += f4{(float)o[4], (float)o[5], (float)o[6], (float)o[7]};
+                }
+                *p = h8{(_Float16)a0.x, (_Float16)a0.y, (_Float16)a0.z, (_Float16)a0.w,
+                        (_Float16)a1.x, (_Float16)a1.y, (_Float16)a1.z, (_Float16)a1.w};
             }
+        } else {
+            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            for (int e = 0; e < 8 && n + e < N; e++) store_out(C, idx + e, v[e], c_f32, accumulate);
         }
     }
 }
@@ -368,6 +382,8 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
         }
         if (u < U) unit(i0{}, u);
         wg_barrier();  // the last stage's barrier
+        wg_barrier();  // the consumers' output tile is in LDS
+        ws_lds_to_c<NB>(lds, g.C, M, N, m0, n0, g.c_f32, g.accumulate);
         return;
     }
 
@@ -501,9 +517,10 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[i][j] *= cl;
     }
-    // Output: lane (ln, lg) of block (i, j) holds row 16i + ln, 4 consecutive columns: one 8-byte
-    // (fp16) or 16-byte (fp32) store per block when the 4 columns are inside C and aligned.
-    store_rows4<4, NB>(g.C, acc, M, N, m0 + 64 * wm, n0 + (BN / 2) * wn, ln, lg, g.c_f32, g.accumulate);
+    ws_tile_to_lds<NB>(lds, acc, wm, wn, ln, lg);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    wg_barrier();
+    ws_lds_to_c<NB>(lds, g.C, M, N, m0, n0, g.c_f32, g.accumulate);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -649,6 +666,8 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q8_0_ws(Ws8Args g) {
         if (t < S2) step(i1{}, t++);
         if (t < S2) step(i2{}, t++);
         if (t < S2) step(i3{}, t++);
+        wg_barrier();  // the consumers' output tile is in LDS
+        ws_lds_to_c<NB>(lds, g.C, M, N, m0, n0, g.c_f32, g.accumulate);
         return;
     }
 
@@ -733,7 +752,10 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q8_0_ws(Ws8Args g) {
         kstep(WsStep<1, 0, 3, true, 1, 0>{});
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the prefetches
-    store_rows4<4, NB>(g.C, acc, M, N, m0 + 64 * wm, n0 + (BN / 2) * wn, ln, lg, g.c_f32, g.accumulate);
+    ws_tile_to_lds<NB>(lds, acc, wm, wn, ln, lg);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    wg_barrier();
+    ws_lds_to_c<NB>(lds, g.C, M, N, m0, n0, g.c_f32, g.accumulate);
 }
 }  // namespace
 
