@@ -332,19 +332,19 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
         using i0 = std::integral_constant<int, 0>;
         using i1 = std::integral_constant<int, 1>;
         const int S2 = 2 * U;  // stages
-        // prologue, phase 1: headers of units 0 and 1 and stage 0's quants; unit 0's scale words and
-        // min-term operands (written before any LDS DMA is in flight: the compiler waits for all
-        // outstanding DMAs before an LDS access); stage 0's activation tile, unit 0's S tile, the
-        // quants of stages 1 and 2, the header of unit 2
+        // prologue, phase 1: headers of units 0 and 1, stage 0's quants, stage 0's activation tile and
+        // unit 0's S tile, all in flight together (the compiler waits for the outstanding DMAs before
+        // the LDS writes that follow, so they cost one memory latency, not two); unit 0's scale words
+        // and min-term operands; the quants of stages 1 and 2, the header of unit 2
         load_hdr(H[0], 0);
         load_hdr(H[1], U > 1 ? 1 : 0);
 #pragma unroll
         for (int i = 0; i < NB; i++) load_q(Q[0], 0, i);
-        write_scales(H[0], 0);
-        write_min(H[0]);
 #pragma unroll
         for (int k = 0; k < 8; k++) dma_a(0, k);
         dma_s(0);
+        write_scales(H[0], 0);
+        write_min(H[0]);
 #pragma unroll
         for (int i = 0; i < NB; i++) load_q(Q[1], 1, i);
 #pragma unroll
