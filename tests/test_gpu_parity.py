@@ -139,7 +139,8 @@ def test_gemm_parity(hqlib, oracle, gtype, N, K, M):
 @pytest.mark.parametrize("gtype,M,N,K", [(synth.Q8_0, 1, 320, 1024), (synth.Q8_0, 48, 320, 1024),
                                          (synth.Q4_K, 1, 320, 1024), (synth.Q4_K, 48, 320, 1024),
                                          (synth.Q4_K, 350, 9728, 256), (synth.Q4_K, 1, 8192, 1024),
-                                         (synth.Q8_0, 512, 9728, 640)])
+                                         (synth.Q8_0, 512, 9728, 640), (synth.Q4_K, 512, 9728, 2560),
+                                         (synth.Q8_0, 512, 9500, 2560)])
 def test_gemm_accumulate_and_fp16_output(hqlib, oracle, gtype, M, N, K):
     blocks = weights(gtype, N, K, 7)
     rng = synth.Rng(77 + M)
