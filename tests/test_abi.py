@@ -68,7 +68,8 @@ def test_upload_rejects_bad_descriptors_before_touching_a_device(dtype, gtype, r
 def test_gemm_kernel_names():
     """hq_gemm_kernel names the kernel the launch plan picks (the names rocprofv3 lists)."""
     cases = {(synth.Q4_K, 512, 9728, 2560): "k_gemm_q4_k_ws<5>", (synth.Q8_0, 512, 9728, 2560): "k_gemm_q8_0_ws<5>",
-             (synth.Q8_0, 2048, 9728, 2560): "k_gemm_q8_0_ws<5>", (synth.Q8_0, 128, 9728, 2560): "k_gemm_q8_0<8, 2>",
+             (synth.Q8_0, 2048, 9728, 2560): "k_gemm_q8_0_ws<5>", (synth.Q8_0, 128, 9728, 2560): "k_gemm_q8_0_ws<2>",
+             (synth.Q8_0, 65, 9728, 2560): "k_gemm_q8_0<8, 2>",
              (synth.Q4_K, 4096, 9728, 2560): "k_gemm_q4_k_w<8>", (synth.Q4_K, 64, 9728, 2560): "k_gemm_q4_k<4, 2>",
              (synth.Q8_0, 16, 9728, 2560): "k_gemm_q8_0<1, 2>", (synth.Q4_K, 1, 9728, 2560): "k_gemv_q4_k_r<4>",
              (synth.Q4_K, 1, 2560, 9728): "k_gemv_q4_k_s<4>", (synth.Q4_K, 1, 100, 512): "k_gemv_q4_k_s<1>",
@@ -91,13 +92,14 @@ def test_gemm_tile_selection():
                 # 8-wave Stream-K kernel (128 x 256)
                 assert (r, c) == (128, 256) or (r == 128 and c in (64, 96, 128, 160))
             elif gtype == synth.Q8_0 and M > 64:
-                # Q8_0 above M = 64: full-K tiles of 128 x 32NB when they fill >= 70 % of the CU
+                # Q8_0 above M = 64: full-K tiles of 128 x 32NB when they fill >= 50 % of the CU
                 # time (any number of rounds), else the narrow Stream-K kernel
                 assert c == 128 or (r == 128 and c in (64, 96, 128, 160))
             else:
                 assert c == 128
     # Stream-K balances any tile count over the CUs (narrow Q8_0 / Q4_K, few Q4_K tiles)
-    assert hq.gemm_tiles(synth.Q8_0, 128, 9728) == (128, 128)
+    assert hq.gemm_tiles(synth.Q8_0, 65, 9728) == (128, 128)
+    assert hq.gemm_tiles(synth.Q8_0, 128, 9728) == (128, 64)
     assert hq.gemm_tiles(synth.Q4_K, 2, 9728) == (32, 128)
     # Q8_0 full-K tiles: 4 x 61 tiles of 128 x 160 at M = 512, 16 x 61 (four rounds) at M = 2048
     assert hq.gemm_tiles(synth.Q8_0, 512, 9728) == (128, 160)
