@@ -86,6 +86,19 @@ DEV void wait_vmcnt(int n) {
     }
 }
 
+// Partial tiles are written and read with device-scope (sc1) buffer accesses: they go to the
+// cross-XCD coherent level, so no L2 write-back or invalidation is needed, and unlike atomics they
+// are not serialized, so a 16-byte access per (row block, column block) is in flight at once.
+constexpr int CPOL_SC1 = 16;
+
+DEV void buf_store16(rsrc_t r, f4 v, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, v), r, voff, soff, CPOL_SC1);
+}
+
+DEV f4 buf_load16_sc1(rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, CPOL_SC1));
+}
+
 DEV u4v buf_load16(rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }

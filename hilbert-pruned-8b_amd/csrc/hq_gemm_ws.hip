@@ -56,6 +56,12 @@ struct WsArgs {
     void *C;
     int c_f32, accumulate;
     int mt, nt;  // M-tiles, N-tiles
+    // K split: each tile's super-blocks are cut into `parts` contiguous ranges, one workgroup each;
+    // with parts > 1 every part stores its fp32 tile in partials[tile][part] and the last to arrive
+    // (per-tile counter, left at zero) sums them in part order and writes C
+    int parts;
+    float *partials;
+    int *counters;
 };
 
 // Workgroup barrier without a memory fence: each role waits for exactly the memory operations the
@@ -143,6 +149,92 @@ DEV void ws_lds_to_c(const char *lds, void *C, int M, int N, int m0, int n0, int
     }
 }
 
+// A K-split tile's end (parts > 1, at most 4): every part stores its fp32 tile (in LDS: rows padded
+// by 4 floats) to partials[tile][part] with device-scope 16-byte stores, waits for them, and counts
+// itself in; the last of the tile's parts loads the others' (device scope) and adds all of them in
+// part order (its own from LDS in its place), so the sum is the same whichever part arrives last,
+// then writes C. flag: an LDS word.
+template <int NB>
+DEV void ws_finish(const char *lds, const WsArgs &g, int m0, int n0, int tile, int part, int *flag) {
+    if (g.parts == 1) {
+        ws_lds_to_c<NB>(lds, g.C, g.M, g.N, m0, n0, g.c_f32, g.accumulate);
+        return;
+    }
+    constexpr int BN = 32 * NB, LD = BN + 4, CH = BN / 8;
+    constexpr uint32_t TILE = WS_BM * BN * 4;  // bytes per partial tile
+    const rsrc_t rp = make_rsrc(g.partials, (uint32_t)g.mt * (uint32_t)g.nt * (uint32_t)g.parts * TILE);
+    const uint32_t own = ((uint32_t)tile * (uint32_t)g.parts + (uint32_t)part) * TILE;
+#pragma unroll
+    for (int i = 0; i < NB; i++) {
+        const int c = (int)threadIdx.x + WS_NT * i, row = c / CH, ch = c - row * CH;
+        const uint32_t off = (uint32_t)(row * BN + 8 * ch) * 4u;
+        buf_store16(rp, *(const f4 *)(lds + (row * LD + 8 * ch) * 4), off, own);
+        buf_store16(rp, *(const f4 *)(lds + (row * LD + 8 * ch + 4) * 4), off + 16u, own);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int last = atomicAdd(&g.counters[tile], 1) == g.parts - 1;
+        if (last) atomicExch(&g.counters[tile], 0);
+        *flag = last;
+    }
+    __syncthreads();
+    if (!*flag) return;
+    // thread t takes chunks t + 512 i (i < NB) of 8 values; every other part's pieces are loaded at
+    // once (one memory round trip), this part's own come from LDS
+    const int M = g.M, N = g.N;
+    const bool wide = (N & 7) == 0 && ((uintptr_t)g.C & 15u) == 0;
+    static_assert(WS_BM * CH == NB * WS_NT, "chunks per thread");
+    f4 pv[4][NB][2];
+#pragma unroll
+    for (int p = 0; p < 4; p++)
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const int c = (int)threadIdx.x + WS_NT * i, row = c / CH, ch = c - row * CH;
+            const uint32_t off = (uint32_t)(row * BN + 8 * ch) * 4u;
+            const uint32_t pb = ((uint32_t)tile * (uint32_t)g.parts + (uint32_t)p) * TILE;
+            if (p < g.parts && p != part) {
+                pv[p][i][0] = buf_load16_sc1(rp, off, pb);
+                pv[p][i][1] = buf_load16_sc1(rp, off + 16u, pb);
+            } else {
+                pv[p][i][0] = *(const f4 *)(lds + (row * LD + 8 * ch) * 4);
+                pv[p][i][1] = *(const f4 *)(lds + (row * LD + 8 * ch + 4) * 4);
+            }
+        }
+#pragma unroll
+    for (int i = 0; i < NB; i++) {
+        const int c = (int)threadIdx.x + WS_NT * i, row = c / CH, ch = c - row * CH, m = m0 + row, n = n0 + 8 * ch;
+        f4 v0 = {0.f, 0.f, 0.f, 0.f}, v1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int p = 0; p < 4; p++)
+            if (p < g.parts) {
+                v0 += pv[p][i][0];
+                v1 += pv[p][i][1];
+            }
+        if (m >= M || n >= N) continue;
+        const size_t idx = (size_t)m * N + n;
+        if (wide && n + 8 <= N) {
+            if (g.c_f32) {
+                f4 *q = (f4 *)((float *)g.C + idx);
+                q[0] = g.accumulate ? q[0] + v0 : v0;
+                q[1] = g.accumulate ? q[1] + v1 : v1;
+            } else {
+                h8 *q = (h8 *)((_Float16 *)g.C + idx);
+                if (g.accumulate) {
+                    const h8 o = *q;
+                    v0 += f4{(float)o[0], (float)o[1], (float)o[2], (float)o[3]};
+                    v1 += f4{(float)o[4], (float)o[5], (float)o[6], (float)o[7]};
+                }
+                *q = h8{(_Float16)v0.x, (_Float16)v0.y, (_Float16)v0.z, (_Float16)v0.w,
+                        (_Float16)v1.x, (_Float16)v1.y, (_Float16)v1.z, (_Float16)v1.w};
+            }
+        } else {
+            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            for (int e = 0; e < 8 && n + e < N; e++) store_out(g.C, idx + e, v[e], g.c_f32, g.accumulate);
+        }
+    }
+}
+
 // LDS arena (bytes): A stages, B stages, S, Bmin, R, CL, scale words, prefetch scratch.
 template <int NB>
 struct WsLds {
@@ -185,14 +277,19 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
 
     // tile of this workgroup: XCD x = b % 8 takes N-tiles x, x + 8, ...; its slots run over the
     // M-tiles of one N-tile first
-    const int b = blockIdx.x, x = b & 7, j8 = b >> 3;
-    const int nt_i = x + 8 * (j8 / g.mt), mt_i = j8 % g.mt;
+    const int b = blockIdx.x, x = b & 7, j8 = b >> 3, per = g.mt * g.parts;
+    const int nt_i = x + 8 * (j8 / per), part = (j8 % per) / g.mt, mt_i = j8 % g.mt;
     if (nt_i >= g.nt) return;
     const int m0 = mt_i * WS_BM, n0 = nt_i * BN;
-    const int M = g.M, N = g.N, K = g.K, U = K / 256;
+    // this part's super-blocks u0 .. u0 + U - 1 of UT; the operand bases are moved to u0 (row
+    // strides stay K, UT), so the body below indexes super-blocks from 0
+    const int M = g.M, N = g.N, K = g.K, UT = K / 256;
+    const int u0 = part * UT / g.parts, U = (part + 1) * UT / g.parts - u0;
+    const uint8_t *const Wb = g.W + (size_t)u0 * 144;
+    const uint16_t *const Ab = g.A + (size_t)u0 * 256, *const Sb = g.S + (size_t)u0 * 16;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const rsrc_t ra = make_rsrc(g.A, (uint32_t)((size_t)M * K * 2));
-    const rsrc_t rw = make_rsrc(g.W, (uint32_t)((size_t)N * g.row_bytes));
+    const rsrc_t ra = make_rsrc(Ab, (uint32_t)((size_t)M * K * 2 - (size_t)u0 * 512));
+    const rsrc_t rw = make_rsrc(Wb, (uint32_t)((size_t)N * g.row_bytes - (size_t)u0 * 144));
 
     if (wave >= 4) {
         // ------------------------------------------------------------------ producers
@@ -203,7 +300,7 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
         // burst); the end-of-stage wait covers the DMAs only (loads issued after them retire later).
         const int pw = __builtin_amdgcn_readfirstlane(wave - 4);  // wave-uniform LDS targets
         const int pt = tid - 256, xi = pt & 7;
-        const rsrc_t rs = make_rsrc(g.S, (uint32_t)((size_t)M * U * 32));
+        const rsrc_t rs = make_rsrc(Sb, (uint32_t)((size_t)M * UT * 32 - (size_t)u0 * 32));
         // activation DMA: instruction qq of wave pw fills rows 4(pw + 4qq) .. +4 (1 KB); lane l takes
         // row 4(pw + 4qq) + l/16, LDS slot l % 16, global chunk (l % 16) ^ (row & 15)
         const int arow = 4 * pw + (lane >> 4);
@@ -212,7 +309,7 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
             dma16(ra, sA(s & 1) + (pw + 4 * qq) * 512, a_voff, (uint32_t)(qq * 16 * K * 2 + s * WS_KS * 2));
         };
         // S tile of unit u: 32 rows (1 KB) per wave; lane l: row 32pw + l/2, half l % 2
-        const uint32_t s_voff = (uint32_t)(((m0 + 32 * pw + (lane >> 1)) * U) * 32 + 16 * (lane & 1));
+        const uint32_t s_voff = (uint32_t)(((m0 + 32 * pw + (lane >> 1)) * UT) * 32 + 16 * (lane & 1));
         auto dma_s = [&](int u) { dma16(rs, sS + pw * 512, s_voff, (uint32_t)(u * 32)); };
         // quant bytes: this thread's columns c_i = pt/8 + 32i (i < NB), half-chunk xi of each stage
         // (bytes 16 + 8(8(s % 2) + xi) of super-block s/2). Four register sets: stage s's go to
@@ -383,7 +480,7 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
         if (u < U) unit(i0{}, u);
         wg_barrier();  // the last stage's barrier
         wg_barrier();  // the consumers' output tile is in LDS
-        ws_lds_to_c<NB>(lds, g.C, M, N, m0, n0, g.c_f32, g.accumulate);
+        ws_finish<NB>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::PF));
         return;
     }
 
@@ -484,7 +581,7 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
     // L2) split the columns. Lane e of the four consumer waves (and of e + 256, ...) touches bytes
     // {0, 72, 143} (e % 3) of column mt_i + mt (e / 3).
     const int pf_cols = (BN - mt_i + g.mt - 1) / g.mt, pf_lanes = 3 * pf_cols;
-    const rsrc_t rw_pf = make_rsrc(g.W, (uint32_t)((size_t)N * g.row_bytes));
+    const rsrc_t rw_pf = rw;
     const uint32_t pf_lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds + L::PF) + 256u * (uint32_t)wave);
     auto prefetch = [&](int v) {
         for (int e0 = 64 * wave; e0 < pf_lanes; e0 += 256) {
@@ -520,7 +617,7 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
     ws_tile_to_lds<NB>(lds, acc, wm, wn, ln, lg);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     wg_barrier();
-    ws_lds_to_c<NB>(lds, g.C, M, N, m0, n0, g.c_f32, g.accumulate);
+    ws_finish<NB>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::PF));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -782,13 +879,16 @@ int hq_ws_choose(int M, int N, int n_cu, float *eff) {
 }
 
 hipError_t hq_launch_gemm_ws(const hq_dev_mat *W, const uint16_t *A, const uint16_t *S, int M, void *C, int c_f32,
-                             int accumulate, int nb, hipStream_t st) {
+                             int accumulate, int nb, int parts, float *partials, int *counters, hipStream_t st) {
     WsArgs g;
     g.W = W->qs, g.row_bytes = (uint32_t)W->row_bytes, g.A = A, g.S = S;
     g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;
     g.mt = (M + WS_BM - 1) / WS_BM;
     g.nt = (g.N + 32 * nb - 1) / (32 * nb);
-    const unsigned grid = (unsigned)(8 * ((g.nt + 7) / 8) * g.mt);
+    g.parts = parts, g.partials = partials, g.counters = counters;
+    if (parts < 1 || parts > 4 || parts > g.K / 256 || (parts > 1 && (!partials || !counters))) return hipErrorInvalidValue;
+    if (parts > 1 && (size_t)g.mt * g.nt * parts * WS_BM * 32 * nb * 4 >= ((size_t)1 << 32)) return hipErrorInvalidValue;
+    const unsigned grid = (unsigned)(8 * ((g.nt + 7) / 8) * g.mt * parts);
     switch (nb) {
     case 2: k_gemm_q4_k_ws<2><<<grid, WS_NT, 0, st>>>(g); break;
     case 3: k_gemm_q4_k_ws<3><<<grid, WS_NT, 0, st>>>(g); break;

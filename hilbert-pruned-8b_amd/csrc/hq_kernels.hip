@@ -663,18 +663,6 @@ DEV int sk_owner(const SkPlan &p, int u) {
 }
 
 
-// Partial tiles are written and read with device-scope (sc1) buffer accesses: they go to the
-// cross-XCD coherent level, so no L2 write-back or invalidation is needed, and unlike atomics they
-// are not serialized, so a 16-byte access per (row block, column block) is in flight at once.
-constexpr int CPOL_SC1 = 16;
-
-DEV void buf_store16(rsrc_t r, f4 v, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, v), r, voff, soff, CPOL_SC1);
-}
-
-DEV f4 buf_load16_sc1(rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, CPOL_SC1));
-}
 
 // Tile finished by this workgroup (NT threads): store it, or run the partial-tile protocol. Partial
 // slot layout: (row block i, column block j) of thread tid at 16 * ((i * NB + j) * NT + tid).
@@ -1448,14 +1436,16 @@ namespace {
 struct GemmCfg {
     int mb, nb, waves;
     bool wide;
-    int ws_nb;   // > 0: the full-K tile kernel k_gemm_q4_k_ws with 32 * ws_nb columns per tile
+    int ws_nb;     // > 0: the full-K tile kernel k_gemm_q4_k_ws with 32 * ws_nb columns per tile
+    int ws_parts;  // with ws_nb: workgroups per tile, each a contiguous range of K (1: whole K)
     int ws8_nb;  // > 0: the Q8_0 full-K tile kernel k_gemm_q8_0_ws, 32 * ws8_nb columns per tile
 };
 
 // Q4_K with M > 64 runs the full-K tile kernel when its tiles fit in one round on the CUs and fill
-// at least 70 % of them (e.g. M = 512, N = 9728: 244 tiles of 128 x 160 on 256 CUs); otherwise the
-// Stream-K wide kernel (few long tiles, such as N = 2560 at M = 512, or many tiles at large M, where
-// its split-tile overhead is amortised: measured faster at M = 4096 and 16384).
+// at least 70 % of them (e.g. M = 512, N = 9728: 244 tiles of 128 x 160 on 256 CUs), or, with each
+// tile's K split over 2 or 4 workgroups, when few tiles cover a long K (M = 512, N = 2560,
+// K = 9728); otherwise the Stream-K wide kernel (many tiles at large M, where its split-tile
+// overhead is amortised: measured faster at M = 4096 and 16384).
 GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
     GemmCfg c;
     c.mb = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
@@ -1464,11 +1454,23 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
     c.wide = W->type == HQ_TYPE_Q4_K && M > 64;
     c.waves = c.wide ? WNW : 4;
     c.ws_nb = 0;
+    c.ws_parts = 1;
     if (c.wide && (size_t)M * W->cols * 2 < ((size_t)1 << 32)) {
         float eff = 0.f;
         const int nb = hq_ws_choose(M, (int)W->rows, n_cu, &eff);
         const long tiles = (long)((M + 127) / 128) * (((int)W->rows + 32 * nb - 1) / (32 * nb));
         if (eff >= 0.7f && tiles <= n_cu) c.ws_nb = nb;
+        // few tiles over a long K (M = 512, N = 2560, K = 9728: 64 tiles of 128 x 160): split each
+        // tile's K over 2 or 4 workgroups, the widest tiles for which that fills at least 3/4 of the
+        // CUs in one round, with >= 8 super-blocks per part
+        for (int parts = 4; !c.ws_nb && parts >= 2; parts /= 2)
+            for (int w = 5; !c.ws_nb && w >= 2; w--) {
+                const long t = (long)((M + 127) / 128) * (((int)W->rows + 32 * w - 1) / (32 * w));
+                if (t * parts <= n_cu && 4 * t * parts >= 3L * n_cu && (int)(W->cols / 256) >= 8 * parts) {
+                    c.ws_nb = w;
+                    c.ws_parts = parts;
+                }
+            }
     }
     // Q8_0 with M > 64: the Q8_0 tile kernel when its tiles fill at least half of the CU time
     // (rounds of tiles included; M = 128, N = 9728: 152 tiles of 128 x 64, 21.7 us against 24.9 for
@@ -1527,6 +1529,11 @@ void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_by
     const bool tile = c.ws_nb || c.ws8_nb;  // full-K tile kernels: no partial tiles
     *partial_bytes = tile ? 0 : (size_t)2 * p.G * 64 * c.waves * c.mb * c.nb * 4 * sizeof(float);
     *counter_bytes = tile ? 0 : (size_t)p.tiles * sizeof(int);
+    if (c.ws_nb && c.ws_parts > 1) {  // K-split tile kernel: one fp32 tile per (tile, part)
+        const size_t tiles = (size_t)((M + 127) / 128) * ((W->rows + 32 * c.ws_nb - 1) / (32 * c.ws_nb));
+        *partial_bytes = tiles * c.ws_parts * 128 * 32 * c.ws_nb * sizeof(float);
+        *counter_bytes = tiles * sizeof(int);
+    }
     *sums_bytes = c.wide ? (size_t)M * (W->cols / KC) * 32 : 0;
 }
 
@@ -1546,7 +1553,8 @@ hipError_t hq_launch_gemm_pre(const hq_dev_mat *W, const uint16_t *A, int M, con
 hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
                                const HqGemmWork &wk, hipStream_t st) {
     const GemmCfg c = gemm_cfg(W, M, wk.n_cu);
-    if (c.ws_nb) return hq_launch_gemm_ws(W, A, wk.sums, M, C, c_f32, accumulate, c.ws_nb, st);
+    if (c.ws_nb)
+        return hq_launch_gemm_ws(W, A, wk.sums, M, C, c_f32, accumulate, c.ws_nb, c.ws_parts, wk.partials, wk.counters, st);
     if (c.ws8_nb) return hq_launch_gemm_ws8(W, A, M, C, c_f32, accumulate, c.ws8_nb, st);
     GemmArgs g;
     g.qs = W->qs, g.d = W->d, g.ldd = W->ldd, g.row_bytes = W->row_bytes, g.A = A;
