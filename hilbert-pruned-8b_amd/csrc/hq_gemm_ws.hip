@@ -154,8 +154,8 @@ DEV void ws_lds_to_c(const char *lds, void *C, int M, int N, int m0, int n0, int
 // itself in; the last of the tile's parts loads the others' (device scope) and adds all of them in
 // part order (its own from LDS in its place), so the sum is the same whichever part arrives last,
 // then writes C. flag: an LDS word.
-template <int NB>
-DEV void ws_finish(const char *lds, const WsArgs &g, int m0, int n0, int tile, int part, int *flag) {
+template <int NB, class Args>
+DEV void ws_finish(const char *lds, const Args &g, int m0, int n0, int tile, int part, int *flag) {
     if (g.parts == 1) {
         ws_lds_to_c<NB>(lds, g.C, g.M, g.N, m0, n0, g.c_f32, g.accumulate);
         return;
@@ -647,6 +647,9 @@ struct Ws8Args {
     void *C;
     int c_f32, accumulate;
     int mt, nt;
+    int parts;  // K split as in WsArgs (ranges of 128-wide stages)
+    float *partials;
+    int *counters;
 };
 
 // 16 fp16 values fp16(q * d) from 16 stored bytes u = q + 128: fp16(1024 + u) - 1152 = q exactly,
@@ -673,14 +676,20 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q8_0_ws(Ws8Args g) {
     _Float16 *const sB0 = (_Float16 *)(lds + L::B);
     auto sA = [&](int h) { return sA0 + h * (L::A_BYTES / 2); };
     auto sB = [&](int h) { return sB0 + h * (L::B_BYTES / 2); };
-    const int b = blockIdx.x, x = b & 7, j8 = b >> 3;
-    const int nt_i = x + 8 * (j8 / g.mt), mt_i = j8 % g.mt;
+    const int b = blockIdx.x, x = b & 7, j8 = b >> 3, per = g.mt * g.parts;
+    const int nt_i = x + 8 * (j8 / per), part = (j8 % per) / g.mt, mt_i = j8 % g.mt;
     if (nt_i >= g.nt) return;
     const int m0 = mt_i * WS_BM, n0 = nt_i * BN;
-    const int M = g.M, N = g.N, K = g.K, S2 = K / WS_KS;
+    // this part's stages s0 .. s0 + S2 - 1 of K / 128; operand bases moved to s0 (row strides stay
+    // K and ldd), so the body below indexes stages from 0
+    const int M = g.M, N = g.N, K = g.K, ST = K / WS_KS;
+    const int s0 = part * ST / g.parts, S2 = (part + 1) * ST / g.parts - s0;
+    const uint16_t *const Ab = g.A + (size_t)s0 * WS_KS;
+    const uint8_t *const Qb = g.Q + (size_t)s0 * WS_KS;
+    const uint16_t *const Db = g.D + (size_t)s0 * (WS_KS / 32);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const rsrc_t ra = make_rsrc(g.A, (uint32_t)((size_t)M * K * 2));
-    const rsrc_t rq = make_rsrc(g.Q, (uint32_t)((size_t)N * K));  // columns >= N read as zero
+    const rsrc_t ra = make_rsrc(Ab, (uint32_t)((size_t)M * K * 2 - (size_t)s0 * WS_KS * 2));
+    const rsrc_t rq = make_rsrc(Qb, (uint32_t)((size_t)N * K - (size_t)s0 * WS_KS));  // columns >= N read as zero
 
     if (wave >= 4) {
         // ------------------------------------------------------------------ producers
@@ -689,7 +698,7 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q8_0_ws(Ws8Args g) {
         // decode. The end-of-stage wait covers the DMAs (issued first) and everything older.
         const int pw = __builtin_amdgcn_readfirstlane(wave - 4);
         const int pt = tid - 256, xi = pt & 7;
-        const rsrc_t rd = make_rsrc(g.D, (uint32_t)((size_t)N * g.ldd * 2));
+        const rsrc_t rd = make_rsrc(Db, (uint32_t)((size_t)N * g.ldd * 2 - (size_t)s0 * (WS_KS / 32) * 2));
         const int arow = 4 * pw + (lane >> 4);
         const uint32_t a_voff = (uint32_t)(((m0 + arow) * K + 8 * ((lane & 15) ^ (arow & 15))) * 2);
         auto dma_a = [&](int s, int qq) {
@@ -764,7 +773,7 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q8_0_ws(Ws8Args g) {
         if (t < S2) step(i2{}, t++);
         if (t < S2) step(i3{}, t++);
         wg_barrier();  // the consumers' output tile is in LDS
-        ws_lds_to_c<NB>(lds, g.C, M, N, m0, n0, g.c_f32, g.accumulate);
+        ws_finish<NB>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::PF));
         return;
     }
 
@@ -852,7 +861,7 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q8_0_ws(Ws8Args g) {
     ws_tile_to_lds<NB>(lds, acc, wm, wn, ln, lg);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     wg_barrier();
-    ws_lds_to_c<NB>(lds, g.C, M, N, m0, n0, g.c_f32, g.accumulate);
+    ws_finish<NB>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::PF));
 }
 }  // namespace
 
@@ -900,14 +909,17 @@ hipError_t hq_launch_gemm_ws(const hq_dev_mat *W, const uint16_t *A, const uint1
 }
 
 hipError_t hq_launch_gemm_ws8(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
-                              int nb, hipStream_t st) {
+                              int nb, int parts, float *partials, int *counters, hipStream_t st) {
     if (W->cols % WS_KS) return hipErrorInvalidValue;
     Ws8Args g;
     g.Q = W->qs, g.D = W->d, g.ldd = W->ldd, g.A = A;
     g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;
     g.mt = (M + WS_BM - 1) / WS_BM;
     g.nt = (g.N + 32 * nb - 1) / (32 * nb);
-    const unsigned grid = (unsigned)(8 * ((g.nt + 7) / 8) * g.mt);
+    g.parts = parts, g.partials = partials, g.counters = counters;
+    if (parts < 1 || parts > 4 || parts > g.K / WS_KS || (parts > 1 && (!partials || !counters))) return hipErrorInvalidValue;
+    if (parts > 1 && (size_t)g.mt * g.nt * parts * WS_BM * 32 * nb * 4 >= ((size_t)1 << 32)) return hipErrorInvalidValue;
+    const unsigned grid = (unsigned)(8 * ((g.nt + 7) / 8) * g.mt * parts);
     switch (nb) {
     case 2: k_gemm_q8_0_ws<2><<<grid, WS_NT, 0, st>>>(g); break;
     case 3: k_gemm_q8_0_ws<3><<<grid, WS_NT, 0, st>>>(g); break;

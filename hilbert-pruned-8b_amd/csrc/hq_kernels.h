@@ -54,6 +54,6 @@ int hq_ws_choose(int M, int N, int n_cu, float *eff);
 hipError_t hq_launch_gemm_ws(const hq_dev_mat *W, const uint16_t *A, const uint16_t *S, int M, void *C, int c_f32,
                              int accumulate, int nb, int parts, float *partials, int *counters, hipStream_t st);
 hipError_t hq_launch_gemm_ws8(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
-                              int nb, hipStream_t st);
+                              int nb, int parts, float *partials, int *counters, hipStream_t st);
 
 #endif

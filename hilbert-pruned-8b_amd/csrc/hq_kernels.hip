@@ -1439,6 +1439,7 @@ struct GemmCfg {
     int ws_nb;     // > 0: the full-K tile kernel k_gemm_q4_k_ws with 32 * ws_nb columns per tile
     int ws_parts;  // with ws_nb: workgroups per tile, each a contiguous range of K (1: whole K)
     int ws8_nb;  // > 0: the Q8_0 full-K tile kernel k_gemm_q8_0_ws, 32 * ws8_nb columns per tile
+    int ws8_parts;  // with ws8_nb: workgroups per tile (K split, as ws_parts)
 };
 
 // Q4_K with M > 64 runs the full-K tile kernel when its tiles fit in one round on the CUs and fill
@@ -1476,11 +1477,26 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
     // (rounds of tiles included; M = 128, N = 9728: 152 tiles of 128 x 64, 21.7 us against 24.9 for
     // the narrow kernel), K is whole 128-wide stages and the byte offsets fit 32 bits
     c.ws8_nb = 0;
+    c.ws8_parts = 1;
     if (W->type == HQ_TYPE_Q8_0 && M > 64 && W->cols % 128 == 0 && (size_t)M * W->cols * 2 < ((size_t)1 << 32) &&
         ((size_t)W->rows + 160) * W->cols < ((size_t)1 << 32)) {
         float eff = 0.f;
         const int nb = hq_ws_choose(M, (int)W->rows, n_cu, &eff);
+        const long tiles = (long)((M + 127) / 128) * (((int)W->rows + 32 * nb - 1) / (32 * nb));
         if (eff >= 0.5f) c.ws8_nb = nb;
+        // fewer tiles than 3/4 of the CUs over a long K (M = 512, N = 2560, K = 9728: 160 tiles of
+        // 128 x 64 through 76 stages, 66 us): each tile's K split over 2 or 4 workgroups of >= 16
+        // stages, the widest tiles that fill >= 3/4 of the CUs in one round
+        if (4 * tiles < 3L * n_cu || !c.ws8_nb)
+            for (int parts = 4, done = 0; !done && parts >= 2; parts /= 2)
+                for (int w = 5; !done && w >= 2; w--) {
+                    const long t = (long)((M + 127) / 128) * (((int)W->rows + 32 * w - 1) / (32 * w));
+                    if (t * parts <= n_cu && 4 * t * parts >= 3L * n_cu && (int)(W->cols / 128) >= 16 * parts) {
+                        c.ws8_nb = w;
+                        c.ws8_parts = parts;
+                        done = 1;
+                    }
+                }
     }
     return c;
 }
@@ -1529,9 +1545,10 @@ void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_by
     const bool tile = c.ws_nb || c.ws8_nb;  // full-K tile kernels: no partial tiles
     *partial_bytes = tile ? 0 : (size_t)2 * p.G * 64 * c.waves * c.mb * c.nb * 4 * sizeof(float);
     *counter_bytes = tile ? 0 : (size_t)p.tiles * sizeof(int);
-    if (c.ws_nb && c.ws_parts > 1) {  // K-split tile kernel: one fp32 tile per (tile, part)
-        const size_t tiles = (size_t)((M + 127) / 128) * ((W->rows + 32 * c.ws_nb - 1) / (32 * c.ws_nb));
-        *partial_bytes = tiles * c.ws_parts * 128 * 32 * c.ws_nb * sizeof(float);
+    const int snb = c.ws_nb ? c.ws_nb : c.ws8_nb, sparts = c.ws_nb ? c.ws_parts : c.ws8_parts;
+    if (snb && sparts > 1) {  // K-split tile kernels: one fp32 tile per (tile, part)
+        const size_t tiles = (size_t)((M + 127) / 128) * ((W->rows + 32 * snb - 1) / (32 * snb));
+        *partial_bytes = tiles * sparts * 128 * 32 * snb * sizeof(float);
         *counter_bytes = tiles * sizeof(int);
     }
     *sums_bytes = c.wide ? (size_t)M * (W->cols / KC) * 32 : 0;
@@ -1555,7 +1572,8 @@ hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, vo
     const GemmCfg c = gemm_cfg(W, M, wk.n_cu);
     if (c.ws_nb)
         return hq_launch_gemm_ws(W, A, wk.sums, M, C, c_f32, accumulate, c.ws_nb, c.ws_parts, wk.partials, wk.counters, st);
-    if (c.ws8_nb) return hq_launch_gemm_ws8(W, A, M, C, c_f32, accumulate, c.ws8_nb, st);
+    if (c.ws8_nb)
+        return hq_launch_gemm_ws8(W, A, M, C, c_f32, accumulate, c.ws8_nb, c.ws8_parts, wk.partials, wk.counters, st);
     GemmArgs g;
     g.qs = W->qs, g.d = W->d, g.ldd = W->ldd, g.row_bytes = W->row_bytes, g.A = A;
     g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;
