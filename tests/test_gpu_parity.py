@@ -281,6 +281,24 @@ def test_gemm_positive_activations(hqlib, oracle, gtype, N, K, M):
     assert np.array_equal(got64, got * 64)
 
 
+
+@pytest.mark.parametrize("gtype", [synth.Q4_K, synth.Q8_0])
+def test_gemm_k_split_repeatable(hqlib, gtype):
+    """The K-split tile kernels (M = 512, N = 2560, K = 9728: each tile's K over 4 workgroups) give
+    the same bits on every call: the last part to arrive adds the parts in part order, and the
+    per-tile counters return to zero after each call."""
+    M, N, K = 512, 2560, 9728
+    blocks = weights(gtype, N, K, 31 + gtype)
+    a = synth.activations_f16(synth.Rng(4242), M, K)
+    W = hqlib.Mat(blocks, gtype, N, K)
+    say(f"k-split repeat type={gtype} kernel={hqlib.gemm_kernel(gtype, M, N, K)}")
+    first = hqlib.gemm_np(W, a)
+    for _ in range(4):
+        assert np.array_equal(hqlib.gemm_np(W, a), first)
+    W.free()
+    assert np.all(np.isfinite(first))
+
+
 def test_gather_special_scales(hqlib, oracle):
     V, K, B, k = 4096, 2560, 64, 5
     blocks = special_q4_k_weights(61, V, K)
