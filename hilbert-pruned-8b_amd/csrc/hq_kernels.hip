@@ -662,8 +662,7 @@ DEV int sk_owner(const SkPlan &p, int u) {
     return u < big ? u / (p.base + 1) : p.extra + (u - big) / p.base;
 }
 
-
-
+// Partial tiles travel through device-scope (sc1) 16-byte accesses (buf_store16 / buf_load16_sc1).
 // Tile finished by this workgroup (NT threads): store it, or run the partial-tile protocol. Partial
 // slot layout: (row block i, column block j) of thread tid at 16 * ((i * NB + j) * NT + tid).
 template <int MB, int NB, int NT>
@@ -1542,7 +1541,7 @@ void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_by
                         size_t *sums_bytes) {
     const GemmCfg c = gemm_cfg(W, M, n_cu);
     const SkPlan p = gemm_plan(W, M, c, n_cu);
-    const bool tile = c.ws_nb || c.ws8_nb;  // full-K tile kernels: no partial tiles
+    const bool tile = c.ws_nb || c.ws8_nb;  // tile kernels: partial tiles only when K is split (below)
     *partial_bytes = tile ? 0 : (size_t)2 * p.G * 64 * c.waves * c.mb * c.nb * 4 * sizeof(float);
     *counter_bytes = tile ? 0 : (size_t)p.tiles * sizeof(int);
     const int snb = c.ws_nb ? c.ws_nb : c.ws8_nb, sparts = c.ws_nb ? c.ws_parts : c.ws8_parts;
