@@ -1,0 +1,494 @@
+// hq_gemm_rb.hip - Q4_K GEMM for mid-size M (33 <= M <= 64, N >= 8192) on gfx950: full-K tiles of
+// 64 rows x 64 columns, one per workgroup, no partial tiles.
+//
+// C[M,N] (+)= A[M,K] . W^T with A fp16 and W GGUF Q4_K super-blocks resident in HBM (reference
+// arithmetic: cleanroom-transformer/src/ggml_quant.h:51-59, :135-150; matmul src/cpu_backend.c:38-54).
+//
+// A workgroup holds PIPE independent pipelines of four waves (PIPE = 2: one wave of each per SIMD);
+// pipeline kh takes the super-blocks u = kh, kh + PIPE, ... of K, so one pipeline's LDS and memory
+// latency is covered by the other's work. In a pipeline, wave w owns all 64 rows and the 16 columns
+// 16w .. 16w + 15 of the tile and decodes its own columns' Q4_K bytes from LDS straight into MFMA
+// fragments (v_mfma_f32_16x16x32_f16, activations as the first operand, so each lane's four
+// accumulators belong to one output column); no decoded B tile is stored. Per pipeline, an LDS ring
+// of NSTG 128-K stages (activation tile + the quant bytes of its columns, both LDS-DMA'd, written as
+// assembly and waited with explicit s_waitcnt vmcnt) and a ring of super-block slots (the
+// activations' sub-block sums from the k_asums pre-pass in (hi, lo) pair layout, and the column
+// headers).
+//
+// Arithmetic as in the full-K tile kernel of hq_gemm_ws.hip: the B operand is the exact integer
+// s*q (fp16 1024 + q via v_perm_b32, one v_pk_fma_f16 with (s, -1024 s) or (s/16, -64 s)); a
+// column's accumulators are in units of c_u = d_u (1 where d_u = 0) during super-block u and are
+// rescaled by c_{u'} / c_u when the pipeline moves on (u' its previous super-block), then by its
+// last c; the min term -dmin * sum_sub m_sub * S_sub is one bf16 MFMA per row block and super-block
+// whose k slots pair (S hi, S lo, S hi, S lo) with (x hi, x hi, x lo, x lo), x = -dmin m / c_u, so a
+// lane needs only the two sub-blocks of its own lane group. Each lane reads its column's 16-byte
+// header and forms every per-column value itself (no cross-lane exchange). The two pipelines' tiles
+// are added in pipeline order through LDS before the store.
+#include <type_traits>
+
+#include "hq_device.h"
+#include "hq_kernels.h"
+
+namespace {
+struct RbArgs {
+    const uint8_t *W;  // Q4_K super-blocks, row n at n * row_bytes
+    uint32_t row_bytes;
+    const uint16_t *A;  // fp16 [M][K]
+    const uint16_t *S;  // activation sub-block sums [M][K/256][8][hi, lo] (k_asums, pair layout)
+    int M, N, K;
+    void *C;
+    int c_f32, accumulate;
+    int mt, nt;  // M-tiles, N-tiles
+};
+}  // namespace
+
+namespace {
+constexpr int RB_KS = 128, RB_NT = 256;
+
+template <int NB, int MBK, int NSTG>
+struct RbLds {
+    static constexpr int BN = 64 * NB;
+    static constexpr int BM = 16 * MBK;
+    static constexpr int A_BYTES = BM * RB_KS * 2;  // activation stage tile
+    static constexpr int B_BYTES = 4 * NB * 1024;      // quant bytes [wave][j][16 cols][64 B]
+    static constexpr int STG = A_BYTES + B_BYTES;      // one stage slot (NSTG slots)
+    static constexpr int S_BYTES = BM * 32;            // sub-block sums of a super-block
+    static constexpr int H_BYTES = BN * 16;            // headers [wave][16 NB cols][16 B]
+    static constexpr int SBS = S_BYTES + H_BYTES;      // one super-block slot (NSB slots)
+    static constexpr int NSB = NSTG / 2 + 2;
+    static constexpr int SB0 = NSTG * STG;
+    static constexpr int TOTAL = SB0 + NSB * SBS;
+    static_assert(TOTAL <= 160 * 1024, "LDS budget");
+    static_assert(BM * (BN + 4) * 4 <= NSTG * STG, "epilogue tile");
+};
+
+// 16-byte LDS DMA with an SGPR offset, untracked by the compiler (explicit s_waitcnt vmcnt).
+DEV void dma16_so(rsrc_t r, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
+    uint32_t save;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 1\n\tbuffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(save)
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(r),
+                   "s"(__builtin_amdgcn_readfirstlane(soff))
+                 : "memory");
+}
+
+using rb_lds_h8 = const __attribute__((address_space(3))) h8;
+using rb_lds_u4 = const __attribute__((address_space(3))) u4v;
+DEV h8 rb_ld8(uint32_t a) { return *(rb_lds_h8 *)(uintptr_t)a; }
+DEV u4v rb_ld16(uint32_t a) { return *(rb_lds_u4 *)(uintptr_t)a; }
+using rb_lds_u2 = const __attribute__((address_space(3))) u2v;
+DEV h8 rb_lds_pairs(uint32_t a) {
+    const u2v p = *(rb_lds_u2 *)(uintptr_t)a;
+    return __builtin_bit_cast(h8, u4v{p.x, p.x, p.y, p.y});
+}
+template <int I, int N, class F>
+DEV void sfor(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        sfor<I + 1, N>(f);
+    }
+}
+DEV void rb_wait_lgkm() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+template <int NB, int MBK, int NSTG, int PIPE>
+__global__ void __launch_bounds__(RB_NT * PIPE) k_gemm_q4_k_rb(RbArgs g) {
+    constexpr int BM = 16 * MBK, HG = MBK / 2, D = NSTG - 1;
+    constexpr int BN = 64 * NB;
+    using L = RbLds<NB, MBK, NSTG>;
+    constexpr int NSB = L::NSB;
+    static_assert(L::TOTAL % 256 == 0, "arena alignment");
+    __shared__ __attribute__((aligned(256))) char lds[L::TOTAL * PIPE];
+    const int b = blockIdx.x, x = b & 7, j8 = b >> 3;
+    const int nt_i = x + 8 * (j8 / g.mt), mt_i = j8 % g.mt;
+    if (nt_i >= g.nt) return;
+    const int m0 = mt_i * BM, n0 = nt_i * BN;
+    // PIPE independent pipelines of 4 waves; pipeline kh takes super-blocks kh, kh + PIPE, ...
+    const int M = g.M, N = g.N, K = g.K, UT = K / 256, U = UT / PIPE, S2 = 2 * U;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 3), kh = __builtin_amdgcn_readfirstlane(tid >> 8);
+    auto ru = [&](int u) __attribute__((always_inline)) { return PIPE * u + kh; };  // real super-block
+    const int ln = lane & 15, lg = lane >> 4;
+    const rsrc_t ra = make_rsrc(g.A, (uint32_t)((size_t)M * K * 2));
+    const rsrc_t rw = make_rsrc(g.W, (uint32_t)((size_t)N * g.row_bytes));
+    const rsrc_t rs = make_rsrc(g.S, (uint32_t)((size_t)M * UT * 32));
+    const uint32_t lds0 = (uint32_t)(uintptr_t)lds + (uint32_t)(kh * L::TOTAL);
+    const int nw = n0 + 16 * NB * wave;  // the wave's first column
+    const uint32_t rb = g.row_bytes;
+
+    // ---- DMA issue (every lane offset holds the row / column part, so rows >= M and columns >= N
+    // fall outside the buffer ranges and read zero)
+    const int arow = 4 * wave + (lane >> 4);
+    const uint32_t a_voff = ((uint32_t)(m0 + arow) * (uint32_t)K + 8u * (uint32_t)((lane & 15) ^ (arow & 15))) * 2u;
+    const uint32_t a_qq = 16u * (uint32_t)K * 2u;
+    auto dma_a = [&](int s, int qq) __attribute__((always_inline)) {
+        dma16_so(ra, lds0 + (uint32_t)((s % NSTG) * L::STG + (wave + 4 * qq) * 1024), a_voff + (uint32_t)qq * a_qq,
+                 (uint32_t)((2 * ru(s >> 1) + (s & 1)) * RB_KS * 2));
+    };
+    uint32_t b_voff[NB];
+#pragma unroll
+    for (int j = 0; j < NB; j++) b_voff[j] = (uint32_t)(nw + 16 * j + (lane >> 2)) * rb + 16u + 16u * (uint32_t)(lane & 3);
+    auto dma_b = [&](int s, int j) __attribute__((always_inline)) {
+        dma16_so(rw, lds0 + (uint32_t)((s % NSTG) * L::STG + L::A_BYTES + (wave * NB + j) * 1024), b_voff[j],
+                 (uint32_t)(ru(s >> 1) * 144 + 64 * (s & 1)));
+    };
+    const uint32_t s_voff = ((uint32_t)(m0 + 4 * MBK * wave + (lane >> 1)) * (uint32_t)UT) * 32u + 16u * (uint32_t)(lane & 1);
+    auto dma_s = [&](int u) __attribute__((always_inline)) {
+        if (lane < 8 * MBK) dma16_so(rs, lds0 + (uint32_t)(L::SB0 + (u % NSB) * L::SBS + wave * 128 * MBK), s_voff, (uint32_t)(ru(u) * 32));
+    };
+    const uint32_t h_voff = (uint32_t)(nw + (lane < 16 * NB ? lane : 0)) * rb;
+    auto dma_h = [&](int u) __attribute__((always_inline)) {
+        if (lane < 16 * NB)
+            dma16_so(rw, lds0 + (uint32_t)(L::SB0 + (u % NSB) * L::SBS + L::S_BYTES + wave * 256 * NB), h_voff,
+                     (uint32_t)(ru(u) * 144));
+    };
+
+    // ---- operands
+    // A fragment of row block i, k-step kk of the stage in slot s % NSTG: row 16i + ln, 16-byte slot
+    // p = 8(lg>>1) + 4(kk>>1) + 2(lg&1) + (kk&1) stored at p ^ ln
+    const uint32_t a_lane = (uint32_t)(ln * 256) + 16u * (uint32_t)((8 * (lg >> 1) + 2 * (lg & 1)) ^ ln);
+    auto a_base = [&](int s, int kk) __attribute__((always_inline)) {
+        return (lds0 + (uint32_t)((s % NSTG) * L::STG) + a_lane) ^ (uint32_t)(64 * (kk >> 1) + 16 * (kk & 1));
+    };
+    // S fragment (min k-step) of row block i: row 16i + ln, the (hi, lo) pairs of sub-blocks 2lg and
+    // 2lg + 1, each pair twice
+    const uint32_t s_lane = (uint32_t)(ln * 32 + 8 * lg);
+    auto s_base = [&](int u) __attribute__((always_inline)) { return lds0 + (uint32_t)(L::SB0 + (u % NSB) * L::SBS) + s_lane; };
+    const uint32_t raw_lane = (uint32_t)(L::A_BYTES + wave * NB * 1024 + ln * 64 + lg * 16);
+    const uint32_t hdr_lane = (uint32_t)(L::SB0 + L::S_BYTES + wave * 256 * NB + ln * 16);
+
+    f4 acc[MBK][NB];
+#pragma unroll
+    for (int i = 0; i < MBK; i++)
+#pragma unroll
+        for (int j = 0; j < NB; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+    h8 fa[MBK], fb[NB], fbn[NB], bm[NB];
+    float rr[NB];
+    u4v raw[NB], hd[NB];
+    uint32_t sws[NB][2], pm[NB][4];
+    float cprev[NB];
+#pragma unroll
+    for (int j = 0; j < NB; j++) cprev[j] = 1.0f;
+
+    auto read_hdr = [&](int u) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < NB; j++) hd[j] = rb_ld16(lds0 + (uint32_t)((u % NSB) * L::SBS) + hdr_lane + (uint32_t)(j * 256));
+    };
+    // super-block values of column 16j + ln (from hd[j]; every lane of the column holds its header):
+    // scale words of sub-blocks 0-3 / 4-7 (zero where d = 0), the lane's min-term B fragment for
+    // sub-blocks 2lg, 2lg + 1 ((hi, hi), (lo, lo) bf16 pairs of x = -dmin m / c, matching the S
+    // fragment's (hi, lo), (hi, lo) pairs) and the column's rescale ratio c_{u-1} / c_u
+    auto sb_col = [&](int j) __attribute__((always_inline)) {
+        const u4v h = hd[j];
+        uint32_t sw0, sw1, mw0, mw1;
+        q4k_scale_words(h.y, h.z, h.w, sw0, sw1, mw0, mw1);
+        const uint32_t nz = (h.x & 0x7fffu) ? 0xffffffffu : 0u;
+        sws[j][0] = sw0 & nz;
+        sws[j][1] = sw1 & nz;
+        const uint32_t mw = lg < 2 ? mw0 : mw1;
+        const float d = h2f((uint16_t)h.x), dmin = h2f((uint16_t)(h.x >> 16));
+        const float c = d != 0.0f ? d : 1.0f, inv = 1.0f / c;
+        const float x0 = (-dmin * (float)byte_of(mw, 2 * (lg & 1))) * inv;
+        const float x1 = (-dmin * (float)byte_of(mw, 2 * (lg & 1) + 1)) * inv;
+        const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
+        const __bf16 l0 = (__bf16)(x0 - (float)h0), l1 = (__bf16)(x1 - (float)h1);
+        const uint32_t uh0 = __builtin_bit_cast(uint16_t, h0), uh1 = __builtin_bit_cast(uint16_t, h1);
+        const uint32_t ul0 = __builtin_bit_cast(uint16_t, l0), ul1 = __builtin_bit_cast(uint16_t, l1);
+        bm[j] = __builtin_bit_cast(h8, u4v{uh0 * 0x10001u, ul0 * 0x10001u, uh1 * 0x10001u, ul1 * 0x10001u});
+        rr[j] = cprev[j] * inv;
+        cprev[j] = c;
+    };
+    // main decode parameters of stage half h: the lane's quant group p = 2h + lg/2 covers sub-blocks
+    // 2p (low nibbles: s, -1024 s) and 2p + 1 (high nibbles: s/16, -64 s)
+    auto make_pm = [&](int h) __attribute__((always_inline)) {
+        const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const h2 kmul = {(_Float16)1.0f, (_Float16)0.0625f}, kadd = {(_Float16)-1024.0f, (_Float16)-64.0f};
+        const uint32_t ssel = (lg >> 1) ? 0x04030402u : 0x04010400u;
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            const h2 sp = as_h2(__builtin_amdgcn_perm(0x64646464u, sws[j][h], ssel)) - k1024;
+            const h2 mu = sp * kmul, ad = sp * kadd;
+            pm[j][0] = __builtin_bit_cast(uint32_t, h2{mu.x, mu.x});
+            pm[j][1] = __builtin_bit_cast(uint32_t, h2{ad.x, ad.x});
+            pm[j][2] = __builtin_bit_cast(uint32_t, h2{mu.y, mu.y});
+            pm[j][3] = __builtin_bit_cast(uint32_t, h2{ad.y, ad.y});
+        }
+    };
+    auto read_raw = [&](int s) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < NB; j++) raw[j] = rb_ld16(lds0 + (uint32_t)((s % NSTG) * L::STG) + raw_lane + (uint32_t)(j * 1024));
+    };
+    auto decode_j = [&](int kk, int j) __attribute__((always_inline)) {
+        const u2v q = (kk & 1) ? u2v{raw[j].z, raw[j].w} : u2v{raw[j].x, raw[j].y};
+        if (kk >> 1) fbn[j] = decode8<true>(q, as_h2(pm[j][2]), as_h2(pm[j][3]));
+        else fbn[j] = decode8<false>(q, as_h2(pm[j][0]), as_h2(pm[j][1]));
+    };
+    auto mfma_row = [&](int i) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < NB; j++) acc[i][j] = mfma(fa[i], fb[j], acc[i][j]);
+    };
+    auto rescale_row = [&](int i) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < NB; j++) acc[i][j] *= rr[j];
+    };
+
+    // vector-memory items issued in stage s = 2u + h for stage t = s + D (if t < S2): S, H of super-block
+    // t / 2 + 1 when t is even (one super-block early: its values are computed during stage t + 1), then A 0..MBK-1 and B 0..NB-1 of stage t. They are spread over the
+    // groups of the stage's first k-steps (h = 0: min k-step and main k-steps 0-1; h = 1: main
+    // k-steps 0-1). count_t = the instructions of stage t.
+    auto count_t = [&](int t) __attribute__((always_inline)) {
+        return t < S2 ? MBK + NB + (((t & 1) == 0 && (t >> 1) + 1 < U) ? 2 : 0) : 0;
+    };
+    auto issue_at = [&](int u, auto hc, auto fc) __attribute__((always_inline)) {
+        constexpr int H = decltype(hc)::value, F = decltype(fc)::value;
+        constexpr bool SH = ((H + D) & 1) == 0;
+        constexpr int NI = (SH ? 2 : 0) + MBK + NB, G = (H == 0 ? 3 : 2) * MBK;
+        static_assert(NI <= G, "issue slots");
+        constexpr int n = (F * NI + G - 1) / G;
+        if constexpr (n < NI && (n * G) / NI == F) {
+            const int t = 2 * u + H + D;
+            if (t < S2) {
+                constexpr int it = SH ? n : n + 2;  // 0 = S, 1 = H, 2.. = A, then B
+                if constexpr (it == 0) {
+                    if ((t >> 1) + 1 < U) dma_s((t >> 1) + 1);
+                } else if constexpr (it == 1) {
+                    if ((t >> 1) + 1 < U) dma_h((t >> 1) + 1);
+                }
+                else if constexpr (it < 2 + MBK) {
+                    dma_a(t, it - 2);
+                } else {
+                    dma_b(t, it - 2 - MBK);
+                }
+            }
+        }
+    };
+    auto sched_fence = []() __attribute__((always_inline)) { __builtin_amdgcn_sched_barrier(0); };
+
+    // ---- prologue: super-block 0's headers and sums, then stages 0 .. D - 1 as in the main loop
+    dma_h(0);
+    dma_s(0);
+    int n_pro = 0;
+    for (int t = 0; t < D && t < S2; t++) {
+        if ((t & 1) == 0 && (t >> 1) + 1 < U) {
+            dma_s((t >> 1) + 1);
+            dma_h((t >> 1) + 1);
+        }
+        for (int qq = 0; qq < MBK; qq++) dma_a(t, qq);
+#pragma unroll
+        for (int j = 0; j < NB; j++) dma_b(t, j);
+        n_pro += count_t(t);
+    }
+    wait_vmcnt(1 + n_pro);  // H(0)
+    read_hdr(0);
+#pragma unroll
+    for (int j = 0; j < NB; j++) sb_col(j);
+    make_pm(0);
+    wait_vmcnt(n_pro - count_t(0));  // stage 0
+    read_raw(0);
+#pragma unroll
+    for (int j = 0; j < NB; j++) decode_j(0, j);
+    rb_wait_lgkm();
+    __syncthreads();
+    {
+        const uint32_t sb = s_base(0);
+#pragma unroll
+        for (int i = 0; i < MBK; i++) fa[i] = rb_lds_pairs(sb + (uint32_t)(i * 16 * 32));
+    }
+
+    // ---- k-steps: 8 groups (row blocks) each, pinned in order by scheduling fences
+    // min k-step of super-block u (stage s = 2u): rescale + S x Bmin; reads stage s's kk = 0 A fragments
+    auto kmin = [&](auto mode, int u) __attribute__((always_inline)) {
+        const int s = 2 * u;
+        const uint32_t ab = a_base(s, 0);
+        rescale_row(0);
+        sched_fence();
+        sfor<0, MBK>([&](auto gc) __attribute__((always_inline)) {
+            constexpr int i = decltype(gc)::value;
+#pragma unroll
+            for (int j = 0; j < NB; j++) {
+                acc[i][j] = mfma_bf16(fa[i], bm[j], acc[i][j]);
+            }
+            if constexpr (i + 1 < MBK) rescale_row(i + 1);
+            fa[i] = rb_ld8(ab + (uint32_t)(i * 16 * 256));
+            issue_at(u, std::integral_constant<int, 0>{}, std::integral_constant<int, i>{});
+            sched_fence();
+        });
+#pragma unroll
+        for (int j = 0; j < NB; j++) fb[j] = fbn[j];
+    };
+    // main k-step kk < 3 of stage s = 2u + h (k = kk + 1): decodes kk + 1's B fragments (block j in
+    // group 2j), reads its A fragments; in k-step 2 waits for the previous stage's DMAs (group 5),
+    // reads the next stage's quant bytes and receives its decode parameters (group 6). In stage
+    // 2u + 1 of a super-block with a successor, k-steps 0-1 compute the next super-block's values.
+    auto kmain = [&](auto mode, auto hc, int u, auto kc, auto nvc) __attribute__((always_inline)) {
+        constexpr int MODE = decltype(mode)::value, H = decltype(hc)::value, KK = decltype(kc)::value;
+        constexpr int NV = decltype(nvc)::value;
+        constexpr bool MORE = !(MODE == 2 && H == 1);
+        const int s = 2 * u + H;
+        const uint32_t ab = a_base(s, KK + 1);
+        sfor<0, MBK>([&](auto gc) __attribute__((always_inline)) {
+            constexpr int i = decltype(gc)::value;
+            mfma_row(i);
+            fa[i] = rb_ld8(ab + (uint32_t)(i * 16 * 256));
+            if constexpr ((i & 1) == 0 && (i >> 1) < NB) decode_j(KK + 1, i >> 1);
+            if constexpr (KK < 2) issue_at(u, hc, std::integral_constant<int, (H == 0 ? MBK : 0) + MBK * KK + i>{});
+            if constexpr (H == 1 && MORE) {
+                if constexpr (KK == 0 && i == 1) read_hdr(u + 1);
+                if constexpr (KK == 0 && i == 3)
+#pragma unroll
+                    for (int j = 0; j < NB; j++) sb_col(j);
+            }
+            if constexpr (KK == 2 && i == 0 && MORE) {
+                int nv = 0;
+#pragma unroll
+                for (int t = 2; t <= D; t++) nv += count_t(s + t);
+                wait_vmcnt(nv);
+                read_raw(s + 1);
+            }
+            if constexpr (KK == 2 && i == 1 && MORE) make_pm(H == 0 ? 1 : 0);
+            sched_fence();
+        });
+#pragma unroll
+        for (int j = 0; j < NB; j++) fb[j] = fbn[j];
+    };
+    // last k-step of stage s: groups 0-3 (decoding the next stage's first B fragments), the stage
+    // hand-off (every wave done with stage s; its DMAs for stage s + 1 landed), the next stage's
+    // first A (or S) fragments, groups 4-7
+    auto klast = [&](auto mode, auto hc, int u) __attribute__((always_inline)) {
+        constexpr int MODE = decltype(mode)::value, H = decltype(hc)::value;
+        constexpr bool MORE = !(MODE == 2 && H == 1), NSB = H == 1;
+        const int s = 2 * u + H;
+        sfor<0, HG>([&](auto gc) __attribute__((always_inline)) {
+            constexpr int i = decltype(gc)::value;
+            mfma_row(i);
+            if constexpr (MORE && i == 1)
+#pragma unroll
+                for (int j = 0; j < NB; j++) decode_j(0, j);
+            sched_fence();
+        });
+        rb_wait_lgkm();
+        __syncthreads();
+        uint32_t nb = 0;
+        constexpr uint32_t nstep = NSB ? 16u * 32u : 16u * 256u;
+        if constexpr (MORE) {
+            nb = NSB ? s_base(u + 1) : a_base(s + 1, 0);
+#pragma unroll
+            for (int i = 0; i < HG; i++) fa[i] = NSB ? rb_lds_pairs(nb + (uint32_t)i * nstep) : rb_ld8(nb + (uint32_t)i * nstep);
+        }
+        sched_fence();
+        sfor<HG, MBK>([&](auto gc) __attribute__((always_inline)) {
+            constexpr int i = decltype(gc)::value;
+            mfma_row(i);
+            if constexpr (MORE) fa[i] = NSB ? rb_lds_pairs(nb + (uint32_t)i * nstep) : rb_ld8(nb + (uint32_t)i * nstep);
+            sched_fence();
+        });
+        if constexpr (MORE && !NSB)
+#pragma unroll
+            for (int j = 0; j < NB; j++) fb[j] = fbn[j];
+    };
+    using i0 = std::integral_constant<int, 0>;
+    using i1 = std::integral_constant<int, 1>;
+    using i2 = std::integral_constant<int, 2>;
+    auto sb_body = [&](auto mode, int u) __attribute__((always_inline)) {
+        constexpr int MODE = decltype(mode)::value;
+        using nv0 = std::integral_constant<int, MODE == 0 ? 2 + MBK + NB : MODE == 1 ? MBK + NB : 0>;
+        using nv1 = std::integral_constant<int, MODE == 2 ? 0 : MBK + NB>;
+        kmin(mode, u);
+        kmain(mode, i0{}, u, i0{}, nv0{});
+        kmain(mode, i0{}, u, i1{}, nv0{});
+        kmain(mode, i0{}, u, i2{}, nv0{});
+        klast(mode, i0{}, u);
+        kmain(mode, i1{}, u, i0{}, nv1{});
+        kmain(mode, i1{}, u, i1{}, nv1{});
+        kmain(mode, i1{}, u, i2{}, nv1{});
+        klast(mode, i1{}, u);
+    };
+    int u = 0;
+    for (; u + 2 < U; u++) sb_body(std::integral_constant<int, 0>{}, u);
+    if (U >= 2) sb_body(std::integral_constant<int, 1>{}, U - 2);
+    sb_body(std::integral_constant<int, 2>{}, U - 1);
+
+    // back to true units: x c of the last super-block (the lane's column of each block)
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int i = 0; i < MBK; i++) acc[i][j] *= cprev[j];
+    // epilogue through LDS (the stage slots are free: every wave passed the last barrier). With two
+    // pipelines, the odd super-blocks' tile is parked first and added to the even ones' (fixed order).
+    constexpr int LD = BN + 4;
+    auto tile_at = [&](int i, int j, int e) __attribute__((always_inline)) {
+        const int r = 16 * i + 4 * lg + e, c = 16 * NB * wave + 16 * j + ln;
+        return (float *)(lds + (r * LD + c) * 4);
+    };
+    if constexpr (PIPE == 2) {
+        if (kh == 1)
+#pragma unroll
+            for (int i = 0; i < MBK; i++)
+#pragma unroll
+                for (int j = 0; j < NB; j++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) *tile_at(i, j, e) = acc[i][j][e];
+        rb_wait_lgkm();
+        __syncthreads();
+    }
+    if (kh == 0)
+#pragma unroll
+        for (int i = 0; i < MBK; i++)
+#pragma unroll
+            for (int j = 0; j < NB; j++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float *t = tile_at(i, j, e);
+                    *t = PIPE == 2 ? acc[i][j][e] + *t : acc[i][j][e];
+                }
+    rb_wait_lgkm();
+    __syncthreads();
+    constexpr int CH = BN / 8;
+    const bool wide = (N & 7) == 0 && ((uintptr_t)g.C & 15u) == 0;
+    for (int c = tid; c < BM * CH; c += RB_NT * PIPE) {
+        const int row = c / CH, ch = c - row * CH, m = m0 + row, n = n0 + 8 * ch;
+        if (m >= M || n >= N) continue;
+        const f4 v0 = *(const f4 *)(lds + (row * LD + 8 * ch) * 4), v1 = *(const f4 *)(lds + (row * LD + 8 * ch + 4) * 4);
+        const size_t idx = (size_t)m * N + n;
+        if (wide && n + 8 <= N) {
+            if (g.c_f32) {
+                f4 *p = (f4 *)((float *)g.C + idx);
+                p[0] = g.accumulate ? p[0] + v0 : v0;
+                p[1] = g.accumulate ? p[1] + v1 : v1;
+            } else {
+                h8 *p = (h8 *)((_Float16 *)g.C + idx);
+                f4 a0 = v0, a1 = v1;
+                if (g.accumulate) {
+                    const h8 o = *p;
+                    a0 += f4{(float)o[0], (float)o[1], (float)o[2], (float)o[3]};
+                    a1 += f4{(float)o[4], (float)o[5], (float)o[6], (float)o[7]};
+                }
+                *p = h8{(_Float16)a0.x, (_Float16)a0.y, (_Float16)a0.z, (_Float16)a0.w,
+                        (_Float16)a1.x, (_Float16)a1.y, (_Float16)a1.z, (_Float16)a1.w};
+            }
+        } else {
+            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            for (int e = 0; e < 8 && n + e < N; e++) store_out(g.C, idx + e, v[e], g.c_f32, g.accumulate);
+        }
+    }
+}
+}  // namespace
+
+
+int hq_rb_fits(int M, int N, int K) {
+    return M > 32 && M <= 64 && N >= 8192 && K % 512 == 0 && (size_t)M * K * 2 < ((size_t)1 << 32) &&
+           (size_t)N * (K / 256) * 144 < ((size_t)1 << 32);
+}
+
+hipError_t hq_launch_gemm_rb(const hq_dev_mat *W, const uint16_t *A, const uint16_t *S, int M, void *C, int c_f32,
+                             int accumulate, hipStream_t st) {
+    if (W->type != HQ_TYPE_Q4_K || !hq_rb_fits(M, (int)W->rows, (int)W->cols)) return hipErrorInvalidValue;
+    RbArgs g;
+    g.W = W->qs, g.row_bytes = (uint32_t)W->row_bytes, g.A = A, g.S = S;
+    g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;
+    g.mt = 1;
+    g.nt = (g.N + 63) / 64;
+    const unsigned grid = (unsigned)(8 * ((g.nt + 7) / 8));
+    k_gemm_q4_k_rb<1, 4, 3, 2><<<grid, 2 * RB_NT, 0, st>>>(g);
+    return hipGetLastError();
+}

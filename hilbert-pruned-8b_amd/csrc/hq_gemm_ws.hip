@@ -86,20 +86,6 @@ DEV void l2_touch(rsrc_t r, uint32_t voff, uint32_t lds_addr) {
                  : "memory");
 }
 
-// Eight fp16 B values s*q for 8 consecutive k from the low (HI = false) or high nibbles of 8 bytes:
-// masked bytes under 0x64 are fp16 1024 + q (or 1024 + 16q); one fma with (s, -1024 s) (or
-// (s/16, -64 s)) gives the exact integer.
-template <bool HI>
-DEV h8 decode8(u2v q, h2 mul, h2 add) {
-    const uint32_t mask = HI ? 0xf0f0f0f0u : 0x0f0f0f0fu;
-    const uint32_t w0 = q.x & mask, w1 = q.y & mask;
-    const h2 v0 = __builtin_elementwise_fma(as_h2(perm_lo(w0)), mul, add);
-    const h2 v1 = __builtin_elementwise_fma(as_h2(perm_hi(w0)), mul, add);
-    const h2 v2 = __builtin_elementwise_fma(as_h2(perm_lo(w1)), mul, add);
-    const h2 v3 = __builtin_elementwise_fma(as_h2(perm_hi(w1)), mul, add);
-    return h8{v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
-}
-
 // Epilogue through LDS. The output leaves the consumers' MFMA layout (lane (ln, lg) of block (i, j):
 // row 16i + ln, 4 consecutive columns) as 16-byte pieces of 16 rows, which the memory system writes
 // as partial lines; instead the consumers park the fp32 tile in LDS (rows padded by 4 floats against

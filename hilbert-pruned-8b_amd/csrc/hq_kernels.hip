@@ -1269,7 +1269,7 @@ __global__ void __launch_bounds__(512) k_gemm_q4_k_w(GemmArgs g) {
 // fp32 sum of activations 256u + 32s .. +32 of row m, in fp16 (BF16 = false: the Stream-K kernel)
 // or bf16 (the full-K tile kernel). One thread per sub-block (four 16-byte loads, 32-bit index math;
 // M * K / 32 < 2^31 is checked by the launcher).
-template <bool BF16>
+template <bool BF16, bool PAIR = false>
 __global__ void __launch_bounds__(256) k_asums(const uint16_t *__restrict__ A, int M, int K,
                                                uint16_t *__restrict__ S) {
     const uint32_t kb = (uint32_t)K / 32u, n = (uint32_t)M * kb;
@@ -1288,9 +1288,15 @@ __global__ void __launch_bounds__(256) k_asums(const uint16_t *__restrict__ A, i
             hb = __builtin_bit_cast(uint16_t, hi);
             lb = __builtin_bit_cast(uint16_t, (_Float16)(v - (float)hi));
         }
-        uint16_t *dst = S + ((size_t)m * (kb / 8) + s / 8) * 16 + (s % 8);
-        dst[0] = hb;
-        dst[8] = lb;
+        if constexpr (PAIR) {  // [M][K/256][8][hi, lo] (mid-M kernel)
+            uint16_t *dst = S + ((size_t)m * (kb / 8) + s / 8) * 16 + 2 * (s % 8);
+            dst[0] = hb;
+            dst[1] = lb;
+        } else {  // [M][K/256][hi x 8, lo x 8]
+            uint16_t *dst = S + ((size_t)m * (kb / 8) + s / 8) * 16 + (s % 8);
+            dst[0] = hb;
+            dst[8] = lb;
+        }
     }
 }
 
@@ -1439,6 +1445,7 @@ struct GemmCfg {
     int ws_parts;  // with ws_nb: workgroups per tile, each a contiguous range of K (1: whole K)
     int ws8_nb;  // > 0: the Q8_0 full-K tile kernel k_gemm_q8_0_ws, 32 * ws8_nb columns per tile
     int ws8_parts;  // with ws8_nb: workgroups per tile (K split, as ws_parts)
+    bool rbm;       // Q4_K mid M: the full-K 64 x 64 tile kernel k_gemm_q4_k_rb (hq_gemm_rb.hip)
 };
 
 // Q4_K with M > 64 runs the full-K tile kernel when its tiles fit in one round on the CUs and fill
@@ -1455,6 +1462,7 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
     c.waves = c.wide ? WNW : 4;
     c.ws_nb = 0;
     c.ws_parts = 1;
+    c.rbm = W->type == HQ_TYPE_Q4_K && hq_rb_fits(M, (int)W->rows, (int)W->cols);
     if (c.wide && (size_t)M * W->cols * 2 < ((size_t)1 << 32)) {
         float eff = 0.f;
         const int nb = hq_ws_choose(M, (int)W->rows, n_cu, &eff);
@@ -1511,8 +1519,8 @@ void hq_gemm_tile_shape(int type, int M, int N, int K, int n_cu, int *rows, int 
     W.rows = (uint32_t)N;
     W.cols = (uint32_t)K;
     const GemmCfg c = gemm_cfg(&W, M, n_cu);
-    *rows = c.ws_nb || c.ws8_nb ? 128 : 16 * c.mb;
-    *cols = c.ws_nb ? 32 * c.ws_nb : c.ws8_nb ? 32 * c.ws8_nb : 16 * c.nb * c.waves;
+    *rows = c.rbm ? 64 : c.ws_nb || c.ws8_nb ? 128 : 16 * c.mb;
+    *cols = c.rbm ? 64 : c.ws_nb ? 32 * c.ws_nb : c.ws8_nb ? 32 * c.ws8_nb : 16 * c.nb * c.waves;
 }
 
 // Name of the kernel that does the work of an M x N x K hq_gemm call (the main kernel for GEMMs
@@ -1531,7 +1539,8 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
         return;
     }
     const GemmCfg c = gemm_cfg(&W, M, n_cu);
-    if (c.ws_nb) snprintf(buf, n, "k_gemm_q4_k_ws<%d>", c.ws_nb);
+    if (c.rbm) snprintf(buf, n, "k_gemm_q4_k_rb<1, 4, 3, 2>");
+    else if (c.ws_nb) snprintf(buf, n, "k_gemm_q4_k_ws<%d>", c.ws_nb);
     else if (c.ws8_nb) snprintf(buf, n, "k_gemm_q8_0_ws<%d>", c.ws8_nb);
     else if (c.wide) snprintf(buf, n, "k_gemm_q4_k_w<%d>", c.mb);  // template argument: row blocks
     else snprintf(buf, n, "%s<%d, %d>", type == HQ_TYPE_Q4_K ? "k_gemm_q4_k" : "k_gemm_q8_0", c.mb, c.nb);
@@ -1550,12 +1559,16 @@ void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_by
         *partial_bytes = tiles * sparts * 128 * 32 * snb * sizeof(float);
         *counter_bytes = tiles * sizeof(int);
     }
-    *sums_bytes = c.wide ? (size_t)M * (W->cols / KC) * 32 : 0;
+    *sums_bytes = c.wide || c.rbm ? (size_t)M * (W->cols / KC) * 32 : 0;
 }
 
 // Pre-pass of a GEMM (the wide Q4_K kernel's activation sub-block sums; nothing otherwise).
 hipError_t hq_launch_gemm_pre(const hq_dev_mat *W, const uint16_t *A, int M, const HqGemmWork &wk, hipStream_t st) {
     const GemmCfg c = gemm_cfg(W, M, wk.n_cu);
+    if (c.rbm) {
+        const size_t nsub = (size_t)M * (W->cols / 32);
+        k_asums<true, true><<<grid_for(nsub, 256, 16384), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
+    }
     if (c.wide) {
         const size_t nsub = (size_t)M * (W->cols / 32);
         if (nsub >= ((size_t)1 << 31)) return hipErrorInvalidValue;
@@ -1569,6 +1582,7 @@ hipError_t hq_launch_gemm_pre(const hq_dev_mat *W, const uint16_t *A, int M, con
 hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
                                const HqGemmWork &wk, hipStream_t st) {
     const GemmCfg c = gemm_cfg(W, M, wk.n_cu);
+    if (c.rbm) return hq_launch_gemm_rb(W, A, wk.sums, M, C, c_f32, accumulate, st);
     if (c.ws_nb)
         return hq_launch_gemm_ws(W, A, wk.sums, M, C, c_f32, accumulate, c.ws_nb, c.ws_parts, wk.partials, wk.counters, st);
     if (c.ws8_nb)
