@@ -492,3 +492,206 @@ hipError_t hq_launch_gemm_rb(const hq_dev_mat *W, const uint16_t *A, const uint1
     k_gemm_q4_k_rb<1, 4, 3, 2><<<grid, 2 * RB_NT, 0, st>>>(g);
     return hipGetLastError();
 }
+
+// ============================================================================ Q8_0, mid M
+// The same structure for Q8_0 (M <= 64, N >= 8192): 16 MBK x 64 full-K tiles, PIPE pipelines of
+// four waves taking 128-wide stages kh, kh + PIPE, ...; wave w decodes columns 16w .. 16w + 15. No
+// min term and no rescale: the B operand is fp16(q * d), one rounding of the exact weight (as in the
+// other Q8_0 kernels), from the biased byte u = q + 128 (fp16 1024 + u by v_perm_b32, minus 1152).
+// Per stage and pipeline, LDS holds the activation tile (rows of 256 B, 16-byte slot p of row r at
+// p ^ (r & 15)), the quant bytes of the wave's 16 columns (16-byte chunk c of column n at chunk
+// c ^ (n & 7)) and their scales (4 per column).
+namespace {
+struct Rb8Args {
+    const uint8_t *Q;   // quant plane [N][K], bytes u = q + 128
+    const uint16_t *D;  // fp16 scale plane [N][ldd]
+    int ldd;
+    const uint16_t *A;  // fp16 [M][K]
+    int M, N, K;
+    void *C;
+    int c_f32, accumulate;
+    int nt;  // N-tiles
+};
+
+template <int MBK, int NSTG>
+struct Rb8Lds {
+    static constexpr int BM = 16 * MBK;
+    static constexpr int A_BYTES = BM * RB_KS * 2;
+    static constexpr int Q_BYTES = 4 * 16 * RB_KS;  // [wave][16 cols][128 B]
+    static constexpr int D_BYTES = 4 * 16 * 16;     // [wave][16 cols][16 B] (scales of 2 stages; 4 used)
+    static constexpr int STG = A_BYTES + Q_BYTES + D_BYTES;
+    static constexpr int TOTAL = NSTG * STG;
+    static_assert(TOTAL % 256 == 0, "arena alignment");
+    static_assert(BM * 68 * 4 <= TOTAL, "epilogue tile");
+};
+
+// 8 fp16 B values fp16(q * d) from 8 stored bytes u = q + 128
+DEV h8 decode8_q8_0(u2v w, h2 d2) {
+    const h2 k1152 = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const h2 v0 = (as_h2(perm_lo(w.x)) - k1152) * d2, v1 = (as_h2(perm_hi(w.x)) - k1152) * d2;
+    const h2 v2 = (as_h2(perm_lo(w.y)) - k1152) * d2, v3 = (as_h2(perm_hi(w.y)) - k1152) * d2;
+    return h8{v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
+}
+
+using rb_lds_u2v = const __attribute__((address_space(3))) u2v;
+DEV u2v rb_ld64(uint32_t a) { return *(rb_lds_u2v *)(uintptr_t)a; }
+
+template <int MBK, int NSTG, int PIPE>
+__global__ void __launch_bounds__(RB_NT * PIPE) k_gemm_q8_0_rb(Rb8Args g) {
+    constexpr int BM = 16 * MBK, BN = 64;
+    using L = Rb8Lds<MBK, NSTG>;
+    __shared__ __attribute__((aligned(256))) char lds[L::TOTAL * PIPE];
+    const int b = blockIdx.x, nt_i = (b & 7) + 8 * (b >> 3);
+    if (nt_i >= g.nt) return;
+    const int n0 = nt_i * BN;
+    const int M = g.M, N = g.N, K = g.K, S2 = K / RB_KS / PIPE;  // this pipeline's stages
+    const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, lg = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 3), kh = __builtin_amdgcn_readfirstlane(tid >> 8);
+    auto rs = [&](int s) __attribute__((always_inline)) { return PIPE * s + kh; };  // real stage
+    const rsrc_t ra = make_rsrc(g.A, (uint32_t)((size_t)M * K * 2));
+    const rsrc_t rq = make_rsrc(g.Q, (uint32_t)((size_t)N * K));
+    const rsrc_t rd = make_rsrc(g.D, (uint32_t)((size_t)N * g.ldd * 2));
+    const uint32_t lds0 = (uint32_t)(uintptr_t)lds + (uint32_t)(kh * L::TOTAL);
+    const int nw = n0 + 16 * wave;
+
+    // DMAs of stage s (MBK + 3 per wave): activation rows 4(wave + 4qq) .. + 3 (1 KB each); quant
+    // bytes of columns nw + 8h .. + 7 (lane l: column l / 8, LDS chunk l % 8 <- global chunk
+    // (l % 8) ^ (column & 7)); the 16 columns' scales (16 lanes, 16 bytes from the stage's first)
+    const int arow = 4 * wave + (lane >> 4);
+    const uint32_t a_voff = ((uint32_t)arow * (uint32_t)K + 8u * (uint32_t)((lane & 15) ^ (arow & 15))) * 2u;
+    const uint32_t a_qq = 16u * (uint32_t)K * 2u;
+    uint32_t q_voff[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int c = 8 * h + (lane >> 3);
+        q_voff[h] = (uint32_t)(nw + c) * (uint32_t)K + 16u * (uint32_t)((lane & 7) ^ (c & 7));
+    }
+    const uint32_t d_voff = (uint32_t)(nw + (lane & 15)) * (uint32_t)g.ldd * 2u;
+    auto slot = [&](int s) __attribute__((always_inline)) { return lds0 + (uint32_t)((s % NSTG) * L::STG); };
+    auto issue_stage = [&](int s) __attribute__((always_inline)) {
+        const uint32_t sl = slot(s);
+        for (int qq = 0; qq < MBK; qq++)
+            dma16_so(ra, sl + (uint32_t)((wave + 4 * qq) * 1024), a_voff + (uint32_t)qq * a_qq, (uint32_t)(rs(s) * RB_KS * 2));
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            dma16_so(rq, sl + (uint32_t)(L::A_BYTES + wave * 2048 + h * 1024), q_voff[h], (uint32_t)(rs(s) * RB_KS));
+        if (lane < 16)
+            dma16_so(rd, sl + (uint32_t)(L::A_BYTES + L::Q_BYTES + wave * 256), d_voff, (uint32_t)(rs(s) * 8));
+    };
+    constexpr int NI = MBK + 3;
+
+    // operand addresses: A fragment i of k-step kk: row 16i + ln, slot (4kk + lg) ^ ln; quant bytes of
+    // k-step kk: column ln, bytes 32kk + 8lg .. + 7 (chunk 2kk + lg/2, stored at chunk ^ (ln & 7))
+    const uint32_t a_lane = (uint32_t)(ln * 256) + 16u * (uint32_t)(lg ^ ln);
+    const uint32_t q_lane = (uint32_t)(L::A_BYTES + wave * 2048 + ln * RB_KS + 8 * (lg & 1));
+    const uint32_t d_lane = (uint32_t)(L::A_BYTES + L::Q_BYTES + wave * 256 + ln * 16);
+
+    f4 acc[MBK];
+#pragma unroll
+    for (int i = 0; i < MBK; i++) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
+
+    for (int s = 0; s < NSTG - 1 && s < S2; s++) issue_stage(s);
+    for (int s = 0; s < S2; s++) {
+        // this wave's DMAs of stage s have landed (those of the later stages issued so far may not)
+        const int later = (s + NSTG - 2 < S2 - 1 ? s + NSTG - 2 : S2 - 1) - s;
+        wait_vmcnt(NI * later);
+        rb_wait_lgkm();
+        __syncthreads();  // every wave's stage-s DMAs landed; every wave done with stage s - 1
+        if (s + NSTG - 1 < S2) issue_stage(s + NSTG - 1);
+        const uint32_t sl = slot(s);
+        const u2v dd = rb_ld64(sl + d_lane);  // the column's 4 block scales of the stage
+        h8 fa[4][MBK], fb[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+#pragma unroll
+            for (int i = 0; i < MBK; i++) fa[kk][i] = rb_ld8(sl + (uint32_t)(i * 16 * 256) + (a_lane ^ (uint32_t)(64 * kk)));
+            const uint32_t chunk = (uint32_t)(2 * kk + (lg >> 1)) ^ (uint32_t)(ln & 7);
+            const u2v w = rb_ld64(sl + q_lane + 16u * chunk);
+            const uint32_t dw = (kk & 2) ? dd.y : dd.x;
+            const uint16_t dh = (uint16_t)((kk & 1) ? (dw >> 16) : (dw & 0xffffu));
+            const _Float16 d = __builtin_bit_cast(_Float16, dh);
+            fb[kk] = decode8_q8_0(w, h2{d, d});
+        }
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+            for (int i = 0; i < MBK; i++) acc[i] = mfma(fa[kk][i], fb[kk], acc[i]);
+    }
+
+    // epilogue: pipeline 1's tile is parked in LDS and added to pipeline 0's (fixed order); the
+    // lane's accumulators are rows 16i + 4lg + e of column 16 wave + ln
+    constexpr int LD = BN + 4;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    rb_wait_lgkm();
+    __syncthreads();
+    auto tile_at = [&](int i, int e) __attribute__((always_inline)) {
+        return (float *)(lds + ((16 * i + 4 * lg + e) * LD + 16 * wave + ln) * 4);
+    };
+    if constexpr (PIPE == 2) {
+        if (kh == 1)
+#pragma unroll
+            for (int i = 0; i < MBK; i++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) *tile_at(i, e) = acc[i][e];
+        rb_wait_lgkm();
+        __syncthreads();
+    }
+    if (kh == 0)
+#pragma unroll
+        for (int i = 0; i < MBK; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float *t = tile_at(i, e);
+                *t = PIPE == 2 ? acc[i][e] + *t : acc[i][e];
+            }
+    rb_wait_lgkm();
+    __syncthreads();
+    constexpr int CH = BN / 8;
+    const bool wide = (N & 7) == 0 && ((uintptr_t)g.C & 15u) == 0;
+    for (int c = tid; c < BM * CH; c += RB_NT * PIPE) {
+        const int row = c / CH, ch = c - row * CH, m = row, n = n0 + 8 * ch;
+        if (m >= M || n >= N) continue;
+        const f4 v0 = *(const f4 *)(lds + (row * LD + 8 * ch) * 4), v1 = *(const f4 *)(lds + (row * LD + 8 * ch + 4) * 4);
+        const size_t idx = (size_t)m * N + n;
+        if (wide && n + 8 <= N) {
+            if (g.c_f32) {
+                f4 *p = (f4 *)((float *)g.C + idx);
+                p[0] = g.accumulate ? p[0] + v0 : v0;
+                p[1] = g.accumulate ? p[1] + v1 : v1;
+            } else {
+                h8 *p = (h8 *)((_Float16 *)g.C + idx);
+                f4 a0 = v0, a1 = v1;
+                if (g.accumulate) {
+                    const h8 o = *p;
+                    a0 += f4{(float)o[0], (float)o[1], (float)o[2], (float)o[3]};
+                    a1 += f4{(float)o[4], (float)o[5], (float)o[6], (float)o[7]};
+                }
+                *p = h8{(_Float16)a0.x, (_Float16)a0.y, (_Float16)a0.z, (_Float16)a0.w,
+                        (_Float16)a1.x, (_Float16)a1.y, (_Float16)a1.z, (_Float16)a1.w};
+            }
+        } else {
+            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            for (int e = 0; e < 8 && n + e < N; e++) store_out(g.C, idx + e, v[e], g.c_f32, g.accumulate);
+        }
+    }
+}
+}  // namespace
+
+int hq_rb8_fits(int M, int N, int K) {
+    return M >= 2 && M <= 64 && N >= 8192 && K % 256 == 0 && (size_t)64 * K * 2 < ((size_t)1 << 32) &&
+           ((size_t)N + 64) * K < ((size_t)1 << 32);
+}
+
+hipError_t hq_launch_gemm_rb8(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
+                              hipStream_t st) {
+    if (W->type != HQ_TYPE_Q8_0 || !hq_rb8_fits(M, (int)W->rows, (int)W->cols)) return hipErrorInvalidValue;
+    Rb8Args g;
+    g.Q = W->qs, g.D = W->d, g.ldd = W->ldd, g.A = A;
+    g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;
+    g.nt = (g.N + 63) / 64;
+    const unsigned grid = (unsigned)(8 * ((g.nt + 7) / 8));
+    if (M <= 16) k_gemm_q8_0_rb<1, 3, 2><<<grid, 2 * RB_NT, 0, st>>>(g);
+    else if (M <= 32) k_gemm_q8_0_rb<2, 3, 2><<<grid, 2 * RB_NT, 0, st>>>(g);
+    else k_gemm_q8_0_rb<4, 3, 2><<<grid, 2 * RB_NT, 0, st>>>(g);
+    return hipGetLastError();
+}

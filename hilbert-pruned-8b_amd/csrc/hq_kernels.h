@@ -59,6 +59,10 @@ hipError_t hq_launch_gemm_ws(const hq_dev_mat *W, const uint16_t *A, const uint1
 int hq_rb_fits(int M, int N, int K);
 hipError_t hq_launch_gemm_rb(const hq_dev_mat *W, const uint16_t *A, const uint16_t *S, int M, void *C, int c_f32,
                              int accumulate, hipStream_t st);
+// Mid-M Q8_0 GEMM (hq_gemm_rb.hip): 2 <= M <= 64, N >= 8192, K a multiple of 256; no pre-pass.
+int hq_rb8_fits(int M, int N, int K);
+hipError_t hq_launch_gemm_rb8(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
+                              hipStream_t st);
 hipError_t hq_launch_gemm_ws8(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
                               int nb, int parts, float *partials, int *counters, hipStream_t st);
 

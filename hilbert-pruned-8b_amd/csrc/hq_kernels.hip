@@ -1446,6 +1446,7 @@ struct GemmCfg {
     int ws8_nb;  // > 0: the Q8_0 full-K tile kernel k_gemm_q8_0_ws, 32 * ws8_nb columns per tile
     int ws8_parts;  // with ws8_nb: workgroups per tile (K split, as ws_parts)
     bool rbm;       // Q4_K mid M: the full-K 64 x 64 tile kernel k_gemm_q4_k_rb (hq_gemm_rb.hip)
+    bool rb8;       // Q8_0 M <= 64: the full-K tile kernel k_gemm_q8_0_rb (hq_gemm_rb.hip)
 };
 
 // Q4_K with M > 64 runs the full-K tile kernel when its tiles fit in one round on the CUs and fill
@@ -1463,6 +1464,7 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
     c.ws_nb = 0;
     c.ws_parts = 1;
     c.rbm = W->type == HQ_TYPE_Q4_K && hq_rb_fits(M, (int)W->rows, (int)W->cols);
+    c.rb8 = W->type == HQ_TYPE_Q8_0 && hq_rb8_fits(M, (int)W->rows, (int)W->cols);
     if (c.wide && (size_t)M * W->cols * 2 < ((size_t)1 << 32)) {
         float eff = 0.f;
         const int nb = hq_ws_choose(M, (int)W->rows, n_cu, &eff);
@@ -1519,8 +1521,8 @@ void hq_gemm_tile_shape(int type, int M, int N, int K, int n_cu, int *rows, int 
     W.rows = (uint32_t)N;
     W.cols = (uint32_t)K;
     const GemmCfg c = gemm_cfg(&W, M, n_cu);
-    *rows = c.rbm ? 64 : c.ws_nb || c.ws8_nb ? 128 : 16 * c.mb;
-    *cols = c.rbm ? 64 : c.ws_nb ? 32 * c.ws_nb : c.ws8_nb ? 32 * c.ws8_nb : 16 * c.nb * c.waves;
+    *rows = c.rbm ? 64 : c.rb8 ? (M <= 16 ? 16 : M <= 32 ? 32 : 64) : c.ws_nb || c.ws8_nb ? 128 : 16 * c.mb;
+    *cols = c.rbm || c.rb8 ? 64 : c.ws_nb ? 32 * c.ws_nb : c.ws8_nb ? 32 * c.ws8_nb : 16 * c.nb * c.waves;
 }
 
 // Name of the kernel that does the work of an M x N x K hq_gemm call (the main kernel for GEMMs
@@ -1540,6 +1542,7 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
     }
     const GemmCfg c = gemm_cfg(&W, M, n_cu);
     if (c.rbm) snprintf(buf, n, "k_gemm_q4_k_rb<1, 4, 3, 2>");
+    else if (c.rb8) snprintf(buf, n, "k_gemm_q8_0_rb<%d, 3, 2>", M <= 16 ? 1 : M <= 32 ? 2 : 4);
     else if (c.ws_nb) snprintf(buf, n, "k_gemm_q4_k_ws<%d>", c.ws_nb);
     else if (c.ws8_nb) snprintf(buf, n, "k_gemm_q8_0_ws<%d>", c.ws8_nb);
     else if (c.wide) snprintf(buf, n, "k_gemm_q4_k_w<%d>", c.mb);  // template argument: row blocks
@@ -1583,6 +1586,7 @@ hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, vo
                                const HqGemmWork &wk, hipStream_t st) {
     const GemmCfg c = gemm_cfg(W, M, wk.n_cu);
     if (c.rbm) return hq_launch_gemm_rb(W, A, wk.sums, M, C, c_f32, accumulate, st);
+    if (c.rb8) return hq_launch_gemm_rb8(W, A, M, C, c_f32, accumulate, st);
     if (c.ws_nb)
         return hq_launch_gemm_ws(W, A, wk.sums, M, C, c_f32, accumulate, c.ws_nb, c.ws_parts, wk.partials, wk.counters, st);
     if (c.ws8_nb)

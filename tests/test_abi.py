@@ -76,7 +76,8 @@ def test_gemm_kernel_names():
              (synth.Q4_K, 512, 2560, 9728): "k_gemm_q4_k_ws<5>", (synth.Q4_K, 256, 2560, 9728): "k_gemm_q4_k_ws<3>",
              (synth.Q4_K, 512, 1024, 2560): "k_gemm_q4_k_w<8>", (synth.Q4_K, 4096, 2560, 9728): "k_gemm_q4_k_w<8>",
              (synth.Q8_0, 512, 2560, 9728): "k_gemm_q8_0_ws<5>", (synth.Q8_0, 256, 2560, 9728): "k_gemm_q8_0_ws<3>",
-             (synth.Q8_0, 16, 9728, 2560): "k_gemm_q8_0<1, 2>", (synth.Q4_K, 1, 9728, 2560): "k_gemv_q4_k_r<4>",
+             (synth.Q8_0, 16, 9728, 2560): "k_gemm_q8_0_rb<1, 3, 2>", (synth.Q8_0, 64, 9728, 2560): "k_gemm_q8_0_rb<4, 3, 2>",
+             (synth.Q8_0, 16, 2560, 9728): "k_gemm_q8_0<1, 2>", (synth.Q4_K, 1, 9728, 2560): "k_gemv_q4_k_r<4>",
              (synth.Q4_K, 1, 2560, 9728): "k_gemv_q4_k_s<4>", (synth.Q4_K, 1, 100, 512): "k_gemv_q4_k_s<1>",
              (synth.Q4_K, 1, 9728, 256): "k_gemv_q4_k_s<16>", (synth.Q8_0, 1, 9728, 2560): "k_gemv_q8_0<2>",
              (synth.Q8_0, 1, 100, 512): "k_gemv_q8_0<1>"}
@@ -100,6 +101,9 @@ def test_gemm_tile_selection():
                 # Q8_0 above M = 64: full-K tiles of 128 x 32NB when they fill >= 50 % of the CU
                 # time (any number of rounds), else the narrow Stream-K kernel
                 assert c == 128 or (r == 128 and c in (64, 96, 128, 160))
+            elif gtype == synth.Q8_0:
+                # Q8_0 up to M = 64 at N >= 8192: the mid-M kernel's full-K tiles of 16/32/64 x 64
+                assert (r, c) == (16 if M <= 16 else 32 if M <= 32 else 64, 64)
             else:
                 assert c == 128
     # Stream-K balances any tile count over the CUs (narrow Q8_0 / Q4_K, few Q4_K tiles)

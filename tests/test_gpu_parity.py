@@ -120,13 +120,16 @@ RAGGED = [(synth.Q8_0, 100, 512, M) for M in (1, 2, 5, 17, 33, 65, 200)] + \
          [(synth.Q8_0, 9500, 768, 500), (synth.Q8_0, 9728, 384, 512)] + \
          [(synth.Q4_K, 2560, 9728, 300), (synth.Q4_K, 2500, 4096, 300)] + \
          [(synth.Q8_0, 2560, 9728, 512), (synth.Q8_0, 2500, 8192, 300)] + \
-         [(synth.Q4_K, 8200, 1536, 40), (synth.Q4_K, 8192, 512, 33)]
+         [(synth.Q4_K, 8200, 1536, 40), (synth.Q4_K, 8192, 512, 33)] + \
+         [(synth.Q8_0, 8200, 1024, 5), (synth.Q8_0, 9728, 512, 40), (synth.Q8_0, 8192, 256, 30)]
 # (the last: full-K tiles; Stream-K with more tiles than CUs; the streamed GEMV with a ragged last
 # row group and an odd K split, with one wave per row group, and with an even split; the Q8_0 tile
 # kernel with ragged M and N, and with an odd number of 128-wide stages; the Q4_K tile kernel with
 # each tile's K split over 4 workgroups of 9 or 10 super-blocks, ragged M, and over 2 workgroups
 # with ragged M and N; the Q8_0 tile kernel with K split over 4 workgroups, also with ragged M, N;
-# the mid-M Q4_K kernel with a ragged last column tile and ragged M, and at M = 33 with K = 512)
+# the mid-M Q4_K kernel with a ragged last column tile and ragged M, and at M = 33 with K = 512; the
+# mid-M Q8_0 kernel with ragged N and M at each of its row-block counts, and with one stage per
+# pipeline)
 
 
 @pytest.mark.parametrize("gtype,N,K,M", FULL + RAGGED)
@@ -147,7 +150,8 @@ def test_gemm_parity(hqlib, oracle, gtype, N, K, M):
                                          (synth.Q4_K, 350, 9728, 256), (synth.Q4_K, 1, 8192, 1024),
                                          (synth.Q8_0, 512, 9728, 640), (synth.Q4_K, 512, 9728, 2560),
                                          (synth.Q8_0, 512, 9500, 2560), (synth.Q4_K, 512, 2560, 9728),
-                                         (synth.Q8_0, 512, 2560, 9728), (synth.Q4_K, 64, 9728, 2560)])
+                                         (synth.Q8_0, 512, 2560, 9728), (synth.Q4_K, 64, 9728, 2560),
+                                         (synth.Q8_0, 16, 9728, 2560)])
 def test_gemm_accumulate_and_fp16_output(hqlib, oracle, gtype, M, N, K):
     blocks = weights(gtype, N, K, 7)
     rng = synth.Rng(77 + M)
