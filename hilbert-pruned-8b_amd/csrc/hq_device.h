@@ -130,6 +130,95 @@ DEV h2 bytes_f16(uint32_t w, bool hi_pair) {
     return as_h2(hi_pair ? perm_hi(w) : perm_lo(w)) - k1024;
 }
 
+// End of a full-K tile kernel's tile, held in LDS as fp32 rows of LD floats (BM x BN, NT threads).
+// parts == 1: stored to C. parts > 1 (a K split, at most MAXP parts): every part stores its tile to
+// partials[tile][part] with device-scope (sc1) 16-byte stores, waits for them and counts itself in
+// on counters[tile]; the last of the tile's parts loads the others' in one round trip and adds all
+// of them in part order (its own from LDS in its place), so the sum is the same whichever part
+// arrives last, then writes C; the counter is left at zero. flag: an LDS word outside the tile.
+template <int BM, int BN, int NT, int MAXP, class Args>
+DEV void tile_finish(const char *lds, const Args &g, int m0, int n0, int tile, int part, int *flag) {
+    constexpr int LD = BN + 4, CH = BN / 8, CPT = BM * CH / NT;  // 8-value chunks per thread
+    static_assert(BM * CH == CPT * NT, "chunks per thread");
+    constexpr uint32_t TILE = BM * BN * 4;  // bytes per partial tile
+    const int M = g.M, N = g.N;
+    const bool wide = (N & 7) == 0 && ((uintptr_t)g.C & 15u) == 0;
+    f4 pv[MAXP][CPT][2];
+    if (g.parts > 1) {
+        const rsrc_t rp = make_rsrc(g.partials, (uint32_t)g.ntiles * (uint32_t)g.parts * TILE);
+        const uint32_t own = ((uint32_t)tile * (uint32_t)g.parts + (uint32_t)part) * TILE;
+#pragma unroll
+        for (int i = 0; i < CPT; i++) {
+            const int c = (int)threadIdx.x + NT * i, row = c / CH, ch = c - row * CH;
+            const uint32_t off = (uint32_t)(row * BN + 8 * ch) * 4u;
+            buf_store16(rp, *(const f4 *)(lds + (row * LD + 8 * ch) * 4), off, own);
+            buf_store16(rp, *(const f4 *)(lds + (row * LD + 8 * ch + 4) * 4), off + 16u, own);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const int last = atomicAdd(&g.counters[tile], 1) == g.parts - 1;
+            if (last) atomicExch(&g.counters[tile], 0);
+            *flag = last;
+        }
+        __syncthreads();
+        if (!*flag) return;
+#pragma unroll
+        for (int p = 0; p < MAXP; p++)
+#pragma unroll
+            for (int i = 0; i < CPT; i++) {
+                const int c = (int)threadIdx.x + NT * i, row = c / CH, ch = c - row * CH;
+                const uint32_t off = (uint32_t)(row * BN + 8 * ch) * 4u;
+                const uint32_t pb = ((uint32_t)tile * (uint32_t)g.parts + (uint32_t)p) * TILE;
+                if (p < g.parts && p != part) {
+                    pv[p][i][0] = buf_load16_sc1(rp, off, pb);
+                    pv[p][i][1] = buf_load16_sc1(rp, off + 16u, pb);
+                } else {
+                    pv[p][i][0] = *(const f4 *)(lds + (row * LD + 8 * ch) * 4);
+                    pv[p][i][1] = *(const f4 *)(lds + (row * LD + 8 * ch + 4) * 4);
+                }
+            }
+    }
+#pragma unroll
+    for (int i = 0; i < CPT; i++) {
+        const int c = (int)threadIdx.x + NT * i, row = c / CH, ch = c - row * CH, m = m0 + row, n = n0 + 8 * ch;
+        f4 v0, v1;
+        if (g.parts > 1) {
+            v0 = f4{0.f, 0.f, 0.f, 0.f}, v1 = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int p = 0; p < MAXP; p++)
+                if (p < g.parts) {
+                    v0 += pv[p][i][0];
+                    v1 += pv[p][i][1];
+                }
+        } else {
+            v0 = *(const f4 *)(lds + (row * LD + 8 * ch) * 4);
+            v1 = *(const f4 *)(lds + (row * LD + 8 * ch + 4) * 4);
+        }
+        if (m >= M || n >= N) continue;
+        const size_t idx = (size_t)m * N + n;
+        if (wide && n + 8 <= N) {
+            if (g.c_f32) {
+                f4 *q = (f4 *)((float *)g.C + idx);
+                q[0] = g.accumulate ? q[0] + v0 : v0;
+                q[1] = g.accumulate ? q[1] + v1 : v1;
+            } else {
+                h8 *q = (h8 *)((_Float16 *)g.C + idx);
+                if (g.accumulate) {
+                    const h8 o = *q;
+                    v0 += f4{(float)o[0], (float)o[1], (float)o[2], (float)o[3]};
+                    v1 += f4{(float)o[4], (float)o[5], (float)o[6], (float)o[7]};
+                }
+                *q = h8{(_Float16)v0.x, (_Float16)v0.y, (_Float16)v0.z, (_Float16)v0.w,
+                        (_Float16)v1.x, (_Float16)v1.y, (_Float16)v1.z, (_Float16)v1.w};
+            }
+        } else {
+            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            for (int e = 0; e < 8 && n + e < N; e++) store_out(g.C, idx + e, v[e], g.c_f32, g.accumulate);
+        }
+    }
+}
+
 // Quad permutes of one VGPR by DPP, written as inline assembly: this compiler merges
 // __builtin_amdgcn_mov_dpp / update_dpp calls that share a DPP control but read different
 // registers into one move of the first register (observed on gfx950, ROCm 7.2). The s_nop gives

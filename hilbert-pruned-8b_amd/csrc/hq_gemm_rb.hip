@@ -39,6 +39,12 @@ struct RbArgs {
     void *C;
     int c_f32, accumulate;
     int mt, nt;  // M-tiles, N-tiles
+    // K split (few tiles, long K): each tile's pairs of super-blocks are cut into `parts` ranges,
+    // one workgroup each, finished by tile_finish (partials[tile][part], per-tile counters)
+    int parts;
+    float *partials;
+    int *counters;
+    int ntiles;
 };
 }  // namespace
 
@@ -99,19 +105,22 @@ __global__ void __launch_bounds__(RB_NT * PIPE) k_gemm_q4_k_rb(RbArgs g) {
     constexpr int NSB = L::NSB;
     static_assert(L::TOTAL % 256 == 0, "arena alignment");
     __shared__ __attribute__((aligned(256))) char lds[L::TOTAL * PIPE];
-    const int b = blockIdx.x, x = b & 7, j8 = b >> 3;
-    const int nt_i = x + 8 * (j8 / g.mt), mt_i = j8 % g.mt;
+    const int b = blockIdx.x, x = b & 7, j8 = b >> 3, per = g.mt * g.parts;
+    const int nt_i = x + 8 * (j8 / per), part = (j8 % per) / g.mt, mt_i = j8 % g.mt;
     if (nt_i >= g.nt) return;
     const int m0 = mt_i * BM, n0 = nt_i * BN;
-    // PIPE independent pipelines of 4 waves; pipeline kh takes super-blocks kh, kh + PIPE, ...
-    const int M = g.M, N = g.N, K = g.K, UT = K / 256, U = UT / PIPE, S2 = 2 * U;
+    // this part's super-blocks u0 .. u0 + PIPE U - 1 (whole groups of PIPE); the operand bases are
+    // moved to u0 (row strides stay K and UT). PIPE independent pipelines of 4 waves; pipeline kh
+    // takes the part's super-blocks kh, kh + PIPE, ...
+    const int M = g.M, N = g.N, K = g.K, UT = K / 256, GT = UT / PIPE;
+    const int g0 = part * GT / g.parts, U = (part + 1) * GT / g.parts - g0, u0 = PIPE * g0, S2 = 2 * U;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 3), kh = __builtin_amdgcn_readfirstlane(tid >> 8);
     auto ru = [&](int u) __attribute__((always_inline)) { return PIPE * u + kh; };  // real super-block
     const int ln = lane & 15, lg = lane >> 4;
-    const rsrc_t ra = make_rsrc(g.A, (uint32_t)((size_t)M * K * 2));
-    const rsrc_t rw = make_rsrc(g.W, (uint32_t)((size_t)N * g.row_bytes));
-    const rsrc_t rs = make_rsrc(g.S, (uint32_t)((size_t)M * UT * 32));
+    const rsrc_t ra = make_rsrc(g.A + (size_t)u0 * 256, (uint32_t)((size_t)M * K * 2 - (size_t)u0 * 512));
+    const rsrc_t rw = make_rsrc(g.W + (size_t)u0 * 144, (uint32_t)((size_t)N * g.row_bytes - (size_t)u0 * 144));
+    const rsrc_t rs = make_rsrc(g.S + (size_t)u0 * 16, (uint32_t)((size_t)M * UT * 32 - (size_t)u0 * 32));
     const uint32_t lds0 = (uint32_t)(uintptr_t)lds + (uint32_t)(kh * L::TOTAL);
     const int nw = n0 + 16 * NB * wave;  // the wave's first column
     const uint32_t rb = g.row_bytes;
@@ -443,52 +452,39 @@ __global__ void __launch_bounds__(RB_NT * PIPE) k_gemm_q4_k_rb(RbArgs g) {
                 }
     rb_wait_lgkm();
     __syncthreads();
-    constexpr int CH = BN / 8;
-    const bool wide = (N & 7) == 0 && ((uintptr_t)g.C & 15u) == 0;
-    for (int c = tid; c < BM * CH; c += RB_NT * PIPE) {
-        const int row = c / CH, ch = c - row * CH, m = m0 + row, n = n0 + 8 * ch;
-        if (m >= M || n >= N) continue;
-        const f4 v0 = *(const f4 *)(lds + (row * LD + 8 * ch) * 4), v1 = *(const f4 *)(lds + (row * LD + 8 * ch + 4) * 4);
-        const size_t idx = (size_t)m * N + n;
-        if (wide && n + 8 <= N) {
-            if (g.c_f32) {
-                f4 *p = (f4 *)((float *)g.C + idx);
-                p[0] = g.accumulate ? p[0] + v0 : v0;
-                p[1] = g.accumulate ? p[1] + v1 : v1;
-            } else {
-                h8 *p = (h8 *)((_Float16 *)g.C + idx);
-                f4 a0 = v0, a1 = v1;
-                if (g.accumulate) {
-                    const h8 o = *p;
-                    a0 += f4{(float)o[0], (float)o[1], (float)o[2], (float)o[3]};
-                    a1 += f4{(float)o[4], (float)o[5], (float)o[6], (float)o[7]};
-                }
-                *p = h8{(_Float16)a0.x, (_Float16)a0.y, (_Float16)a0.z, (_Float16)a0.w,
-                        (_Float16)a1.x, (_Float16)a1.y, (_Float16)a1.z, (_Float16)a1.w};
-            }
-        } else {
-            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-            for (int e = 0; e < 8 && n + e < N; e++) store_out(g.C, idx + e, v[e], g.c_f32, g.accumulate);
-        }
-    }
+    tile_finish<BM, BN, RB_NT * PIPE, 8>(lds, g, m0, n0, nt_i * g.mt + mt_i, part,
+                                        (int *)(lds + L::TOTAL * PIPE - 16));
 }
 }  // namespace
 
 
-int hq_rb_fits(int M, int N, int K) {
-    return M > 32 && M <= 64 && N >= 8192 && K % 512 == 0 && (size_t)M * K * 2 < ((size_t)1 << 32) &&
-           (size_t)N * (K / 256) * 144 < ((size_t)1 << 32);
+int hq_rb_fits(int M, int K) { return M > 32 && M <= 64 && K % 512 == 0 && (size_t)M * K * 2 < ((size_t)1 << 32); }
+
+// Workgroups per 64 x 64 tile for the mid-M Q4_K kernel, or 0 where the narrow kernel serves better:
+// one when the tiles alone number >= n_cu / 2 (N >= 8192 on 256 CUs), else the most parts (<= 8,
+// >= 2 super-block pairs each) that keep one round, when they reach >= n_cu / 2 workgroups
+int hq_rb_parts(int M, int N, int K, int n_cu) {
+    if (!hq_rb_fits(M, K) || (size_t)N * (K / 256) * 144 >= ((size_t)1 << 32)) return 0;
+    const int tiles = (N + 63) / 64, pairs = K / 512;
+    if (2 * tiles >= n_cu) return 1;
+    for (int p = 8; p >= 2; p--)
+        if (tiles * p <= n_cu && 2 * tiles * p >= n_cu && pairs >= 2 * p) return p;
+    return 0;
 }
 
 hipError_t hq_launch_gemm_rb(const hq_dev_mat *W, const uint16_t *A, const uint16_t *S, int M, void *C, int c_f32,
-                             int accumulate, hipStream_t st) {
-    if (W->type != HQ_TYPE_Q4_K || !hq_rb_fits(M, (int)W->rows, (int)W->cols)) return hipErrorInvalidValue;
+                             int accumulate, int parts, float *partials, int *counters, hipStream_t st) {
+    if (W->type != HQ_TYPE_Q4_K || !hq_rb_fits(M, (int)W->cols)) return hipErrorInvalidValue;
+    if (parts < 1 || parts > 8 || 2 * parts > (int)W->cols / 256 || (parts > 1 && (!partials || !counters)))
+        return hipErrorInvalidValue;
     RbArgs g;
     g.W = W->qs, g.row_bytes = (uint32_t)W->row_bytes, g.A = A, g.S = S;
     g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;
     g.mt = 1;
     g.nt = (g.N + 63) / 64;
-    const unsigned grid = (unsigned)(8 * ((g.nt + 7) / 8));
+    g.parts = parts, g.partials = partials, g.counters = counters, g.ntiles = g.nt;
+    if ((size_t)W->rows * W->row_bytes >= ((size_t)1 << 32)) return hipErrorInvalidValue;
+    const unsigned grid = (unsigned)(8 * ((g.nt + 7) / 8) * parts);
     k_gemm_q4_k_rb<1, 4, 3, 2><<<grid, 2 * RB_NT, 0, st>>>(g);
     return hipGetLastError();
 }

@@ -62,6 +62,7 @@ struct WsArgs {
     int parts;
     float *partials;
     int *counters;
+    int ntiles;  // mt * nt
 };
 
 // Workgroup barrier without a memory fence: each role waits for exactly the memory operations the
@@ -90,7 +91,7 @@ DEV void l2_touch(rsrc_t r, uint32_t voff, uint32_t lds_addr) {
 // row 16i + ln, 4 consecutive columns) as 16-byte pieces of 16 rows, which the memory system writes
 // as partial lines; instead the consumers park the fp32 tile in LDS (rows padded by 4 floats against
 // bank conflicts; the stage buffers are free once the main loop is done) and all 512 threads store
-// it as whole row segments, 8 values per thread and access.
+// it as whole row segments, 8 values per thread and access (tile_finish).
 template <int NB>
 DEV void ws_tile_to_lds(char *lds, const f4 (&acc)[4][NB], int wm, int wn, int ln, int lg) {
     constexpr int BN = 32 * NB, LD = BN + 4;
@@ -101,124 +102,6 @@ DEV void ws_tile_to_lds(char *lds, const f4 (&acc)[4][NB], int wm, int wn, int l
             const int r = 64 * wm + 16 * i + ln, c = (BN / 2) * wn + 16 * j + 4 * lg;
             *(f4 *)(lds + (r * LD + c) * 4) = acc[i][j];
         }
-}
-
-template <int NB>
-DEV void ws_lds_to_c(const char *lds, void *C, int M, int N, int m0, int n0, int c_f32, int accumulate) {
-    constexpr int BN = 32 * NB, LD = BN + 4, CH = BN / 8;
-    const bool wide = (N & 7) == 0 && ((uintptr_t)C & 15u) == 0;
-    for (int c = threadIdx.x; c < WS_BM * CH; c += WS_NT) {
-        const int row = c / CH, ch = c - row * CH, m = m0 + row, n = n0 + 8 * ch;
-        if (m >= M || n >= N) continue;
-        const f4 v0 = *(const f4 *)(lds + (row * LD + 8 * ch) * 4), v1 = *(const f4 *)(lds + (row * LD + 8 * ch + 4) * 4);
-        const size_t idx = (size_t)m * N + n;
-        if (wide && n + 8 <= N) {
-            if (c_f32) {
-                f4 *p = (f4 *)((float *)C + idx);
-                p[0] = accumulate ? p[0] + v0 : v0;
-                p[1] = accumulate ? p[1] + v1 : v1;
-            } else {
-                h8 *p = (h8 *)((_Float16 *)C + idx);
-                f4 a0 = v0, a1 = v1;
-                if (accumulate) {
-                    const h8 o = *p;
-                    a0 += f4{(float)o[0], (float)o[1], (float)o[2], (float)o[3]};
-                    a1 += f4{(float)o[4], (float)o[5], (float)o[6], (float)o[7]};
-                }
-                *p = h8{(_Float16)a0.x, (_Float16)a0.y, (_Float16)a0.z, (_Float16)a0.w,
-                        (_Float16)a1.x, (_Float16)a1.y, (_Float16)a1.z, (_Float16)a1.w};
-            }
-        } else {
-            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-            for (int e = 0; e < 8 && n + e < N; e++) store_out(C, idx + e, v[e], c_f32, accumulate);
-        }
-    }
-}
-
-// A K-split tile's end (parts > 1, at most 4): every part stores its fp32 tile (in LDS: rows padded
-// by 4 floats) to partials[tile][part] with device-scope 16-byte stores, waits for them, and counts
-// itself in; the last of the tile's parts loads the others' (device scope) and adds all of them in
-// part order (its own from LDS in its place), so the sum is the same whichever part arrives last,
-// then writes C. flag: an LDS word.
-template <int NB, class Args>
-DEV void ws_finish(const char *lds, const Args &g, int m0, int n0, int tile, int part, int *flag) {
-    if (g.parts == 1) {
-        ws_lds_to_c<NB>(lds, g.C, g.M, g.N, m0, n0, g.c_f32, g.accumulate);
-        return;
-    }
-    constexpr int BN = 32 * NB, LD = BN + 4, CH = BN / 8;
-    constexpr uint32_t TILE = WS_BM * BN * 4;  // bytes per partial tile
-    const rsrc_t rp = make_rsrc(g.partials, (uint32_t)g.mt * (uint32_t)g.nt * (uint32_t)g.parts * TILE);
-    const uint32_t own = ((uint32_t)tile * (uint32_t)g.parts + (uint32_t)part) * TILE;
-#pragma unroll
-    for (int i = 0; i < NB; i++) {
-        const int c = (int)threadIdx.x + WS_NT * i, row = c / CH, ch = c - row * CH;
-        const uint32_t off = (uint32_t)(row * BN + 8 * ch) * 4u;
-        buf_store16(rp, *(const f4 *)(lds + (row * LD + 8 * ch) * 4), off, own);
-        buf_store16(rp, *(const f4 *)(lds + (row * LD + 8 * ch + 4) * 4), off + 16u, own);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int last = atomicAdd(&g.counters[tile], 1) == g.parts - 1;
-        if (last) atomicExch(&g.counters[tile], 0);
-        *flag = last;
-    }
-    __syncthreads();
-    if (!*flag) return;
-    // thread t takes chunks t + 512 i (i < NB) of 8 values; every other part's pieces are loaded at
-    // once (one memory round trip), this part's own come from LDS
-    const int M = g.M, N = g.N;
-    const bool wide = (N & 7) == 0 && ((uintptr_t)g.C & 15u) == 0;
-    static_assert(WS_BM * CH == NB * WS_NT, "chunks per thread");
-    f4 pv[4][NB][2];
-#pragma unroll
-    for (int p = 0; p < 4; p++)
-#pragma unroll
-        for (int i = 0; i < NB; i++) {
-            const int c = (int)threadIdx.x + WS_NT * i, row = c / CH, ch = c - row * CH;
-            const uint32_t off = (uint32_t)(row * BN + 8 * ch) * 4u;
-            const uint32_t pb = ((uint32_t)tile * (uint32_t)g.parts + (uint32_t)p) * TILE;
-            if (p < g.parts && p != part) {
-                pv[p][i][0] = buf_load16_sc1(rp, off, pb);
-                pv[p][i][1] = buf_load16_sc1(rp, off + 16u, pb);
-            } else {
-                pv[p][i][0] = *(const f4 *)(lds + (row * LD + 8 * ch) * 4);
-                pv[p][i][1] = *(const f4 *)(lds + (row * LD + 8 * ch + 4) * 4);
-            }
-        }
-#pragma unroll
-    for (int i = 0; i < NB; i++) {
-        const int c = (int)threadIdx.x + WS_NT * i, row = c / CH, ch = c - row * CH, m = m0 + row, n = n0 + 8 * ch;
-        f4 v0 = {0.f, 0.f, 0.f, 0.f}, v1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int p = 0; p < 4; p++)
-            if (p < g.parts) {
-                v0 += pv[p][i][0];
-                v1 += pv[p][i][1];
-            }
-        if (m >= M || n >= N) continue;
-        const size_t idx = (size_t)m * N + n;
-        if (wide && n + 8 <= N) {
-            if (g.c_f32) {
-                f4 *q = (f4 *)((float *)g.C + idx);
-                q[0] = g.accumulate ? q[0] + v0 : v0;
-                q[1] = g.accumulate ? q[1] + v1 : v1;
-            } else {
-                h8 *q = (h8 *)((_Float16 *)g.C + idx);
-                if (g.accumulate) {
-                    const h8 o = *q;
-                    v0 += f4{(float)o[0], (float)o[1], (float)o[2], (float)o[3]};
-                    v1 += f4{(float)o[4], (float)o[5], (float)o[6], (float)o[7]};
-                }
-                *q = h8{(_Float16)v0.x, (_Float16)v0.y, (_Float16)v0.z, (_Float16)v0.w,
-                        (_Float16)v1.x, (_Float16)v1.y, (_Float16)v1.z, (_Float16)v1.w};
-            }
-        } else {
-            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-            for (int e = 0; e < 8 && n + e < N; e++) store_out(g.C, idx + e, v[e], g.c_f32, g.accumulate);
-        }
-    }
 }
 
 // LDS arena (bytes): A stages, B stages, S, Bmin, R, CL, scale words, prefetch scratch.
@@ -466,7 +349,7 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
         if (u < U) unit(i0{}, u);
         wg_barrier();  // the last stage's barrier
         wg_barrier();  // the consumers' output tile is in LDS
-        ws_finish<NB>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::PF));
+        tile_finish<WS_BM, 32 * NB, WS_NT, 4>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::PF));
         return;
     }
 
@@ -603,7 +486,7 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
     ws_tile_to_lds<NB>(lds, acc, wm, wn, ln, lg);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     wg_barrier();
-    ws_finish<NB>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::PF));
+    tile_finish<WS_BM, 32 * NB, WS_NT, 4>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::PF));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -636,6 +519,7 @@ struct Ws8Args {
     int parts;  // K split as in WsArgs (ranges of 128-wide stages)
     float *partials;
     int *counters;
+    int ntiles;
 };
 
 // 16 fp16 values fp16(q * d) from 16 stored bytes u = q + 128: fp16(1024 + u) - 1152 = q exactly,
@@ -759,7 +643,7 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q8_0_ws(Ws8Args g) {
         if (t < S2) step(i2{}, t++);
         if (t < S2) step(i3{}, t++);
         wg_barrier();  // the consumers' output tile is in LDS
-        ws_finish<NB>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::PF));
+        tile_finish<WS_BM, 32 * NB, WS_NT, 4>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::PF));
         return;
     }
 
@@ -847,7 +731,7 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q8_0_ws(Ws8Args g) {
     ws_tile_to_lds<NB>(lds, acc, wm, wn, ln, lg);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     wg_barrier();
-    ws_finish<NB>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::PF));
+    tile_finish<WS_BM, 32 * NB, WS_NT, 4>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::PF));
 }
 }  // namespace
 
@@ -880,7 +764,7 @@ hipError_t hq_launch_gemm_ws(const hq_dev_mat *W, const uint16_t *A, const uint1
     g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;
     g.mt = (M + WS_BM - 1) / WS_BM;
     g.nt = (g.N + 32 * nb - 1) / (32 * nb);
-    g.parts = parts, g.partials = partials, g.counters = counters;
+    g.parts = parts, g.partials = partials, g.counters = counters, g.ntiles = g.mt * g.nt;
     if (parts < 1 || parts > 4 || parts > g.K / 256 || (parts > 1 && (!partials || !counters))) return hipErrorInvalidValue;
     if (parts > 1 && (size_t)g.mt * g.nt * parts * WS_BM * 32 * nb * 4 >= ((size_t)1 << 32)) return hipErrorInvalidValue;
     const unsigned grid = (unsigned)(8 * ((g.nt + 7) / 8) * g.mt * parts);
@@ -902,7 +786,7 @@ hipError_t hq_launch_gemm_ws8(const hq_dev_mat *W, const uint16_t *A, int M, voi
     g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;
     g.mt = (M + WS_BM - 1) / WS_BM;
     g.nt = (g.N + 32 * nb - 1) / (32 * nb);
-    g.parts = parts, g.partials = partials, g.counters = counters;
+    g.parts = parts, g.partials = partials, g.counters = counters, g.ntiles = g.mt * g.nt;
     if (parts < 1 || parts > 4 || parts > g.K / WS_KS || (parts > 1 && (!partials || !counters))) return hipErrorInvalidValue;
     if (parts > 1 && (size_t)g.mt * g.nt * parts * WS_BM * 32 * nb * 4 >= ((size_t)1 << 32)) return hipErrorInvalidValue;
     const unsigned grid = (unsigned)(8 * ((g.nt + 7) / 8) * g.mt * parts);

@@ -53,12 +53,13 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
 int hq_ws_choose(int M, int N, int n_cu, float *eff);
 hipError_t hq_launch_gemm_ws(const hq_dev_mat *W, const uint16_t *A, const uint16_t *S, int M, void *C, int c_f32,
                              int accumulate, int nb, int parts, float *partials, int *counters, hipStream_t st);
-// Mid-M Q4_K GEMM (hq_gemm_rb.hip): whether an M x N x K problem takes it (33 <= M <= 64,
-// N >= 8192, K a multiple of 512, 32-bit offsets), and the launch (S = k_asums output for A in the
-// (hi, lo) pair layout).
-int hq_rb_fits(int M, int N, int K);
+// Mid-M Q4_K GEMM (hq_gemm_rb.hip): whether M, K suit it (33 <= M <= 64, K a multiple of 512,
+// 32-bit offsets), its workgroups per tile for a shape, and the launch (S = k_asums output for A in
+// the (hi, lo) pair layout; partials / counters as for the other K splits when parts > 1).
+int hq_rb_fits(int M, int K);
+int hq_rb_parts(int M, int N, int K, int n_cu);  // 0: not this kernel; else workgroups per tile
 hipError_t hq_launch_gemm_rb(const hq_dev_mat *W, const uint16_t *A, const uint16_t *S, int M, void *C, int c_f32,
-                             int accumulate, hipStream_t st);
+                             int accumulate, int parts, float *partials, int *counters, hipStream_t st);
 // Mid-M Q8_0 GEMM (hq_gemm_rb.hip): 2 <= M <= 64, N >= 8192, K a multiple of 256; no pre-pass.
 int hq_rb8_fits(int M, int N, int K);
 hipError_t hq_launch_gemm_rb8(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,

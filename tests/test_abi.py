@@ -71,7 +71,7 @@ def test_gemm_kernel_names():
              (synth.Q8_0, 2048, 9728, 2560): "k_gemm_q8_0_ws<5>", (synth.Q8_0, 128, 9728, 2560): "k_gemm_q8_0_ws<2>",
              (synth.Q8_0, 65, 9728, 2560): "k_gemm_q8_0<8, 2>",
              (synth.Q4_K, 4096, 9728, 2560): "k_gemm_q4_k_w<8>", (synth.Q4_K, 64, 9728, 2560): "k_gemm_q4_k_rb<1, 4, 3, 2>",
-             (synth.Q4_K, 64, 2560, 9728): "k_gemm_q4_k<4, 2>", (synth.Q4_K, 32, 9728, 2560): "k_gemm_q4_k<2, 2>",
+             (synth.Q4_K, 64, 2560, 9728): "k_gemm_q4_k_rb<1, 4, 3, 2>", (synth.Q4_K, 64, 1024, 2560): "k_gemm_q4_k<4, 2>", (synth.Q4_K, 32, 9728, 2560): "k_gemm_q4_k<2, 2>",
              (synth.Q4_K, 64, 9728, 2304): "k_gemm_q4_k<4, 2>",
              (synth.Q4_K, 512, 2560, 9728): "k_gemm_q4_k_ws<5>", (synth.Q4_K, 256, 2560, 9728): "k_gemm_q4_k_ws<3>",
              (synth.Q4_K, 512, 1024, 2560): "k_gemm_q4_k_w<8>", (synth.Q4_K, 4096, 2560, 9728): "k_gemm_q4_k_w<8>",
