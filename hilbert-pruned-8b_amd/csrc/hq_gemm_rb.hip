@@ -1,5 +1,7 @@
-// hq_gemm_rb.hip - Q4_K GEMM for mid-size M (33 <= M <= 64, N >= 8192) on gfx950: full-K tiles of
-// 64 rows x 64 columns, one per workgroup, no partial tiles.
+// hq_gemm_rb.hip - Q4_K and Q8_0 GEMMs for mid-size M on gfx950 (Q4_K: 33 <= M <= 64; Q8_0:
+// 2 <= M <= 64, N >= 8192): full-K tiles of up to 64 rows x 64 columns, one per workgroup; where a
+// Q4_K shape has too few tiles for the CUs, each tile's K is split over up to 8 workgroups whose
+// partial tiles are added in a fixed order (tile_finish).
 //
 // C[M,N] (+)= A[M,K] . W^T with A fp16 and W GGUF Q4_K super-blocks resident in HBM (reference
 // arithmetic: cleanroom-transformer/src/ggml_quant.h:51-59, :135-150; matmul src/cpu_backend.c:38-54).
