@@ -138,8 +138,8 @@ DEV h2 bytes_f16(uint32_t w, bool hi_pair) {
 // arrives last, then writes C; the counter is left at zero. flag: an LDS word outside the tile.
 template <int BM, int BN, int NT, int MAXP, class Args>
 DEV void tile_finish(const char *lds, const Args &g, int m0, int n0, int tile, int part, int *flag) {
-    constexpr int LD = BN + 4, CH = BN / 8, CPT = BM * CH / NT;  // 8-value chunks per thread
-    static_assert(BM * CH == CPT * NT, "chunks per thread");
+    constexpr int LD = BN + 4, CH = BN / 8, NCH = BM * CH, CPT = (NCH + NT - 1) / NT;  // 8-value chunks
+    static_assert(NCH % NT == 0 || NCH < NT, "chunks per thread");
     constexpr uint32_t TILE = BM * BN * 4;  // bytes per partial tile
     const int M = g.M, N = g.N;
     const bool wide = (N & 7) == 0 && ((uintptr_t)g.C & 15u) == 0;
@@ -150,6 +150,7 @@ DEV void tile_finish(const char *lds, const Args &g, int m0, int n0, int tile, i
 #pragma unroll
         for (int i = 0; i < CPT; i++) {
             const int c = (int)threadIdx.x + NT * i, row = c / CH, ch = c - row * CH;
+            if (c >= NCH) break;
             const uint32_t off = (uint32_t)(row * BN + 8 * ch) * 4u;
             buf_store16(rp, *(const f4 *)(lds + (row * LD + 8 * ch) * 4), off, own);
             buf_store16(rp, *(const f4 *)(lds + (row * LD + 8 * ch + 4) * 4), off + 16u, own);
@@ -170,7 +171,9 @@ DEV void tile_finish(const char *lds, const Args &g, int m0, int n0, int tile, i
                 const int c = (int)threadIdx.x + NT * i, row = c / CH, ch = c - row * CH;
                 const uint32_t off = (uint32_t)(row * BN + 8 * ch) * 4u;
                 const uint32_t pb = ((uint32_t)tile * (uint32_t)g.parts + (uint32_t)p) * TILE;
-                if (p < g.parts && p != part) {
+                if (c >= NCH) {
+                    pv[p][i][0] = pv[p][i][1] = f4{0.f, 0.f, 0.f, 0.f};
+                } else if (p < g.parts && p != part) {
                     pv[p][i][0] = buf_load16_sc1(rp, off, pb);
                     pv[p][i][1] = buf_load16_sc1(rp, off + 16u, pb);
                 } else {
@@ -182,6 +185,7 @@ DEV void tile_finish(const char *lds, const Args &g, int m0, int n0, int tile, i
 #pragma unroll
     for (int i = 0; i < CPT; i++) {
         const int c = (int)threadIdx.x + NT * i, row = c / CH, ch = c - row * CH, m = m0 + row, n = n0 + 8 * ch;
+        if (c >= NCH) break;
         f4 v0, v1;
         if (g.parts > 1) {
             v0 = f4{0.f, 0.f, 0.f, 0.f}, v1 = f4{0.f, 0.f, 0.f, 0.f};

@@ -1,7 +1,7 @@
 // hq_gemm_rb.hip - Q4_K and Q8_0 GEMMs for mid-size M on gfx950 (Q4_K: 33 <= M <= 64; Q8_0:
-// 2 <= M <= 64, N >= 8192): full-K tiles of up to 64 rows x 64 columns, one per workgroup; where a
-// Q4_K shape has too few tiles for the CUs, each tile's K is split over up to 8 workgroups whose
-// partial tiles are added in a fixed order (tile_finish).
+// 2 <= M <= 64): full-K tiles of up to 64 rows x 64 columns, one per workgroup; where a shape has
+// too few tiles for the CUs, each tile's K is split over up to 8 workgroups whose partial tiles are
+// added in a fixed order (tile_finish).
 //
 // C[M,N] (+)= A[M,K] . W^T with A fp16 and W GGUF Q4_K super-blocks resident in HBM (reference
 // arithmetic: cleanroom-transformer/src/ggml_quant.h:51-59, :135-150; matmul src/cpu_backend.c:38-54).
@@ -477,7 +477,7 @@ int hq_rb_parts(int M, int N, int K, int n_cu) {
 hipError_t hq_launch_gemm_rb(const hq_dev_mat *W, const uint16_t *A, const uint16_t *S, int M, void *C, int c_f32,
                              int accumulate, int parts, float *partials, int *counters, hipStream_t st) {
     if (W->type != HQ_TYPE_Q4_K || !hq_rb_fits(M, (int)W->cols)) return hipErrorInvalidValue;
-    if (parts < 1 || parts > 8 || 2 * parts > (int)W->cols / 256 || (parts > 1 && (!partials || !counters)))
+    if (parts < 1 || parts > 8 || (parts > 1 && (4 * parts > (int)W->cols / 256 || !partials || !counters)))
         return hipErrorInvalidValue;
     RbArgs g;
     g.W = W->qs, g.row_bytes = (uint32_t)W->row_bytes, g.A = A, g.S = S;
@@ -492,7 +492,7 @@ hipError_t hq_launch_gemm_rb(const hq_dev_mat *W, const uint16_t *A, const uint1
 }
 
 // ============================================================================ Q8_0, mid M
-// The same structure for Q8_0 (M <= 64, N >= 8192): 16 MBK x 64 full-K tiles, PIPE pipelines of
+// The same structure for Q8_0 (M <= 64; N >= 8192, or a K split as for Q4_K): 16 MBK x 64 tiles, PIPE pipelines of
 // four waves taking 128-wide stages kh, kh + PIPE, ...; wave w decodes columns 16w .. 16w + 15. No
 // min term and no rescale: the B operand is fp16(q * d), one rounding of the exact weight (as in the
 // other Q8_0 kernels), from the biased byte u = q + 128 (fp16 1024 + u by v_perm_b32, minus 1152).
@@ -509,6 +509,10 @@ struct Rb8Args {
     void *C;
     int c_f32, accumulate;
     int nt;  // N-tiles
+    int parts;  // K split as for the Q4_K kernel (groups of PIPE stages)
+    float *partials;
+    int *counters;
+    int ntiles;
 };
 
 template <int MBK, int NSTG>
@@ -539,16 +543,18 @@ __global__ void __launch_bounds__(RB_NT * PIPE) k_gemm_q8_0_rb(Rb8Args g) {
     constexpr int BM = 16 * MBK, BN = 64;
     using L = Rb8Lds<MBK, NSTG>;
     __shared__ __attribute__((aligned(256))) char lds[L::TOTAL * PIPE];
-    const int b = blockIdx.x, nt_i = (b & 7) + 8 * (b >> 3);
+    const int b = blockIdx.x, j8 = b >> 3, nt_i = (b & 7) + 8 * (j8 / g.parts), part = j8 % g.parts;
     if (nt_i >= g.nt) return;
     const int n0 = nt_i * BN;
-    const int M = g.M, N = g.N, K = g.K, S2 = K / RB_KS / PIPE;  // this pipeline's stages
+    // this part's stages s0 .. s0 + PIPE S2 - 1 (whole groups of PIPE); operand bases moved to s0
+    const int M = g.M, N = g.N, K = g.K, GT = K / RB_KS / PIPE;
+    const int g0 = part * GT / g.parts, S2 = (part + 1) * GT / g.parts - g0, s0 = PIPE * g0;
     const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, lg = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 3), kh = __builtin_amdgcn_readfirstlane(tid >> 8);
     auto rs = [&](int s) __attribute__((always_inline)) { return PIPE * s + kh; };  // real stage
-    const rsrc_t ra = make_rsrc(g.A, (uint32_t)((size_t)M * K * 2));
-    const rsrc_t rq = make_rsrc(g.Q, (uint32_t)((size_t)N * K));
-    const rsrc_t rd = make_rsrc(g.D, (uint32_t)((size_t)N * g.ldd * 2));
+    const rsrc_t ra = make_rsrc(g.A + (size_t)s0 * RB_KS, (uint32_t)((size_t)M * K * 2 - (size_t)s0 * RB_KS * 2));
+    const rsrc_t rq = make_rsrc(g.Q + (size_t)s0 * RB_KS, (uint32_t)((size_t)N * K - (size_t)s0 * RB_KS));
+    const rsrc_t rd = make_rsrc(g.D + (size_t)s0 * 4, (uint32_t)((size_t)N * g.ldd * 2 - (size_t)s0 * 8));
     const uint32_t lds0 = (uint32_t)(uintptr_t)lds + (uint32_t)(kh * L::TOTAL);
     const int nw = n0 + 16 * wave;
 
@@ -644,50 +650,36 @@ __global__ void __launch_bounds__(RB_NT * PIPE) k_gemm_q8_0_rb(Rb8Args g) {
             }
     rb_wait_lgkm();
     __syncthreads();
-    constexpr int CH = BN / 8;
-    const bool wide = (N & 7) == 0 && ((uintptr_t)g.C & 15u) == 0;
-    for (int c = tid; c < BM * CH; c += RB_NT * PIPE) {
-        const int row = c / CH, ch = c - row * CH, m = row, n = n0 + 8 * ch;
-        if (m >= M || n >= N) continue;
-        const f4 v0 = *(const f4 *)(lds + (row * LD + 8 * ch) * 4), v1 = *(const f4 *)(lds + (row * LD + 8 * ch + 4) * 4);
-        const size_t idx = (size_t)m * N + n;
-        if (wide && n + 8 <= N) {
-            if (g.c_f32) {
-                f4 *p = (f4 *)((float *)g.C + idx);
-                p[0] = g.accumulate ? p[0] + v0 : v0;
-                p[1] = g.accumulate ? p[1] + v1 : v1;
-            } else {
-                h8 *p = (h8 *)((_Float16 *)g.C + idx);
-                f4 a0 = v0, a1 = v1;
-                if (g.accumulate) {
-                    const h8 o = *p;
-                    a0 += f4{(float)o[0], (float)o[1], (float)o[2], (float)o[3]};
-                    a1 += f4{(float)o[4], (float)o[5], (float)o[6], (float)o[7]};
-                }
-                *p = h8{(_Float16)a0.x, (_Float16)a0.y, (_Float16)a0.z, (_Float16)a0.w,
-                        (_Float16)a1.x, (_Float16)a1.y, (_Float16)a1.z, (_Float16)a1.w};
-            }
-        } else {
-            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-            for (int e = 0; e < 8 && n + e < N; e++) store_out(g.C, idx + e, v[e], g.c_f32, g.accumulate);
-        }
-    }
+    tile_finish<BM, BN, RB_NT * PIPE, 8>(lds, g, 0, n0, nt_i, part, (int *)(lds + L::TOTAL * PIPE - 16));
 }
 }  // namespace
 
-int hq_rb8_fits(int M, int N, int K) {
-    return M >= 2 && M <= 64 && N >= 8192 && K % 256 == 0 && (size_t)64 * K * 2 < ((size_t)1 << 32) &&
-           ((size_t)N + 64) * K < ((size_t)1 << 32);
+// Workgroups per tile of the mid-M Q8_0 kernel (2 <= M <= 64, K a multiple of 256), or 0: one when
+// the tiles number >= n_cu / 2 (N >= 8192 on 256 CUs), else the most parts (<= 8, >= 2 pairs of
+// 128-wide stages each) that keep one round and reach >= n_cu / 2 workgroups
+int hq_rb8_parts(int M, int N, int K, int n_cu) {
+    if (M < 2 || M > 64 || K % 256 || (size_t)64 * K * 2 >= ((size_t)1 << 32) || ((size_t)N + 64) * K >= ((size_t)1 << 32))
+        return 0;
+    const int tiles = (N + 63) / 64, groups = K / 256;
+    if (2 * tiles >= n_cu) return 1;
+    for (int p = 8; p >= 2; p--)
+        if (tiles * p <= n_cu && 2 * tiles * p >= n_cu && groups >= 2 * p) return p;
+    return 0;
 }
 
 hipError_t hq_launch_gemm_rb8(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
-                              hipStream_t st) {
-    if (W->type != HQ_TYPE_Q8_0 || !hq_rb8_fits(M, (int)W->rows, (int)W->cols)) return hipErrorInvalidValue;
+                              int parts, float *partials, int *counters, hipStream_t st) {
+    if (W->type != HQ_TYPE_Q8_0 || M < 2 || M > 64 || W->cols % 256) return hipErrorInvalidValue;
+    if (parts < 1 || parts > 8 || (parts > 1 && (2 * parts > (int)W->cols / 256 || !partials || !counters)))
+        return hipErrorInvalidValue;
+    if ((size_t)64 * W->cols * 2 >= ((size_t)1 << 32) || ((size_t)W->rows + 64) * W->cols >= ((size_t)1 << 32))
+        return hipErrorInvalidValue;
     Rb8Args g;
     g.Q = W->qs, g.D = W->d, g.ldd = W->ldd, g.A = A;
     g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;
     g.nt = (g.N + 63) / 64;
-    const unsigned grid = (unsigned)(8 * ((g.nt + 7) / 8));
+    g.parts = parts, g.partials = partials, g.counters = counters, g.ntiles = g.nt;
+    const unsigned grid = (unsigned)(8 * ((g.nt + 7) / 8) * parts);
     if (M <= 16) k_gemm_q8_0_rb<1, 3, 2><<<grid, 2 * RB_NT, 0, st>>>(g);
     else if (M <= 32) k_gemm_q8_0_rb<2, 3, 2><<<grid, 2 * RB_NT, 0, st>>>(g);
     else k_gemm_q8_0_rb<4, 3, 2><<<grid, 2 * RB_NT, 0, st>>>(g);

@@ -60,10 +60,11 @@ int hq_rb_fits(int M, int K);
 int hq_rb_parts(int M, int N, int K, int n_cu);  // 0: not this kernel; else workgroups per tile
 hipError_t hq_launch_gemm_rb(const hq_dev_mat *W, const uint16_t *A, const uint16_t *S, int M, void *C, int c_f32,
                              int accumulate, int parts, float *partials, int *counters, hipStream_t st);
-// Mid-M Q8_0 GEMM (hq_gemm_rb.hip): 2 <= M <= 64, N >= 8192, K a multiple of 256; no pre-pass.
-int hq_rb8_fits(int M, int N, int K);
+// Mid-M Q8_0 GEMM (hq_gemm_rb.hip): workgroups per tile for a shape (0: not this kernel), and the
+// launch (no pre-pass; partials / counters as for the other K splits when parts > 1).
+int hq_rb8_parts(int M, int N, int K, int n_cu);
 hipError_t hq_launch_gemm_rb8(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
-                              hipStream_t st);
+                              int parts, float *partials, int *counters, hipStream_t st);
 hipError_t hq_launch_gemm_ws8(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
                               int nb, int parts, float *partials, int *counters, hipStream_t st);
 

@@ -1446,7 +1446,7 @@ struct GemmCfg {
     int ws8_nb;  // > 0: the Q8_0 full-K tile kernel k_gemm_q8_0_ws, 32 * ws8_nb columns per tile
     int ws8_parts;  // with ws8_nb: workgroups per tile (K split, as ws_parts)
     int rbm;        // Q4_K mid M: workgroups per tile of k_gemm_q4_k_rb (hq_gemm_rb.hip); 0: not used
-    bool rb8;       // Q8_0 M <= 64: the full-K tile kernel k_gemm_q8_0_rb (hq_gemm_rb.hip)
+    int rb8;        // Q8_0 M <= 64: workgroups per tile of k_gemm_q8_0_rb (hq_gemm_rb.hip); 0: not used
 };
 
 // Q4_K with M > 64 runs the full-K tile kernel when its tiles fit in one round on the CUs and fill
@@ -1464,7 +1464,7 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
     c.ws_nb = 0;
     c.ws_parts = 1;
     c.rbm = W->type == HQ_TYPE_Q4_K ? hq_rb_parts(M, (int)W->rows, (int)W->cols, n_cu) : 0;
-    c.rb8 = W->type == HQ_TYPE_Q8_0 && hq_rb8_fits(M, (int)W->rows, (int)W->cols);
+    c.rb8 = W->type == HQ_TYPE_Q8_0 ? hq_rb8_parts(M, (int)W->rows, (int)W->cols, n_cu) : 0;
     if (c.wide && (size_t)M * W->cols * 2 < ((size_t)1 << 32)) {
         float eff = 0.f;
         const int nb = hq_ws_choose(M, (int)W->rows, n_cu, &eff);
@@ -1562,9 +1562,10 @@ void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_by
         *partial_bytes = tiles * sparts * 128 * 32 * snb * sizeof(float);
         *counter_bytes = tiles * sizeof(int);
     }
-    if (c.rbm > 1) {  // mid-M Q4_K kernel with a K split: 64 x 64 fp32 tiles
+    const int rparts = c.rbm > 1 ? c.rbm : c.rb8 > 1 ? c.rb8 : 0;
+    if (rparts) {  // mid-M kernels with a K split: tiles of at most 64 x 64 fp32
         const size_t tiles = (W->rows + 63) / 64;
-        *partial_bytes = tiles * c.rbm * 64 * 64 * sizeof(float);
+        *partial_bytes = tiles * rparts * 64 * 64 * sizeof(float);
         *counter_bytes = tiles * sizeof(int);
     }
     *sums_bytes = c.wide || c.rbm ? (size_t)M * (W->cols / KC) * 32 : 0;
@@ -1591,7 +1592,7 @@ hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, vo
                                const HqGemmWork &wk, hipStream_t st) {
     const GemmCfg c = gemm_cfg(W, M, wk.n_cu);
     if (c.rbm) return hq_launch_gemm_rb(W, A, wk.sums, M, C, c_f32, accumulate, c.rbm, wk.partials, wk.counters, st);
-    if (c.rb8) return hq_launch_gemm_rb8(W, A, M, C, c_f32, accumulate, st);
+    if (c.rb8) return hq_launch_gemm_rb8(W, A, M, C, c_f32, accumulate, c.rb8, wk.partials, wk.counters, st);
     if (c.ws_nb)
         return hq_launch_gemm_ws(W, A, wk.sums, M, C, c_f32, accumulate, c.ws_nb, c.ws_parts, wk.partials, wk.counters, st);
     if (c.ws8_nb)

@@ -77,7 +77,7 @@ def test_gemm_kernel_names():
              (synth.Q4_K, 512, 1024, 2560): "k_gemm_q4_k_w<8>", (synth.Q4_K, 4096, 2560, 9728): "k_gemm_q4_k_w<8>",
              (synth.Q8_0, 512, 2560, 9728): "k_gemm_q8_0_ws<5>", (synth.Q8_0, 256, 2560, 9728): "k_gemm_q8_0_ws<3>",
              (synth.Q8_0, 16, 9728, 2560): "k_gemm_q8_0_rb<1, 3, 2>", (synth.Q8_0, 64, 9728, 2560): "k_gemm_q8_0_rb<4, 3, 2>",
-             (synth.Q8_0, 16, 2560, 9728): "k_gemm_q8_0<1, 2>", (synth.Q4_K, 1, 9728, 2560): "k_gemv_q4_k_r<4>",
+             (synth.Q8_0, 16, 2560, 9728): "k_gemm_q8_0_rb<1, 3, 2>", (synth.Q8_0, 16, 1024, 1024): "k_gemm_q8_0<1, 2>", (synth.Q4_K, 1, 9728, 2560): "k_gemv_q4_k_r<4>",
              (synth.Q4_K, 1, 2560, 9728): "k_gemv_q4_k_s<4>", (synth.Q4_K, 1, 100, 512): "k_gemv_q4_k_s<1>",
              (synth.Q4_K, 1, 9728, 256): "k_gemv_q4_k_s<16>", (synth.Q8_0, 1, 9728, 2560): "k_gemv_q8_0<2>",
              (synth.Q8_0, 1, 100, 512): "k_gemv_q8_0<1>"}

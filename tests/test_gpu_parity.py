@@ -122,7 +122,8 @@ RAGGED = [(synth.Q8_0, 100, 512, M) for M in (1, 2, 5, 17, 33, 65, 200)] + \
          [(synth.Q8_0, 2560, 9728, 512), (synth.Q8_0, 2500, 8192, 300)] + \
          [(synth.Q4_K, 8200, 1536, 40), (synth.Q4_K, 8192, 512, 33)] + \
          [(synth.Q8_0, 8200, 1024, 5), (synth.Q8_0, 9728, 512, 40), (synth.Q8_0, 8192, 256, 30)] + \
-         [(synth.Q4_K, 2500, 4096, 40), (synth.Q4_K, 4096, 2560, 48)]
+         [(synth.Q4_K, 2500, 4096, 40), (synth.Q4_K, 4096, 2560, 48)] + \
+         [(synth.Q8_0, 2560, 9728, 16), (synth.Q8_0, 2500, 4096, 40)]
 # (the last: full-K tiles; Stream-K with more tiles than CUs; the streamed GEMV with a ragged last
 # row group and an odd K split, with one wave per row group, and with an even split; the Q8_0 tile
 # kernel with ragged M and N, and with an odd number of 128-wide stages; the Q4_K tile kernel with
@@ -130,7 +131,8 @@ RAGGED = [(synth.Q8_0, 100, 512, M) for M in (1, 2, 5, 17, 33, 65, 200)] + \
 # with ragged M and N; the Q8_0 tile kernel with K split over 4 workgroups, also with ragged M, N;
 # the mid-M Q4_K kernel with a ragged last column tile and ragged M, and at M = 33 with K = 512; the
 # mid-M Q8_0 kernel with ragged N and M at each of its row-block counts, and with one stage per
-# pipeline; the mid-M Q4_K kernel with each tile's K split over 4 (ragged N, M) and 2 workgroups)
+# pipeline; the mid-M Q4_K kernel with each tile's K split over 4 (ragged N, M) and 2 workgroups; the
+# mid-M Q8_0 kernel with K splits over 6 and (ragged N, M) 4 workgroups)
 
 
 @pytest.mark.parametrize("gtype,N,K,M", FULL + RAGGED)
@@ -289,7 +291,7 @@ def test_gemm_positive_activations(hqlib, oracle, gtype, N, K, M):
 
 
 
-@pytest.mark.parametrize("gtype,M", [(synth.Q4_K, 512), (synth.Q8_0, 512), (synth.Q4_K, 64)])
+@pytest.mark.parametrize("gtype,M", [(synth.Q4_K, 512), (synth.Q8_0, 512), (synth.Q4_K, 64), (synth.Q8_0, 16)])
 def test_gemm_k_split_repeatable(hqlib, gtype, M):
     """The K-split tile kernels (N = 2560, K = 9728: M = 512, each tile's K over 4 workgroups; the
     mid-M Q4_K kernel at M = 64 over 6) give the same bits on every call: the last part to arrive
