@@ -3,6 +3,7 @@
 // the host before a kernel is launched, so no launch can read or write outside its buffers.
 #include <hip/hip_runtime.h>
 
+#include <map>
 #include <mutex>
 #include <stdarg.h>
 #include <stdio.h>
@@ -108,8 +109,15 @@ extern "C" int hq_mat_upload(const hq_wmat_t *w, int device, hq_mat **out) {
     if (w->rows > (1u << 30) || w->cols > (1u << 24)) return fail("hq_mat_upload: shape [%u, %u] too large", w->rows, w->cols);
     if (w->perm_heads && (w->rows % w->perm_heads || (w->rows / w->perm_heads) % 2))
         return fail("hq_mat_upload: %u rows do not split into %u heads of even size", w->rows, w->perm_heads);
-    if (use_device(device)) return -1;
     const size_t rb = (size_t)(w->cols / per) * block_bytes(w->ggml_type);
+    // the kernels address a matrix through 32-bit buffer ranges: its device bytes stay below 4 GiB
+    const size_t dev_bytes = w->ggml_type == HQ_GGML_Q4_K
+                                 ? rb * w->rows
+                                 : round_up((size_t)w->rows * w->cols, 256) + (size_t)w->rows * round_up(w->cols / 32, 8) * 2;
+    if (dev_bytes >= ((size_t)1 << 32))
+        return fail("hq_mat_upload: shape [%u, %u] needs %zu device bytes; one matrix is limited to 4 GiB (split its rows)",
+                    w->rows, w->cols, dev_bytes);
+    if (use_device(device)) return -1;
     const uint8_t *src = (const uint8_t *)w->data;
     hq_mat *m = (hq_mat *)calloc(1, sizeof *m);
     if (!m) return fail("hq_mat_upload: out of host memory");
@@ -205,69 +213,93 @@ static hipStream_t S(void *s) { return (hipStream_t)s; }
 
 static int aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
-// Library-owned device buffers, per device: staging for host-pointer entry points and the GEMM
-// workspace. Grown on demand (hipMalloc), so the first call of a larger shape allocates: capture a
-// call into a HIP graph only after an eager call of the same shape.
+// Library-owned device buffers, per (device, stream): staging for host-pointer entry points and
+// the GEMM workspace. Work queued on one stream runs in order, so a stream's buffers are never used
+// by two launches at once; calls on different streams (which may run concurrently) get different
+// buffers. Grown on demand (hipMalloc), so the first call of a larger shape allocates: capture a
+// call into a HIP graph only after an eager call of the same shape on the same stream.
 namespace {
 struct Staging {  // slots: 0 x fp32, 1 x fp16, 2 y fp32 (hq_matmul_host), 3 embedding ids, 4 readout ids,
                   // 5 GEMM partial tiles, 6 GEMM tile counters (kept zero), 7 activation sub-block sums
     void *buf[8] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
     size_t cap[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    int n_cu = 0;
 };
 std::mutex g_staging_mu;
-std::vector<Staging> g_staging;
+std::map<std::pair<int, void *>, Staging> g_staging;
+std::map<int, int> g_n_cu;
 
-int staging(int device, int slot, size_t bytes, void **p) {
+// The slot's buffer of at least `bytes` for (device, stream); *grew = 1 when it was (re)allocated.
+int staging(int device, void *stream, int slot, size_t bytes, void **p, int *grew = nullptr) {
     std::lock_guard<std::mutex> lk(g_staging_mu);
-    if ((int)g_staging.size() <= device) g_staging.resize(device + 1);
-    Staging &s = g_staging[device];
+    Staging &s = g_staging[std::make_pair(device, stream)];
+    if (grew) *grew = 0;
     if (s.cap[slot] < bytes) {
         if (s.buf[slot]) HIPCK(hipFree(s.buf[slot]));
         s.buf[slot] = nullptr;
         s.cap[slot] = 0;
         HIPCK(hipMalloc(&s.buf[slot], bytes));
         s.cap[slot] = bytes;
+        if (grew) *grew = 1;
     }
     *p = s.buf[slot];
     return 0;
 }
 
-// Stream-K workspace for hq_gemm on W's device. A counter array that grows is zeroed once here,
-// synchronously; the kernels leave every counter back at zero.
-int gemm_work(const hq_mat *W, int M, HqGemmWork *wk) {
-    int n_cu;
-    {
-        std::lock_guard<std::mutex> lk(g_staging_mu);
-        if ((int)g_staging.size() <= W->device) g_staging.resize(W->device + 1);
-        if (!g_staging[W->device].n_cu) {
-            int v = 0;
-            HIPCK(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, W->device));
-            g_staging[W->device].n_cu = v > 0 ? v : 1;
+// Frees the buffers of every device's workspace for `stream` (its work has finished).
+void staging_release(void *stream) {
+    std::lock_guard<std::mutex> lk(g_staging_mu);
+    for (auto it = g_staging.begin(); it != g_staging.end();) {
+        if (it->first.second != stream) {
+            ++it;
+            continue;
         }
-        n_cu = g_staging[W->device].n_cu;
+        int cur = -1;
+        if (hipGetDevice(&cur) == hipSuccess && cur != it->first.first) (void)hipSetDevice(it->first.first);
+        for (void *b : it->second.buf)
+            if (b) (void)hipFree(b);
+        if (cur >= 0 && cur != it->first.first) (void)hipSetDevice(cur);
+        it = g_staging.erase(it);
     }
+}
+
+int device_cus(int device, int *n_cu) {
+    std::lock_guard<std::mutex> lk(g_staging_mu);
+    int &v = g_n_cu[device];
+    if (!v) {
+        int x = 0;
+        HIPCK(hipDeviceGetAttribute(&x, hipDeviceAttributeMultiprocessorCount, device));
+        v = x > 0 ? x : 1;
+    }
+    *n_cu = v;
+    return 0;
+}
+
+// GEMM workspace of an M-row hq_gemm on W's device and `stream`. A counter array that grows is
+// zeroed once here, synchronously; the kernels leave every counter back at zero.
+int gemm_work(const hq_mat *W, int M, void *stream, HqGemmWork *wk) {
+    int n_cu;
+    if (device_cus(W->device, &n_cu)) return -1;
     size_t pb, cb, sb;
     hq_gemm_work_bytes(&W->m, M, n_cu, &pb, &cb, &sb);
     void *part, *cnt, *sums = nullptr;
-    size_t old_cap;
-    {
-        std::lock_guard<std::mutex> lk(g_staging_mu);
-        old_cap = g_staging[W->device].cap[6];
-    }
-    if (staging(W->device, 5, pb, &part) || staging(W->device, 6, cb, &cnt)) return -1;
-    if (sb && staging(W->device, 7, sb, &sums)) return -1;
-    size_t new_cap;
-    {
-        std::lock_guard<std::mutex> lk(g_staging_mu);
-        new_cap = g_staging[W->device].cap[6];
-    }
-    if (new_cap != old_cap) HIPCK(hipMemset(cnt, 0, new_cap));
+    int grew = 0;
+    if (staging(W->device, stream, 5, pb, &part) || staging(W->device, stream, 6, cb, &cnt, &grew)) return -1;
+    if (sb && staging(W->device, stream, 7, sb, &sums)) return -1;
+    if (grew && cb) HIPCK(hipMemset(cnt, 0, cb));
     wk->partials = (float *)part;
     wk->counters = (int *)cnt;
     wk->sums = (uint16_t *)sums;
     wk->n_cu = n_cu;
     return 0;
+}
+
+// Rows of A per GEMM launch: the kernels address A through 32-bit buffer ranges and form a row's
+// element offset (row * K, rows up to one tile past the last) in 32-bit signed arithmetic, so one
+// launch keeps (rows + 128) * K below 2^31; a longer M is cut into launches of whole 128-row tiles
+// (the reference cuts at 512 rows, src/cuda_backend.cu:866-875).
+size_t gemm_rows_per_launch(size_t K) {
+    const long r = (long)(((size_t)1 << 31) - 1) / (long)K - 128;
+    return r >= 128 ? (size_t)r & ~(size_t)127 : r >= 1 ? (size_t)r : 1;
 }
 }  // namespace
 
@@ -288,13 +320,19 @@ extern "C" int hq_gemm(const hq_mat *W, const uint16_t *A, int M, void *C, int c
     if (!aligned(A, 16)) return fail("hq_gemm: A must be 16-byte aligned");
     if (!aligned(C, c_is_f32 ? 4 : 2)) return fail("hq_gemm: C is misaligned");
     if (use_device(W->device)) return -1;
-    if (M == 1) {
-        HIPCK(hq_launch_gemv(&W->m, A, C, c_is_f32, accumulate, S(stream)));
-        return 0;
+    const size_t K = W->m.cols, N = W->m.rows, c_bytes = c_is_f32 ? 4 : 2, step = gemm_rows_per_launch(K);
+    for (size_t m0 = 0; m0 < (size_t)M; m0 += step) {
+        const int mc = (int)((size_t)M - m0 < step ? (size_t)M - m0 : step);
+        const uint16_t *Ap = A + m0 * K;
+        void *Cp = (char *)C + m0 * N * c_bytes;
+        if (mc == 1) {
+            HIPCK(hq_launch_gemv(&W->m, Ap, Cp, c_is_f32, accumulate, S(stream)));
+            continue;
+        }
+        HqGemmWork wk;
+        if (gemm_work(W, mc, stream, &wk)) return -1;
+        HIPCK(hq_launch_gemm(&W->m, Ap, mc, Cp, c_is_f32, accumulate, wk, S(stream)));
     }
-    HqGemmWork wk;
-    if (gemm_work(W, M, &wk)) return -1;
-    HIPCK(hq_launch_gemm(&W->m, A, M, C, c_is_f32, accumulate, wk, S(stream)));
     return 0;
 }
 
@@ -324,7 +362,7 @@ extern "C" int hq_gather_dot(const hq_mat *head, const uint16_t *H, const uint32
     if (n == 0) return 0;
     if (use_device(head->device)) return -1;
     void *d_ids;
-    if (staging(head->device, 4, n * sizeof(uint32_t), &d_ids)) return -1;
+    if (staging(head->device, stream, 4, n * sizeof(uint32_t), &d_ids)) return -1;
     HIPCK(hipMemcpyAsync(d_ids, ids, n * sizeof(uint32_t), hipMemcpyHostToDevice, S(stream)));
     return hq_gather_dot_dev(head, H, (const uint32_t *)d_ids, B, k, out, stream);
 }
@@ -338,7 +376,7 @@ extern "C" int hq_embed_f32(const hq_mat *W, const uint32_t *ids, int n, float *
     if (n == 0) return 0;
     if (use_device(W->device)) return -1;
     void *d_ids;
-    if (staging(W->device, 3, (size_t)n * sizeof(uint32_t), &d_ids)) return -1;
+    if (staging(W->device, stream, 3, (size_t)n * sizeof(uint32_t), &d_ids)) return -1;
     HIPCK(hipMemcpyAsync(d_ids, ids, (size_t)n * sizeof(uint32_t), hipMemcpyHostToDevice, S(stream)));
     HIPCK(hq_launch_dequant(&W->m, 0, (const uint32_t *)d_ids, (uint32_t)n, out, S(stream)));
     return 0;
@@ -351,8 +389,8 @@ extern "C" int hq_matmul_host(const hq_mat *W, const float *x, size_t T, float *
     const size_t K = W->m.cols, N = W->m.rows;
     if (use_device(W->device)) return -1;
     void *dx, *dh, *dy;
-    if (staging(W->device, 0, T * K * sizeof(float), &dx) || staging(W->device, 1, T * K * 2, &dh) ||
-        staging(W->device, 2, T * N * sizeof(float), &dy))
+    if (staging(W->device, nullptr, 0, T * K * sizeof(float), &dx) || staging(W->device, nullptr, 1, T * K * 2, &dh) ||
+        staging(W->device, nullptr, 2, T * N * sizeof(float), &dy))
         return -1;
     HIPCK(hipMemcpy(dx, x, T * K * sizeof(float), hipMemcpyHostToDevice));
     if (accumulate) HIPCK(hipMemcpy(dy, y, T * N * sizeof(float), hipMemcpyHostToDevice));
@@ -397,6 +435,8 @@ extern "C" int hq_stream_create(void **stream) {
     return 0;
 }
 extern "C" int hq_stream_destroy(void *stream) {
+    HIPCK(hipStreamSynchronize(S(stream)));
+    staging_release(stream);  // the stream's workspace: a later stream may get the same handle
     HIPCK(hipStreamDestroy(S(stream)));
     return 0;
 }
@@ -486,7 +526,10 @@ extern "C" int hq_time_gemm_kernel(hq_mat *const *Ws, int n_w, const uint16_t *A
     if (!aligned(A, 16)) return fail("hq_time_gemm_kernel: A must be 16-byte aligned");
     if (use_device(Ws[0]->device)) return -1;
     HqGemmWork wk;
-    if (gemm_work(Ws[0], M, &wk)) return -1;
+    if ((size_t)M > gemm_rows_per_launch(Ws[0]->m.cols))
+        return fail("hq_time_gemm_kernel: M = %d exceeds one launch's %zu rows at K = %u", M,
+                    gemm_rows_per_launch(Ws[0]->m.cols), Ws[0]->m.cols);
+    if (gemm_work(Ws[0], M, stream, &wk)) return -1;
     // the pre-pass depends on A only: run it once, then time the main kernel alone
     HIPCK(hq_launch_gemm_pre(&Ws[0]->m, A, M, wk, S(stream)));
     HIPCK(hq_launch_gemm_main(&Ws[0]->m, A, M, C, c_is_f32, 0, wk, S(stream)));

@@ -135,15 +135,17 @@ class DevBuf:
         b.upload(a)
         return b
 
-    def upload(self, a, stream=None):
+    def upload(self, a, stream=None, offset=0):
+        """Copy array a into the buffer at byte `offset` (synchronous)."""
         a = np.ascontiguousarray(a)
-        assert a.nbytes <= self.nbytes
-        _check(_lib.hq_memcpy_h2d(self.ptr, _ptr(a), a.nbytes, stream))
+        assert 0 <= offset and offset + a.nbytes <= self.nbytes
+        _check(_lib.hq_memcpy_h2d(self.ptr + offset, _ptr(a), a.nbytes, stream))
 
-    def download(self, shape, dtype, stream=None):
+    def download(self, shape, dtype, stream=None, offset=0):
+        """A new array of `shape` from the buffer's bytes at `offset` (synchronous)."""
         out = np.empty(shape, dtype=dtype)
-        assert out.nbytes <= self.nbytes
-        _check(_lib.hq_memcpy_d2h(_ptr(out), self.ptr, out.nbytes, stream))
+        assert 0 <= offset and offset + out.nbytes <= self.nbytes
+        _check(_lib.hq_memcpy_d2h(_ptr(out), self.ptr + offset, out.nbytes, stream))
         return out
 
     def zero(self, stream=None):

@@ -65,6 +65,18 @@ def test_upload_rejects_bad_descriptors_before_touching_a_device(dtype, gtype, r
     assert h.value is None
 
 
+def test_upload_rejects_matrices_of_4gib_or_more():
+    """The kernels address one matrix through 32-bit buffer ranges: 3,000,000 Q4_K rows of 2560
+    values (4.32e9 bytes) are refused before any device is touched."""
+    lib = hq.load()
+    buf = np.zeros(16, np.uint8)
+    w = hq.WMat(3, 3_000_000, 2560, buf.ctypes.data, synth.Q4_K, 0)
+    h = C.c_void_p()
+    assert lib.hq_mat_upload(C.byref(w), 0, C.byref(h)) == -1
+    assert "limited to 4 GiB" in hq.last_error()
+    assert h.value is None
+
+
 def test_gemm_kernel_names():
     """hq_gemm_kernel names the kernel the launch plan picks (the names rocprofv3 lists)."""
     cases = {(synth.Q4_K, 512, 9728, 2560): "k_gemm_q4_k_ws<5>", (synth.Q8_0, 512, 9728, 2560): "k_gemm_q8_0_ws<5>",
@@ -80,7 +92,9 @@ def test_gemm_kernel_names():
              (synth.Q8_0, 16, 2560, 9728): "k_gemm_q8_0_rb<1, 3, 2>", (synth.Q8_0, 16, 1024, 1024): "k_gemm_q8_0<1, 2>", (synth.Q4_K, 1, 9728, 2560): "k_gemv_q4_k_r<4>",
              (synth.Q4_K, 1, 2560, 9728): "k_gemv_q4_k_s<4>", (synth.Q4_K, 1, 100, 512): "k_gemv_q4_k_s<1>",
              (synth.Q4_K, 1, 9728, 256): "k_gemv_q4_k_s<16>", (synth.Q8_0, 1, 9728, 2560): "k_gemv_q8_0<2>",
-             (synth.Q8_0, 1, 100, 512): "k_gemv_q8_0<1>"}
+             (synth.Q8_0, 1, 100, 512): "k_gemv_q8_0<1>",
+             # special-scale cases: the narrow kernel at M = 16, the mid-M kernel with a 6-way K split
+             (synth.Q4_K, 16, 9728, 2560): "k_gemm_q4_k<2, 2>", (synth.Q4_K, 48, 9728, 2560): "k_gemm_q4_k_rb<1, 4, 3, 2>"}
     for (gtype, M, N, K), name in cases.items():
         assert hq.gemm_kernel(gtype, M, N, K) == name, (gtype, M, N, K)
 

@@ -235,10 +235,12 @@ def f64_reference(oracle, blocks, gtype, N, K, a16):
     return a @ w.T, np.abs(a) @ np.abs(w).T
 
 
-# the tile kernel (M = 350, 512 at N = 9728), Stream-K wide (N = 2560), the narrow M <= 64 kernel
-# and the GEMV (M = 1)
-SPECIAL = [(9728, 512, 350), (9728, 2560, 512), (2560, 9728, 512), (9728, 2560, 48), (9728, 2560, 1),
-           (2560, 9728, 1)]
+# the tile kernel (M = 350, 512 at N = 9728; M = 512 at N = 2560 with each tile's K split over 4
+# workgroups), the mid-M kernel (M = 48 at N = 9728: one workgroup per tile; M = 64 at N = 2560,
+# K = 9728: each tile's K split over 6, so every part restarts its accumulator units), the narrow
+# kernel (M = 16) and the GEMVs (M = 1)
+SPECIAL = [(9728, 512, 350), (9728, 2560, 512), (2560, 9728, 512), (9728, 2560, 48), (2560, 9728, 64),
+           (9728, 2560, 16), (9728, 2560, 1), (2560, 9728, 1)]
 
 
 @pytest.mark.parametrize("N,K,M", SPECIAL)
