@@ -336,6 +336,124 @@ extern "C" int hq_gemm(const hq_mat *W, const uint16_t *A, int M, void *C, int c
     return 0;
 }
 
+// ------------------------------------------------------------------------------------ no-alloc GEMM
+// hq_gemm_noalloc's workspace: one file-scope device array per GPU (allocated with the code object,
+// held until the process ends). Fixed layout: the per-tile counters first (HQ_NOALLOC_COUNTER_BYTES;
+// only counter logic touches them, and every kernel leaves them at zero), then the partial tiles,
+// then the activation sub-block sums. Host code never passes `scratch` itself to a kernel: its
+// device address comes from hipGetSymbolAddress, per device.
+static __device__ __align__(256) unsigned char scratch[HQ_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+std::mutex g_scratch_mu;
+std::map<int, unsigned char *> g_scratch;  // device -> address of that device's `scratch`
+
+__global__ void k_zero_words(uint32_t *p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+// Address of `scratch` on `device` (the current device); the first call per device looks it up and
+// zeroes the counter region with a fill kernel on `stream`, then waits for it.
+int scratch_ptr(int device, void *stream, unsigned char **out) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    auto it = g_scratch.find(device);
+    if (it != g_scratch.end()) {
+        *out = it->second;
+        return 0;
+    }
+    unsigned char *ptr = nullptr;
+    HIPCK(hipGetSymbolAddress((void **)&ptr, HIP_SYMBOL(scratch)));
+    k_zero_words<<<64, 256, 0, S(stream)>>>((uint32_t *)ptr, HQ_NOALLOC_COUNTER_BYTES / 4);
+    HIPCK(hipGetLastError());
+    HIPCK(hipStreamSynchronize(S(stream)));
+    g_scratch[device] = ptr;
+    *out = ptr;
+    return 0;
+}
+
+// Byte offsets of the partial tiles and the sums inside `scratch` for an M-row launch, and whether
+// the launch's workspace fits.
+struct NoallocLayout {
+    size_t partials, sums, end;
+    bool fits;
+};
+NoallocLayout noalloc_layout(size_t pb, size_t cb, size_t sb) {
+    NoallocLayout L;
+    L.partials = HQ_NOALLOC_COUNTER_BYTES;
+    L.sums = round_up(L.partials + pb, 256);
+    L.end = L.sums + sb;
+    L.fits = cb <= HQ_NOALLOC_COUNTER_BYTES && L.end <= HQ_NOALLOC_SCRATCH_BYTES;
+    return L;
+}
+}  // namespace
+
+extern "C" int hq_gemm_workspace_bytes(int ggml_type, int M, uint32_t N, uint32_t K, int n_cu, size_t *partial_bytes,
+                                       size_t *counter_bytes, size_t *sums_bytes, int *fits_noalloc) {
+    if (ggml_type != HQ_GGML_Q8_0 && ggml_type != HQ_GGML_Q4_K) return fail("hq_gemm_workspace_bytes: type %d", ggml_type);
+    if (M < 2 || N == 0 || K == 0 || K % block_values(ggml_type) || n_cu < 1)
+        return fail("hq_gemm_workspace_bytes: M = %d, N = %u, K = %u, n_cu = %d", M, N, K, n_cu);
+    if ((size_t)M > gemm_rows_per_launch(K))
+        return fail("hq_gemm_workspace_bytes: M = %d is more than one launch (%zu rows at K = %u)", M,
+                    gemm_rows_per_launch(K), K);
+    hq_dev_mat W = {};
+    W.type = ggml_type;
+    W.rows = N;
+    W.cols = K;
+    W.row_bytes = (size_t)(K / block_values(ggml_type)) * block_bytes(ggml_type);
+    size_t pb, cb, sb;
+    hq_gemm_work_bytes(&W, M, n_cu, &pb, &cb, &sb);
+    if (partial_bytes) *partial_bytes = pb;
+    if (counter_bytes) *counter_bytes = cb;
+    if (sums_bytes) *sums_bytes = sb;
+    if (fits_noalloc) *fits_noalloc = noalloc_layout(pb, cb, sb).fits ? 1 : 0;
+    return 0;
+}
+
+extern "C" int hq_gemm_noalloc(const hq_mat *W, const uint16_t *A, int M, void *C, int c_is_f32, int accumulate,
+                               void *stream) {
+    if (!W || !A || !C) return fail("hq_gemm_noalloc: null argument");
+    if (M < 1 || M > (1 << 23)) return fail("hq_gemm_noalloc: M = %d (1 .. 8388608)", M);
+    if (!aligned(A, 16)) return fail("hq_gemm_noalloc: A must be 16-byte aligned");
+    if (!aligned(C, c_is_f32 ? 4 : 2)) return fail("hq_gemm_noalloc: C is misaligned");
+    if (use_device(W->device)) return -1;
+    int n_cu;
+    if (device_cus(W->device, &n_cu)) return -1;
+    const size_t K = W->m.cols, N = W->m.rows, c_bytes = c_is_f32 ? 4 : 2, step = gemm_rows_per_launch(K);
+    // every launch's workspace is checked before the first one is queued
+    for (size_t m0 = 0; m0 < (size_t)M; m0 += step) {
+        const int mc = (int)((size_t)M - m0 < step ? (size_t)M - m0 : step);
+        if (mc == 1) continue;
+        size_t pb, cb, sb;
+        hq_gemm_work_bytes(&W->m, mc, n_cu, &pb, &cb, &sb);
+        const NoallocLayout L = noalloc_layout(pb, cb, sb);
+        if (!L.fits)
+            return fail("hq_gemm_noalloc: an M = %d launch needs %zu bytes of workspace (%zu of counters); the "
+                        "preallocated scratch holds %d (%d of counters): use hq_gemm",
+                        mc, L.end, cb, HQ_NOALLOC_SCRATCH_BYTES, HQ_NOALLOC_COUNTER_BYTES);
+    }
+    unsigned char *ptr;
+    if (scratch_ptr(W->device, stream, &ptr)) return -1;
+    for (size_t m0 = 0; m0 < (size_t)M; m0 += step) {
+        const int mc = (int)((size_t)M - m0 < step ? (size_t)M - m0 : step);
+        const uint16_t *Ap = A + m0 * K;
+        void *Cp = (char *)C + m0 * N * c_bytes;
+        if (mc == 1) {
+            HIPCK(hq_launch_gemv(&W->m, Ap, Cp, c_is_f32, accumulate, S(stream)));
+            continue;
+        }
+        size_t pb, cb, sb;
+        hq_gemm_work_bytes(&W->m, mc, n_cu, &pb, &cb, &sb);
+        const NoallocLayout L = noalloc_layout(pb, cb, sb);
+        HqGemmWork wk;
+        wk.counters = (int *)ptr;
+        wk.partials = (float *)(ptr + L.partials);
+        wk.sums = sb ? (uint16_t *)(ptr + L.sums) : nullptr;
+        wk.n_cu = n_cu;
+        HIPCK(hq_launch_gemm(&W->m, Ap, mc, Cp, c_is_f32, accumulate, wk, S(stream)));
+    }
+    return 0;
+}
+
 extern "C" int hq_gemv(const hq_mat *W, const uint16_t *a, void *c, int c_is_f32, int accumulate, void *stream) {
     return hq_gemm(W, a, 1, c, c_is_f32, accumulate, stream);
 }

@@ -1562,6 +1562,7 @@ void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_by
         *partial_bytes = tiles * sparts * 128 * 32 * snb * sizeof(float);
         *counter_bytes = tiles * sizeof(int);
     }
+    if (c.rbm == 1 || c.rb8 == 1) *partial_bytes = *counter_bytes = 0;  // mid-M kernels, one part per tile
     const int rparts = c.rbm > 1 ? c.rbm : c.rb8 > 1 ? c.rb8 : 0;
     if (rparts) {  // mid-M kernels with a K split: tiles of at most 64 x 64 fp32
         const size_t tiles = (W->rows + 63) / 64;

@@ -23,7 +23,7 @@ EXPORTS = (
     "hq_gather_dot", "hq_gather_dot_dev", "hq_matmul_host", "hq_malloc", "hq_free", "hq_memcpy_h2d",
     "hq_memcpy_d2h", "hq_memcpy_d2d", "hq_memset", "hq_stream_create", "hq_stream_destroy", "hq_stream_synchronize",
     "hq_device_synchronize", "hq_time_gemm", "hq_time_gemm_kernel", "hq_time_gather", "hq_gemm_tiles", "hq_llama_forward",
-    "hq_embed_f32", "hq_gemm_kernel",
+    "hq_embed_f32", "hq_gemm_kernel", "hq_gemm_noalloc", "hq_gemm_workspace_bytes",
 )
 
 
@@ -94,6 +94,9 @@ def load(path=LIB_PATH):
         "hq_gemm_kernel": (None, [i, i, i, i, C.c_char_p, i]),
         "hq_llama_forward": (i, [C.POINTER(Llama), vp, sz, vp, u32, vp]),
         "hq_embed_f32": (i, [vp, vp, i, vp, vp]),
+        "hq_gemm_noalloc": (i, [vp, vp, i, vp, i, i, vp]),
+        "hq_gemm_workspace_bytes": (i, [i, i, u32, u32, i, C.POINTER(sz), C.POINTER(sz), C.POINTER(sz),
+                                        C.POINTER(i)]),
     }
     for name in EXPORTS:
         fn = getattr(L, name)
@@ -223,6 +226,20 @@ def gemm(W, A, M, C_buf, c_f32=True, accumulate=False, stream=None):
     a = A.ptr if isinstance(A, DevBuf) else A
     c = C_buf.ptr if isinstance(C_buf, DevBuf) else C_buf
     _check(_lib.hq_gemm(W.h, a, M, c, int(c_f32), int(accumulate), stream))
+
+
+def gemm_noalloc(W, A, M, C_buf, c_f32=True, accumulate=False, stream=None):
+    """hq_gemm_noalloc: as gemm(), with the GEMM workspace in the library's preallocated scratch."""
+    a = A.ptr if isinstance(A, DevBuf) else A
+    c = C_buf.ptr if isinstance(C_buf, DevBuf) else C_buf
+    _check(_lib.hq_gemm_noalloc(W.h, a, M, c, int(c_f32), int(accumulate), stream))
+
+
+def gemm_workspace_bytes(gtype, M, N, K, n_cu=256):
+    """(partial bytes, counter bytes, sum bytes, fits hq_gemm_noalloc's scratch) of one M-row launch."""
+    pb, cb, sb, fits = C.c_size_t(), C.c_size_t(), C.c_size_t(), C.c_int()
+    _check(load().hq_gemm_workspace_bytes(gtype, M, N, K, n_cu, C.byref(pb), C.byref(cb), C.byref(sb), C.byref(fits)))
+    return pb.value, cb.value, sb.value, bool(fits.value)
 
 
 def gemm_np(W, a_f16_bits, c_f32=True, c_init=None):

@@ -77,6 +77,25 @@ int hq_gemm(const hq_mat *W, const uint16_t *A, int M, void *C, int c_is_f32, in
 /* M = 1: c[N] (+)= W . a, the HBM-bound wavefront-reduction GEMV (k_gemv_q at M = 1, :445-481). */
 int hq_gemv(const hq_mat *W, const uint16_t *a, void *c, int c_is_f32, int accumulate, void *stream);
 
+/* hq_gemm that allocates nothing: no hipMalloc, hipFree or allocating library call on any path.
+ * No counterpart in the reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation). The GEMM workspace
+ * (partial tiles, per-tile counters, activation sums) lives in one preallocated device array of
+ * HQ_NOALLOC_SCRATCH_BYTES per GPU, held from the library's first use of that GPU until the
+ * process ends; a call whose launches need more (see hq_gemm_workspace_bytes) fails with -1 before
+ * anything is queued. Same kernels and results as hq_gemm, bit for bit. Every call on one GPU
+ * shares that GPU's array: calls that overlap in time on one GPU (other streams, other threads)
+ * race and must be serialised by the caller. The first call on a device also waits for a small
+ * clearing kernel on `stream` (not capturable); later calls only queue the GEMM's kernels. */
+#define HQ_NOALLOC_SCRATCH_BYTES (96 << 20)
+#define HQ_NOALLOC_COUNTER_BYTES (1 << 20)
+int hq_gemm_noalloc(const hq_mat *W, const uint16_t *A, int M, void *C, int c_is_f32, int accumulate, void *stream);
+/* Workspace of one M-row GEMM launch (2 <= M <= rows per launch) of an N x K matrix of the given
+ * ggml type on a GPU with n_cu CUs: fp32 partial-tile bytes, counter bytes, activation-sum bytes,
+ * and whether it fits hq_gemm_noalloc's scratch (diagnostics; no device is touched). */
+int hq_gemm_workspace_bytes(int ggml_type, int M, uint32_t N, uint32_t K, int n_cu, size_t *partial_bytes,
+                            size_t *counter_bytes, size_t *sums_bytes, int *fits_noalloc);
+
 /* Option-row readout: out[b*k + j] = dot(H[b], head[ids[b*k + j]]) for b < B, j < k, fp32.
  * H fp16 [B, K] and out on the device; ids on the HOST (checked against rows, then staged).
  * Replaces the quantized readout of k_readout_q / k_norm_readout (src/cuda_backend.cu:490-502,

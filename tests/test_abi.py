@@ -77,6 +77,21 @@ def test_upload_rejects_matrices_of_4gib_or_more():
     assert h.value is None
 
 
+def test_gemm_workspace_bytes():
+    """Workspace of one GEMM launch (computed on the host, no device): the K-split tile kernel keeps
+    one fp32 tile per (tile, part) plus a counter per tile; the Stream-K kernel two 128 x 256 fp32
+    tiles per CU; hq_gemm_noalloc's 96 MiB scratch holds the BASELINE shapes and refuses larger."""
+    pb, cb, sb, fits = hq.gemm_workspace_bytes(synth.Q4_K, 512, 2560, 9728)
+    assert (pb, cb, sb, fits) == (64 * 4 * 128 * 160 * 4, 64 * 4, 512 * 38 * 32, True)
+    pb, cb, sb, fits = hq.gemm_workspace_bytes(synth.Q4_K, 4096, 9728, 2560)
+    assert (pb, cb, fits) == (2 * 256 * 128 * 256 * 4, 32 * 38 * 4, True)
+    assert hq.gemm_workspace_bytes(synth.Q8_0, 512, 9728, 2560) == (0, 0, 0, True)
+    assert hq.gemm_workspace_bytes(synth.Q4_K, 16384, 2560, 9216)[3]
+    assert not hq.gemm_workspace_bytes(synth.Q4_K, 65536, 256, 9216)[3]
+    with pytest.raises(hq.HQError, match="M = 1"):
+        hq.gemm_workspace_bytes(synth.Q4_K, 1, 256, 256)
+
+
 def test_gemm_kernel_names():
     """hq_gemm_kernel names the kernel the launch plan picks (the names rocprofv3 lists)."""
     cases = {(synth.Q4_K, 512, 9728, 2560): "k_gemm_q4_k_ws<5>", (synth.Q8_0, 512, 9728, 2560): "k_gemm_q8_0_ws<5>",
