@@ -103,18 +103,21 @@ DEV u4v buf_load16(rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
-// Eight fp16 B values s*q for 8 consecutive k from the low (HI = false) or high nibbles of 8 bytes:
-// masked bytes under 0x64 are fp16 1024 + q (or 1024 + 16q); one fma with (s, -1024 s) (or
-// (s/16, -64 s)) gives the exact integer.
-template <bool HI>
-DEV h8 decode8(u2v q, h2 mul, h2 add) {
-    const uint32_t mask = HI ? 0xf0f0f0f0u : 0x0f0f0f0fu;
+// Eight fp16 B values s*q for 8 consecutive k from the low (mask 0x0f0f0f0f) or high (0xf0f0f0f0)
+// nibbles of 8 bytes: masked bytes under 0x64 are fp16 1024 + q (or 1024 + 16q); one fma with
+// (s, -1024 s) (or (s/16, -64 s)) gives the exact integer. The mask may differ per lane.
+DEV h8 decode8m(u2v q, uint32_t mask, h2 mul, h2 add) {
     const uint32_t w0 = q.x & mask, w1 = q.y & mask;
     const h2 v0 = __builtin_elementwise_fma(as_h2(perm_lo(w0)), mul, add);
     const h2 v1 = __builtin_elementwise_fma(as_h2(perm_hi(w0)), mul, add);
     const h2 v2 = __builtin_elementwise_fma(as_h2(perm_lo(w1)), mul, add);
     const h2 v3 = __builtin_elementwise_fma(as_h2(perm_hi(w1)), mul, add);
     return h8{v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
+}
+
+template <bool HI>
+DEV h8 decode8(u2v q, h2 mul, h2 add) {
+    return decode8m(q, HI ? 0xf0f0f0f0u : 0x0f0f0f0fu, mul, add);
 }
 
 DEV f4 mfma(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
