@@ -174,6 +174,9 @@ extern "C" void hq_mat_free(hq_mat *m) {
     free(m);
 }
 
+const hq_dev_mat *hq_mat_dev(const hq_mat *m) { return &m->m; }
+int hq_mat_device(const hq_mat *m) { return m->device; }
+
 extern "C" int hq_mat_shape(const hq_mat *m, uint32_t *rows, uint32_t *cols, int *ggml_type) {
     if (!m) return fail("hq_mat_shape: no matrix");
     if (rows) *rows = m->m.rows;

@@ -18,6 +18,11 @@ typedef struct {
     size_t row_bytes;    // GGUF bytes per row
 } hq_dev_mat;
 
+// The device view and device of a resident matrix (hq_api.hip), for the library's own host code.
+struct hq_mat;
+const hq_dev_mat *hq_mat_dev(const struct hq_mat *m);
+int hq_mat_device(const struct hq_mat *m);
+
 // rows row0 .. row0 + nrows - 1, or rows ids[0 .. nrows - 1] when ids (device) is not null
 hipError_t hq_launch_dequant(const hq_dev_mat *W, uint32_t row0, const uint32_t *ids, uint32_t nrows, float *out,
                              hipStream_t st);

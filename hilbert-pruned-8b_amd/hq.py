@@ -25,6 +25,8 @@ EXPORTS = (
     "hq_device_synchronize", "hq_time_gemm", "hq_time_gemm_kernel", "hq_time_gather", "hq_gemm_tiles", "hq_llama_forward",
     "hq_embed_f32", "hq_gemm_kernel", "hq_gemm_noalloc", "hq_gemm_workspace_bytes",
 )
+# include/hq_backend.h (no hq_ prefix: the names of the reference entry points they replace)
+BACKEND_EXPORTS = ("hip_backend_create", "hip_selftest")
 
 
 class WMat(C.Structure):
@@ -43,6 +45,47 @@ class Llama(C.Structure):
                                           "head_dim", "rot_dim")] + [
         ("eps", C.c_float), ("rope_theta", C.c_float), ("embed", C.c_void_p), ("lm_head", C.c_void_p),
         ("final_norm", C.c_void_p), ("layers", C.c_void_p)]
+
+
+# Layout mirrors of the reference's config_t, layer_t, st_set_t, model_t and backend_t
+# (cleanroom-transformer/src/transformer.h:229-235, :278-364), as include/hq_backend.h declares them.
+class RefConfig(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("hidden", "n_layers", "intermediate", "vocab", "n_heads", "n_kv_heads",
+                                          "head_dim", "rot_dim", "lin_k_heads", "lin_v_heads", "lin_k_dim",
+                                          "lin_v_dim", "conv_k", "arch")] + [
+        ("eps", C.c_float), ("rope_theta", C.c_float), ("norm_offset", C.c_float), ("attn_gate", C.c_bool),
+        ("qk_norm", C.c_bool), ("tied", C.c_bool), ("rope_llama3", C.c_bool), ("rope_factor", C.c_float),
+        ("rope_low_freq", C.c_float), ("rope_high_freq", C.c_float), ("rope_orig_ctx", C.c_float),
+        ("layer_type", C.c_uint8 * 256), ("n_full", C.c_uint32), ("n_linear", C.c_uint32)]
+
+
+class RefLayer(C.Structure):
+    _fields_ = [("type", C.c_uint32), ("slot", C.c_uint32), ("in_norm", C.c_void_p), ("post_norm", C.c_void_p)] + \
+        [(n, WMat) for n in ("gate", "up", "down", "q", "k", "v", "o")] + \
+        [("q_norm", C.c_void_p), ("k_norm", C.c_void_p)] + [(n, WMat) for n in ("qkv", "z", "b", "a", "out")] + \
+        [(n, C.c_void_p) for n in ("conv_w", "A_log", "dt_bias", "lin_norm")]
+
+
+class RefStSet(C.Structure):
+    _fields_ = [("files", C.c_void_p), ("n_files", C.c_size_t), ("tensors", C.c_void_p), ("n_tensors", C.c_size_t)]
+
+
+class RefModel(C.Structure):
+    _fields_ = [("cfg", RefConfig), ("st", RefStSet), ("embed", WMat), ("lm_head", WMat), ("final_norm", C.c_void_p),
+                ("layers", C.c_void_p), ("rope_inv_freq", C.c_void_p), ("gguf", C.c_void_p), ("source", C.c_char * 512)]
+
+
+class RefBackend(C.Structure):
+    pass
+
+
+_BP = C.POINTER(RefBackend)
+RefBackend._fields_ = [
+    ("name", C.c_char_p), ("reset", C.CFUNCTYPE(C.c_int, _BP)),
+    ("forward", C.CFUNCTYPE(C.c_int, _BP, C.c_void_p, C.c_size_t, C.c_void_p, C.c_uint32, C.c_void_p)),
+    ("snapshot", C.CFUNCTYPE(C.c_int, _BP)), ("restore", C.CFUNCTYPE(C.c_int, _BP)),
+    ("destroy", C.CFUNCTYPE(None, _BP)), ("pos", C.c_size_t), ("max_seq", C.c_size_t),
+    ("last_hidden", C.CFUNCTYPE(C.c_int, _BP, C.c_void_p))]
 
 
 class HQError(RuntimeError):
@@ -95,10 +138,12 @@ def load(path=LIB_PATH):
         "hq_llama_forward": (i, [C.POINTER(Llama), vp, sz, vp, u32, vp]),
         "hq_embed_f32": (i, [vp, vp, i, vp, vp]),
         "hq_gemm_noalloc": (i, [vp, vp, i, vp, i, i, vp]),
+        "hip_backend_create": (C.POINTER(RefBackend), [C.POINTER(RefModel), sz, i, C.c_bool]),
+        "hip_selftest": (i, [C.POINTER(RefModel), i, sz, i]),
         "hq_gemm_workspace_bytes": (i, [i, i, u32, u32, i, C.POINTER(sz), C.POINTER(sz), C.POINTER(sz),
                                         C.POINTER(i)]),
     }
-    for name in EXPORTS:
+    for name in EXPORTS + BACKEND_EXPORTS:
         fn = getattr(L, name)
         fn.restype, fn.argtypes = sig[name]
     _lib = L
@@ -386,3 +431,113 @@ class LlamaModel:
         for m in self.mats:
             m.free()
         self.mats = []
+
+
+def rope_inv_freq(theta, rot_dim):
+    """The reference's RoPE table without Llama 3.1 scaling (src/model.c:453-454): float32
+    1 / powf(theta, 2k / rot_dim), computed with the C library's powf."""
+    libm = C.CDLL("libm.so.6")
+    libm.powf.restype, libm.powf.argtypes = C.c_float, [C.c_float, C.c_float]
+    out = np.empty(rot_dim // 2, np.float32)
+    for k in range(rot_dim // 2):
+        e = np.float32(np.float32(2 * k) / np.float32(rot_dim))
+        out[k] = np.float32(1.0) / np.float32(libm.powf(np.float32(theta), e))
+    return out
+
+
+class RefModelView:
+    """A reference model_t (layout mirror RefModel) over a synth.tiny_llama()-style dict of Q8_0 /
+    Q4_K block arrays, as the reference's model_load would fill it for a GGUF Llama model: q/k in
+    llama.cpp storage order with perm_heads, every layer LAYER_FULL, RMSNorm offset 0. Keeps the
+    arrays alive while the view exists."""
+
+    def __init__(self, model, gtype=Q8_0):
+        c = model["cfg"]
+        self.keep = []
+        H, I, V = c["hidden"], c["intermediate"], c["vocab"]
+        qw, kvw = c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
+
+        def wm(blocks, rows, cols, perm=0):
+            blocks = np.ascontiguousarray(blocks, np.uint8)
+            self.keep.append(blocks)
+            return WMat(DT_GGML, rows, cols, blocks.ctypes.data, gtype, perm)
+
+        def vec(v):
+            v = np.ascontiguousarray(v, np.float32)
+            self.keep.append(v)
+            return v.ctypes.data
+
+        cfg = RefConfig()
+        for k in ("hidden", "n_layers", "intermediate", "vocab", "n_heads", "n_kv_heads", "head_dim", "rot_dim"):
+            setattr(cfg, k, c[k])
+        cfg.arch, cfg.eps, cfg.rope_theta, cfg.norm_offset = 1, c["eps"], c["rope_theta"], 0.0
+        cfg.n_full, cfg.n_linear = c["n_layers"], 0
+        for li in range(c["n_layers"]):
+            cfg.layer_type[li] = 1
+        self.layers = (RefLayer * c["n_layers"])()
+        for li, L in enumerate(model["layers"]):
+            d = self.layers[li]
+            d.type, d.slot = 1, li
+            d.in_norm, d.post_norm = vec(L["in_norm"]), vec(L["post_norm"])
+            d.q = wm(L["q"], qw, H, c["n_heads"])
+            d.k = wm(L["k"], kvw, H, c["n_kv_heads"])
+            d.v, d.o = wm(L["v"], kvw, H), wm(L["o"], H, qw)
+            d.gate, d.up, d.down = wm(L["gate"], I, H), wm(L["up"], I, H), wm(L["down"], H, I)
+        self.m = RefModel()
+        self.m.cfg = cfg
+        self.m.embed, self.m.lm_head = wm(model["embed"], V, H), wm(model["lm_head"], V, H)
+        self.m.final_norm = vec(model["final_norm"])
+        self.m.layers = C.cast(self.layers, C.c_void_p).value
+        self.m.rope_inv_freq = vec(rope_inv_freq(c["rope_theta"], c["rot_dim"]))
+
+
+class HipBackend:
+    """hip_backend_create's backend_t, driven through its vtable exactly as the reference engine does."""
+
+    def __init__(self, view, max_seq, device=0, keep_quantized=True):
+        self.view = view
+        p = load().hip_backend_create(C.byref(view.m), max_seq, device, keep_quantized)
+        if not p:
+            raise HQError(last_error())
+        self.p = p
+
+    @property
+    def pos(self):
+        return self.p.contents.pos
+
+    def _call(self, rc):
+        if rc != 0:
+            raise HQError(last_error())
+
+    def reset(self):
+        self._call(self.p.contents.reset(self.p))
+
+    def forward(self, tokens, ids=None):
+        tokens = np.ascontiguousarray(tokens, np.uint32)
+        n_ids = 0 if ids is None else len(ids)
+        ids = None if ids is None else np.ascontiguousarray(ids, np.uint32)
+        out = np.empty(n_ids, np.float32)
+        self._call(self.p.contents.forward(self.p, tokens.ctypes.data, len(tokens),
+                                           ids.ctypes.data if n_ids else None, n_ids,
+                                           out.ctypes.data if n_ids else None))
+        return out
+
+    def snapshot(self):
+        self._call(self.p.contents.snapshot(self.p))
+
+    def restore(self):
+        self._call(self.p.contents.restore(self.p))
+
+    def last_hidden(self):
+        out = np.empty(self.view.m.cfg.hidden, np.float32)
+        self._call(self.p.contents.last_hidden(self.p, out.ctypes.data))
+        return out
+
+    def destroy(self):
+        if self.p:
+            self.p.contents.destroy(self.p)
+            self.p = None
+
+
+def hip_selftest(view, device=0, n_tokens=64, verbose=1):
+    return load().hip_selftest(C.byref(view.m), device, n_tokens, verbose)

@@ -19,7 +19,7 @@ def declared_functions():
     for path in HEADERS:
         text = open(path).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-        for m in re.finditer(r"^[A-Za-z_][\w\s\*]*?\b(hq_\w+)\s*\(", text, flags=re.M):
+        for m in re.finditer(r"^[A-Za-z_][\w\s\*]*?\b((?:hq|hip)_\w+)\s*\(", text, flags=re.M):
             names.add(m.group(1))
     return names
 
@@ -31,7 +31,7 @@ def test_library_built_and_exports_every_declared_function():
     assert len(declared) >= 25
     missing = [n for n in sorted(declared) if not hasattr(lib, n)]
     assert not missing, missing
-    assert declared == set(hq.EXPORTS), declared ^ set(hq.EXPORTS)
+    assert declared == set(hq.EXPORTS + hq.BACKEND_EXPORTS), declared ^ set(hq.EXPORTS + hq.BACKEND_EXPORTS)
 
 
 def test_binding_signatures_load():
@@ -158,3 +158,82 @@ def test_synth_is_deterministic():
     q = synth.q8_0_blocks(synth.Rng(4), 8, 256)
     d = q.reshape(-1, 34)[:, :2].copy().view(np.float16)
     assert (d >= 0).all() and np.isfinite(d).all()
+
+
+# ------------------------------------------------------------------ HIP backend (include/hq_backend.h)
+REF_SRC = "/root/reference/cleanroom-transformer/src"
+LAYOUT_FIELDS = {
+    ("config_t", "hq_ref_config_t"): ["hidden", "n_layers", "intermediate", "vocab", "n_heads", "n_kv_heads",
+                                       "head_dim", "rot_dim", "lin_k_heads", "lin_v_heads", "lin_k_dim", "lin_v_dim",
+                                       "conv_k", "arch", "eps", "rope_theta", "norm_offset", "attn_gate", "qk_norm",
+                                       "tied", "rope_llama3", "rope_factor", "rope_low_freq", "rope_high_freq",
+                                       "rope_orig_ctx", "layer_type", "n_full", "n_linear"],
+    ("layer_t", "hq_ref_layer_t"): ["type", "slot", "in_norm", "post_norm", "gate", "up", "down", "q", "k", "v", "o",
+                                     "q_norm", "k_norm", "qkv", "z", "b", "a", "out", "conv_w", "A_log", "dt_bias",
+                                     "lin_norm"],
+    ("st_set_t", "hq_ref_st_set_t"): ["files", "n_files", "tensors", "n_tensors"],
+    ("model_t", "hq_ref_model_t"): ["cfg", "st", "embed", "lm_head", "final_norm", "layers", "rope_inv_freq", "gguf",
+                                     "source"],
+    ("backend_t", "hq_ref_backend_t"): ["name", "reset", "forward", "snapshot", "restore", "destroy", "pos", "max_seq",
+                                         "last_hidden"],
+    ("wmat_t", "hq_wmat_t"): ["dtype", "rows", "cols", "data", "ggml_type", "perm_heads"],
+}
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(REF_SRC, "transformer.h")), reason="needs /root/reference")
+def test_backend_structs_match_reference_header(tmp_path):
+    """Every mirror struct of include/hq_backend.h has the size and field offsets of the reference's
+    own declaration (compiled together, checked with _Static_assert)."""
+    import shutil
+    import subprocess
+    if not shutil.which("gcc"):
+        pytest.skip("gcc not found")
+    lines = ['#include <stddef.h>', '#include "transformer.h"', '#include "hq_backend.h"']
+    for (ref, mine), fields in LAYOUT_FIELDS.items():
+        lines.append(f'_Static_assert(sizeof({ref}) == sizeof({mine}), "size {mine}");')
+        for f in fields:
+            lines.append(f'_Static_assert(offsetof({ref}, {f}) == offsetof({mine}, {f}), "{mine}.{f}");')
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    r = subprocess.run(["gcc", "-std=c11", "-fsyntax-only", f"-I{REF_SRC}", f"-I{os.path.join(ROOT, 'include')}",
+                        str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+
+
+def test_backend_ctypes_mirrors_match_header(tmp_path):
+    """hq.py's ctypes mirrors (used by the tests) have the header's offsets."""
+    import shutil
+    import subprocess
+    if not shutil.which("gcc"):
+        pytest.skip("gcc not found")
+    py = {"hq_ref_config_t": hq.RefConfig, "hq_ref_layer_t": hq.RefLayer, "hq_ref_st_set_t": hq.RefStSet,
+          "hq_ref_model_t": hq.RefModel, "hq_ref_backend_t": hq.RefBackend, "hq_wmat_t": hq.WMat}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "hq_backend.h"', 'int main(void) {']
+    for (_, mine), fields in LAYOUT_FIELDS.items():
+        lines.append(f'printf("{mine} sizeof %zu\\n", sizeof({mine}));')
+        for f in fields:
+            lines.append(f'printf("{mine} {f} %zu\\n", offsetof({mine}, {f}));')
+    lines.append("return 0; }")
+    src, exe = tmp_path / "probe.c", tmp_path / "probe"
+    src.write_text("\n".join(lines) + "\n")
+    subprocess.run(["gcc", "-std=c11", f"-I{os.path.join(ROOT, 'include')}", str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    for line in filter(None, out):
+        name, field, val = line.split()
+        cls = py[name]
+        got = C.sizeof(cls) if field == "sizeof" else getattr(cls, field).offset
+        assert got == int(val), line
+
+
+def test_backend_create_refuses_before_touching_a_device():
+    lib = hq.load()
+    m = hq.RefModel()
+    assert not lib.hip_backend_create(C.byref(m), 16, 0, False)
+    assert "keep_quantized" in hq.last_error()
+    m.cfg.hidden, m.cfg.n_layers, m.cfg.vocab, m.cfg.n_heads, m.cfg.n_kv_heads = 64, 1, 100, 1, 1
+    m.cfg.head_dim, m.cfg.intermediate, m.cfg.rot_dim = 64, 128, 64
+    layers = (hq.RefLayer * 1)()
+    layers[0].type = 0  # LAYER_LINEAR
+    m.layers = C.cast(layers, C.c_void_p).value
+    assert not lib.hip_backend_create(C.byref(m), 16, 0, True)
+    assert "Gated-DeltaNet" in hq.last_error()

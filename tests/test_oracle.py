@@ -278,6 +278,20 @@ def test_llama_forward_matches_reference(oracle, reference, tiny_model, tmp_path
                           reference.logits(path, t2, i2).view(np.uint32))
 
 
+def test_llama_forward_gqa_matches_reference(oracle, reference, tmp_path):
+    """Grouped-query attention (8 query heads over 2 kv heads, src/cpu_backend.c:110) and a prompt of
+    300 tokens: the oracle forward is bit-exact with the reference's model_load + cpu_forward."""
+    import gguf_writer
+    cfg = dict(synth.TINY_LLAMA, n_layers=2, n_kv_heads=2, vocab=4096)
+    model = synth.tiny_llama(3, cfg)
+    path = str(tmp_path / "gqa.gguf")
+    gguf_writer.write_tiny_llama(path, model)
+    tokens, ids = synth.tiny_llama_prompt(4, T=300, vocab=cfg["vocab"], n_ids=8)
+    a = oracle.llama_forward(model, tokens, ids)
+    b = reference.logits(path, tokens, ids)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 def test_llama_forward_rejects_bad_ids(oracle, tiny_model):
     with pytest.raises(ValueError):
         oracle.llama_forward(tiny_model, np.array([32000], np.uint32), np.array([1], np.uint32))
