@@ -85,8 +85,13 @@ extern "C" int hq_device_init(int device) {
 }
 
 // ------------------------------------------------------------------------------------ residency
-static uint32_t block_values(int t) { return t == HQ_GGML_Q8_0 ? 32u : t == HQ_GGML_Q4_K ? 256u : 0u; }
-static uint32_t block_bytes(int t) { return t == HQ_GGML_Q8_0 ? 34u : t == HQ_GGML_Q4_K ? 144u : 0u; }
+static uint32_t block_values(int t) {
+    return t == HQ_GGML_Q8_0 ? 32u : t == HQ_GGML_Q4_K || t == HQ_GGML_Q6_K ? 256u : 0u;
+}
+static uint32_t block_bytes(int t) {
+    return t == HQ_GGML_Q8_0 ? 34u : t == HQ_GGML_Q4_K ? 144u : t == HQ_GGML_Q6_K ? 210u : 0u;
+}
+constexpr size_t Q6K_SLOT = 224;  // device bytes of one Q6_K super-block (210 GGUF bytes + zero padding)
 
 // Storage row of Hugging Face row r (llama.cpp q/k interleave; reference src/model.c:283-289).
 static uint32_t storage_row(uint32_t rows, uint32_t perm_heads, uint32_t r) {
@@ -102,7 +107,7 @@ extern "C" int hq_mat_upload(const hq_wmat_t *w, int device, hq_mat **out) {
     if (!w || !w->data) return fail("hq_mat_upload: no matrix");
     if (w->dtype != HQ_DT_GGML) return fail("hq_mat_upload: dtype %d is not a GGUF block type", w->dtype);
     const uint32_t per = block_values(w->ggml_type);
-    if (!per) return fail("hq_mat_upload: ggml type %d is not supported (Q8_0 = 8, Q4_K = 12)", w->ggml_type);
+    if (!per) return fail("hq_mat_upload: ggml type %d is not supported (Q8_0 = 8, Q4_K = 12, Q6_K = 14)", w->ggml_type);
     if (w->rows == 0 || w->cols == 0 || w->cols % per)
         return fail("hq_mat_upload: shape [%u, %u] is not a whole number of %u-value blocks per row", w->rows, w->cols,
                     per);
@@ -111,9 +116,10 @@ extern "C" int hq_mat_upload(const hq_wmat_t *w, int device, hq_mat **out) {
         return fail("hq_mat_upload: %u rows do not split into %u heads of even size", w->rows, w->perm_heads);
     const size_t rb = (size_t)(w->cols / per) * block_bytes(w->ggml_type);
     // the kernels address a matrix through 32-bit buffer ranges: its device bytes stay below 4 GiB
-    const size_t dev_bytes = w->ggml_type == HQ_GGML_Q4_K
-                                 ? rb * w->rows
-                                 : round_up((size_t)w->rows * w->cols, 256) + (size_t)w->rows * round_up(w->cols / 32, 8) * 2;
+    const size_t dev_bytes = w->ggml_type == HQ_GGML_Q4_K   ? rb * w->rows
+                             : w->ggml_type == HQ_GGML_Q6_K ? (size_t)(w->cols / 256) * Q6K_SLOT * w->rows
+                                                            : round_up((size_t)w->rows * w->cols, 256) +
+                                                                  (size_t)w->rows * round_up(w->cols / 32, 8) * 2;
     if (dev_bytes >= ((size_t)1 << 32))
         return fail("hq_mat_upload: shape [%u, %u] needs %zu device bytes; one matrix is limited to 4 GiB (split its rows)",
                     w->rows, w->cols, dev_bytes);
@@ -127,7 +133,17 @@ extern "C" int hq_mat_upload(const hq_wmat_t *w, int device, hq_mat **out) {
     m->m.cols = w->cols;
     m->m.row_bytes = rb;
     std::vector<uint8_t> host;
-    if (w->ggml_type == HQ_GGML_Q4_K) {
+    if (w->ggml_type == HQ_GGML_Q6_K) {
+        // each 210-byte super-block in a 224-byte slot (16-byte aligned loads), zero padded
+        const size_t nb = w->cols / 256, drb = nb * Q6K_SLOT;
+        m->m.row_bytes = drb;
+        m->bytes = drb * w->rows;
+        host.assign(m->bytes, 0);
+        for (uint32_t r = 0; r < w->rows; r++) {
+            const uint8_t *row = src + (size_t)storage_row(w->rows, w->perm_heads, r) * rb;
+            for (size_t b = 0; b < nb; b++) memcpy(host.data() + (size_t)r * drb + b * Q6K_SLOT, row + 210 * b, 210);
+        }
+    } else if (w->ggml_type == HQ_GGML_Q4_K) {
         m->bytes = rb * w->rows;
         host.resize(m->bytes);
         for (uint32_t r = 0; r < w->rows; r++)
@@ -189,7 +205,7 @@ extern "C" size_t hq_mat_device_bytes(const hq_mat *m) { return m ? m->bytes : 0
 
 extern "C" int hq_mat_download(const hq_mat *m, void *out, size_t nbytes) {
     if (!m || !out) return fail("hq_mat_download: null argument");
-    const size_t rb = m->m.row_bytes, total = rb * m->m.rows;
+    const size_t rb = (size_t)(m->m.cols / block_values(m->m.type)) * block_bytes(m->m.type), total = rb * m->m.rows;
     if (nbytes < total) return fail("hq_mat_download: need %zu bytes, got %zu", total, nbytes);
     if (use_device(m->device)) return -1;
     std::vector<uint8_t> host(m->bytes);
@@ -197,6 +213,13 @@ extern "C" int hq_mat_download(const hq_mat *m, void *out, size_t nbytes) {
     uint8_t *dst = (uint8_t *)out;
     if (m->m.type == HQ_GGML_Q4_K) {
         memcpy(dst, host.data(), total);
+        return 0;
+    }
+    if (m->m.type == HQ_GGML_Q6_K) {
+        const size_t nb = m->m.cols / 256;
+        for (uint32_t r = 0; r < m->m.rows; r++)
+            for (size_t b = 0; b < nb; b++)
+                memcpy(dst + (size_t)r * rb + 210 * b, host.data() + (size_t)r * m->m.row_bytes + b * Q6K_SLOT, 210);
         return 0;
     }
     const size_t K = m->m.cols, nb = K / 32, ldd = (size_t)m->m.ldd;

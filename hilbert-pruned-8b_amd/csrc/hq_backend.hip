@@ -48,13 +48,27 @@ constexpr int MAX_IDS = 4096;  // readout ids per forward
 
 // ------------------------------------------------------------------------------------ kernels
 // Eight consecutive weights 8g .. 8g + 7 of row r as fp32, bit-identical to the reference decoder
-// (src/ggml_quant.h:95-99 Q8_0, :135-150 Q4_K; device layouts as in hq_kernels.hip).
+// (src/ggml_quant.h:95-99 Q8_0, :135-150 Q4_K, :151-169 Q6_K; device layouts as in hq_kernels.hip
+// and hq_q6k.hip).
 DEV void deq8(const hq_dev_mat &W, size_t r, int g, float (&w)[8]) {
     if (W.type == HQ_TYPE_Q8_0) {
         const u2v q = *(const u2v *)(W.qs + r * W.cols + 8 * (size_t)g);
         const float d = h2f(W.d[r * (size_t)W.ldd + g / 4]);
 #pragma unroll
         for (int j = 0; j < 8; j++) w[j] = (float)(int8_t)(byte_of(j < 4 ? q.x : q.y, j & 3) ^ 0x80u) * d;
+        return;
+    }
+    if (W.type == HQ_TYPE_Q6_K) {  // src/ggml_quant.h:151-169, 224-byte device slots
+        const int v = (8 * g) % 256, h = v >> 7, rr = (v >> 5) & 3, l0 = v & 31;
+        const uint8_t *b = W.qs + r * W.row_bytes + (size_t)(8 * g / 256) * 224;
+        const u2v ql = *(const u2v *)(b + 64 * h + 32 * (rr & 1) + l0), qh = *(const u2v *)(b + 128 + 32 * h + l0);
+        const float ds = h2f(*(const uint16_t *)(b + 208)) * (float)(int8_t)b[192 + 8 * h + 2 * rr + (l0 >> 4)];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int lo = (int)((((j < 4 ? ql.x : ql.y) >> (8 * (j & 3))) >> (rr >= 2 ? 4 : 0)) & 0xfu);
+            const int hb = (int)((((j < 4 ? qh.x : qh.y) >> (8 * (j & 3))) >> (2 * rr)) & 3u);
+            w[j] = ds * (float)((lo | (hb << 4)) - 32);
+        }
         return;
     }
     const int v0 = 8 * g, sub = (v0 % 256) / 32, l0 = v0 % 32;
@@ -643,6 +657,20 @@ void compare(const char *what, const float *ref, const float *got, uint32_t n, d
 }
 
 }  // namespace
+
+extern "C" int hq_gemv_swiglu(const hq_mat *gate, const hq_mat *up, const uint16_t *a, uint16_t *out, void *stream) {
+    if (!gate || !up || !a || !out) return hq_internal_fail("hq_gemv_swiglu: null argument");
+    uint32_t rg, kg, ru, ku;
+    if (hq_mat_shape(gate, &rg, &kg, nullptr) || hq_mat_shape(up, &ru, &ku, nullptr)) return -1;
+    if (rg != ru || kg != ku) return hq_internal_fail("hq_gemv_swiglu: gate [%u, %u] and up [%u, %u] differ", rg, kg, ru, ku);
+    if (hq_mat_device(gate) != hq_mat_device(up)) return hq_internal_fail("hq_gemv_swiglu: gate and up on different devices");
+    if ((uintptr_t)a % 16 || (uintptr_t)out % 2) return hq_internal_fail("hq_gemv_swiglu: a must be 16-byte aligned");
+    BCK(hipSetDevice(hq_mat_device(gate)));
+    k_gateup_swiglu<<<(rg + 3) / 4, 256, 0, (hipStream_t)stream>>>(*hq_mat_dev(gate), *hq_mat_dev(up), (const _Float16 *)a,
+                                                                  (_Float16 *)out, (int)rg, (int)kg);
+    BCK(hipGetLastError());
+    return 0;
+}
 
 // The reference CPU backend, when the program that loads this library provides it (the reference
 // binary does: src/cpu_backend.c); a weak reference, so the library loads without it.

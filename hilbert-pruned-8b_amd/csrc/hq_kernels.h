@@ -6,16 +6,16 @@
 #include <stddef.h>
 #include <stdint.h>
 
-enum { HQ_TYPE_Q8_0 = 8, HQ_TYPE_Q4_K = 12 };
+enum { HQ_TYPE_Q8_0 = 8, HQ_TYPE_Q4_K = 12, HQ_TYPE_Q6_K = 14 };
 
 // A weight matrix resident in HBM, rows in Hugging Face order (see hq_kernels.hip for layouts).
 typedef struct {
     int type;
     uint32_t rows, cols;
-    const uint8_t *qs;   // Q8_0: biased quant plane [rows][cols]; Q4_K: super-blocks [rows][row_bytes]
+    const uint8_t *qs;   // Q8_0: biased quant plane [rows][cols]; Q4_K / Q6_K: super-blocks [rows][row_bytes]
     const uint16_t *d;   // Q8_0: fp16 scale plane [rows][ldd]; Q4_K: unused
     int ldd;             // Q8_0 scale-plane row stride in halves (cols/32 rounded up to 8)
-    size_t row_bytes;    // GGUF bytes per row
+    size_t row_bytes;    // Q8_0 / Q4_K: GGUF bytes per row; Q6_K: device bytes per row (224 per super-block)
 } hq_dev_mat;
 
 // The device view and device of a resident matrix (hq_api.hip), for the library's own host code.
@@ -72,5 +72,14 @@ hipError_t hq_launch_gemm_rb8(const hq_dev_mat *W, const uint16_t *A, int M, voi
                               int parts, float *partials, int *counters, hipStream_t st);
 hipError_t hq_launch_gemm_ws8(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
                               int nb, int parts, float *partials, int *counters, hipStream_t st);
+
+// Q6_K (hq_q6k.hip)
+struct GemmArgs;
+hipError_t hq_launch_dequant_q6k(const hq_dev_mat *W, uint32_t row0, const uint32_t *ids, uint32_t nrows, float *out,
+                                 hipStream_t st);
+hipError_t hq_launch_gemv_q6k(const hq_dev_mat *W, const uint16_t *a, void *C, int c_f32, int accumulate, hipStream_t st);
+hipError_t hq_launch_gather_q6k(const hq_dev_mat *W, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
+                                hipStream_t st);
+hipError_t hq_launch_gemm_q6k(const GemmArgs &g, int mb, hipStream_t st);
 
 #endif

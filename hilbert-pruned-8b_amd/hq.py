@@ -11,10 +11,10 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libhq.so")
 
-Q8_0, Q4_K = 8, 12
+Q8_0, Q4_K, Q6_K = 8, 12, 14
 DT_GGML = 3
-BLOCK_VALUES = {Q8_0: 32, Q4_K: 256}
-BLOCK_BYTES = {Q8_0: 34, Q4_K: 144}
+BLOCK_VALUES = {Q8_0: 32, Q4_K: 256, Q6_K: 256}
+BLOCK_BYTES = {Q8_0: 34, Q4_K: 144, Q6_K: 210}
 
 # Every function declared in include/hq.h and include/hq_llama.h.
 EXPORTS = (
@@ -23,7 +23,7 @@ EXPORTS = (
     "hq_gather_dot", "hq_gather_dot_dev", "hq_matmul_host", "hq_malloc", "hq_free", "hq_memcpy_h2d",
     "hq_memcpy_d2h", "hq_memcpy_d2d", "hq_memset", "hq_stream_create", "hq_stream_destroy", "hq_stream_synchronize",
     "hq_device_synchronize", "hq_time_gemm", "hq_time_gemm_kernel", "hq_time_gather", "hq_gemm_tiles", "hq_llama_forward",
-    "hq_embed_f32", "hq_gemm_kernel", "hq_gemm_noalloc", "hq_gemm_workspace_bytes",
+    "hq_embed_f32", "hq_gemm_kernel", "hq_gemm_noalloc", "hq_gemm_workspace_bytes", "hq_gemv_swiglu",
 )
 # include/hq_backend.h (no hq_ prefix: the names of the reference entry points they replace)
 BACKEND_EXPORTS = ("hip_backend_create", "hip_selftest")
@@ -138,6 +138,7 @@ def load(path=LIB_PATH):
         "hq_llama_forward": (i, [C.POINTER(Llama), vp, sz, vp, u32, vp]),
         "hq_embed_f32": (i, [vp, vp, i, vp, vp]),
         "hq_gemm_noalloc": (i, [vp, vp, i, vp, i, i, vp]),
+        "hq_gemv_swiglu": (i, [vp, vp, vp, vp, vp]),
         "hip_backend_create": (C.POINTER(RefBackend), [C.POINTER(RefModel), sz, i, C.c_bool]),
         "hip_selftest": (i, [C.POINTER(RefModel), i, sz, i]),
         "hq_gemm_workspace_bytes": (i, [i, i, u32, u32, i, C.POINTER(sz), C.POINTER(sz), C.POINTER(sz),
@@ -285,6 +286,17 @@ def gemm_workspace_bytes(gtype, M, N, K, n_cu=256):
     pb, cb, sb, fits = C.c_size_t(), C.c_size_t(), C.c_size_t(), C.c_int()
     _check(load().hq_gemm_workspace_bytes(gtype, M, N, K, n_cu, C.byref(pb), C.byref(cb), C.byref(sb), C.byref(fits)))
     return pb.value, cb.value, sb.value, bool(fits.value)
+
+
+def gemv_swiglu_np(gate, up, a_f16_bits):
+    """hq_gemv_swiglu on a numpy fp16 row [cols]: fp16 bits [rows] of silu(gate . a) * (up . a)."""
+    dA = DevBuf.from_array(np.ascontiguousarray(a_f16_bits, dtype=np.uint16))
+    dO = DevBuf(gate.rows * 2)
+    _check(_lib.hq_gemv_swiglu(gate.h, up.h, dA.ptr, dO.ptr, None))
+    synchronize()
+    out = dO.download((gate.rows,), np.uint16)
+    dA.free(), dO.free()
+    return out
 
 
 def gemm_np(W, a_f16_bits, c_f32=True, c_init=None):

@@ -6,6 +6,7 @@ same bytes are produced here, on the GPU box, in tests and in bench.py.
 Block layouts (GGUF, little-endian; reference cleanroom-transformer/src/ggml_quant.h):
   Q8_0  34 B / 32 values : fp16 d, int8 q[32]                          (ggml_quant.h:95-99)
   Q4_K 144 B / 256 values: fp16 d, fp16 dmin, u8 scales[12], u8 qs[128] (ggml_quant.h:135-150)
+  Q6_K 210 B / 256 values: u8 ql[128], u8 qh[64], int8 scales[16], fp16 d (ggml_quant.h:151-169)
 
 Workloads:
   config 2  Q8_0 9728x2560, q uniform in [-127, 127], d = fp16(|N(0,1)| * 2e-4)
@@ -17,9 +18,9 @@ Activations are fp16(N(0,1)), returned as uint16 bit patterns.
 """
 import numpy as np
 
-Q8_0, Q4_K = 8, 12
-BLOCK_VALUES = {Q8_0: 32, Q4_K: 256}
-BLOCK_BYTES = {Q8_0: 34, Q4_K: 144}
+Q8_0, Q4_K, Q6_K = 8, 12, 14
+BLOCK_VALUES = {Q8_0: 32, Q4_K: 256, Q6_K: 256}
+BLOCK_BYTES = {Q8_0: 34, Q4_K: 144, Q6_K: 210}
 
 _M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
 
@@ -114,7 +115,18 @@ def q4_k_blocks(rng, rows, cols, scale=1e-3):
     return blk.reshape(rows, row_bytes(Q4_K, cols))
 
 
+def q6_k_blocks(rng, rows, cols, scale=2e-5):
+    """Q6_K super-blocks [rows, row_bytes] (uint8): ql, qh uniform bytes, int8 scales uniform in
+    [-128, 127], d = fp16(|N(0,1)| * scale) (weights of a few 1e-2, as in real models)."""
+    nb = rows * (cols // 256)
+    blk = rng.bytes(nb * 210).reshape(nb, 210)
+    blk[:, 208:210] = f16_bits(np.abs(rng.normal(nb)) * scale).view(np.uint8).reshape(nb, 2)
+    return blk.reshape(rows, row_bytes(Q6_K, cols))
+
+
 def random_blocks(gtype, rng, rows, cols):
+    if gtype == Q6_K:
+        return q6_k_blocks(rng, rows, cols)
     return q8_0_blocks(rng, rows, cols) if gtype == Q8_0 else q4_k_blocks(rng, rows, cols)
 
 

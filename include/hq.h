@@ -10,8 +10,8 @@
  *     (src/cpu_backend.c:38-54, src/cuda_backend.cu:701-715);
  *   - every fallible call returns 0, or -1 after recording a message for hq_last_error()
  *     (the reference's set_error/last_error convention, src/transformer.h:17-21, src/base.c:11-21).
- * Supported block types: Q8_0 (ggml type 8) and Q4_K (12) (src/ggml_quant.h:16-19); K must be a
- * multiple of the block (32 / 256), as src/gguf.c:331-335 enforces for GGUF tensors.
+ * Supported block types: Q8_0 (ggml type 8), Q4_K (12) and Q6_K (14) (src/ggml_quant.h:16-19); K must
+ * be a multiple of the block (32 / 256 / 256), as src/gguf.c:331-335 enforces for GGUF tensors.
  * Not thread-safe across concurrent calls that share a matrix's device (as the reference engine,
  * which is single threaded: src/transformer.h:18-19).
  */
@@ -27,7 +27,7 @@ extern "C" {
 #endif
 
 enum { HQ_DT_GGML = 3 };                     /* dtype_t DT_GGML (src/transformer.h:214) */
-enum { HQ_GGML_Q8_0 = 8, HQ_GGML_Q4_K = 12 }; /* src/ggml_quant.h:16-19 */
+enum { HQ_GGML_Q8_0 = 8, HQ_GGML_Q4_K = 12, HQ_GGML_Q6_K = 14 }; /* src/ggml_quant.h:16-19 */
 
 /* Host matrix descriptor, field for field the reference wmat_t (src/transformer.h:293-300):
  * data points at GGUF blocks (typically into the model's mmap), rows in storage order;
@@ -56,7 +56,8 @@ int hq_device_name(int device, char *name, size_t name_len, char *arch, size_t a
 /* Weight residency. Replaces upload_mat (src/cuda_backend.cu:677-699) for GGUF-quantized
  * matrices: the blocks are copied to `device` with rows reordered into Hugging Face order
  * (perm_heads, as src/cuda_backend.cu:689-696). Q4_K blocks are kept byte-identical; Q8_0 is
- * repacked losslessly into a quant plane and a scale plane (hq_mat_download restores the bytes).
+ * repacked losslessly into a quant plane and a scale plane, Q6_K into 224-byte aligned slots
+ * (hq_mat_download restores the bytes).
  * There is no bf16 fallback: non-GGML dtypes and other block types are rejected. */
 int hq_mat_upload(const hq_wmat_t *w, int device, hq_mat **out);
 void hq_mat_free(hq_mat *m);
@@ -95,6 +96,12 @@ int hq_gemm_noalloc(const hq_mat *W, const uint16_t *A, int M, void *C, int c_is
  * and whether it fits hq_gemm_noalloc's scratch (diagnostics; no device is touched). */
 int hq_gemm_workspace_bytes(int ggml_type, int M, uint32_t N, uint32_t K, int n_cu, size_t *partial_bytes,
                             size_t *counter_bytes, size_t *sums_bytes, int *fits_noalloc);
+
+/* Single-token FFN input: out[i] = fp16(silu(gate_i . a) * (up_i . a)) for i < rows, with a fp16
+ * [cols] and out fp16 [rows] in device memory, fp32 dots of the exactly decoded weights. gate and up
+ * share a shape and a device; their block types may differ (Q4_K_M files pair a Q4_K gate with a
+ * Q6_K up). Replaces k_gateup_swiglu (src/cuda_backend.cu:548-559); one pass over both matrices. */
+int hq_gemv_swiglu(const hq_mat *gate, const hq_mat *up, const uint16_t *a, uint16_t *out, void *stream);
 
 /* Option-row readout: out[b*k + j] = dot(H[b], head[ids[b*k + j]]) for b < B, j < k, fp32.
  * H fp16 [B, K] and out on the device; ids on the HOST (checked against rows, then staged).

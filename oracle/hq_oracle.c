@@ -35,9 +35,13 @@ void or_f16_to_f32_array(const uint16_t *in, float *out, size_t n) {
     for (size_t i = 0; i < n; i++) out[i] = or_f16_to_f32(in[i]);
 }
 
-/* src/ggml_quant.h:22-47 (the two formats on this path; 0 = unsupported) */
-uint32_t or_block_values(int type) { return type == OR_GGML_Q8_0 ? 32u : type == OR_GGML_Q4_K ? 256u : 0u; }
-uint32_t or_block_bytes(int type) { return type == OR_GGML_Q8_0 ? 34u : type == OR_GGML_Q4_K ? 144u : 0u; }
+/* src/ggml_quant.h:22-47 (the formats on this path; 0 = unsupported) */
+uint32_t or_block_values(int type) {
+    return type == OR_GGML_Q8_0 ? 32u : type == OR_GGML_Q4_K || type == OR_GGML_Q6_K ? 256u : 0u;
+}
+uint32_t or_block_bytes(int type) {
+    return type == OR_GGML_Q8_0 ? 34u : type == OR_GGML_Q4_K ? 144u : type == OR_GGML_Q6_K ? 210u : 0u;
+}
 
 /* src/gguf.c:54-57 */
 size_t or_row_bytes(int type, uint64_t cols) {
@@ -80,6 +84,24 @@ void or_dequant_sub32(int type, const uint8_t *b, int sub, float *y) {
         const uint8_t *qs = b + 16 + 32 * (sub >> 1);
         const int shift = (sub & 1) ? 4 : 0;
         for (int l = 0; l < 32; l++) y[l] = ds * (float)((qs[l] >> shift) & 0x0f) - dm;
+        return;
+    }
+    if (type == OR_GGML_Q6_K) {
+        /* Q6_K (src/ggml_quant.h:151-169): {u8 ql[128], u8 qh[64], int8 scales[16], fp16 d}. The
+         * 256 values form two halves of 128; in half h, value 32r + l (r = 0..3, l = 0..31) takes
+         * its low 4 bits from ql[64h + l + 32(r % 2)] (low nibble for r < 2, high for r >= 2), its
+         * top 2 bits from bits 2r, 2r+1 of qh[32h + l], is offset by -32, and is scaled by
+         * scales[8h + 2r + l/16] and d: y = (d * sc) * q, where d * sc is exact in float and the
+         * second product can round. */
+        const int h = sub >> 2, r = sub & 3;
+        const uint8_t *ql = b + 64 * h + 32 * (r & 1), *qh = b + 128 + 32 * h;
+        const int8_t *sc = (const int8_t *)(b + 192) + 8 * h + 2 * r;
+        const float d = le_f16(b + 208);
+        for (int l = 0; l < 32; l++) {
+            const int lo = (r < 2 ? ql[l] : ql[l] >> 4) & 0x0f, hi = (qh[l] >> (2 * r)) & 3;
+            const int q = (lo | (hi << 4)) - 32;
+            y[l] = d * (float)sc[l >> 4] * (float)q;
+        }
     }
 }
 

@@ -5,8 +5,10 @@ oracle/Makefile):  python tests/golden/make_golden.py
 Every expected output below comes from the reference build (Reference), never from the oracle.
 Inputs are synthetic (hilbert-pruned-8b_amd/synth.py), so only inputs and outputs are stored.
 
-  dequant_q8_0.npz / dequant_q4_k.npz  blocks (random + special scales) -> fp32 rows (wmat_row_f32)
-  matmul_q8_0.npz / matmul_q4_k.npz    blocks, x, y0 -> y = matmul(W, x, accumulate) (cpu_backend.c:39)
+  dequant_q8_0.npz / dequant_q4_k.npz / dequant_q6_k.npz
+                                       blocks (random + special scales) -> fp32 rows (wmat_row_f32)
+  matmul_q8_0.npz / matmul_q4_k.npz / matmul_q6_k.npz
+                                       blocks, x, y0 -> y = matmul(W, x, accumulate) (cpu_backend.c:39)
   tiny_llama.npz                       config-1 prompt -> logits (model_load + cpu backend forward),
                                        with the sha256 of synth.tiny_llama(1) to catch generator drift
 """
@@ -25,7 +27,7 @@ sys.path[:0] = [os.path.join(ROOT, "hilbert-pruned-8b_amd"), os.path.join(ROOT, 
 import gguf_writer  # noqa: E402
 import oracle  # noqa: E402
 import synth  # noqa: E402
-from test_oracle import special_q4_k_blocks, special_q8_0_blocks  # noqa: E402
+from test_oracle import special_q4_k_blocks, special_q6_k_blocks, special_q8_0_blocks  # noqa: E402
 
 
 def digest(model):
@@ -75,6 +77,20 @@ def main():
         logits = ref.logits(path, tokens, ids)
     np.savez_compressed(os.path.join(HERE, "tiny_llama.npz"), tokens=tokens, ids=ids, logits=logits,
                         model_sha256=digest(model))
+    # Q6_K (its own generator, so the fixtures above do not change): dequant of random + special
+    # blocks with perm_heads, and a matmul with accumulate
+    rng6 = synth.Rng(6666)
+    sp = special_q6_k_blocks()  # 2 rows x 1024 values
+    blocks = np.ascontiguousarray(np.concatenate([sp, synth.q6_k_blocks(rng6, 6, 1024)]))
+    vals = ref.dequantize(blocks, synth.Q6_K, 8, 1024, perm_heads=2)
+    np.savez_compressed(os.path.join(HERE, "dequant_q6_k.npz"), blocks=blocks, values=vals, gtype=synth.Q6_K, rows=8,
+                        cols=1024, perm_heads=2)
+    blocks = synth.q6_k_blocks(rng6, 40, 512)
+    x = synth.activations_f16(rng6, 5, 512).view(np.float16).astype(np.float32)
+    y0 = rng6.normal(5 * 40).astype(np.float32).reshape(5, 40)
+    y = ref.matmul(blocks, synth.Q6_K, 40, 512, x, y0.copy(), True)
+    np.savez_compressed(os.path.join(HERE, "matmul_q6_k.npz"), blocks=blocks, x=x, y0=y0, y=y, gtype=synth.Q6_K, rows=40,
+                        cols=512, accumulate=True)
     print("golden fixtures written:", logits)
 
 

@@ -108,17 +108,61 @@ def special_q4_k_blocks():
     return blk.reshape(2, -1)  # two rows of four super-blocks (1024 values)
 
 
-@pytest.mark.parametrize("gtype", [synth.Q8_0, synth.Q4_K])
+def special_q6_k_blocks():
+    """Q6_K super-blocks with d = 0, +-1, the smallest subnormal, the largest finite value, inf
+    and NaN; scales at -128, 127, 0 and 1; quants all 0 (q = -32) in one block and all 63 (q = 31)
+    in another."""
+    rng = synth.Rng(53)
+    ds = [0x0000, 0x3C00, 0xBC00, 0x0001, 0x7BFF, 0x7C00, 0x7E00, 0x1400]
+    blk = rng.bytes(len(ds) * 210).reshape(len(ds), 210)
+    for i, d in enumerate(ds):
+        blk[i, 208:210] = [d & 0xFF, d >> 8]
+    blk[1, 192:208] = np.array([-128, 127, 0, 1] * 4, np.int8).view(np.uint8)
+    blk[2, :192] = 0
+    blk[3, :192] = 0xFF
+    return blk.reshape(2, -1)
+
+
+SPECIAL_BLOCKS = {synth.Q8_0: lambda: special_q8_0_blocks(), synth.Q4_K: lambda: special_q4_k_blocks(),
+                  synth.Q6_K: lambda: special_q6_k_blocks()}
+
+
+@pytest.mark.parametrize("gtype", [synth.Q8_0, synth.Q4_K, synth.Q6_K])
 def test_dequant_matches_reference(oracle, reference, gtype):
     rng = synth.Rng(31)
     rows, cols = 24, 1024
     blocks = synth.random_blocks(gtype, rng, rows, cols)
     assert same_bits_nan_aware(oracle.dequantize(blocks, gtype, rows, cols),
                                reference.dequantize(blocks, gtype, rows, cols))
-    sp = special_q8_0_blocks() if gtype == synth.Q8_0 else special_q4_k_blocks()
+    sp = SPECIAL_BLOCKS[gtype]()
     r = sp.shape[0]
     c = sp.shape[1] // synth.BLOCK_BYTES[gtype] * synth.BLOCK_VALUES[gtype]
     assert same_bits_nan_aware(oracle.dequantize(sp, gtype, r, c), reference.dequantize(sp, gtype, r, c))
+
+
+def test_dequant_q6_k_closed_form(oracle):
+    """Every 6-bit code under every int8 scale: y is the exact product d * sc * (q - 32) (25
+    significant bits at most, exact in float64) rounded once to float32."""
+    rng = synth.Rng(59)
+    n_blocks = 256
+    blk = rng.bytes(n_blocks * 210).reshape(n_blocks, 210)
+    blk[:, 192:208] = np.arange(n_blocks * 16, dtype=np.int64).reshape(n_blocks, 16).astype(np.uint8)  # all 256 scales
+    d = synth.f16_bits(np.abs(rng.normal(n_blocks)) * 1e-2)
+    blk[:, 208:210] = d.view(np.uint8).reshape(-1, 2)
+    got = oracle.dequantize(blk.reshape(8, -1), synth.Q6_K, 8, 32 * 256).reshape(n_blocks, 256)
+    dv = d.view(np.float16).astype(np.float64)
+    sc = blk[:, 192:208].view(np.int8).astype(np.float64)
+    ql, qh = blk[:, :128].astype(np.int64), blk[:, 128:192].astype(np.int64)
+    codes = set()
+    for v in range(256):
+        h, r, l = v // 128, (v % 128) // 32, v % 32
+        lo = ql[:, 64 * h + 32 * (r % 2) + l]
+        lo = (lo >> 4) if r >= 2 else (lo & 0xF)
+        q = (lo | (((qh[:, 32 * h + l] >> (2 * r)) & 3) << 4)) - 32
+        codes.update(q.tolist())
+        want = (dv * sc[:, 8 * h + 2 * r + l // 16] * q).astype(np.float32)
+        assert np.array_equal(got[:, v], want), v
+    assert codes == set(range(-32, 32))
 
 
 def test_dequant_q8_0_closed_form(oracle):
@@ -191,7 +235,8 @@ def test_src_row_matches_reference(oracle, reference):
 # quantized shapes of the reference selftest (cuda_backend.cu:1110) plus Q8_0 rows that end mid
 # 256-value chunk (K = 1408, the config-1 FFN width) and a perm_heads matrix
 MATMUL_CASES = [(synth.Q8_0, 40, 512, 5), (synth.Q8_0, 40, 512, 40), (synth.Q4_K, 40, 512, 5),
-                (synth.Q4_K, 40, 512, 40), (synth.Q8_0, 33, 1408, 7), (synth.Q4_K, 130, 2560, 3)]
+                (synth.Q4_K, 40, 512, 40), (synth.Q8_0, 33, 1408, 7), (synth.Q4_K, 130, 2560, 3),
+                (synth.Q6_K, 40, 512, 5), (synth.Q6_K, 130, 2560, 3)]
 
 
 @pytest.mark.parametrize("gtype,N,K,T", MATMUL_CASES)
@@ -307,14 +352,14 @@ def load_golden(name):
     return np.load(path, allow_pickle=False)
 
 
-@pytest.mark.parametrize("name", ["dequant_q8_0.npz", "dequant_q4_k.npz"])
+@pytest.mark.parametrize("name", ["dequant_q8_0.npz", "dequant_q4_k.npz", "dequant_q6_k.npz"])
 def test_golden_dequant(oracle, name):
     g = load_golden(name)
     got = oracle.dequantize(g["blocks"], int(g["gtype"]), int(g["rows"]), int(g["cols"]), int(g["perm_heads"]))
     assert same_bits_nan_aware(got, g["values"])
 
 
-@pytest.mark.parametrize("name", ["matmul_q8_0.npz", "matmul_q4_k.npz"])
+@pytest.mark.parametrize("name", ["matmul_q8_0.npz", "matmul_q4_k.npz", "matmul_q6_k.npz"])
 def test_golden_matmul(oracle, name):
     g = load_golden(name)
     got = oracle.matmul(g["blocks"], int(g["gtype"]), int(g["rows"]), int(g["cols"]), g["x"], g["y0"].copy(),
