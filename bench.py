@@ -144,6 +144,25 @@ def bench_gather(hq, synth, k, stream, reps=3):
                 tflops=2.0 * B * k * K / (ms * 1e-3) / 1e12, id_sets=n_sets)
 
 
+def bench_upload(hq, synth, reps=3):
+    """hq_mat_upload of the config-5 lm_head (151936 x 2560 Q8_0, 413 MB of GGUF blocks) from host
+    memory: rows through the pinned staging buffers, asynchronous copies, device-side plane repack.
+    GB/s of GGUF bytes, median of `reps` after one warm-up."""
+    V, K = 151936, 2560
+    blocks = synth.q8_0_blocks(synth.Rng(5151), V, K)
+    times = []
+    for i in range(reps + 1):
+        t0 = time.perf_counter()
+        W = hq.Mat(blocks, synth.Q8_0, V, K)
+        dt = time.perf_counter() - t0
+        W.free()
+        if i:
+            times.append(dt)
+    t = statistics.median(times)
+    return dict(type="upload_q8_0", rows=V, cols=K, bytes=int(blocks.nbytes), ms=round(t * 1e3, 2),
+                gbs=round(blocks.nbytes / t / 1e9, 2))
+
+
 def cpu_baseline(synth, gtype, N, K, M):
     import oracle
     O = oracle.Oracle()
@@ -184,6 +203,8 @@ def main():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run 20 device-to-device copies of BYTES bytes (the known-size kernel the "
                          "FETCH_SIZE / WRITE_SIZE counters are scaled by) and exit")
+    ap.add_argument("--upload-only", action="store_true",
+                    help="only time the upload of the 413 MB config-5 head and exit")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only time the three M = 1 GEMV shapes of the sweep (for profiling) and exit")
     ap.add_argument("--shape", default="", metavar="TYPE:M:N:K",
@@ -214,6 +235,9 @@ def main():
         g = {"q8_0": synth.Q8_0, "q4_k": synth.Q4_K}[t]
         r = bench_gemm(hq, synth, g, int(n), int(k), int(m), False, args.steps, args.warmup, stream, settle_s=0.2)
         log("shape", main_kernel_name(hq, g, int(m), int(n), int(k)), r)
+        return
+    if args.upload_only:
+        log("upload", bench_upload(hq, synth))
         return
     if args.gemv_only:
         for g, n, k in [(synth.Q8_0, 9728, 2560), (synth.Q4_K, 9728, 2560), (synth.Q4_K, 2560, 9728)]:
@@ -246,6 +270,9 @@ def main():
             log("sweep", r)
             sweep.append({key: (round(v, 4) if isinstance(v, float) else v) for key, v in r.items()})
         r = bench_config4(hq, synth, stream)
+        log("sweep", r)
+        sweep.append(r)
+        r = bench_upload(hq, synth)
         log("sweep", r)
         sweep.append(r)
 

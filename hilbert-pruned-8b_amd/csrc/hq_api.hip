@@ -5,6 +5,7 @@
 
 #include <map>
 #include <mutex>
+#include <thread>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -102,6 +103,103 @@ static uint32_t storage_row(uint32_t rows, uint32_t perm_heads, uint32_t r) {
 
 static size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// ------------------------------------------------------------------------------------ upload
+// Matrices reach HBM through a per-device uploader: two pinned host staging buffers and two device
+// staging buffers of UP_CHUNK bytes on a stream of its own. Chunk i of whole rows is copied (rows
+// in Hugging Face order) from the caller's blocks (e.g. a mapped GGUF file) into pinned buffer i % 2
+// by a few host threads, sent with an asynchronous host-to-device copy, and turned into the device
+// layout by a repack kernel (Q8_0: quant and scale planes; Q6_K: 224-byte slots; Q4_K: copied into
+// place directly), while the host already fills the other buffer.
+namespace {
+constexpr size_t UP_CHUNK = (size_t)32 << 20;
+
+struct Uploader {
+    hipStream_t st = nullptr;
+    void *pinned[2] = {nullptr, nullptr}, *raw[2] = {nullptr, nullptr};
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    std::mutex mu;  // one upload at a time per device
+};
+std::mutex g_up_mu;
+std::map<int, Uploader *> g_up;
+
+int uploader(int device, Uploader **out) {
+    std::lock_guard<std::mutex> lk(g_up_mu);
+    auto it = g_up.find(device);
+    if (it != g_up.end()) {
+        *out = it->second;
+        return 0;
+    }
+    Uploader *u = new Uploader();
+    hipError_t e = hipStreamCreateWithFlags(&u->st, hipStreamNonBlocking);
+    for (int b = 0; b < 2 && e == hipSuccess; b++) {
+        e = hipHostMalloc(&u->pinned[b], UP_CHUNK, hipHostMallocDefault);
+        if (e == hipSuccess) e = hipMalloc(&u->raw[b], UP_CHUNK);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&u->ev[b], hipEventDisableTiming);
+    }
+    if (e != hipSuccess) {
+        for (int b = 0; b < 2; b++) {
+            if (u->pinned[b]) (void)hipHostFree(u->pinned[b]);
+            if (u->raw[b]) (void)hipFree(u->raw[b]);
+            if (u->ev[b]) (void)hipEventDestroy(u->ev[b]);
+        }
+        if (u->st) (void)hipStreamDestroy(u->st);
+        delete u;
+        return fail("hq_mat_upload: staging buffers: %s", hipGetErrorString(e));
+    }
+    g_up[device] = u;
+    *out = u;
+    return 0;
+}
+
+// rows [r0, r0 + n) of w (Hugging Face order) into dst, rb bytes per row, split over a few threads
+void gather_rows(const hq_wmat_t *w, size_t rb, uint32_t r0, uint32_t n, uint8_t *dst) {
+    const uint8_t *src = (const uint8_t *)w->data;
+    const size_t bytes = (size_t)n * rb;
+    const int nthr = bytes >= ((size_t)8 << 20) ? 8 : 1;
+    auto work = [&](int t) {
+        const uint32_t a = (uint32_t)((uint64_t)n * t / nthr), b = (uint32_t)((uint64_t)n * (t + 1) / nthr);
+        if (!w->perm_heads) {
+            memcpy(dst + (size_t)a * rb, src + (size_t)(r0 + a) * rb, (size_t)(b - a) * rb);
+            return;
+        }
+        for (uint32_t r = a; r < b; r++)
+            memcpy(dst + (size_t)r * rb, src + (size_t)storage_row(w->rows, w->perm_heads, r0 + r) * rb, rb);
+    };
+    if (nthr == 1) {
+        work(0);
+        return;
+    }
+    std::vector<std::thread> th;
+    for (int t = 1; t < nthr; t++) th.emplace_back(work, t);
+    work(0);
+    for (auto &x : th) x.join();
+}
+
+// GGUF Q8_0 rows (34-byte blocks) -> quant plane bytes q ^ 0x80 and fp16 scale plane
+__global__ void k_repack_q8_0(const uint8_t *__restrict__ raw, uint32_t n, uint32_t nb, uint32_t ldd, uint8_t *qs,
+                              uint16_t *d) {
+    const size_t total = (size_t)n * nb;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t r = i / nb, b = i % nb;
+        const uint8_t *blk = raw + i * 34;
+        d[r * ldd + b] = (uint16_t)(blk[0] | (blk[1] << 8));
+        uint8_t *q = qs + r * (size_t)nb * 32 + b * 32;
+#pragma unroll
+        for (int j = 0; j < 32; j++) q[j] = blk[2 + j] ^ 0x80u;
+    }
+}
+
+// GGUF Q6_K rows (210-byte super-blocks, 2-byte aligned) -> 224-byte slots (the tail zeroed)
+__global__ void k_repack_q6_k(const uint16_t *__restrict__ raw, size_t nblk, uint16_t *dst) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < nblk * 112; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t b = i / 112, h = i % 112;
+        dst[i] = h < 105 ? raw[b * 105 + h] : (uint16_t)0;
+    }
+}
+
+unsigned up_grid(size_t n) { return (unsigned)((n + 255) / 256 < 16384 ? (n + 255) / 256 : 16384); }
+}  // namespace
+
 extern "C" int hq_mat_upload(const hq_wmat_t *w, int device, hq_mat **out) {
     *out = nullptr;
     if (!w || !w->data) return fail("hq_mat_upload: no matrix");
@@ -116,70 +214,69 @@ extern "C" int hq_mat_upload(const hq_wmat_t *w, int device, hq_mat **out) {
         return fail("hq_mat_upload: %u rows do not split into %u heads of even size", w->rows, w->perm_heads);
     const size_t rb = (size_t)(w->cols / per) * block_bytes(w->ggml_type);
     // the kernels address a matrix through 32-bit buffer ranges: its device bytes stay below 4 GiB
-    const size_t dev_bytes = w->ggml_type == HQ_GGML_Q4_K   ? rb * w->rows
-                             : w->ggml_type == HQ_GGML_Q6_K ? (size_t)(w->cols / 256) * Q6K_SLOT * w->rows
-                                                            : round_up((size_t)w->rows * w->cols, 256) +
-                                                                  (size_t)w->rows * round_up(w->cols / 32, 8) * 2;
+    const size_t K = w->cols, nb = K / per, ldd = round_up(K / 32, 8), qbytes = round_up((size_t)w->rows * K, 256);
+    const size_t drb = w->ggml_type == HQ_GGML_Q6_K ? nb * Q6K_SLOT : rb;
+    const size_t dev_bytes = w->ggml_type == HQ_GGML_Q8_0 ? qbytes + (size_t)w->rows * ldd * 2 : drb * w->rows;
     if (dev_bytes >= ((size_t)1 << 32))
         return fail("hq_mat_upload: shape [%u, %u] needs %zu device bytes; one matrix is limited to 4 GiB (split its rows)",
                     w->rows, w->cols, dev_bytes);
+    if (rb > UP_CHUNK) return fail("hq_mat_upload: a row of %zu bytes exceeds the %zu-byte staging buffer", rb, UP_CHUNK);
     if (use_device(device)) return -1;
-    const uint8_t *src = (const uint8_t *)w->data;
+    Uploader *u;
+    if (uploader(device, &u)) return -1;
     hq_mat *m = (hq_mat *)calloc(1, sizeof *m);
     if (!m) return fail("hq_mat_upload: out of host memory");
     m->device = device;
     m->m.type = w->ggml_type;
     m->m.rows = w->rows;
     m->m.cols = w->cols;
-    m->m.row_bytes = rb;
-    std::vector<uint8_t> host;
-    if (w->ggml_type == HQ_GGML_Q6_K) {
-        // each 210-byte super-block in a 224-byte slot (16-byte aligned loads), zero padded
-        const size_t nb = w->cols / 256, drb = nb * Q6K_SLOT;
-        m->m.row_bytes = drb;
-        m->bytes = drb * w->rows;
-        host.assign(m->bytes, 0);
-        for (uint32_t r = 0; r < w->rows; r++) {
-            const uint8_t *row = src + (size_t)storage_row(w->rows, w->perm_heads, r) * rb;
-            for (size_t b = 0; b < nb; b++) memcpy(host.data() + (size_t)r * drb + b * Q6K_SLOT, row + 210 * b, 210);
-        }
-    } else if (w->ggml_type == HQ_GGML_Q4_K) {
-        m->bytes = rb * w->rows;
-        host.resize(m->bytes);
-        for (uint32_t r = 0; r < w->rows; r++)
-            memcpy(host.data() + (size_t)r * rb, src + (size_t)storage_row(w->rows, w->perm_heads, r) * rb, rb);
-    } else {
-        const size_t K = w->cols, nb = K / 32, ldd = round_up(nb, 8);
-        const size_t qbytes = round_up((size_t)w->rows * K, 256);
-        m->m.ldd = (int)ldd;
-        m->bytes = qbytes + (size_t)w->rows * ldd * 2;
-        host.assign(m->bytes, 0);
-        uint16_t *dpl = (uint16_t *)(host.data() + qbytes);
-        for (uint32_t r = 0; r < w->rows; r++) {
-            const uint8_t *row = src + (size_t)storage_row(w->rows, w->perm_heads, r) * rb;
-            uint8_t *q = host.data() + (size_t)r * K;
-            for (size_t b = 0; b < nb; b++) {
-                const uint8_t *blk = row + 34 * b;
-                dpl[(size_t)r * ldd + b] = (uint16_t)(blk[0] | (blk[1] << 8));
-                for (int j = 0; j < 32; j++) q[32 * b + j] = blk[2 + j] ^ 0x80u;
-            }
-        }
-    }
+    m->m.row_bytes = drb;
+    m->m.ldd = w->ggml_type == HQ_GGML_Q8_0 ? (int)ldd : 0;
+    m->bytes = dev_bytes;
     hipError_t e = hipMalloc(&m->alloc, m->bytes);
     if (e != hipSuccess) {
         free(m);
-        return fail("hq_mat_upload: hipMalloc(%zu) failed: %s", m->bytes, hipGetErrorString(e));
+        return fail("hq_mat_upload: hipMalloc(%zu) failed: %s", dev_bytes, hipGetErrorString(e));
     }
-    e = hipMemcpy(m->alloc, host.data(), m->bytes, hipMemcpyHostToDevice);
-    if (e != hipSuccess) {
+    uint8_t *base = (uint8_t *)m->alloc;
+    m->m.qs = base;
+    m->m.d = w->ggml_type == HQ_GGML_Q8_0 ? (const uint16_t *)(base + qbytes) : nullptr;
+    std::lock_guard<std::mutex> lk(u->mu);
+    auto fail_free = [&](hipError_t err) {
+        (void)hipStreamSynchronize(u->st);
         (void)hipFree(m->alloc);
         free(m);
-        return fail("hq_mat_upload: copy failed: %s", hipGetErrorString(e));
+        return fail("hq_mat_upload: %s", hipGetErrorString(err));
+    };
+    if (w->ggml_type == HQ_GGML_Q8_0 && (e = hipMemsetAsync(base, 0, dev_bytes, u->st)) != hipSuccess) return fail_free(e);
+    const uint32_t rows_per = (uint32_t)(UP_CHUNK / rb < w->rows ? UP_CHUNK / rb : w->rows);
+    bool used[2] = {false, false};
+    for (uint32_t r0 = 0, i = 0; r0 < w->rows; r0 += rows_per, i++) {
+        const int b = (int)(i & 1);
+        const uint32_t n = w->rows - r0 < rows_per ? w->rows - r0 : rows_per;
+        if (used[b] && (e = hipEventSynchronize(u->ev[b])) != hipSuccess) return fail_free(e);
+        gather_rows(w, rb, r0, n, (uint8_t *)u->pinned[b]);
+        const size_t bytes = (size_t)n * rb;
+        if (w->ggml_type == HQ_GGML_Q4_K) {
+            e = hipMemcpyAsync(base + (size_t)r0 * rb, u->pinned[b], bytes, hipMemcpyHostToDevice, u->st);
+        } else {
+            e = hipMemcpyAsync(u->raw[b], u->pinned[b], bytes, hipMemcpyHostToDevice, u->st);
+            if (e == hipSuccess && w->ggml_type == HQ_GGML_Q8_0) {
+                k_repack_q8_0<<<up_grid((size_t)n * nb), 256, 0, u->st>>>((const uint8_t *)u->raw[b], n, (uint32_t)nb,
+                                                                          (uint32_t)ldd, base + (size_t)r0 * K,
+                                                                          (uint16_t *)(base + qbytes) + (size_t)r0 * ldd);
+                e = hipGetLastError();
+            } else if (e == hipSuccess) {
+                k_repack_q6_k<<<up_grid((size_t)n * nb * 112), 256, 0, u->st>>>((const uint16_t *)u->raw[b], (size_t)n * nb,
+                                                                                (uint16_t *)(base + (size_t)r0 * drb));
+                e = hipGetLastError();
+            }
+        }
+        if (e == hipSuccess) e = hipEventRecord(u->ev[b], u->st);
+        if (e != hipSuccess) return fail_free(e);
+        used[b] = true;
     }
-    m->m.qs = (const uint8_t *)m->alloc;
-    m->m.d = w->ggml_type == HQ_GGML_Q8_0 ? (const uint16_t *)((const uint8_t *)m->alloc +
-                                                                 round_up((size_t)w->rows * w->cols, 256))
-                                          : nullptr;
+    if ((e = hipStreamSynchronize(u->st)) != hipSuccess) return fail_free(e);
     *out = m;
     return 0;
 }

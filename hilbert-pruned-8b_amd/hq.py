@@ -24,6 +24,8 @@ EXPORTS = (
     "hq_memcpy_d2h", "hq_memcpy_d2d", "hq_memset", "hq_stream_create", "hq_stream_destroy", "hq_stream_synchronize",
     "hq_device_synchronize", "hq_time_gemm", "hq_time_gemm_kernel", "hq_time_gather", "hq_gemm_tiles", "hq_llama_forward",
     "hq_embed_f32", "hq_gemm_kernel", "hq_gemm_noalloc", "hq_gemm_workspace_bytes", "hq_gemv_swiglu",
+    "hq_gguf_open", "hq_gguf_close", "hq_gguf_n_tensors", "hq_gguf_tensor_info", "hq_gguf_find", "hq_gguf_get_uint",
+    "hq_gguf_wmat",
 )
 # include/hq_backend.h (no hq_ prefix: the names of the reference entry points they replace)
 BACKEND_EXPORTS = ("hip_backend_create", "hip_selftest")
@@ -139,6 +141,14 @@ def load(path=LIB_PATH):
         "hq_embed_f32": (i, [vp, vp, i, vp, vp]),
         "hq_gemm_noalloc": (i, [vp, vp, i, vp, i, i, vp]),
         "hq_gemv_swiglu": (i, [vp, vp, vp, vp, vp]),
+        "hq_gguf_open": (i, [C.c_char_p, C.POINTER(vp)]),
+        "hq_gguf_close": (None, [vp]),
+        "hq_gguf_n_tensors": (sz, [vp]),
+        "hq_gguf_tensor_info": (i, [vp, sz, C.POINTER(C.c_char_p), C.POINTER(i), C.POINTER(u32),
+                                    C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+        "hq_gguf_find": (i, [vp, C.c_char_p, C.POINTER(sz)]),
+        "hq_gguf_get_uint": (i, [vp, C.c_char_p, C.POINTER(C.c_uint64)]),
+        "hq_gguf_wmat": (i, [vp, C.c_char_p, u32, C.POINTER(WMat)]),
         "hip_backend_create": (C.POINTER(RefBackend), [C.POINTER(RefModel), sz, i, C.c_bool]),
         "hip_selftest": (i, [C.POINTER(RefModel), i, sz, i]),
         "hq_gemm_workspace_bytes": (i, [i, i, u32, u32, i, C.POINTER(sz), C.POINTER(sz), C.POINTER(sz),
@@ -553,3 +563,51 @@ class HipBackend:
 
 def hip_selftest(view, device=0, n_tokens=64, verbose=1):
     return load().hip_selftest(C.byref(view.m), device, n_tokens, verbose)
+
+
+class Gguf:
+    """hq_gguf_open: a read-only mapping of a GGUF file and its tensor table (include/hq_gguf.h)."""
+
+    def __init__(self, path):
+        h = C.c_void_p()
+        _check(load().hq_gguf_open(str(path).encode(), C.byref(h)))
+        self.h = h.value
+
+    def tensors(self):
+        out = []
+        for i in range(_lib.hq_gguf_n_tensors(self.h)):
+            name, t, nd = C.c_char_p(), C.c_int(), C.c_uint32()
+            ne, off = (C.c_uint64 * 4)(), C.c_uint64()
+            _check(_lib.hq_gguf_tensor_info(self.h, i, C.byref(name), C.byref(t), C.byref(nd), ne, C.byref(off)))
+            out.append(dict(name=name.value.decode(), type=t.value, n_dims=nd.value, ne=tuple(ne), offset=off.value))
+        return out
+
+    def get_uint(self, key):
+        v = C.c_uint64()
+        _check(_lib.hq_gguf_get_uint(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def wmat(self, name, perm_heads=0):
+        w = WMat()
+        _check(_lib.hq_gguf_wmat(self.h, name.encode(), perm_heads, C.byref(w)))
+        return w
+
+    def view_bytes(self, name):
+        """The bytes of a quantized matrix as the mapping holds them (a copy)."""
+        w = self.wmat(name)
+        n = w.rows * row_bytes(w.ggml_type, w.cols)
+        return np.ctypeslib.as_array((C.c_uint8 * n).from_address(w.data)).reshape(w.rows, -1).copy()
+
+    def upload(self, name, perm_heads=0, device=0):
+        """hq_mat_upload of the named matrix straight from the mapping."""
+        w = self.wmat(name, perm_heads)
+        m = Mat.__new__(Mat)
+        h = C.c_void_p()
+        _check(_lib.hq_mat_upload(C.byref(w), device, C.byref(h)))
+        m.h, m.gtype, m.rows, m.cols = h.value, w.ggml_type, w.rows, w.cols
+        return m
+
+    def close(self):
+        if self.h:
+            _lib.hq_gguf_close(self.h)
+            self.h = None

@@ -154,6 +154,9 @@ class Reference:
         L.ref_dot.argtypes = [_f32p, _f32p, C.c_size_t]
         L.ref_matmul.argtypes = [C.POINTER(WMat), _f32p, C.c_size_t, _f32p, C.c_int]
         L.ref_last_error.restype = C.c_char_p
+        L.ref_gguf_tensor.restype = C.c_int
+        L.ref_gguf_tensor.argtypes = [C.c_char_p, C.c_char_p, C.POINTER(C.c_int), C.POINTER(C.c_uint64), C.c_void_p,
+                                      C.c_size_t, C.POINTER(C.c_size_t)]
         L.ref_logits.restype = C.c_int
         L.ref_logits.argtypes = [C.c_char_p, _u32p, C.c_size_t, _u32p, C.c_uint32, _f32p, C.c_void_p]
 
@@ -172,6 +175,14 @@ class Reference:
             y = np.zeros((T, rows), dtype=np.float32)
         self.lib.ref_matmul(C.byref(w), x.reshape(-1), T, y.reshape(-1), int(accumulate))
         return y
+
+    def gguf_tensor(self, path, name, cap=1 << 26):
+        """(type, ne, data bytes) of a tensor as the reference's GGUF reader finds it."""
+        t, ne, n = C.c_int(), (C.c_uint64 * 4)(), C.c_size_t()
+        buf = np.empty(cap, np.uint8)
+        if self.lib.ref_gguf_tensor(str(path).encode(), name.encode(), C.byref(t), ne, buf.ctypes.data, cap, C.byref(n)):
+            raise RuntimeError("reference: " + (self.lib.ref_last_error() or b"?").decode())
+        return t.value, tuple(ne), buf[:n.value].copy()
 
     def logits(self, gguf_path, tokens, ids):
         out = np.empty(len(ids), dtype=np.float32)

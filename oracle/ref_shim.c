@@ -38,3 +38,24 @@ int ref_logits(const char *path, const uint32_t *tokens, size_t n, const uint32_
     model_free(&m);
     return rc;
 }
+
+/* gguf_open + gguf_tensor + gguf_tensor_data (src/gguf.c:134-219, :317-344): the tensor's type,
+ * extents and data bytes as the reference reader locates them. 0, or -1 (ref_last_error). */
+int ref_gguf_tensor(const char *path, const char *name, int *type, uint64_t ne[4], void *out, size_t cap, size_t *bytes) {
+    gguf_t *g;
+    if (gguf_open(path, &g)) return -1;
+    const gguf_tensor_t *t = gguf_tensor(g, name);
+    const void *p = t ? gguf_tensor_data(g, t) : NULL;
+    if (!p) {
+        if (!t) set_error("no tensor %s", name);
+        gguf_close(g);
+        return -1;
+    }
+    *type = t->type;
+    for (int d = 0; d < 4; d++) ne[d] = t->ne[d];
+    const size_t n = ggml_row_bytes(t->type, t->ne[0]) * (size_t)(t->ne[1] * t->ne[2] * t->ne[3]);
+    *bytes = n;
+    if (n <= cap) memcpy(out, p, n);
+    gguf_close(g);
+    return n <= cap ? 0 : -1;
+}

@@ -19,9 +19,12 @@ def _str(s):
     return struct.pack("<Q", len(b)) + b
 
 
-def write(path, kv, tensors):
+def write(path, kv, tensors, alignment=ALIGN):
     """kv: list of (key, kind, value) with kind in {"u32", "f32", "str"}.
-    tensors: list of (name, ne tuple (ne[0] contiguous), ggml type id, raw uint8 bytes)."""
+    tensors: list of (name, ne tuple (ne[0] contiguous), ggml type id, raw uint8 bytes).
+    alignment != 32 is written as general.alignment (u32) and used for the data section."""
+    if alignment != ALIGN:
+        kv = list(kv) + [("general.alignment", "u32", alignment)]
     head = bytearray()
     head += b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(kv))
     for key, kind, val in kv:
@@ -38,11 +41,11 @@ def write(path, kv, tensors):
     for name, ne, gtype, data in tensors:
         offsets.append(off)
         off += np.asarray(data).nbytes
-        off = (off + ALIGN - 1) // ALIGN * ALIGN
+        off = (off + alignment - 1) // alignment * alignment
     for (name, ne, gtype, data), o in zip(tensors, offsets):
         head += _str(name) + struct.pack("<I", len(ne)) + struct.pack("<%dQ" % len(ne), *ne)
         head += struct.pack("<IQ", gtype, o)
-    pad = (-len(head)) % ALIGN
+    pad = (-len(head)) % alignment
     with open(path, "wb") as f:
         f.write(head + b"\0" * pad)
         pos = 0
