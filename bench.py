@@ -144,6 +144,31 @@ def bench_gather(hq, synth, k, stream, reps=3):
                 tflops=2.0 * B * k * K / (ms * 1e-3) / 1e12, id_sets=n_sets)
 
 
+def bench_swiglu(hq, synth, gtype, stream, M=512, I=9728, K=2560, steps=20):
+    """The SwiGLU FFN input silu(A gate^T) * (A up^T) of config 3's up/gate shape as one pair GEMM
+    (hq_gemm_swiglu; the epilogue in the tile kernel) against the unfused sequence's two GEMMs alone
+    (hq_gemm on gate and on up, fp16 outputs; the reference adds a k_swiglu pass on top)."""
+    gb = synth.random_blocks(gtype, synth.Rng(4242 + gtype + I), I, K)
+    rb = synth.row_bytes(gtype, K)
+    copies = max(2, -(-ROTATE_BYTES // (2 * I * rb)))
+    pairs = [hq.PairMat(gb, gb, gtype, I, K) for _ in range(copies)]
+    A = hq.DevBuf.from_array(synth.activations_f16(synth.Rng(99 + M), M, K))
+    out = hq.DevBuf(M * I * 2)
+    ms = hq.time_gemm_swiglu(pairs, A, M, out, steps, 1, stream)
+    for p in pairs:
+        p.free()
+    mats = [hq.Mat(gb, gtype, I, K) for _ in range(2 * copies)]
+    C = hq.DevBuf(M * I * 2)
+    ms2 = hq.time_gemm(mats, A, M, C, False, 2 * steps, 1, stream) * 2
+    for m in mats:
+        m.free()
+    A.free(), out.free(), C.free()
+    flop = 2.0 * 2 * M * I * K
+    return dict(type=("q4_k" if gtype == synth.Q4_K else "q8_0") + "_gate_up_swiglu", M=M, I=I, K=K,
+                us=round(ms * 1e3, 2), tflops=round(flop / (ms * 1e-3) / 1e12, 1),
+                unfused_two_gemms_us=round(ms2 * 1e3, 2), copies=copies)
+
+
 def bench_upload(hq, synth, reps=3):
     """hq_mat_upload of the config-5 lm_head (151936 x 2560 Q8_0, 413 MB of GGUF blocks) from host
     memory: rows through the pinned staging buffers, asynchronous copies, device-side plane repack.
@@ -203,6 +228,8 @@ def main():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run 20 device-to-device copies of BYTES bytes (the known-size kernel the "
                          "FETCH_SIZE / WRITE_SIZE counters are scaled by) and exit")
+    ap.add_argument("--swiglu-only", action="store_true",
+                    help="only time the fused gate/up+SwiGLU pair GEMM against two GEMMs and exit")
     ap.add_argument("--upload-only", action="store_true",
                     help="only time the upload of the 413 MB config-5 head and exit")
     ap.add_argument("--gemv-only", action="store_true",
@@ -235,6 +262,10 @@ def main():
         g = {"q8_0": synth.Q8_0, "q4_k": synth.Q4_K}[t]
         r = bench_gemm(hq, synth, g, int(n), int(k), int(m), False, args.steps, args.warmup, stream, settle_s=0.2)
         log("shape", main_kernel_name(hq, g, int(m), int(n), int(k)), r)
+        return
+    if args.swiglu_only:
+        for g in (synth.Q4_K, synth.Q8_0):
+            log("swiglu", bench_swiglu(hq, synth, g, stream))
         return
     if args.upload_only:
         log("upload", bench_upload(hq, synth))
@@ -272,6 +303,10 @@ def main():
         r = bench_config4(hq, synth, stream)
         log("sweep", r)
         sweep.append(r)
+        for g in (synth.Q4_K, synth.Q8_0):
+            r = bench_swiglu(hq, synth, g, stream)
+            log("sweep", r)
+            sweep.append(r)
         r = bench_upload(hq, synth)
         log("sweep", r)
         sweep.append(r)

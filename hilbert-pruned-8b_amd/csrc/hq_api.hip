@@ -22,6 +22,7 @@ struct hq_mat {
     int device;
     void *alloc;
     size_t bytes;
+    int pair;  // a gate/up pair matrix (hq_mat_upload_pair): rows 16k .. 16k + 7 gate, + 8 .. + 15 up
 };
 
 // ------------------------------------------------------------------------------------ errors
@@ -151,19 +152,22 @@ int uploader(int device, Uploader **out) {
     return 0;
 }
 
-// rows [r0, r0 + n) of w (Hugging Face order) into dst, rb bytes per row, split over a few threads
-void gather_rows(const hq_wmat_t *w, size_t rb, uint32_t r0, uint32_t n, uint8_t *dst) {
-    const uint8_t *src = (const uint8_t *)w->data;
+// rows [r0, r0 + n) of a matrix into dst (rb bytes per row), row r read from row_ptr(r); split over
+// a few host threads
+template <class F>
+void gather_rows(F row_ptr, size_t rb, uint32_t r0, uint32_t n, uint8_t *dst) {
     const size_t bytes = (size_t)n * rb;
     const int nthr = bytes >= ((size_t)8 << 20) ? 8 : 1;
     auto work = [&](int t) {
         const uint32_t a = (uint32_t)((uint64_t)n * t / nthr), b = (uint32_t)((uint64_t)n * (t + 1) / nthr);
-        if (!w->perm_heads) {
-            memcpy(dst + (size_t)a * rb, src + (size_t)(r0 + a) * rb, (size_t)(b - a) * rb);
-            return;
+        for (uint32_t r = a; r < b;) {
+            // runs of rows that are consecutive in the source go in one copy
+            const uint8_t *p = row_ptr(r0 + r);
+            uint32_t e = r + 1;
+            while (e < b && row_ptr(r0 + e) == p + (size_t)(e - r) * rb) e++;
+            memcpy(dst + (size_t)r * rb, p, (size_t)(e - r) * rb);
+            r = e;
         }
-        for (uint32_t r = a; r < b; r++)
-            memcpy(dst + (size_t)r * rb, src + (size_t)storage_row(w->rows, w->perm_heads, r0 + r) * rb, rb);
     };
     if (nthr == 1) {
         work(0);
@@ -200,68 +204,78 @@ __global__ void k_repack_q6_k(const uint16_t *__restrict__ raw, size_t nblk, uin
 unsigned up_grid(size_t n) { return (unsigned)((n + 255) / 256 < 16384 ? (n + 255) / 256 : 16384); }
 }  // namespace
 
-extern "C" int hq_mat_upload(const hq_wmat_t *w, int device, hq_mat **out) {
-    *out = nullptr;
-    if (!w || !w->data) return fail("hq_mat_upload: no matrix");
-    if (w->dtype != HQ_DT_GGML) return fail("hq_mat_upload: dtype %d is not a GGUF block type", w->dtype);
+// Checks shared by the upload entry points: a GGUF block type hq_mat_upload supports, whole blocks
+// per row, the size limits; *rb = GGUF bytes per row.
+static int check_wmat(const hq_wmat_t *w, const char *who, size_t *rb) {
+    if (!w || !w->data) return fail("%s: no matrix", who);
+    if (w->dtype != HQ_DT_GGML) return fail("%s: dtype %d is not a GGUF block type", who, w->dtype);
     const uint32_t per = block_values(w->ggml_type);
-    if (!per) return fail("hq_mat_upload: ggml type %d is not supported (Q8_0 = 8, Q4_K = 12, Q6_K = 14)", w->ggml_type);
+    if (!per) return fail("%s: ggml type %d is not supported (Q8_0 = 8, Q4_K = 12, Q6_K = 14)", who, w->ggml_type);
     if (w->rows == 0 || w->cols == 0 || w->cols % per)
-        return fail("hq_mat_upload: shape [%u, %u] is not a whole number of %u-value blocks per row", w->rows, w->cols,
-                    per);
-    if (w->rows > (1u << 30) || w->cols > (1u << 24)) return fail("hq_mat_upload: shape [%u, %u] too large", w->rows, w->cols);
+        return fail("%s: shape [%u, %u] is not a whole number of %u-value blocks per row", who, w->rows, w->cols, per);
+    if (w->rows > (1u << 30) || w->cols > (1u << 24)) return fail("%s: shape [%u, %u] too large", who, w->rows, w->cols);
     if (w->perm_heads && (w->rows % w->perm_heads || (w->rows / w->perm_heads) % 2))
-        return fail("hq_mat_upload: %u rows do not split into %u heads of even size", w->rows, w->perm_heads);
-    const size_t rb = (size_t)(w->cols / per) * block_bytes(w->ggml_type);
+        return fail("%s: %u rows do not split into %u heads of even size", who, w->rows, w->perm_heads);
+    *rb = (size_t)(w->cols / per) * block_bytes(w->ggml_type);
+    return 0;
+}
+
+// A rows x cols matrix of `type` whose GGUF row r (Hugging Face order) is row_ptr(r), into the
+// device layout through the uploader.
+template <class F>
+static int upload_rows(int type, uint32_t rows, uint32_t cols, F row_ptr, int device, const char *who, hq_mat **out) {
+    *out = nullptr;
+    const uint32_t per = block_values(type);
+    const size_t rb = (size_t)(cols / per) * block_bytes(type);
     // the kernels address a matrix through 32-bit buffer ranges: its device bytes stay below 4 GiB
-    const size_t K = w->cols, nb = K / per, ldd = round_up(K / 32, 8), qbytes = round_up((size_t)w->rows * K, 256);
-    const size_t drb = w->ggml_type == HQ_GGML_Q6_K ? nb * Q6K_SLOT : rb;
-    const size_t dev_bytes = w->ggml_type == HQ_GGML_Q8_0 ? qbytes + (size_t)w->rows * ldd * 2 : drb * w->rows;
+    const size_t K = cols, nb = K / per, ldd = round_up(K / 32, 8), qbytes = round_up((size_t)rows * K, 256);
+    const size_t drb = type == HQ_GGML_Q6_K ? nb * Q6K_SLOT : rb;
+    const size_t dev_bytes = type == HQ_GGML_Q8_0 ? qbytes + (size_t)rows * ldd * 2 : drb * rows;
     if (dev_bytes >= ((size_t)1 << 32))
-        return fail("hq_mat_upload: shape [%u, %u] needs %zu device bytes; one matrix is limited to 4 GiB (split its rows)",
-                    w->rows, w->cols, dev_bytes);
-    if (rb > UP_CHUNK) return fail("hq_mat_upload: a row of %zu bytes exceeds the %zu-byte staging buffer", rb, UP_CHUNK);
+        return fail("%s: shape [%u, %u] needs %zu device bytes; one matrix is limited to 4 GiB (split its rows)", who, rows,
+                    cols, dev_bytes);
+    if (rb > UP_CHUNK) return fail("%s: a row of %zu bytes exceeds the %zu-byte staging buffer", who, rb, UP_CHUNK);
     if (use_device(device)) return -1;
     Uploader *u;
     if (uploader(device, &u)) return -1;
     hq_mat *m = (hq_mat *)calloc(1, sizeof *m);
-    if (!m) return fail("hq_mat_upload: out of host memory");
+    if (!m) return fail("%s: out of host memory", who);
     m->device = device;
-    m->m.type = w->ggml_type;
-    m->m.rows = w->rows;
-    m->m.cols = w->cols;
+    m->m.type = type;
+    m->m.rows = rows;
+    m->m.cols = cols;
     m->m.row_bytes = drb;
-    m->m.ldd = w->ggml_type == HQ_GGML_Q8_0 ? (int)ldd : 0;
+    m->m.ldd = type == HQ_GGML_Q8_0 ? (int)ldd : 0;
     m->bytes = dev_bytes;
     hipError_t e = hipMalloc(&m->alloc, m->bytes);
     if (e != hipSuccess) {
         free(m);
-        return fail("hq_mat_upload: hipMalloc(%zu) failed: %s", dev_bytes, hipGetErrorString(e));
+        return fail("%s: hipMalloc(%zu) failed: %s", who, dev_bytes, hipGetErrorString(e));
     }
     uint8_t *base = (uint8_t *)m->alloc;
     m->m.qs = base;
-    m->m.d = w->ggml_type == HQ_GGML_Q8_0 ? (const uint16_t *)(base + qbytes) : nullptr;
+    m->m.d = type == HQ_GGML_Q8_0 ? (const uint16_t *)(base + qbytes) : nullptr;
     std::lock_guard<std::mutex> lk(u->mu);
     auto fail_free = [&](hipError_t err) {
         (void)hipStreamSynchronize(u->st);
         (void)hipFree(m->alloc);
         free(m);
-        return fail("hq_mat_upload: %s", hipGetErrorString(err));
+        return fail("%s: %s", who, hipGetErrorString(err));
     };
-    if (w->ggml_type == HQ_GGML_Q8_0 && (e = hipMemsetAsync(base, 0, dev_bytes, u->st)) != hipSuccess) return fail_free(e);
-    const uint32_t rows_per = (uint32_t)(UP_CHUNK / rb < w->rows ? UP_CHUNK / rb : w->rows);
+    if (type == HQ_GGML_Q8_0 && (e = hipMemsetAsync(base, 0, dev_bytes, u->st)) != hipSuccess) return fail_free(e);
+    const uint32_t rows_per = (uint32_t)(UP_CHUNK / rb < rows ? UP_CHUNK / rb : rows);
     bool used[2] = {false, false};
-    for (uint32_t r0 = 0, i = 0; r0 < w->rows; r0 += rows_per, i++) {
+    for (uint32_t r0 = 0, i = 0; r0 < rows; r0 += rows_per, i++) {
         const int b = (int)(i & 1);
-        const uint32_t n = w->rows - r0 < rows_per ? w->rows - r0 : rows_per;
+        const uint32_t n = rows - r0 < rows_per ? rows - r0 : rows_per;
         if (used[b] && (e = hipEventSynchronize(u->ev[b])) != hipSuccess) return fail_free(e);
-        gather_rows(w, rb, r0, n, (uint8_t *)u->pinned[b]);
+        gather_rows(row_ptr, rb, r0, n, (uint8_t *)u->pinned[b]);
         const size_t bytes = (size_t)n * rb;
-        if (w->ggml_type == HQ_GGML_Q4_K) {
+        if (type == HQ_GGML_Q4_K) {
             e = hipMemcpyAsync(base + (size_t)r0 * rb, u->pinned[b], bytes, hipMemcpyHostToDevice, u->st);
         } else {
             e = hipMemcpyAsync(u->raw[b], u->pinned[b], bytes, hipMemcpyHostToDevice, u->st);
-            if (e == hipSuccess && w->ggml_type == HQ_GGML_Q8_0) {
+            if (e == hipSuccess && type == HQ_GGML_Q8_0) {
                 k_repack_q8_0<<<up_grid((size_t)n * nb), 256, 0, u->st>>>((const uint8_t *)u->raw[b], n, (uint32_t)nb,
                                                                           (uint32_t)ldd, base + (size_t)r0 * K,
                                                                           (uint16_t *)(base + qbytes) + (size_t)r0 * ldd);
@@ -278,6 +292,35 @@ extern "C" int hq_mat_upload(const hq_wmat_t *w, int device, hq_mat **out) {
     }
     if ((e = hipStreamSynchronize(u->st)) != hipSuccess) return fail_free(e);
     *out = m;
+    return 0;
+}
+
+extern "C" int hq_mat_upload(const hq_wmat_t *w, int device, hq_mat **out) {
+    *out = nullptr;
+    size_t rb;
+    if (check_wmat(w, "hq_mat_upload", &rb)) return -1;
+    const uint8_t *src = (const uint8_t *)w->data;
+    auto row_ptr = [&](uint32_t r) { return src + (size_t)storage_row(w->rows, w->perm_heads, r) * rb; };
+    return upload_rows(w->ggml_type, w->rows, w->cols, row_ptr, device, "hq_mat_upload", out);
+}
+
+extern "C" int hq_mat_upload_pair(const hq_wmat_t *gate, const hq_wmat_t *up, int device, hq_mat **out) {
+    *out = nullptr;
+    size_t rb, rbu;
+    if (check_wmat(gate, "hq_mat_upload_pair", &rb) || check_wmat(up, "hq_mat_upload_pair", &rbu)) return -1;
+    if (gate->ggml_type != up->ggml_type || gate->rows != up->rows || gate->cols != up->cols)
+        return fail("hq_mat_upload_pair: gate (type %d, [%u, %u]) and up (type %d, [%u, %u]) differ", gate->ggml_type,
+                    gate->rows, gate->cols, up->ggml_type, up->rows, up->cols);
+    if (gate->rows % 8) return fail("hq_mat_upload_pair: %u rows is not a multiple of 8", gate->rows);
+    if (gate->rows > (1u << 29)) return fail("hq_mat_upload_pair: %u rows too many", gate->rows);
+    const uint8_t *g = (const uint8_t *)gate->data, *u = (const uint8_t *)up->data;
+    auto row_ptr = [&](uint32_t r) {
+        const uint32_t k = r / 16, e = r % 16;
+        return e < 8 ? g + (size_t)storage_row(gate->rows, gate->perm_heads, 8 * k + e) * rb
+                     : u + (size_t)storage_row(up->rows, up->perm_heads, 8 * k + e - 8) * rb;
+    };
+    if (upload_rows(gate->ggml_type, 2 * gate->rows, gate->cols, row_ptr, device, "hq_mat_upload_pair", out)) return -1;
+    (*out)->pair = 1;
     return 0;
 }
 
@@ -343,9 +386,10 @@ static int aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 // call into a HIP graph only after an eager call of the same shape on the same stream.
 namespace {
 struct Staging {  // slots: 0 x fp32, 1 x fp16, 2 y fp32 (hq_matmul_host), 3 embedding ids, 4 readout ids,
-                  // 5 GEMM partial tiles, 6 GEMM tile counters (kept zero), 7 activation sub-block sums
-    void *buf[8] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
-    size_t cap[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                  // 5 GEMM partial tiles, 6 GEMM tile counters (kept zero), 7 activation sub-block sums,
+                  // 8 fp32 gate/up product of the unfused hq_gemm_swiglu path
+    void *buf[9] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    size_t cap[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
 };
 std::mutex g_staging_mu;
 std::map<std::pair<int, void *>, Staging> g_staging;
@@ -581,6 +625,37 @@ extern "C" int hq_gemv(const hq_mat *W, const uint16_t *a, void *c, int c_is_f32
     return hq_gemm(W, a, 1, c, c_is_f32, accumulate, stream);
 }
 
+extern "C" int hq_gemm_swiglu(const hq_mat *pair, const uint16_t *A, int M, uint16_t *out, void *stream) {
+    if (!pair || !A || !out) return fail("hq_gemm_swiglu: null argument");
+    if (!pair->pair) return fail("hq_gemm_swiglu: not a gate/up pair matrix (hq_mat_upload_pair)");
+    if (M < 1 || M > (1 << 23)) return fail("hq_gemm_swiglu: M = %d (1 .. 8388608)", M);
+    if (!aligned(A, 16) || !aligned(out, 16)) return fail("hq_gemm_swiglu: A and out must be 16-byte aligned");
+    if (use_device(pair->device)) return -1;
+    const size_t K = pair->m.cols, N2 = pair->m.rows, step = gemm_rows_per_launch(K);
+    for (size_t m0 = 0; m0 < (size_t)M; m0 += step) {
+        const int mc = (int)((size_t)M - m0 < step ? (size_t)M - m0 : step);
+        const uint16_t *Ap = A + m0 * K;
+        uint16_t *Op = out + m0 * (N2 / 2);
+        HqGemmWork wk = {};
+        int fused = 0;
+        if (mc > 1) {
+            if (gemm_work(pair, mc, stream, &wk)) return -1;
+            HIPCK(hq_launch_gemm_swiglu(&pair->m, Ap, mc, Op, wk, S(stream), &fused));
+        }
+        if (fused) continue;
+        // other shapes: the product in fp32 (one pass over A for both halves), then the epilogue
+        void *tmp;
+        if (staging(pair->device, stream, 8, (size_t)mc * N2 * sizeof(float), &tmp)) return -1;
+        if (mc == 1) {
+            HIPCK(hq_launch_gemv(&pair->m, Ap, tmp, 1, 0, S(stream)));
+        } else {
+            HIPCK(hq_launch_gemm(&pair->m, Ap, mc, tmp, 1, 0, wk, S(stream)));
+        }
+        HIPCK(hq_launch_swiglu_pairs((const float *)tmp, Op, (size_t)mc * (N2 / 2), S(stream)));
+    }
+    return 0;
+}
+
 extern "C" int hq_gather_dot_dev(const hq_mat *head, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
                                  void *stream) {
     if (!head || !H || !ids || !out) return fail("hq_gather_dot: null argument");
@@ -779,6 +854,18 @@ extern "C" int hq_time_gemm_kernel(hq_mat *const *Ws, int n_w, const uint16_t *A
         HIPCK(hq_launch_gemm_main(&Ws[i % n_w]->m, A, M, C, c_is_f32, 0, wk, S(stream)));
         return 0;
     });
+}
+
+extern "C" int hq_time_gemm_swiglu(hq_mat *const *pairs, int n_w, const uint16_t *A, int M, uint16_t *out, int iters,
+                                   int reps, void *stream, float *ms) {
+    if (!pairs || n_w < 1) return fail("hq_time_gemm_swiglu: no matrices");
+    for (int i = 0; i < n_w; i++)
+        if (!pairs[i] || pairs[i]->m.rows != pairs[0]->m.rows || pairs[i]->m.cols != pairs[0]->m.cols ||
+            pairs[i]->m.type != pairs[0]->m.type)
+            return fail("hq_time_gemm_swiglu: matrices differ in shape or type");
+    if (hq_gemm_swiglu(pairs[0], A, M, out, stream)) return -1;  // sizes the workspace outside the capture
+    HIPCK(hipStreamSynchronize(S(stream)));
+    return time_graph(iters, reps, stream, ms, [&](int i) { return hq_gemm_swiglu(pairs[i % n_w], A, M, out, stream); });
 }
 
 extern "C" int hq_time_gather(hq_mat *const *Ws, int n_w, const uint16_t *H, const uint32_t *ids_dev, int n_sets,

@@ -133,6 +133,10 @@ DEV h2 bytes_f16(uint32_t w, bool hi_pair) {
     return as_h2(hi_pair ? perm_hi(w) : perm_lo(w)) - k1024;
 }
 
+// Output mode of the tile kernels besides fp32 (1) and fp16 (0) C: silu(gate) * up of a gate/up
+// pair matrix, fp16 (see tile_finish).
+constexpr int HQ_OUT_SWIGLU = 2;
+
 // End of a full-K tile kernel's tile, held in LDS as fp32 rows of LD floats (BM x BN, NT threads).
 // parts == 1: stored to C. parts > 1 (a K split, at most MAXP parts): every part stores its tile to
 // partials[tile][part] with device-scope (sc1) 16-byte stores, waits for them and counts itself in
@@ -184,6 +188,29 @@ DEV void tile_finish(const char *lds, const Args &g, int m0, int n0, int tile, i
                     pv[p][i][1] = *(const f4 *)(lds + (row * LD + 8 * ch + 4) * 4);
                 }
             }
+    }
+    if (g.c_f32 == HQ_OUT_SWIGLU) {
+        // gate/up pair matrix (one workgroup per tile, parts == 1): columns 16 c .. 16 c + 7 of the
+        // tile are gate rows and 16 c + 8 .. + 15 the matching up rows; C is fp16 [M, N / 2] and
+        // takes silu(gate) * up at columns (n0 + 16 c) / 2 .. + 7 (16-byte stores)
+        constexpr int PCH = CH / 2, NP = BM * PCH, PPT = (NP + NT - 1) / NT;
+        static_assert(CH % 2 == 0, "pairs of chunks");
+        const int Nh = N / 2;
+#pragma unroll
+        for (int i = 0; i < PPT; i++) {
+            const int pc = (int)threadIdx.x + NT * i, row = pc / PCH, c = pc - row * PCH, m = m0 + row, n = n0 + 16 * c;
+            if (pc >= NP) break;
+            if (m >= M || n >= N) continue;
+            const float *r = (const float *)(lds + (row * LD + 16 * c) * 4);
+            h8 y;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float gv = r[e], uv = r[8 + e];
+                y[e] = (_Float16)(gv / (1.0f + expf(-gv)) * uv);
+            }
+            *(h8 *)((_Float16 *)g.C + (size_t)m * Nh + n / 2) = y;
+        }
+        return;
     }
 #pragma unroll
     for (int i = 0; i < CPT; i++) {

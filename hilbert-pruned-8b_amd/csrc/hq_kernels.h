@@ -48,6 +48,12 @@ hipError_t hq_launch_gemm(const hq_dev_mat *W, const uint16_t *A, int M, void *C
 hipError_t hq_launch_gather(const hq_dev_mat *W, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
                             hipStream_t st);
 hipError_t hq_launch_f32_to_f16(const float *in, uint16_t *out, size_t n, hipStream_t st);
+// gate/up pair matrices (rows 16k .. 16k + 7 of gate, 16k + 8 .. + 15 of up): the GEMM with the SwiGLU
+// epilogue fused into the tile kernels (*fused = 0 when the shape does not run them), and the
+// epilogue as a separate pass over an fp32 [M, 2I] product (n_out = M * I)
+hipError_t hq_launch_gemm_swiglu(const hq_dev_mat *W, const uint16_t *A, int M, uint16_t *out, const HqGemmWork &wk,
+                                 hipStream_t st, int *fused);
+hipError_t hq_launch_swiglu_pairs(const float *C, uint16_t *out, size_t n_out, hipStream_t st);
 // rows x columns of one GEMM output tile (M >= 2) on a device with n_cu CUs
 void hq_gemm_tile_shape(int type, int M, int N, int K, int n_cu, int *rows, int *cols);
 void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, size_t n);

@@ -1421,6 +1421,44 @@ hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, vo
     return hipErrorInvalidValue;
 }
 
+// gate/up pair GEMM with the SwiGLU epilogue inside the full-K tile kernels (M > 64; any number of
+// tile rounds, each tile's K in one workgroup). *fused = 0 when the shape does not suit them: the
+// caller then runs hq_launch_gemm into fp32 and hq_launch_swiglu_pairs.
+hipError_t hq_launch_gemm_swiglu(const hq_dev_mat *W, const uint16_t *A, int M, uint16_t *out, const HqGemmWork &wk,
+                                 hipStream_t st, int *fused) {
+    *fused = 0;
+    const int N = (int)W->rows, K = (int)W->cols;
+    if (M <= 64 || (size_t)M * K * 2 >= ((size_t)1 << 32) || N % 16) return hipSuccess;
+    float eff = 0.f;
+    const int nb = hq_ws_choose(M, N, wk.n_cu, &eff);
+    if (W->type == HQ_TYPE_Q4_K && wk.sums) {
+        const size_t nsub = (size_t)M * (W->cols / 32);
+        if (nsub >= ((size_t)1 << 31)) return hipSuccess;
+        k_asums<true><<<grid_for(nsub, 256, 16384), 256, 0, st>>>(A, M, K, wk.sums);
+        *fused = 1;
+        return hq_launch_gemm_ws(W, A, wk.sums, M, out, HQ_OUT_SWIGLU, 0, nb, 1, nullptr, nullptr, st);
+    }
+    if (W->type == HQ_TYPE_Q8_0 && K % 128 == 0 && ((size_t)N + 160) * K < ((size_t)1 << 32)) {
+        *fused = 1;
+        return hq_launch_gemm_ws8(W, A, M, out, HQ_OUT_SWIGLU, 0, nb, 1, nullptr, nullptr, st);
+    }
+    return hipSuccess;
+}
+
+// out[m][8k + e] = silu(C[m][16k + e]) * C[m][16k + 8 + e]: the pair epilogue as its own pass
+__global__ void __launch_bounds__(256) k_swiglu_pairs(const float *__restrict__ C, uint16_t *__restrict__ out, size_t n_out) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n_out; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t k = i / 8, e = i % 8;
+        const float g = C[16 * k + e], u = C[16 * k + 8 + e];
+        out[i] = __builtin_bit_cast(uint16_t, (_Float16)(g / (1.0f + expf(-g)) * u));
+    }
+}
+
+hipError_t hq_launch_swiglu_pairs(const float *C, uint16_t *out, size_t n_out, hipStream_t st) {
+    k_swiglu_pairs<<<grid_for(n_out, 256, 16384), 256, 0, st>>>(C, out, n_out);
+    return hipGetLastError();
+}
+
 hipError_t hq_launch_gemm(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
                           const HqGemmWork &wk, hipStream_t st) {
     const hipError_t e = hq_launch_gemm_pre(W, A, M, wk, st);

@@ -25,7 +25,7 @@ EXPORTS = (
     "hq_device_synchronize", "hq_time_gemm", "hq_time_gemm_kernel", "hq_time_gather", "hq_gemm_tiles", "hq_llama_forward",
     "hq_embed_f32", "hq_gemm_kernel", "hq_gemm_noalloc", "hq_gemm_workspace_bytes", "hq_gemv_swiglu",
     "hq_gguf_open", "hq_gguf_close", "hq_gguf_n_tensors", "hq_gguf_tensor_info", "hq_gguf_find", "hq_gguf_get_uint",
-    "hq_gguf_wmat",
+    "hq_gguf_wmat", "hq_mat_upload_pair", "hq_gemm_swiglu", "hq_time_gemm_swiglu",
 )
 # include/hq_backend.h (no hq_ prefix: the names of the reference entry points they replace)
 BACKEND_EXPORTS = ("hip_backend_create", "hip_selftest")
@@ -141,6 +141,9 @@ def load(path=LIB_PATH):
         "hq_embed_f32": (i, [vp, vp, i, vp, vp]),
         "hq_gemm_noalloc": (i, [vp, vp, i, vp, i, i, vp]),
         "hq_gemv_swiglu": (i, [vp, vp, vp, vp, vp]),
+        "hq_mat_upload_pair": (i, [C.POINTER(WMat), C.POINTER(WMat), i, C.POINTER(vp)]),
+        "hq_gemm_swiglu": (i, [vp, vp, i, vp, vp]),
+        "hq_time_gemm_swiglu": (i, [C.POINTER(vp), i, vp, i, vp, i, i, vp, C.POINTER(C.c_float)]),
         "hq_gguf_open": (i, [C.c_char_p, C.POINTER(vp)]),
         "hq_gguf_close": (None, [vp]),
         "hq_gguf_n_tensors": (sz, [vp]),
@@ -296,6 +299,50 @@ def gemm_workspace_bytes(gtype, M, N, K, n_cu=256):
     pb, cb, sb, fits = C.c_size_t(), C.c_size_t(), C.c_size_t(), C.c_int()
     _check(load().hq_gemm_workspace_bytes(gtype, M, N, K, n_cu, C.byref(pb), C.byref(cb), C.byref(sb), C.byref(fits)))
     return pb.value, cb.value, sb.value, bool(fits.value)
+
+
+class PairMat:
+    """hq_mat_upload_pair: gate and up of one FFN as one interleaved resident matrix."""
+
+    def __init__(self, gate_blocks, up_blocks, gtype, rows, cols, device=0):
+        load()
+        g = np.ascontiguousarray(gate_blocks, dtype=np.uint8)
+        u = np.ascontiguousarray(up_blocks, dtype=np.uint8)
+        wg = WMat(DT_GGML, rows, cols, g.ctypes.data, gtype, 0)
+        wu = WMat(DT_GGML, rows, cols, u.ctypes.data, gtype, 0)
+        h = C.c_void_p()
+        _check(_lib.hq_mat_upload_pair(C.byref(wg), C.byref(wu), device, C.byref(h)))
+        self.h, self.gtype, self.rows, self.cols = h.value, gtype, rows, cols
+
+    def free(self):
+        if self.h:
+            _lib.hq_mat_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def gemm_swiglu_np(pair, a_f16_bits):
+    """hq_gemm_swiglu on numpy fp16 bits [M, K]: fp16 bits [M, rows] of silu(A gate^T) * (A up^T)."""
+    a = np.ascontiguousarray(a_f16_bits, dtype=np.uint16)
+    M = a.shape[0]
+    dA, dO = DevBuf.from_array(a), DevBuf(M * pair.rows * 2)
+    _check(_lib.hq_gemm_swiglu(pair.h, dA.ptr, M, dO.ptr, None))
+    synchronize()
+    out = dO.download((M, pair.rows), np.uint16)
+    dA.free(), dO.free()
+    return out
+
+
+def time_gemm_swiglu(pairs, A, M, out, iters, reps, stream):
+    arr = (C.c_void_p * len(pairs))(*[m.h for m in pairs])
+    ms = C.c_float()
+    _check(_lib.hq_time_gemm_swiglu(arr, len(pairs), A.ptr, M, out.ptr, iters, reps, stream.ptr, C.byref(ms)))
+    return ms.value
 
 
 def gemv_swiglu_np(gate, up, a_f16_bits):

@@ -103,6 +103,17 @@ int hq_gemm_workspace_bytes(int ggml_type, int M, uint32_t N, uint32_t K, int n_
  * Q6_K up). Replaces k_gateup_swiglu (src/cuda_backend.cu:548-559); one pass over both matrices. */
 int hq_gemv_swiglu(const hq_mat *gate, const hq_mat *up, const uint16_t *a, uint16_t *out, void *stream);
 
+/* Gate/up pair for the SwiGLU FFN input: one resident matrix of 2 * rows rows, rows 16k .. 16k + 7 of
+ * gate interleaved with rows 16k + 8 .. 16k + 15 of up (gate and up: same type and shape, rows a
+ * multiple of 8), so that one GEMM tile covers matching gate and up columns and the activations are
+ * read once for both. */
+int hq_mat_upload_pair(const hq_wmat_t *gate, const hq_wmat_t *up, int device, hq_mat **out);
+/* out[M, rows] fp16 = silu(A . gate^T) * (A . up^T) for a pair matrix, A fp16 [M, K]; out 16-byte
+ * aligned. Replaces gemm_w(gate) + gemm_w(up) + k_swiglu (src/cuda_backend.cu:845-849, :413-416):
+ * for M > 64 the product never leaves the GEMM's tile (the epilogue of the full-K tile kernels
+ * applies silu(g) * u), other shapes run one GEMM for both halves and a separate epilogue pass. */
+int hq_gemm_swiglu(const hq_mat *pair, const uint16_t *A, int M, uint16_t *out, void *stream);
+
 /* Option-row readout: out[b*k + j] = dot(H[b], head[ids[b*k + j]]) for b < B, j < k, fp32.
  * H fp16 [B, K] and out on the device; ids on the HOST (checked against rows, then staged).
  * Replaces the quantized readout of k_readout_q / k_norm_readout (src/cuda_backend.cu:490-502,
@@ -141,6 +152,9 @@ int hq_time_gemm(hq_mat *const *Ws, int n_w, const uint16_t *A, int M, void *C, 
  * kernel needs (it depends on A alone) runs once before the capture. */
 int hq_time_gemm_kernel(hq_mat *const *Ws, int n_w, const uint16_t *A, int M, void *C, int c_is_f32, int iters,
                         int reps, void *stream, float *ms);
+/* As hq_time_gemm for hq_gemm_swiglu over pair matrices. */
+int hq_time_gemm_swiglu(hq_mat *const *pairs, int n_w, const uint16_t *A, int M, uint16_t *out, int iters, int reps,
+                        void *stream, float *ms);
 int hq_time_gather(hq_mat *const *Ws, int n_w, const uint16_t *H, const uint32_t *ids_dev, int n_sets, int B, int k,
                    float *out, int iters, int reps, void *stream, float *ms);
 
