@@ -107,11 +107,12 @@ def bench_gemm(hq, synth, gtype, N, K, M, c_f32, steps, warmup, stream, eager_wa
     return r
 
 
-def bench_config4(hq, synth, stream, M=16384):
+def bench_config4(hq, synth, stream, M=16384, reading="baseline"):
     """Config 4: the hybrid 4B projection sequence (32 layers) at M = 16384; each distinct shape timed
-    once (3 launches), total = sum over the sequence."""
+    once (3 launches), total = sum over the sequence. reading: BASELINE's literal widths or the
+    reference's layer_weights() list (synth.hybrid_4b_projections)."""
     counts = {}
-    for layer in synth.hybrid_4b_projections():
+    for layer in synth.hybrid_4b_projections(reading):
         for _, n, k in layer:
             counts[(n, k)] = counts.get((n, k), 0) + 1
     total_us, flop, shapes = 0.0, 0.0, []
@@ -119,8 +120,10 @@ def bench_config4(hq, synth, stream, M=16384):
         r = bench_gemm(hq, synth, synth.Q4_K, n, k, M, False, 3, 1, stream, rotate=False)
         total_us += cnt * r["us"]
         flop += cnt * 2.0 * M * n * k
-        shapes.append({"N": n, "K": k, "count": cnt, "us": round(r["us"], 2), "tflops": round(r["tflops"], 1)})
-    return dict(type="config4_hybrid_4b_q4_k", M=M, projections=sum(counts.values()), total_ms=round(total_us / 1e3, 3),
+        shapes.append({"N": n, "K": k, "count": cnt, "us": round(r["us"], 2), "tflops": round(r["tflops"], 1),
+                       "kernel": hq.gemm_kernel(synth.Q4_K, M, n, k)})
+    return dict(type="config4_hybrid_4b_q4_k", reading=reading, M=M, projections=sum(counts.values()),
+                total_ms=round(total_us / 1e3, 3),
                 tflop=round(flop / 1e12, 2), tflops=round(flop / (total_us * 1e-6) / 1e12, 1),
                 frac=round(flop / (total_us * 1e-6) / 1e12 / PEAK_TFLOPS, 4), bound="mfma", shapes=shapes)
 
@@ -228,6 +231,8 @@ def main():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run 20 device-to-device copies of BYTES bytes (the known-size kernel the "
                          "FETCH_SIZE / WRITE_SIZE counters are scaled by) and exit")
+    ap.add_argument("--config4-only", action="store_true",
+                    help="only time config 4 (both readings of its shape list) and exit")
     ap.add_argument("--swiglu-only", action="store_true",
                     help="only time the fused gate/up+SwiGLU pair GEMM against two GEMMs and exit")
     ap.add_argument("--upload-only", action="store_true",
@@ -262,6 +267,10 @@ def main():
         g = {"q8_0": synth.Q8_0, "q4_k": synth.Q4_K}[t]
         r = bench_gemm(hq, synth, g, int(n), int(k), int(m), False, args.steps, args.warmup, stream, settle_s=0.2)
         log("shape", main_kernel_name(hq, g, int(m), int(n), int(k)), r)
+        return
+    if args.config4_only:
+        for reading in ("baseline", "layer_weights"):
+            log("config4", bench_config4(hq, synth, stream, reading=reading))
         return
     if args.swiglu_only:
         for g in (synth.Q4_K, synth.Q8_0):
@@ -300,9 +309,10 @@ def main():
             r["bound"], r["frac"] = "hbm", round(r["gbs"] / PEAK_GBS, 4)
             log("sweep", r)
             sweep.append({key: (round(v, 4) if isinstance(v, float) else v) for key, v in r.items()})
-        r = bench_config4(hq, synth, stream)
-        log("sweep", r)
-        sweep.append(r)
+        for reading in ("baseline", "layer_weights"):
+            r = bench_config4(hq, synth, stream, reading=reading)
+            log("sweep", r)
+            sweep.append(r)
         for g in (synth.Q4_K, synth.Q8_0):
             r = bench_swiglu(hq, synth, g, stream)
             log("sweep", r)

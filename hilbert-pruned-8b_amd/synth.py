@@ -187,12 +187,28 @@ def tiny_llama_prompt(seed=2, T=128, vocab=32000, n_ids=4):
 # ---------------------------------------------------------------- config 4: hybrid layer list
 
 def hybrid_4b_projections(reading="baseline"):
-    """(name, N=out rows, K=in cols) per projection of one 4-layer period (3 Gated-DeltaNet, 1 full
-    attention), in model order. reading="baseline": BASELINE.json config 4's literal widths
-    (attention Q 4096 / KV 1024, DeltaNet in/out 4096, FFN 9216, d=2560)."""
+    """(name, N=out rows, K=in cols) per projection of the 32-layer hybrid (3 Gated-DeltaNet : 1 full
+    attention), in model order.
+    reading="baseline": BASELINE.json config 4's literal widths (attention Q 4096 / KV 1024,
+      DeltaNet in/out 4096, FFN 9216, d=2560).
+    reading="layer_weights": the reference's own list (cleanroom-transformer/src/shapes.c:12-39)
+      for its Qwen3.5-4B config (tests/configs/qwen3.5-4b/config.json: hidden 2560, 16 heads of 256
+      with the output gate, 4 kv heads, DeltaNet 16 key heads x 128 and 32 value heads x 128, FFN
+      9216): q_proj 8192 (q and gate), k/v 1024, o 2560 x 4096; in_proj_qkv 8192, z 4096, b and a 32,
+      out_proj 2560 x 4096."""
     H, I = 2560, 9216
-    lin = [("linear.in_proj", 4096, H), ("linear.out_proj", H, 4096)]
-    full = [("attn.q", 4096, H), ("attn.k", 1024, H), ("attn.v", 1024, H), ("attn.o", H, 4096)]
+    if reading == "baseline":
+        lin = [("linear.in_proj", 4096, H), ("linear.out_proj", H, 4096)]
+        full = [("attn.q", 4096, H), ("attn.k", 1024, H), ("attn.v", 1024, H), ("attn.o", H, 4096)]
+    elif reading == "layer_weights":
+        hd, nh, nkv, Dk, Dv = 256, 16, 4, 16 * 128, 32 * 128
+        full = [("self_attn.q_proj", nh * hd * 2, H), ("self_attn.k_proj", nkv * hd, H),
+                ("self_attn.v_proj", nkv * hd, H), ("self_attn.o_proj", H, nh * hd)]
+        lin = [("linear_attn.in_proj_qkv", 2 * Dk + Dv, H), ("linear_attn.in_proj_z", Dv, H),
+               ("linear_attn.in_proj_b", 32, H), ("linear_attn.in_proj_a", 32, H),
+               ("linear_attn.out_proj", H, Dv)]
+    else:
+        raise ValueError(reading)
     ffn = [("mlp.gate", I, H), ("mlp.up", I, H), ("mlp.down", H, I)]
     layers = []
     for li in range(32):

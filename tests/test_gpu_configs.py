@@ -76,8 +76,11 @@ def sampled_check(hqlib, oracle, gtype, N, K, M, seed, what):
     assert np.all(np.isfinite(got))
 
 
-# config 4: the five distinct Q4_K projection shapes of the 32-layer hybrid at M = 16384
-CONFIG4 = [(4096, 2560), (1024, 2560), (9216, 2560), (2560, 4096), (2560, 9216)]
+# config 4: the distinct Q4_K projection shapes of the 32-layer hybrid at M = 16384, in
+# BASELINE's literal reading and in the reference's layer_weights() reading (src/shapes.c:12-39),
+# which adds the 8192-wide q_proj / in_proj_qkv and the 32-row b / a projections
+CONFIG4 = sorted({(n, k) for reading in ("baseline", "layer_weights")
+                  for layer in synth.hybrid_4b_projections(reading) for _, n, k in layer})
 
 
 @pytest.mark.parametrize("N,K", CONFIG4)
