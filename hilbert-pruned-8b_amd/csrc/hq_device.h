@@ -73,6 +73,17 @@ DEV void dma16_untracked(rsrc_t r, uint32_t lds_addr, uint32_t voff) {
                  : "memory");
 }
 
+// 16-byte LDS DMA with an SGPR offset, untracked by the compiler (explicit s_waitcnt vmcnt).
+DEV void dma16_so(rsrc_t r, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
+    uint32_t save;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 1\n\tbuffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(save)
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(r),
+                   "s"(__builtin_amdgcn_readfirstlane(soff))
+                 : "memory");
+}
+
 // s_waitcnt vmcnt(n) for a wave-uniform n in 0 .. 31 (the count is an immediate of the instruction).
 DEV void wait_vmcnt(int n) {
     switch (n) {

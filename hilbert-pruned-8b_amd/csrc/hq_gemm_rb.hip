@@ -70,17 +70,6 @@ struct RbLds {
     static_assert(BM * (BN + 4) * 4 <= NSTG * STG, "epilogue tile");
 };
 
-// 16-byte LDS DMA with an SGPR offset, untracked by the compiler (explicit s_waitcnt vmcnt).
-DEV void dma16_so(rsrc_t r, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
-    uint32_t save;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 1\n\tbuffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
-                 "s_mov_b32 m0, %0"
-                 : "=&s"(save)
-                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(r),
-                   "s"(__builtin_amdgcn_readfirstlane(soff))
-                 : "memory");
-}
-
 using rb_lds_h8 = const __attribute__((address_space(3))) h8;
 using rb_lds_u4 = const __attribute__((address_space(3))) u4v;
 DEV h8 rb_ld8(uint32_t a) { return *(rb_lds_h8 *)(uintptr_t)a; }

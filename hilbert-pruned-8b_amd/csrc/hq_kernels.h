@@ -64,6 +64,11 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
 int hq_ws_choose(int M, int N, int n_cu, float *eff);
 hipError_t hq_launch_gemm_ws(const hq_dev_mat *W, const uint16_t *A, const uint16_t *S, int M, void *C, int c_f32,
                              int accumulate, int nb, int parts, float *partials, int *counters, hipStream_t st);
+// Large-M Q4_K GEMM (hq_gemm_bt.hip): 256 x 256 tiles over the whole of K, one workgroup each (S =
+// k_asums<true> output for A); whether a shape's byte offsets suit it, and the launch.
+int hq_bt_fits(const hq_dev_mat *W, int M);
+hipError_t hq_launch_gemm_bt(const hq_dev_mat *W, const uint16_t *A, const uint16_t *S, int M, void *C, int c_f32,
+                             int accumulate, hipStream_t st);
 // Mid-M Q4_K GEMM (hq_gemm_rb.hip): whether M, K suit it (33 <= M <= 64, K a multiple of 512,
 // 32-bit offsets), its workgroups per tile for a shape, and the launch (S = k_asums output for A in
 // the (hi, lo) pair layout; partials / counters as for the other K splits when parts > 1).

@@ -1237,6 +1237,7 @@ struct GemmCfg {
     int ws8_parts;  // with ws8_nb: workgroups per tile (K split, as ws_parts)
     int rbm;        // Q4_K mid M: workgroups per tile of k_gemm_q4_k_rb (hq_gemm_rb.hip); 0: not used
     int rb8;        // Q8_0 M <= 64: workgroups per tile of k_gemm_q8_0_rb (hq_gemm_rb.hip); 0: not used
+    bool bt;        // Q4_K large M: the 256 x 256 tile kernel k_gemm_q4_k_bt (hq_gemm_bt.hip)
 };
 
 // Q4_K with M > 64 runs the full-K tile kernel when its tiles fit in one round on the CUs and fill
@@ -1272,6 +1273,13 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
                     c.ws_parts = parts;
                 }
             }
+    }
+    // Q4_K where the Stream-K wide kernel would run: the 256 x 256 tile kernel when its rounds of
+    // tiles fill at least 3/4 of the CU time (M = 16384, N = 9728: 2432 tiles in 9.5 rounds)
+    c.bt = false;
+    if (c.wide && !c.ws_nb && hq_bt_fits(W, M)) {
+        const long t = (long)((M + 255) / 256) * (((long)W->rows + 255) / 256), rounds = (t + n_cu - 1) / n_cu;
+        c.bt = 4 * t >= 3 * rounds * n_cu;
     }
     // Q8_0 with M > 64: the Q8_0 tile kernel when its tiles fill at least half of the CU time
     // (rounds of tiles included; M = 128, N = 9728: 152 tiles of 128 x 64, 21.7 us against 24.9 for
@@ -1312,8 +1320,8 @@ void hq_gemm_tile_shape(int type, int M, int N, int K, int n_cu, int *rows, int 
     W.rows = (uint32_t)N;
     W.cols = (uint32_t)K;
     const GemmCfg c = gemm_cfg(&W, M, n_cu);
-    *rows = c.rbm ? 64 : c.rb8 ? (M <= 16 ? 16 : M <= 32 ? 32 : 64) : c.ws_nb || c.ws8_nb ? 128 : 16 * c.mb;
-    *cols = c.rbm || c.rb8 ? 64 : c.ws_nb ? 32 * c.ws_nb : c.ws8_nb ? 32 * c.ws8_nb : 16 * c.nb * c.waves;
+    *rows = c.bt ? 256 : c.rbm ? 64 : c.rb8 ? (M <= 16 ? 16 : M <= 32 ? 32 : 64) : c.ws_nb || c.ws8_nb ? 128 : 16 * c.mb;
+    *cols = c.bt ? 256 : c.rbm || c.rb8 ? 64 : c.ws_nb ? 32 * c.ws_nb : c.ws8_nb ? 32 * c.ws8_nb : 16 * c.nb * c.waves;
 }
 
 // Name of the kernel that does the work of an M x N x K hq_gemm call (the main kernel for GEMMs
@@ -1338,6 +1346,7 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
     const GemmCfg c = gemm_cfg(&W, M, n_cu);
     if (c.rbm) snprintf(buf, n, "k_gemm_q4_k_rb<1, 4, 3, 2>");
     else if (c.rb8) snprintf(buf, n, "k_gemm_q8_0_rb<%d, 3, 2>", M <= 16 ? 1 : M <= 32 ? 2 : 4);
+    else if (c.bt) snprintf(buf, n, "k_gemm_q4_k_bt");
     else if (c.ws_nb) snprintf(buf, n, "k_gemm_q4_k_ws<%d>", c.ws_nb);
     else if (c.ws8_nb) snprintf(buf, n, "k_gemm_q8_0_ws<%d>", c.ws8_nb);
     else if (c.wide) snprintf(buf, n, "k_gemm_q4_k_w<%d>", c.mb);  // template argument: row blocks
@@ -1349,7 +1358,7 @@ void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_by
                         size_t *sums_bytes) {
     const GemmCfg c = gemm_cfg(W, M, n_cu);
     const SkPlan p = gemm_plan(W, M, c, n_cu);
-    const bool tile = c.ws_nb || c.ws8_nb;  // tile kernels: partial tiles only when K is split (below)
+    const bool tile = c.ws_nb || c.ws8_nb || c.bt;  // tile kernels: partial tiles only when K is split (below)
     *partial_bytes = tile ? 0 : (size_t)2 * p.G * 64 * c.waves * c.mb * c.nb * 4 * sizeof(float);
     *counter_bytes = tile ? 0 : (size_t)p.tiles * sizeof(int);
     const int snb = c.ws_nb ? c.ws_nb : c.ws8_nb, sparts = c.ws_nb ? c.ws_parts : c.ws8_parts;
@@ -1378,7 +1387,7 @@ hipError_t hq_launch_gemm_pre(const hq_dev_mat *W, const uint16_t *A, int M, con
     if (c.wide) {
         const size_t nsub = (size_t)M * (W->cols / 32);
         if (nsub >= ((size_t)1 << 31)) return hipErrorInvalidValue;
-        if (c.ws_nb) k_asums<true><<<grid_for(nsub, 256, 16384), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
+        if (c.ws_nb || c.bt) k_asums<true><<<grid_for(nsub, 256, 16384), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
         else k_asums<false><<<grid_for(nsub, 256, 16384), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
     }
     return hipGetLastError();
@@ -1390,6 +1399,7 @@ hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, vo
     const GemmCfg c = gemm_cfg(W, M, wk.n_cu);
     if (c.rbm) return hq_launch_gemm_rb(W, A, wk.sums, M, C, c_f32, accumulate, c.rbm, wk.partials, wk.counters, st);
     if (c.rb8) return hq_launch_gemm_rb8(W, A, M, C, c_f32, accumulate, c.rb8, wk.partials, wk.counters, st);
+    if (c.bt) return hq_launch_gemm_bt(W, A, wk.sums, M, C, c_f32, accumulate, st);
     if (c.ws_nb)
         return hq_launch_gemm_ws(W, A, wk.sums, M, C, c_f32, accumulate, c.ws_nb, c.ws_parts, wk.partials, wk.counters, st);
     if (c.ws8_nb)

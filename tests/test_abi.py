@@ -80,14 +80,16 @@ def test_upload_rejects_matrices_of_4gib_or_more():
 def test_gemm_workspace_bytes():
     """Workspace of one GEMM launch (computed on the host, no device): the K-split tile kernel keeps
     one fp32 tile per (tile, part) plus a counter per tile; the Stream-K kernel two 128 x 256 fp32
-    tiles per CU; hq_gemm_noalloc's 96 MiB scratch holds the BASELINE shapes and refuses larger."""
+    tiles per CU; the large-M tile kernel only the activation sub-block sums; hq_gemm_noalloc's
+    96 MiB scratch holds the BASELINE shapes and refuses larger."""
     pb, cb, sb, fits = hq.gemm_workspace_bytes(synth.Q4_K, 512, 2560, 9728)
     assert (pb, cb, sb, fits) == (64 * 4 * 128 * 160 * 4, 64 * 4, 512 * 38 * 32, True)
-    pb, cb, sb, fits = hq.gemm_workspace_bytes(synth.Q4_K, 4096, 9728, 2560)
-    assert (pb, cb, fits) == (2 * 256 * 128 * 256 * 4, 32 * 38 * 4, True)
+    pb, cb, sb, fits = hq.gemm_workspace_bytes(synth.Q4_K, 4096, 2560, 9728)
+    assert (pb, cb, fits) == (2 * 256 * 128 * 256 * 4, 32 * 10 * 4, True)
+    assert hq.gemm_workspace_bytes(synth.Q4_K, 4096, 9728, 2560) == (0, 0, 4096 * 10 * 32, True)
     assert hq.gemm_workspace_bytes(synth.Q8_0, 512, 9728, 2560) == (0, 0, 0, True)
     assert hq.gemm_workspace_bytes(synth.Q4_K, 16384, 2560, 9216)[3]
-    assert not hq.gemm_workspace_bytes(synth.Q4_K, 65536, 256, 9216)[3]
+    assert not hq.gemm_workspace_bytes(synth.Q4_K, 131072, 256, 9216)[3]  # 151 MB of sub-block sums
     with pytest.raises(hq.HQError, match="M = 1"):
         hq.gemm_workspace_bytes(synth.Q4_K, 1, 256, 256)
 
@@ -97,7 +99,9 @@ def test_gemm_kernel_names():
     cases = {(synth.Q4_K, 512, 9728, 2560): "k_gemm_q4_k_ws<5>", (synth.Q8_0, 512, 9728, 2560): "k_gemm_q8_0_ws<5>",
              (synth.Q8_0, 2048, 9728, 2560): "k_gemm_q8_0_ws<5>", (synth.Q8_0, 128, 9728, 2560): "k_gemm_q8_0_ws<2>",
              (synth.Q8_0, 65, 9728, 2560): "k_gemm_q8_0<8, 2>",
-             (synth.Q4_K, 4096, 9728, 2560): "k_gemm_q4_k_w<8>", (synth.Q4_K, 64, 9728, 2560): "k_gemm_q4_k_rb<1, 4, 3, 2>",
+             (synth.Q4_K, 4096, 9728, 2560): "k_gemm_q4_k_bt", (synth.Q4_K, 16384, 2560, 9216): "k_gemm_q4_k_bt",
+             (synth.Q4_K, 16384, 1024, 2560): "k_gemm_q4_k_bt", (synth.Q4_K, 2048, 9728, 2560): "k_gemm_q4_k_w<8>",
+             (synth.Q4_K, 64, 9728, 2560): "k_gemm_q4_k_rb<1, 4, 3, 2>",
              (synth.Q4_K, 64, 2560, 9728): "k_gemm_q4_k_rb<1, 4, 3, 2>", (synth.Q4_K, 64, 1024, 2560): "k_gemm_q4_k<4, 2>", (synth.Q4_K, 32, 9728, 2560): "k_gemm_q4_k<2, 2>",
              (synth.Q4_K, 64, 9728, 2304): "k_gemm_q4_k<4, 2>",
              (synth.Q4_K, 512, 2560, 9728): "k_gemm_q4_k_ws<5>", (synth.Q4_K, 256, 2560, 9728): "k_gemm_q4_k_ws<3>",
@@ -120,12 +124,13 @@ def test_gemm_tile_selection():
         assert hq.gemm_tiles(gtype, 1, 9728) == (1, 16)
         for M in (2, 16, 17, 33, 64, 65, 512, 4096):
             r, c = hq.gemm_tiles(gtype, M, 9728)
-            assert r in (16, 32, 64, 128)
-            assert r >= min(M, 128) or r == 128
+            assert r in (16, 32, 64, 128, 256)
+            assert r >= min(M, 128)
             if gtype == synth.Q4_K and M > 64:
-                # Q4_K above M = 64: full-K tiles of 128 x 32NB when they fill the CUs, else the
-                # 8-wave Stream-K kernel (128 x 256)
-                assert (r, c) == (128, 256) or (r == 128 and c in (64, 96, 128, 160))
+                # Q4_K above M = 64: full-K tiles of 128 x 32NB when they fill the CUs, 256 x 256
+                # full-K tiles at large M when their rounds fill the CUs, else the 8-wave Stream-K
+                # kernel (128 x 256)
+                assert (r, c) in ((128, 256), (256, 256)) or (r == 128 and c in (64, 96, 128, 160))
             elif gtype == synth.Q8_0 and M > 64:
                 # Q8_0 above M = 64: full-K tiles of 128 x 32NB when they fill >= 50 % of the CU
                 # time (any number of rounds), else the narrow Stream-K kernel
@@ -143,9 +148,12 @@ def test_gemm_tile_selection():
     assert hq.gemm_tiles(synth.Q8_0, 512, 9728) == (128, 160)
     assert hq.gemm_tiles(synth.Q8_0, 2048, 9728) == (128, 160)
     assert hq.gemm_tiles(synth.Q4_K, 65, 9728) == (128, 256)
-    # full-K tiles: 4 x 61 tiles of 128 x 160 on 256 CUs; more tiles than CUs: Stream-K
+    # full-K tiles: 4 x 61 tiles of 128 x 160 on 256 CUs; more tiles than CUs: Stream-K, or at large
+    # M the 256 x 256 tiles when their rounds fill >= 3/4 of the CU time (M = 4096: 608 tiles in 3
+    # rounds; M = 2048: 304 tiles in 2 rounds, 59 %)
     assert hq.gemm_tiles(synth.Q4_K, 512, 9728) == (128, 160)
-    assert hq.gemm_tiles(synth.Q4_K, 4096, 9728) == (128, 256)
+    assert hq.gemm_tiles(synth.Q4_K, 2048, 9728) == (128, 256)
+    assert hq.gemm_tiles(synth.Q4_K, 4096, 9728) == (256, 256)
 
 
 def test_synth_is_deterministic():
