@@ -4,7 +4,7 @@ against the CPU oracle on sampled rows.
 
 Shapes: M = 4196 (16 whole 256-row tiles and a ragged one of 100 rows), N = 9672 (37 whole
 256-column tiles and a ragged one of 200) or 9674 (N not a multiple of 4: the scalar store path),
-K = 256 (one super-block: no rescale between units), 512 and 1024. Sampling: 8 rows of every
+K = 256 (one super-block: no rescale between units), 512, 1024 and 4096. Sampling: 8 rows of every
 256-row tile plus the first and last row, every column. Bars as in test_gpu_parity.py: rel-L2 <=
 1e-3 and max-abs <= 1e-2 (2e-3 for Q4_K); against the float64 product, 2^-13 |W| @ |a| per output.
 """
@@ -13,7 +13,7 @@ import pytest
 
 import synth
 from conftest import max_abs, rel_l2
-from test_gpu_configs import sample_rows
+from test_gpu_configs import sample_cols, sample_rows
 from test_gpu_parity import f64_reference, special_q4_k_weights
 
 pytestmark = pytest.mark.gpu
@@ -98,3 +98,24 @@ def test_bt_positive_activations(hqlib, oracle):
     assert r <= REL_L2
     r64, bound = f64_reference(oracle, blocks, synth.Q4_K, N, K, a[rows])
     assert np.all(np.abs(got[rows] - r64) <= 2.0 ** -13 * bound)
+
+
+def test_bt_long_k_repeatable(hqlib, oracle):
+    """K = 4096 (16 super-blocks, 64 stages through the triple-buffered LDS rings and the per-super-
+    block tables written while the previous super-block is read): sampled parity, and three calls
+    give the same bits (each output is one workgroup's fixed sequence of MFMAs, so any difference
+    would come from a race between the waves' LDS writes and reads)."""
+    N, K = 9672, 4096
+    blocks = synth.random_blocks(synth.Q4_K, synth.Rng(101), N, K)
+    a = synth.activations_f16(synth.Rng(102), M_BT, K)
+    name = hqlib.gemm_kernel(synth.Q4_K, M_BT, N, K)
+    say(f"bt long K: M={M_BT} N={N} K={K} kernel={name}")
+    assert name == "k_gemm_q4_k_bt"
+    W = hqlib.Mat(blocks, synth.Q4_K, N, K)
+    got = [hqlib.gemm_np(W, a) for _ in range(3)]
+    W.free()
+    assert np.array_equal(got[0], got[1]) and np.array_equal(got[0], got[2])
+    rows = sample_rows(M_BT, per_tile=4, tile=256)
+    cols = sample_cols(N)
+    ref = oracle.matmul(np.ascontiguousarray(blocks[cols]), synth.Q4_K, len(cols), K, oracle.f16_to_f32(a[rows]))
+    check(got[0][np.ix_(rows, cols)], ref, f"bt long K ({len(rows)} rows x {len(cols)} columns)")
