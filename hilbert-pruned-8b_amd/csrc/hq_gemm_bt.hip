@@ -102,11 +102,13 @@ __global__ void __launch_bounds__(BT_NT) k_gemm_q4_k_bt(BtArgs g) {
     const uint32_t a_ch = (uint32_t)((lane & 7) ^ ((a_row0 >> 1) & 7));
     const uint32_t a_rowoff = (uint32_t)(m0 + a_row0) * (uint32_t)K * 2u;
     const uint32_t a_voff0 = a_rowoff + 16u * a_ch, a_voff1 = a_rowoff + 16u * (a_ch ^ 4u);
+    auto dma_a1 = [&](int s, int buf, int q) {
+        dma16_so(ra, lds0 + (uint32_t)(L::A + buf * L::A_BYTES + wave * 4096 + q * 1024), q & 1 ? a_voff1 : a_voff0,
+                 (uint32_t)(q * 8 * K * 2 + s * BT_KS * 2));
+    };
     auto dma_a = [&](int s, int buf) {
-        const uint32_t dst = lds0 + (uint32_t)(L::A + buf * L::A_BYTES + wave * 4096);
 #pragma unroll
-        for (int q = 0; q < 4; q++)
-            dma16_so(ra, dst + q * 1024, q & 1 ? a_voff1 : a_voff0, (uint32_t)(q * 8 * K * 2 + s * BT_KS * 2));
+        for (int q = 0; q < 4; q++) dma_a1(s, buf, q);
     };
     // S of super-block u: wave w moves rows 32w .. + 32 (1 KB); lane i: row 32w + i/2, half i % 2
     const uint32_t s_voff = (uint32_t)(m0 + 32 * wave + (lane >> 1)) * (uint32_t)U * 32u + 16u * (uint32_t)(lane & 1);
@@ -215,7 +217,7 @@ __global__ void __launch_bounds__(BT_NT) k_gemm_q4_k_bt(BtArgs g) {
     // scale words sw (sub-blocks 2p, 2p + 1: bytes 2(p % 2), 2(p % 2) + 1 of word p / 2), activation
     // operands from A buffer at offset boff. Group g (0 .. 15): k-step g / 8, block row g % 8; the
     // k-step 1 weight operands are decoded behind the first four groups.
-    auto stage_mfma = [&](int p, int buf, int u) {
+    auto stage_mfma = [&](int p, int buf, int u, auto issue) {
         const uint32_t boff = (uint32_t)(buf * L::A_BYTES);
         u2v q[4];
 #pragma unroll
@@ -241,6 +243,7 @@ __global__ void __launch_bounds__(BT_NT) k_gemm_q4_k_bt(BtArgs g) {
 #pragma unroll
             for (int j = 0; j < 4; j++) acc[g & 7][j] = mfma(g < 8 ? b0[j] : b1[j], af[g % 3], acc[g & 7][j]);
             if (g < 4) b1[g] = decode8<true>(q[g], h2{mu[g].y, mu[g].y}, h2{ad[g].y, ad[g].y});
+            issue(g);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -271,13 +274,17 @@ __global__ void __launch_bounds__(BT_NT) k_gemm_q4_k_bt(BtArgs g) {
             const int s = 4 * u + p;
             const int ab2 = ab == 0 ? 2 : ab - 1;  // (s + 2) % 3
             const int s_src = s + 2 < S2 ? s + 2 : S2 - 1;
-            dma_a(s_src, ab2);
-            dma_q(s_src, ab2);
-            if (p == 1) dma_s(u_next);  // unit u's min k-step is behind the previous barrier
-            if (p == 0) H = load_h(u_next);
+            // the stage's loads, issued between its MFMA groups (a burst of them at the stage start
+            // would hold up every wave's first MFMAs while the address unit works through them)
+            auto issue = [&](int g) {
+                if (g == 1 || g == 3 || g == 5 || g == 7) dma_a1(s_src, ab2, g >> 1);
+                if (g == 9) dma_q(s_src, ab2);
+                if (p == 1 && g == 11) dma_s(u_next);  // unit u's min k-step is behind the previous barrier
+                if (p == 0 && g == 13) H = load_h(u_next);
+            };
             __builtin_amdgcn_sched_barrier(0);
             if (p == 0) min_step();
-            stage_mfma(p, ab, u);
+            stage_mfma(p, ab, u, issue);
             __builtin_amdgcn_sched_barrier(0);
             if (p == 3 && u + 1 < U && half == 0) write_tables(H, u + 1);
             // end of stage s: every load issued before this stage has landed (the loads this stage
