@@ -234,6 +234,8 @@ static int upload_rows(int type, uint32_t rows, uint32_t cols, F row_ptr, int de
     if (dev_bytes >= ((size_t)1 << 32))
         return fail("%s: shape [%u, %u] needs %zu device bytes; one matrix is limited to 4 GiB (split its rows)", who, rows,
                     cols, dev_bytes);
+    // Q4_K: the GEMM kernels' per-super-block column tables follow the blocks (a third of their bytes)
+    const size_t tab_at = round_up(dev_bytes, 256), tab_bytes = type == HQ_GGML_Q4_K ? (size_t)rows * nb * HQ_Q4K_TAB_BYTES : 0;
     if (rb > UP_CHUNK) return fail("%s: a row of %zu bytes exceeds the %zu-byte staging buffer", who, rb, UP_CHUNK);
     if (use_device(device)) return -1;
     Uploader *u;
@@ -246,14 +248,15 @@ static int upload_rows(int type, uint32_t rows, uint32_t cols, F row_ptr, int de
     m->m.cols = cols;
     m->m.row_bytes = drb;
     m->m.ldd = type == HQ_GGML_Q8_0 ? (int)ldd : 0;
-    m->bytes = dev_bytes;
+    m->bytes = tab_bytes ? tab_at + tab_bytes : dev_bytes;
     hipError_t e = hipMalloc(&m->alloc, m->bytes);
     if (e != hipSuccess) {
         free(m);
-        return fail("%s: hipMalloc(%zu) failed: %s", who, dev_bytes, hipGetErrorString(e));
+        return fail("%s: hipMalloc(%zu) failed: %s", who, m->bytes, hipGetErrorString(e));
     }
     uint8_t *base = (uint8_t *)m->alloc;
     m->m.qs = base;
+    m->m.tab = tab_bytes ? base + tab_at : nullptr;
     m->m.d = type == HQ_GGML_Q8_0 ? (const uint16_t *)(base + qbytes) : nullptr;
     std::lock_guard<std::mutex> lk(u->mu);
     auto fail_free = [&](hipError_t err) {
@@ -290,6 +293,7 @@ static int upload_rows(int type, uint32_t rows, uint32_t cols, F row_ptr, int de
         if (e != hipSuccess) return fail_free(e);
         used[b] = true;
     }
+    if (tab_bytes && (e = hq_launch_q4k_tables(&m->m, base + tab_at, u->st)) != hipSuccess) return fail_free(e);
     if ((e = hipStreamSynchronize(u->st)) != hipSuccess) return fail_free(e);
     *out = m;
     return 0;
@@ -348,8 +352,9 @@ extern "C" int hq_mat_download(const hq_mat *m, void *out, size_t nbytes) {
     const size_t rb = (size_t)(m->m.cols / block_values(m->m.type)) * block_bytes(m->m.type), total = rb * m->m.rows;
     if (nbytes < total) return fail("hq_mat_download: need %zu bytes, got %zu", total, nbytes);
     if (use_device(m->device)) return -1;
-    std::vector<uint8_t> host(m->bytes);
-    HIPCK(hipMemcpy(host.data(), m->alloc, m->bytes, hipMemcpyDeviceToHost));
+    const size_t copy = m->m.type == HQ_GGML_Q4_K ? total : m->bytes;  // (not the Q4_K column tables)
+    std::vector<uint8_t> host(copy);
+    HIPCK(hipMemcpy(host.data(), m->alloc, copy, hipMemcpyDeviceToHost));
     uint8_t *dst = (uint8_t *)out;
     if (m->m.type == HQ_GGML_Q4_K) {
         memcpy(dst, host.data(), total);

@@ -1,0 +1,477 @@
+// hq_gemm_wr.hip - Q4_K GEMM for prefill shapes of one tile round (M = 128 .. ~512 at N ~ 10k) on
+// gfx950: 128 x 64NB output tiles; 4 MFMA waves that each own all 128 rows and 16NB columns, and 4
+// loader waves.
+//
+// C[M,N] (+)= A[M,K] . W^T with A fp16 and W GGUF Q4_K super-blocks resident in HBM (reference
+// arithmetic: cleanroom-transformer/src/ggml_quant.h:51-59, :135-150; matmul src/cpu_backend.c:38-54).
+//
+// Why this shape. Measured on gfx950 (one CU): an MFMA 16x16x32 takes 16 clocks and two independent
+// VALU instructions issued behind it in the same wave cost nothing (each one more costs ~4 clocks);
+// LDS reads run at 256 bytes per clock but ds_write_b128 at ~64. A Q4_K weight fragment (16 columns
+// x 32 k) costs 10 VALU instructions to decode, so it has to feed 8 row blocks (128 rows) to stay
+// inside that budget: each MFMA wave decodes, in registers, only its own 16NB columns and uses them
+// against all 128 rows of the tile (no decode is repeated, no decoded weight goes through LDS). The
+// activation tile is the only operand shared through LDS. An LDS DMA instruction holds its wave until
+// the address unit takes it (~20-25 clocks per 1 KB per CU, ~30 per stage here), which would idle the
+// MFMA pipe of a multiplying wave: the loads are issued by the loader waves, one beside each MFMA wave
+// on its SIMD. M = 512, N = 9728: 4 x 51 tiles of 128 x 192 on 256 CUs, one round.
+//
+// Pipeline. K is walked in stages of 64 (one 32-byte quant group p of a super-block u). Per stage an
+// MFMA wave runs 16 groups of NB MFMAs (group g: k-step g / 8, row block g % 8), each closed by a
+// scheduling barrier, and spreads the rest of its work over the groups so that it issues while the
+// MFMAs run: the activation read of the group three ahead, half a weight fragment's decode per group
+// (k-step 1 in groups 0 .. 5, the next stage's k-step 0 in groups 9 .. 14; each pinned to its group,
+// the loop body has no branches for the compiler to sink work across). The 8 waves meet at one
+// s_barrier per stage, in group 6; after it the loaders fill ring slot s + 2 (4 stages of activations
+// and quants; each load has two stages to land) and the MFMA waves read the next stage's quant words.
+//
+// Arithmetic: as hq_gemm_ws.hip and hq_gemm_bt.hip (accumulators in units of c_u = d_u, weight operand
+// the exact integer s*q). The min term of super-block u (bf16 hi/lo S x Bmin, x = -dmin*m/c_u) is added
+// in its own units during stage p = 1, each row block four groups away from its own MFMAs; the row
+// blocks are rescaled by c_u / c_{u+1} right after their last MFMA of super-block u; at the end by
+// c_{U-1}. The per-column tables (scale words, Bmin, R, CL) depend on the weights only: they are
+// computed once at upload (k_q4k_tables) and moved into LDS with the loads.
+//
+// LDS (108 KB for NB = 3): A [4][128 rows][64 k] fp16 (16-byte slot p of row r at p ^ ((r >> 1) & 7));
+// quant groups [4][4 waves][16NB columns][32 B] (the two halves of column c swapped where
+// (c >> 3) & 1); S [2][128][16] bf16; per wave Bmin [16NB][32 B] and records [2][16NB][16 B]. The
+// output goes from the accumulators straight to C.
+#include "hq_device.h"
+#include "hq_kernels.h"
+
+namespace {
+constexpr int WR_BM = 128, WR_KS = 64, WR_NT = 512, WR_RING = 4;
+#ifndef WR_AD
+#define WR_AD 3  // activation operand read-ahead in groups (< WR_AF; reads of the next stage start after its barrier)
+#endif
+constexpr int WR_AF = 4;
+static_assert(WR_AD < WR_AF && 16 - WR_AD > 6 && 16 % WR_AF == 0, "activation read-ahead");
+
+struct WrArgs {
+    const uint8_t *W;  // Q4_K super-blocks, row n at n * row_bytes
+    uint32_t row_bytes;
+    const uint16_t *A;  // fp16 [M][K]
+    const uint16_t *S;  // activation sub-block sums [M][K/256][16] (k_asums, bf16 hi/lo)
+    const uint8_t *tab; // per-super-block column tables (hq_launch_q4k_tables)
+    int M, N, K;
+    void *C;
+    int c_f32, accumulate;
+    int mt, nt;
+};
+
+template <int NB>
+struct WrLds {
+    static constexpr int BN = 64 * NB, WC = 16 * NB;
+    static constexpr int A = 0, A_BYTES = WR_BM * WR_KS * 2;            // per ring slot
+    static constexpr int Q = WR_RING * A_BYTES, Q_WAVE = WC * 32;        // per wave and ring slot
+    static constexpr int Q_BYTES = 4 * Q_WAVE;                           // per ring slot
+    static constexpr int S = Q + WR_RING * Q_BYTES, S_BYTES = WR_BM * 32;  // per parity
+    static constexpr int T = S + 2 * S_BYTES;                            // per-wave tables
+    static constexpr int T_BM = 0, T_REC = WC * 32;                      // REC: 2 parities
+    static constexpr int T_WAVE = T_REC + 2 * WC * 16;
+    static constexpr int MAIN = T + 4 * T_WAVE;
+    static constexpr int TOTAL = MAIN;
+    static_assert(TOTAL <= 160 * 1024, "LDS budget");
+};
+
+DEV void wr_barrier() { asm volatile("s_barrier" ::: "memory"); }
+// keeps a computed operand in the group that computes it (the compiler would otherwise sink the work
+// to the operand's first use)
+DEV void wr_pin(h8 &x) { asm volatile("" : "+v"(x)); }
+// half hf of a weight operand (decode8m's values 4hf .. 4hf + 3, from quant word hf), in place
+DEV void wr_dec_half(h8 &b, u2v q, int hf, uint32_t mask, h2 mul, h2 add) {
+    const uint32_t w = (hf ? q.y : q.x) & mask;
+    const h2 v0 = __builtin_elementwise_fma(as_h2(perm_lo(w)), mul, add);
+    const h2 v1 = __builtin_elementwise_fma(as_h2(perm_hi(w)), mul, add);
+    b[4 * hf] = v0.x, b[4 * hf + 1] = v0.y, b[4 * hf + 2] = v1.x, b[4 * hf + 3] = v1.y;
+    wr_pin(b);
+}
+
+
+template <int NB>
+__global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
+    using L = WrLds<NB>;
+    constexpr int BN = L::BN, WC = L::WC, QI = (WC + 31) / 32;  // quant DMA instructions per wave
+    __shared__ __attribute__((aligned(256))) char lds[L::TOTAL];
+    // tile: XCD x = b % 8 takes N-tiles x, x + 8, ...; its slots run over the M-tiles of one N-tile
+    // first (the weight slab is then fetched once per XCD)
+    const int b = blockIdx.x, x = b & 7, j8 = b >> 3;
+    const int nt_i = x + 8 * (j8 / g.mt), mt_i = j8 % g.mt;
+    if (nt_i >= g.nt) return;
+    const int m0 = mt_i * WR_BM, n0 = nt_i * BN;
+    const int M = g.M, N = g.N, K = g.K, U = K / 256, S2 = 4 * U;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, ln = lane & 15, lg = lane >> 4;
+    // roles: waves 0-3 multiply (wave w: columns 16NB w .. of the tile, all 128 rows); waves 4-7 load
+    // (wave 4 + w: every load for MFMA wave w's columns and tables and a quarter of the shared
+    // activation and S tiles)
+    const int role = wave >> 2, w4 = wave & 3;
+    const rsrc_t ra = make_rsrc(g.A, (uint32_t)((size_t)M * K * 2));
+    const rsrc_t rw = make_rsrc(g.W, (uint32_t)((size_t)N * g.row_bytes));
+    const rsrc_t rs = make_rsrc(g.S, (uint32_t)((size_t)M * U * 32));
+    const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
+    const int nw = n0 + WC * w4;  // first column of MFMA wave w4
+
+    // ---- loads. Activation DMA of stage s into ring slot buf: instruction q (0..3) of wave w fills rows
+    // 8(4w + q) .. + 8; lane i: row r = 8(4w + q) + i/8, LDS slot i % 8, global chunk
+    // (i % 8) ^ ((r >> 1) & 7) (the q = 0 chunk ^ 4 for odd q)
+    const int a_row0 = 32 * w4 + (lane >> 3);
+    const uint32_t a_ch = (uint32_t)((lane & 7) ^ ((a_row0 >> 1) & 7));
+    const uint32_t a_rowoff = (uint32_t)(m0 + a_row0) * (uint32_t)K * 2u;
+    const uint32_t a_voff0 = a_rowoff + 16u * a_ch, a_voff1 = a_rowoff + 16u * (a_ch ^ 4u);
+    auto dma_a1 = [&](int s, int buf, int q) {
+        dma16_so(ra, lds0 + (uint32_t)(L::A + buf * L::A_BYTES + w4 * 4096 + q * 1024), q & 1 ? a_voff1 : a_voff0,
+                 (uint32_t)(q * 8 * K * 2 + s * WR_KS * 2));
+    };
+    // quant DMA of stage s (the wave's own columns): instruction k, lane i: column c = 32k + i/2, LDS
+    // half i % 2 of the column's 32 bytes, holding the group's half (i % 2) ^ ((c >> 3) & 1)
+    uint32_t q_voff[QI];
+#pragma unroll
+    for (int k = 0; k < QI; k++) {
+        const int c = 32 * k + (lane >> 1), cc = c < WC ? c : WC - 1;
+        q_voff[k] = (uint32_t)(nw + cc) * g.row_bytes + 16u * (uint32_t)((lane & 1) ^ ((c >> 3) & 1));
+    }
+    auto dma_q1 = [&](int s, int buf, int k) {
+        const uint32_t dst = lds0 + (uint32_t)(L::Q + buf * L::Q_BYTES + w4 * L::Q_WAVE + k * 1024);
+        const uint32_t so = (uint32_t)((s >> 2) * 144 + 16 + 32 * (s & 3));
+        if (32 * k + 32 <= WC || lane < 2 * (WC - 32 * k)) dma16_so(rw, dst, q_voff[k], so);
+    };
+    // S of super-block u into parity slot u & 1: wave w moves rows 32w .. + 32; lane i: row 32w + i/2
+    const uint32_t s_voff = (uint32_t)(m0 + 32 * w4 + (lane >> 1)) * (uint32_t)U * 32u + 16u * (uint32_t)(lane & 1);
+    auto dma_s = [&](int u) {
+        dma16_so(rs, lds0 + (uint32_t)(L::S + (u & 1) * L::S_BYTES + w4 * 1024), s_voff, (uint32_t)(u * 32));
+    };
+    // tables of super-block u for MFMA wave w4's columns into its table area: Bmin (1536 bytes, two
+    // instructions) and the records (768 bytes, lanes < WC) in parity u & 1
+    const rsrc_t rt = make_rsrc(g.tab, (uint32_t)((size_t)N * U * HQ_Q4K_TAB_BYTES));
+    const uint32_t tw = lds0 + (uint32_t)(L::T + w4 * L::T_WAVE);
+    auto dma_t = [&](int u) {
+        const uint32_t so = (uint32_t)u * (uint32_t)N * HQ_Q4K_TAB_BYTES;
+        dma16_so(rt, tw + L::T_BM, 16u * (uint32_t)lane, so + (uint32_t)nw * 32u);
+        if (lane < WC * 2 - 64) dma16_so(rt, tw + L::T_BM + 1024, 16u * (uint32_t)lane, so + (uint32_t)nw * 32u + 1024u);
+        if (lane < WC)
+            dma16_so(rt, tw + L::T_REC + (uint32_t)((u & 1) * WC * 16), 16u * (uint32_t)lane,
+                     so + (uint32_t)N * 32u + (uint32_t)nw * 16u);
+    };
+
+    // ---- operand addresses. Activation fragment of row block i, k-step f, ring slot buf: lane (ln, lg)
+    // reads row 16i + ln, slot (4f + lg) ^ ((ln >> 1) & 7)
+    const uint32_t a_lane = lds0 + (uint32_t)(L::A + ln * 128) + 16u * ((uint32_t)lg ^ (uint32_t)((ln >> 1) & 7));
+    auto rd = [&](int buf, int gg) {
+        return *(const __attribute__((address_space(3))) h8 *)(uintptr_t)(((a_lane ^ (64u * (uint32_t)(gg >> 3))) +
+                                                                           (uint32_t)(buf * L::A_BYTES)) +
+                                                                          (uint32_t)((gg & 7) * 16 * 128));
+    };
+    // quant words of column block j (column 16j + ln of the wave, bytes 8lg .. + 7 of the group)
+    const uint32_t q_lane = lds0 + (uint32_t)(L::Q + w4 * L::Q_WAVE + ln * 32 + 16 * ((lg >> 1) ^ ((ln >> 3) & 1)) + 8 * (lg & 1));
+    auto rdq = [&](int buf, int j) {
+        return *(const __attribute__((address_space(3))) u2v *)(uintptr_t)(q_lane + (uint32_t)(buf * L::Q_BYTES + j * 16 * 32));
+    };
+    // scale word p / 2 of column block j in super-block v, shifted to sub-blocks 2p, 2p + 1 in its low bytes
+    auto rdsw = [&](int p, int v, int j) {
+        return *(const __attribute__((address_space(3))) uint32_t *)(uintptr_t)(tw + (uint32_t)(L::T_REC + ((v & 1) * WC + 16 * j + ln) * 16 +
+                                                                                                 (p >> 1) * 4)) >>
+               ((p & 1) * 16);
+    };
+    const uint32_t s_lane = lds0 + (uint32_t)(L::S + ln * 32 + 16 * (lg & 1));
+    auto rds = [&](int par, int i) {
+        return *(const __attribute__((address_space(3))) h8 *)(uintptr_t)(s_lane + (uint32_t)(par * L::S_BYTES + i * 16 * 32));
+    };
+    auto rdbm = [&](int j) {
+        return *(const __attribute__((address_space(3))) h8 *)(uintptr_t)(tw + (uint32_t)(L::T_BM + (16 * j + ln) * 32 + 16 * (lg >> 1)));
+    };
+    // field f (2: R, 3: CL) of the records of columns 16j + 4lg .. + 3 of super-block v
+    auto rdr = [&](int j, int v, int f) {
+        f4 r;
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            r[c] = *(const __attribute__((address_space(3))) float *)(uintptr_t)(tw + (uint32_t)(L::T_REC + ((v & 1) * WC + 16 * j + 4 * lg + c) * 16 + 4 * f));
+        return r;
+    };
+
+    f4 acc[8][NB];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int j = 0; j < NB; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+    // decode scales of stage p: (s_lo, s_hi) of sub-blocks 2p, 2p + 1 -> multipliers and addends for
+    // the low (x) and high (y) nibbles
+    auto scales = [&](uint32_t w, h2 &mu, h2 &ad) {
+        const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const h2 sp = as_h2(__builtin_amdgcn_perm(0x64646464u, w, 0x04010400u)) - k1024;
+        mu = sp * h2{(_Float16)1.0f, (_Float16)0.0625f};
+        ad = sp * h2{(_Float16)-1024.0f, (_Float16)-64.0f};
+    };
+
+    const int u_last = U - 1;
+    if (role == 1) {
+        // ------------------------------------------------------------------------------ loaders
+        // prologue: stage 0 of activations and quants, S and tables of unit 0, then stage 1, which
+        // (as in every loader stage) is still in flight at the barrier
+#pragma unroll
+        for (int q = 0; q < 4; q++) dma_a1(0, 0, q);
+#pragma unroll
+        for (int k = 0; k < QI; k++) dma_q1(0, 0, k);
+        dma_s(0);
+        dma_t(0);
+        {
+            const int s1 = S2 > 1 ? 1 : 0;
+#pragma unroll
+            for (int q = 0; q < 4; q++) dma_a1(s1, 1, q);
+#pragma unroll
+            for (int k = 0; k < QI; k++) dma_q1(s1, 1, k);
+        }
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 + QI) : "memory");
+        wr_barrier();
+        // loader stage s = 4u + p runs between the MFMA waves' barriers of stages s - 1 and s (the
+        // prologue's barrier counts as stage -1's), while they finish stage s - 1 and start stage s:
+        // the loads of stage s + 2 (ring slot (s + 2) % 4, last read in stage s - 2), at p = 0 S of unit
+        // u + 1, at p = 2 unit u + 1's tables (Bmin of unit u was read at p = 0, the records of unit
+        // u - 1 are done with); then wait for everything but this stage's loads (stage s + 1's land:
+        // each load has two stages) and meet the MFMA waves at their barrier. Past the last unit the
+        // S and table loads repeat it (same bytes).
+        for (int u = 0; u < U; u++) {
+            const int u_next = u < u_last ? u + 1 : u_last;
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                const int s = 4 * u + p, ld = (s + 2) & 3, s_src = s + 2 < S2 ? s + 2 : S2 - 1;
+#pragma unroll
+                for (int q = 0; q < 4; q++) dma_a1(s_src, ld, q);
+#pragma unroll
+                for (int k = 0; k < QI; k++) dma_q1(s_src, ld, k);
+                if (p == 0) dma_s(u_next);
+                if (p == 2) dma_t(u_next);
+                if (p == 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 + QI + 1) : "memory");
+                else if (p == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 + QI + 3) : "memory");
+                else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 + QI) : "memory");
+                wr_barrier();
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last (clamped, unused) loads
+        return;
+    }
+
+    // ---------------------------------------------------------------------------------- MFMA waves
+    wr_barrier();  // the loaders' prologue
+    // stage 0's first operands and k-step 0 weights
+    // af: ring of WR_AF (a stage's 16 groups wrap it exactly), each read WR_AD groups ahead
+    h8 af[WR_AF], b0[NB], b1[NB];
+    u2v qc[NB];
+    h2 muh[NB], adh[NB];
+#pragma unroll
+    for (int k = 0; k < WR_AD; k++) af[k] = rd(0, k);
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+        qc[j] = rdq(0, j);
+        h2 mu, ad;
+        scales(rdsw(0, 0, j), mu, ad);
+        muh[j] = h2{mu.y, mu.y}, adh[j] = h2{ad.y, ad.y};
+        b0[j] = decode8<false>(qc[j], h2{mu.x, mu.x}, h2{ad.x, ad.x});
+    }
+    h8 bm[NB], sa[3];
+    f4 r[NB];
+#pragma unroll
+    for (int j = 0; j < NB; j++) bm[j] = rdbm(j), r[j] = f4{1.f, 1.f, 1.f, 1.f};
+
+    // main loop: one super-block (4 stages) per iteration; stage s = 4u + p, ring slot s % 4. The
+    // super-block's min k-step (S x Bmin in units of c_u, tables read at p = 0) runs at p = 1: group g
+    // < 8 adds it to block row (g + 4) % 8, four groups away from that row's own MFMAs on either side.
+    // Rescale to the next super-block's units: block row i two groups after its last MFMA of the
+    // super-block (group 10 + i at p = 3; rows 6 and 7 in the next super-block's groups 0 and 1, ahead
+    // of their first MFMAs there).
+    uint32_t swn[NB];  // the next stage's scale words
+    h2 mul0[NB], add0[NB];  // and its k-step 0 multipliers and addends
+    for (int u = 0; u < U; u++) {
+        const bool more = u + 1 < U;
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const int s = 4 * u + p, cur = s & 3, nxt = (s + 1) & 3;
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int gg = 0; gg < 16; gg++) {
+                // the activation operand WR_AD groups ahead (the next stage's first ones from group
+                // 16 - WR_AD, after the barrier)
+                if (gg + WR_AD < 16) af[(gg + WR_AD) % WR_AF] = rd(cur, gg + WR_AD);
+                else af[(gg + WR_AD) % WR_AF] = rd(nxt, gg + WR_AD - 16);
+#pragma unroll
+                for (int j = 0; j < NB; j++) acc[gg & 7][j] = mfma(gg < 8 ? b0[j] : b1[j], af[gg % WR_AF], acc[gg & 7][j]);
+                if (p == 1 && gg < 8) {
+                    const int i = (gg + 4) & 7;
+#pragma unroll
+                    for (int j = 0; j < NB; j++) acc[i][j] = mfma_bf16(bm[j], sa[gg % 3], acc[i][j]);
+                }
+                // sub-block sums of the row the min k-step reaches three groups later (p = 1, group g
+                // < 8: row (g + 4) % 8, read from group 13 of p = 0, after this group's use of the slot)
+                if ((p == 0 && gg >= 13) || (p == 1 && gg < 5)) {
+                    const int g = p == 0 ? gg - 13 : gg + 3;
+                    sa[g % 3] = rds(u & 1, (g + 4) & 7);
+                }
+                // this stage's k-step 1 weights, half a column block per group
+                if (gg < 2 * NB) wr_dec_half(b1[gg / 2], qc[gg / 2], gg & 1, 0xf0f0f0f0u, muh[gg / 2], adh[gg / 2]);
+                if (p == 3 && gg >= 10) {
+                    const int i = gg - 10;
+#pragma unroll
+                    for (int j = 0; j < NB; j++) acc[i][j] *= r[j];
+                }
+                if (p == 0 && gg < 2)
+#pragma unroll
+                    for (int j = 0; j < NB; j++) acc[6 + gg][j] *= r[j];
+                if (gg == 6) {
+                    // the loaders' wait before the barrier lands the next stage's activations and
+                    // quants; after it they refill the slot of stage s - 1, whose reads have all been
+                    // consumed (this stage's quants are decoded, so qc is free)
+                    wr_barrier();
+                    const int pn = (p + 1) & 3, un = p == 3 ? u + 1 : u;
+#pragma unroll
+                    for (int j = 0; j < NB; j++) qc[j] = rdq(nxt, j), swn[j] = rdsw(pn, un, j);
+                    // this super-block's Bmin, before the loaders rewrite the table at p = 2; the
+                    // next one's R (its records land by this barrier at p = 3)
+                    if (p == 0)
+#pragma unroll
+                        for (int j = 0; j < NB; j++) bm[j] = rdbm(j);
+                    if (p == 3)
+#pragma unroll
+                        for (int j = 0; j < NB; j++) {
+                            const f4 rn = rdr(j, u + 1, 2);
+#pragma unroll
+                            for (int c = 0; c < 4; c++) r[j][c] = more ? rn[c] : 1.0f;
+                        }
+                }
+                // the next stage's scales and k-step 0 weights (b0 is free after group 7), half a
+                // column block per group
+                if (gg >= 9 && gg < 9 + 2 * NB) {
+                    const int j = (gg - 9) / 2, hf = (gg - 9) & 1;
+                    if (hf == 0) {
+                        h2 mu, ad;
+                        scales(swn[j], mu, ad);
+                        muh[j] = h2{mu.y, mu.y}, adh[j] = h2{ad.y, ad.y};
+                        mul0[j] = h2{mu.x, mu.x}, add0[j] = h2{ad.x, ad.x};
+                    }
+                    wr_dec_half(b0[j], qc[j], hf, 0x0f0f0f0fu, mul0[j], add0[j]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+    // ---- output: back to true units (the last super-block's c), then straight from the accumulators:
+    // lane (ln, lg) of block (i, j) holds row 16i + ln, columns 16j + 4lg .. + 3 of the wave's
+    // columns (one 16-byte fp32 or 8-byte fp16 store; element by element at the matrix edge or where
+    // N % 4 or C's alignment does not allow it)
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+        const f4 cl = rdr(j, U - 1, 3);
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[i][j] *= cl;
+    }
+    const bool vec = (N & 3) == 0 && ((uintptr_t)g.C & (g.c_f32 ? 15u : 7u)) == 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int m = m0 + 16 * i + ln;
+        if (m >= M) break;
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            const int n = nw + 16 * j + 4 * lg;
+            if (n >= N) continue;
+            const size_t idx = (size_t)m * N + n;
+            f4 v = acc[i][j];
+            if (vec) {
+                if (g.c_f32) {
+                    f4 *q = (f4 *)((float *)g.C + idx);
+                    *q = g.accumulate ? *q + v : v;
+                } else {
+                    h4 *q = (h4 *)((_Float16 *)g.C + idx);
+                    if (g.accumulate) {
+                        const h4 o = *q;
+                        v += f4{(float)o[0], (float)o[1], (float)o[2], (float)o[3]};
+                    }
+                    *q = h4{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    if (n + e >= N) break;
+                    if (g.c_f32) {
+                        float *q = (float *)g.C + idx + e;
+                        *q = g.accumulate ? *q + v[e] : v[e];
+                    } else {
+                        _Float16 *q = (_Float16 *)g.C + idx + e;
+                        *q = (_Float16)(g.accumulate ? (float)*q + v[e] : v[e]);
+                    }
+                }
+            }
+        }
+    }
+}
+}  // namespace
+
+// Per-column tables of every super-block of a Q4_K matrix (one thread per row, super-blocks in order):
+// for super-block v, Bmin [rows][32 B] = bf16 hi[8], lo[8] of x_i = -dmin * m_i / c_v at v * rows * 48,
+// then records [rows][16 B] = scale words sw0, sw1 (zero where d = 0), R = c_{v-1} / c_v (c_{-1} = 1),
+// CL = c_v; c_v = d_v, or 1 where d_v = 0 (-dmin * m_i is exact in fp32).
+__global__ void __launch_bounds__(256) k_q4k_tables(const uint8_t *W, uint32_t rows, uint32_t nb, uint32_t row_bytes,
+                                                    uint8_t *tab) {
+    const uint32_t n = blockIdx.x * 256u + threadIdx.x;
+    if (n >= rows) return;
+    float c_prev = 1.0f;
+    for (uint32_t v = 0; v < nb; v++) {
+        const u4v hm = *(const u4v *)(W + (size_t)n * row_bytes + (size_t)v * 144);
+        uint32_t sw0, sw1, mw0, mw1;
+        q4k_scale_words(hm.y, hm.z, hm.w, sw0, sw1, mw0, mw1);
+        const uint32_t nz = (hm.x & 0x7fffu) ? 0xffffffffu : 0u;
+        const float d = h2f((uint16_t)hm.x), dmin = h2f((uint16_t)(hm.x >> 16));
+        const float c = d != 0.0f ? d : 1.0f, inv = 1.0f / c;
+        uint32_t bh[4], bl[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint32_t w = q < 2 ? mw0 : mw1;
+            const float x0 = (-dmin * (float)byte_of(w, 2 * (q & 1))) * inv;
+            const float x1 = (-dmin * (float)byte_of(w, 2 * (q & 1) + 1)) * inv;
+            const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
+            const __bf16 l0 = (__bf16)(x0 - (float)h0), l1 = (__bf16)(x1 - (float)h1);
+            bh[q] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+            bl[q] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+        }
+        uint8_t *t = tab + (size_t)v * rows * HQ_Q4K_TAB_BYTES;
+        *(u4v *)(t + (size_t)n * 32) = u4v{bh[0], bh[1], bh[2], bh[3]};
+        *(u4v *)(t + (size_t)n * 32 + 16) = u4v{bl[0], bl[1], bl[2], bl[3]};
+        *(u4v *)(t + (size_t)rows * 32 + (size_t)n * 16) =
+            u4v{sw0 & nz, sw1 & nz, __builtin_bit_cast(uint32_t, c_prev / c), __builtin_bit_cast(uint32_t, c)};
+        c_prev = c;
+    }
+}
+
+hipError_t hq_launch_q4k_tables(const hq_dev_mat *W, uint8_t *tab, hipStream_t st) {
+    if (W->type != HQ_TYPE_Q4_K || W->cols % 256) return hipErrorInvalidValue;
+    k_q4k_tables<<<(W->rows + 255) / 256, 256, 0, st>>>(W->qs, W->rows, W->cols / 256, (uint32_t)W->row_bytes, tab);
+    return hipGetLastError();
+}
+
+// tiles of 128 x 64nb: the number of tile rounds on n_cu CUs and the fraction of CU time they fill
+int hq_wr_choose(int M, int N, int n_cu, float *eff) {
+    const int mt = (M + WR_BM - 1) / WR_BM, nb = 3;
+    const int nt = (N + 64 * nb - 1) / (64 * nb);
+    const long tiles = (long)mt * nt, rounds = (tiles + n_cu - 1) / n_cu;
+    if (eff) *eff = (float)((double)M * N / ((double)rounds * n_cu * WR_BM * 64.0 * nb));
+    return nb;
+}
+
+// every byte offset of the kernel (tile rows and columns past the matrix included) fits 32 bits
+int hq_wr_fits(const hq_dev_mat *W, int M) {
+    const size_t lim = (size_t)1 << 32, mr = (size_t)M + WR_BM;
+    return W->type == HQ_TYPE_Q4_K && W->cols % 256 == 0 && M >= 1 && mr * W->cols * 2 < lim &&
+           mr * (W->cols / 256) * 32 < lim && ((size_t)W->rows + 64 * 3) * W->row_bytes < lim;
+}
+
+hipError_t hq_launch_gemm_wr(const hq_dev_mat *W, const uint16_t *A, const uint16_t *S, int M, void *C, int c_f32,
+                             int accumulate, hipStream_t st) {
+    if (!hq_wr_fits(W, M) || !W->tab) return hipErrorInvalidValue;  // (every uploaded Q4_K matrix has its tables)
+    constexpr int NB = 3;
+    WrArgs g;
+    g.W = W->qs, g.row_bytes = (uint32_t)W->row_bytes, g.A = A, g.S = S, g.tab = W->tab;
+    g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;
+    g.mt = (M + WR_BM - 1) / WR_BM;
+    g.nt = (g.N + 64 * NB - 1) / (64 * NB);
+    if (c_f32 != 0 && c_f32 != 1) return hipErrorInvalidValue;  // (fp32 or fp16 C)
+    const unsigned grid = (unsigned)(8 * ((g.nt + 7) / 8) * g.mt);
+    k_gemm_q4_k_wr<NB><<<grid, WR_NT, 0, st>>>(g);
+    return hipGetLastError();
+}

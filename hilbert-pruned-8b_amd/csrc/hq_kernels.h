@@ -16,7 +16,12 @@ typedef struct {
     const uint16_t *d;   // Q8_0: fp16 scale plane [rows][ldd]; Q4_K: unused
     int ldd;             // Q8_0 scale-plane row stride in halves (cols/32 rounded up to 8)
     size_t row_bytes;    // Q8_0 / Q4_K: GGUF bytes per row; Q6_K: device bytes per row (224 per super-block)
+    const uint8_t *tab;  // Q4_K: per-super-block column tables of the GEMM kernels (hq_launch_q4k_tables)
 } hq_dev_mat;
+
+// Q4_K column tables: HQ_Q4K_TAB_BYTES per row and super-block (Bmin hi / lo, scale words, R, CL)
+#define HQ_Q4K_TAB_BYTES 48u
+hipError_t hq_launch_q4k_tables(const hq_dev_mat *W, uint8_t *tab, hipStream_t st);
 
 // The device view and device of a resident matrix (hq_api.hip), for the library's own host code.
 struct hq_mat;
@@ -68,6 +73,13 @@ hipError_t hq_launch_gemm_ws(const hq_dev_mat *W, const uint16_t *A, const uint1
 // k_asums<true> output for A); whether a shape's byte offsets suit it, and the launch.
 int hq_bt_fits(const hq_dev_mat *W, int M);
 hipError_t hq_launch_gemm_bt(const hq_dev_mat *W, const uint16_t *A, const uint16_t *S, int M, void *C, int c_f32,
+                             int accumulate, hipStream_t st);
+// Prefill Q4_K GEMM of one tile round (hq_gemm_wr.hip): 128 x 192 tiles over the whole of K, 4 waves
+// that each decode their own 48 columns (S = k_asums<true> output for A); the tile width chooser,
+// whether a shape's byte offsets suit it, and the launch (c_f32 may be HQ_OUT_SWIGLU).
+int hq_wr_choose(int M, int N, int n_cu, float *eff);
+int hq_wr_fits(const hq_dev_mat *W, int M);
+hipError_t hq_launch_gemm_wr(const hq_dev_mat *W, const uint16_t *A, const uint16_t *S, int M, void *C, int c_f32,
                              int accumulate, hipStream_t st);
 // Mid-M Q4_K GEMM (hq_gemm_rb.hip): whether M, K suit it (33 <= M <= 64, K a multiple of 512,
 // 32-bit offsets), its workgroups per tile for a shape, and the launch (S = k_asums output for A in

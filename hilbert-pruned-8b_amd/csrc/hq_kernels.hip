@@ -1238,6 +1238,7 @@ struct GemmCfg {
     int rbm;        // Q4_K mid M: workgroups per tile of k_gemm_q4_k_rb (hq_gemm_rb.hip); 0: not used
     int rb8;        // Q8_0 M <= 64: workgroups per tile of k_gemm_q8_0_rb (hq_gemm_rb.hip); 0: not used
     bool bt;        // Q4_K large M: the 256 x 256 tile kernel k_gemm_q4_k_bt (hq_gemm_bt.hip)
+    bool wr;        // Q4_K, one round of full-K tiles: the 128 x 192 tile kernel k_gemm_q4_k_wr (hq_gemm_wr.hip)
 };
 
 // Q4_K with M > 64 runs the full-K tile kernel when its tiles fit in one round on the CUs and fill
@@ -1274,6 +1275,9 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
                 }
             }
     }
+    // Q4_K full-K tiles without a K split: the 128 x 192 tile kernel, whose waves decode their own
+    // columns (M = 512, N = 9728: 204 tiles)
+    c.wr = c.ws_nb && c.ws_parts == 1 && hq_wr_fits(W, M);
     // Q4_K where the Stream-K wide kernel would run: the 256 x 256 tile kernel when its rounds of
     // tiles fill at least 3/4 of the CU time (M = 16384, N = 9728: 2432 tiles in 9.5 rounds)
     c.bt = false;
@@ -1320,8 +1324,8 @@ void hq_gemm_tile_shape(int type, int M, int N, int K, int n_cu, int *rows, int 
     W.rows = (uint32_t)N;
     W.cols = (uint32_t)K;
     const GemmCfg c = gemm_cfg(&W, M, n_cu);
-    *rows = c.bt ? 256 : c.rbm ? 64 : c.rb8 ? (M <= 16 ? 16 : M <= 32 ? 32 : 64) : c.ws_nb || c.ws8_nb ? 128 : 16 * c.mb;
-    *cols = c.bt ? 256 : c.rbm || c.rb8 ? 64 : c.ws_nb ? 32 * c.ws_nb : c.ws8_nb ? 32 * c.ws8_nb : 16 * c.nb * c.waves;
+    *rows = c.bt ? 256 : c.wr ? 128 : c.rbm ? 64 : c.rb8 ? (M <= 16 ? 16 : M <= 32 ? 32 : 64) : c.ws_nb || c.ws8_nb ? 128 : 16 * c.mb;
+    *cols = c.bt ? 256 : c.wr ? 192 : c.rbm || c.rb8 ? 64 : c.ws_nb ? 32 * c.ws_nb : c.ws8_nb ? 32 * c.ws8_nb : 16 * c.nb * c.waves;
 }
 
 // Name of the kernel that does the work of an M x N x K hq_gemm call (the main kernel for GEMMs
@@ -1347,6 +1351,7 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
     if (c.rbm) snprintf(buf, n, "k_gemm_q4_k_rb<1, 4, 3, 2>");
     else if (c.rb8) snprintf(buf, n, "k_gemm_q8_0_rb<%d, 3, 2>", M <= 16 ? 1 : M <= 32 ? 2 : 4);
     else if (c.bt) snprintf(buf, n, "k_gemm_q4_k_bt");
+    else if (c.wr) snprintf(buf, n, "k_gemm_q4_k_wr<3>");
     else if (c.ws_nb) snprintf(buf, n, "k_gemm_q4_k_ws<%d>", c.ws_nb);
     else if (c.ws8_nb) snprintf(buf, n, "k_gemm_q8_0_ws<%d>", c.ws8_nb);
     else if (c.wide) snprintf(buf, n, "k_gemm_q4_k_w<%d>", c.mb);  // template argument: row blocks
@@ -1400,6 +1405,7 @@ hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, vo
     if (c.rbm) return hq_launch_gemm_rb(W, A, wk.sums, M, C, c_f32, accumulate, c.rbm, wk.partials, wk.counters, st);
     if (c.rb8) return hq_launch_gemm_rb8(W, A, M, C, c_f32, accumulate, c.rb8, wk.partials, wk.counters, st);
     if (c.bt) return hq_launch_gemm_bt(W, A, wk.sums, M, C, c_f32, accumulate, st);
+    if (c.wr) return hq_launch_gemm_wr(W, A, wk.sums, M, C, c_f32, accumulate, st);
     if (c.ws_nb)
         return hq_launch_gemm_ws(W, A, wk.sums, M, C, c_f32, accumulate, c.ws_nb, c.ws_parts, wk.partials, wk.counters, st);
     if (c.ws8_nb)

@@ -87,6 +87,8 @@ def test_gemm_workspace_bytes():
     pb, cb, sb, fits = hq.gemm_workspace_bytes(synth.Q4_K, 4096, 2560, 9728)
     assert (pb, cb, fits) == (2 * 256 * 128 * 256 * 4, 32 * 10 * 4, True)
     assert hq.gemm_workspace_bytes(synth.Q4_K, 4096, 9728, 2560) == (0, 0, 4096 * 10 * 32, True)
+    # the 128 x 192 loader-wave kernel (M = 512, N = 9728): one round of tiles, the sub-block sums only
+    assert hq.gemm_workspace_bytes(synth.Q4_K, 512, 9728, 2560) == (0, 0, 512 * 10 * 32, True)
     assert hq.gemm_workspace_bytes(synth.Q8_0, 512, 9728, 2560) == (0, 0, 0, True)
     assert hq.gemm_workspace_bytes(synth.Q4_K, 16384, 2560, 9216)[3]
     assert not hq.gemm_workspace_bytes(synth.Q4_K, 131072, 256, 9216)[3]  # 151 MB of sub-block sums
@@ -96,7 +98,7 @@ def test_gemm_workspace_bytes():
 
 def test_gemm_kernel_names():
     """hq_gemm_kernel names the kernel the launch plan picks (the names rocprofv3 lists)."""
-    cases = {(synth.Q4_K, 512, 9728, 2560): "k_gemm_q4_k_ws<5>", (synth.Q8_0, 512, 9728, 2560): "k_gemm_q8_0_ws<5>",
+    cases = {(synth.Q4_K, 512, 9728, 2560): "k_gemm_q4_k_wr<3>", (synth.Q4_K, 256, 9728, 2560): "k_gemm_q4_k_wr<3>", (synth.Q8_0, 512, 9728, 2560): "k_gemm_q8_0_ws<5>",
              (synth.Q8_0, 2048, 9728, 2560): "k_gemm_q8_0_ws<5>", (synth.Q8_0, 128, 9728, 2560): "k_gemm_q8_0_ws<2>",
              (synth.Q8_0, 65, 9728, 2560): "k_gemm_q8_0<8, 2>",
              (synth.Q4_K, 4096, 9728, 2560): "k_gemm_q4_k_bt", (synth.Q4_K, 16384, 2560, 9216): "k_gemm_q4_k_bt",
@@ -127,10 +129,10 @@ def test_gemm_tile_selection():
             assert r in (16, 32, 64, 128, 256)
             assert r >= min(M, 128)
             if gtype == synth.Q4_K and M > 64:
-                # Q4_K above M = 64: full-K tiles of 128 x 32NB when they fill the CUs, 256 x 256
-                # full-K tiles at large M when their rounds fill the CUs, else the 8-wave Stream-K
-                # kernel (128 x 256)
-                assert (r, c) in ((128, 256), (256, 256)) or (r == 128 and c in (64, 96, 128, 160))
+                # Q4_K above M = 64: full-K tiles of 128 x 32NB when they fill the CUs (128 x 192 with
+                # loader waves when one round of them does), 256 x 256 full-K tiles at large M when
+                # their rounds fill the CUs, else the 8-wave Stream-K kernel (128 x 256)
+                assert (r, c) in ((128, 256), (256, 256), (128, 192)) or (r == 128 and c in (64, 96, 128, 160))
             elif gtype == synth.Q8_0 and M > 64:
                 # Q8_0 above M = 64: full-K tiles of 128 x 32NB when they fill >= 50 % of the CU
                 # time (any number of rounds), else the narrow Stream-K kernel
@@ -148,10 +150,10 @@ def test_gemm_tile_selection():
     assert hq.gemm_tiles(synth.Q8_0, 512, 9728) == (128, 160)
     assert hq.gemm_tiles(synth.Q8_0, 2048, 9728) == (128, 160)
     assert hq.gemm_tiles(synth.Q4_K, 65, 9728) == (128, 256)
-    # full-K tiles: 4 x 61 tiles of 128 x 160 on 256 CUs; more tiles than CUs: Stream-K, or at large
+    # full-K tiles: 4 x 51 tiles of 128 x 192 on 256 CUs; more tiles than CUs: Stream-K, or at large
     # M the 256 x 256 tiles when their rounds fill >= 3/4 of the CU time (M = 4096: 608 tiles in 3
     # rounds; M = 2048: 304 tiles in 2 rounds, 59 %)
-    assert hq.gemm_tiles(synth.Q4_K, 512, 9728) == (128, 160)
+    assert hq.gemm_tiles(synth.Q4_K, 512, 9728) == (128, 192)
     assert hq.gemm_tiles(synth.Q4_K, 2048, 9728) == (128, 256)
     assert hq.gemm_tiles(synth.Q4_K, 4096, 9728) == (256, 256)
 

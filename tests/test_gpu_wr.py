@@ -1,0 +1,135 @@
+"""GPU parity of the one-round Q4_K tile kernel with loader waves (k_gemm_q4_k_wr<3>: 128 x 192
+tiles over the whole of K, 4 MFMA waves and 4 loader waves; the headline shape M = 512, N = 9728,
+K = 2560), through the C ABI, against the CPU oracle.
+
+Shapes: M = 350 (two whole 128-row tiles and a ragged one of 94 rows) and 512; N = 9672 (50 whole
+192-column tiles and a ragged one of 72: one MFMA wave's columns whole, the next one's half, two
+waves with none) or 9674 (N not a multiple of 4: the element-wise store path); K = 256 (one
+super-block: no rescale between super-blocks), 512, 1024 and 4096. The per-super-block column
+tables come from the upload (k_q4k_tables), so every test also checks them. Bars as in
+test_gpu_parity.py: rel-L2 <= 1e-3 and max-abs <= 2e-3 (Q4_K); against the float64 product,
+2^-13 |W| @ |a| per output.
+"""
+import numpy as np
+import pytest
+
+import synth
+from conftest import max_abs, rel_l2
+from test_gpu_configs import sample_cols, sample_rows
+from test_gpu_parity import f64_reference, special_q4_k_weights
+
+pytestmark = pytest.mark.gpu
+
+REL_L2, Q4K_MAX_ABS = 1e-3, 2e-3
+KERNEL = "k_gemm_q4_k_wr<3>"
+
+
+def say(*a):
+    print("[gpu]", *a, flush=True)
+
+
+def check(got, ref, what):
+    r, m = rel_l2(got, ref), max_abs(got, ref)
+    say(f"{what}: rel_l2 {r:.2e} max_abs {m:.2e}")
+    assert r <= REL_L2 and m <= Q4K_MAX_ABS, what
+
+
+def run(hqlib, blocks, a, N, K, what, c_f32=True, c_init=None):
+    M = a.shape[0]
+    name = hqlib.gemm_kernel(synth.Q4_K, M, N, K)
+    say(f"{what}: M={M} N={N} K={K} kernel={name}")
+    assert name == KERNEL
+    W = hqlib.Mat(blocks, synth.Q4_K, N, K)
+    got = hqlib.gemm_np(W, a, c_f32=c_f32, c_init=c_init)
+    W.free()
+    return got
+
+
+@pytest.mark.parametrize("N,K", [(9672, 512), (9674, 256)])
+def test_wr_special_scales_ragged(hqlib, oracle, N, K):
+    """Weights with zero, negative, subnormal and widely varying super-block scales (and one all-zero
+    row, one min-term-only row); ragged last row and column tiles; N % 4 != 0 at N = 9674."""
+    M = 350
+    blocks = special_q4_k_weights(171 + N, N, K)
+    a = synth.activations_f16(synth.Rng(172 + N), M, K)
+    got = run(hqlib, blocks, a, N, K, "wr special scales")
+    rows = sample_rows(M)
+    ref = oracle.matmul(blocks, synth.Q4_K, N, K, oracle.f16_to_f32(a[rows]))
+    check(got[rows], ref, f"wr special scales ({len(rows)} rows)")
+    r64, bound = f64_reference(oracle, blocks, synth.Q4_K, N, K, a[rows])
+    assert np.all(np.abs(got[rows] - r64) <= 2.0 ** -13 * bound)
+    assert np.all(got[:, N // 7] == 0.0)
+    assert np.all(np.isfinite(got))
+
+
+@pytest.mark.parametrize("N", [9728, 9674])
+def test_wr_accumulate_and_fp16_output(hqlib, oracle, N):
+    M, K = 512, 1024
+    blocks = synth.random_blocks(synth.Q4_K, synth.Rng(181 + N), N, K)
+    rng = synth.Rng(182)
+    a = synth.activations_f16(rng, M, K)
+    c0 = rng.normal(M * N).astype(np.float32).reshape(M, N)
+    rows = sample_rows(M)
+    plain = oracle.matmul(blocks, synth.Q4_K, N, K, oracle.f16_to_f32(a[rows]))
+    got = run(hqlib, blocks, a, N, K, "wr accumulate fp32", c_init=c0)
+    check(got[rows], plain + c0[rows], "wr accumulate fp32")
+    got16 = run(hqlib, blocks, a, N, K, "wr fp16 out", c_f32=False).view(np.float16).astype(np.float32)
+    assert np.all(np.abs(got16[rows] - plain) <= 1e-2 + np.abs(plain) * 2.0 ** -11)
+    c16 = synth.f16_bits(c0)
+    acc16 = run(hqlib, blocks, a, N, K, "wr accumulate fp16", c_f32=False, c_init=c16)
+    acc16 = acc16.view(np.float16).astype(np.float32)
+    want = plain + c16.view(np.float16).astype(np.float32)[rows]
+    assert np.all(np.abs(acc16[rows] - want) <= 1e-2 + np.abs(want) * 2.0 ** -11)
+
+
+def test_wr_positive_activations(hqlib, oracle):
+    """Non-negative activations up to ~16: the min term no longer cancels within a sub-block, so the
+    bf16 hi/lo split of the sub-block sums carries its largest error; scaling the activations by
+    2^6 scales every output by 2^6 bit for bit."""
+    M, N, K = 512, 9728, 1024
+    blocks = synth.random_blocks(synth.Q4_K, synth.Rng(191), N, K)
+    rng = synth.Rng(192)
+    a = synth.f16_bits(np.abs(rng.normal(M * K)) * 4).reshape(M, K)
+    got = run(hqlib, blocks, a, N, K, "wr positive activations")
+    a64 = synth.f16_bits(oracle.f16_to_f32(a) * 64).reshape(M, K)
+    got64 = run(hqlib, blocks, a64, N, K, "wr positive activations x 2^6")
+    assert np.array_equal(got64, got * 64)
+    rows = sample_rows(M)
+    ref = oracle.matmul(blocks, synth.Q4_K, N, K, oracle.f16_to_f32(a[rows]))
+    r = rel_l2(got[rows], ref)
+    say(f"wr positive activations: rel_l2 {r:.2e} max_abs {max_abs(got[rows], ref):.2e}")
+    assert r <= REL_L2
+    r64, bound = f64_reference(oracle, blocks, synth.Q4_K, N, K, a[rows])
+    assert np.all(np.abs(got[rows] - r64) <= 2.0 ** -13 * bound)
+
+
+def test_wr_long_k_repeatable(hqlib, oracle):
+    """K = 4096 (16 super-blocks, 64 stages through the 4-slot LDS ring and the double-buffered table
+    records): sampled parity, and three calls give the same bits (each output is one workgroup's
+    fixed sequence of MFMAs, so any difference would come from a race between the loader waves'
+    DMA and the MFMA waves' reads)."""
+    M, N, K = 350, 9672, 4096
+    blocks = synth.random_blocks(synth.Q4_K, synth.Rng(201), N, K)
+    a = synth.activations_f16(synth.Rng(202), M, K)
+    name = hqlib.gemm_kernel(synth.Q4_K, M, N, K)
+    say(f"wr long K: M={M} N={N} K={K} kernel={name}")
+    assert name == KERNEL
+    W = hqlib.Mat(blocks, synth.Q4_K, N, K)
+    got = [hqlib.gemm_np(W, a) for _ in range(3)]
+    W.free()
+    assert np.array_equal(got[0], got[1]) and np.array_equal(got[0], got[2])
+    rows = sample_rows(M, per_tile=4)
+    cols = sample_cols(N)
+    ref = oracle.matmul(np.ascontiguousarray(blocks[cols]), synth.Q4_K, len(cols), K, oracle.f16_to_f32(a[rows]))
+    check(got[0][np.ix_(rows, cols)], ref, f"wr long K ({len(rows)} rows x {len(cols)} columns)")
+
+
+def test_wr_download_round_trip(hqlib):
+    """The column tables sit after the blocks in the matrix's allocation: a download returns the
+    GGUF blocks alone, and the device bytes count both."""
+    N, K = 200, 512
+    blocks = synth.random_blocks(synth.Q4_K, synth.Rng(211), N, K)
+    W = hqlib.Mat(blocks, synth.Q4_K, N, K)
+    assert np.array_equal(W.download(), blocks)
+    assert W.device_bytes >= N * (K // 256) * (144 + 48)
+    W.free()
