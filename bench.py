@@ -5,21 +5,26 @@ Headline workload (the BASELINE north-star target): Q4_K GEMM, M = 512, K = 2560
 launch over one batch; weights rotate over enough distinct device copies (> 512 MB) that every
 launch streams its weights from HBM, not from the 256 MB Infinity Cache. The timed steps are one
 HIP-graph replay of exactly `steps` launches, timed with HIP events on the launch stream, after
-`warmup` eager launches and one untimed replay of the same graph.
+`warmup` eager launches and one untimed replay of the same graph (`ms_per_step`, `value`). The
+median over >= 50 launches is reported beside it (`us_median` of the headline and the roofline's
+`kernel_us`): five replays of 20-launch graphs that continue the rotation, a HIP event between
+replays, median of the five per-launch times.
 
 Also reported (key "sweep"): the config 2 / 3 M sweeps and the config 5 option readout, each as
 achieved TFLOP/s and GB/s of algorithmic bytes (W blocks once + A + C) and their roofline fractions,
 and config 4 (the 4B-class hybrid's 32-layer projection sequence at M = 16384, BASELINE's literal
 widths: each distinct projection shape timed, weighted by its count in the sequence).
 
-roofline: the headline GEMM's main kernel (k_gemm_q4_k_ws<5>: full-K 128 x 160 tiles), timed alone
-(hq_time_gemm_kernel; the Q4_K activation pre-pass runs once outside the timed graph) with HIP
-events on its stream; `traffic` is its HBM bytes per launch from the committed rocprofv3
+roofline: the headline GEMM's main kernel (k_gemm_q4_k_wr<3>: full-K 128 x 192 tiles), timed alone
+(hq_time_gemm_kernel; the Q4_K activation pre-pass runs once outside the timed graphs) with HIP
+events on its stream, median of five replays of 20 launches; `traffic` is its HBM bytes per launch from the committed rocprofv3
 FETCH_SIZE / WRITE_SIZE summary (calibrated against a device copy of known size), null when that
 summary was taken for a different kernel.
 
 cpu_baseline: the CPU oracle (a restatement of the reference's cpu_backend.c matmul, compiled with
-the reference's flags, OpenMP) on the headline GEMM, timed on this host's cores.
+the reference's flags, OpenMP with OMP_PROC_BIND=close and the box's OMP_NUM_THREADS) on the
+headline GEMM and on the three M = 1 GEMV shapes of the sweep, timed on this host's cores (median
+of 3 after 1 warm-up); `cores` is the physical cores of the process's CPU set.
 """
 import argparse
 import json
@@ -65,6 +70,9 @@ def read_traffic(name, kernel):
     return None
 
 
+MEDIAN_ITERS, MEDIAN_REPS = 20, 5  # the median figures: 5 graph replays of 20 launches
+
+
 def main_kernel_name(hq, gtype, M, N, K):
     """Name of the kernel hq_gemm dispatches for this shape (the main kernel where a pre-pass runs
     first), as rocprofv3 lists it."""
@@ -93,7 +101,9 @@ def bench_gemm(hq, synth, gtype, N, K, M, c_f32, steps, warmup, stream, eager_wa
     t0 = time.perf_counter()
     ms = hq.time_gemm(mats, A, M, C, c_f32, steps, 1, stream)
     wall = time.perf_counter() - t0
-    ms_kernel = hq.time_gemm_kernel(mats, A, M, C, c_f32, steps, 1, stream) if (kernel_time and M > 1) else None
+    ms_med = hq.time_gemm(mats, A, M, C, c_f32, MEDIAN_ITERS, MEDIAN_REPS, stream) if kernel_time else None
+    ms_kernel = (hq.time_gemm_kernel(mats, A, M, C, c_f32, MEDIAN_ITERS, MEDIAN_REPS, stream)
+                 if (kernel_time and M > 1) else None)
     for m in mats:
         m.free()
     A.free(), C.free()
@@ -101,6 +111,8 @@ def bench_gemm(hq, synth, gtype, N, K, M, c_f32, steps, warmup, stream, eager_wa
     nbytes = gemm_bytes(gtype, M, N, K, 4 if c_f32 else 2)
     r = dict(type="q8_0" if gtype == synth.Q8_0 else "q4_k", M=M, N=N, K=K, us=ms * 1e3,
              tflops=flop / (ms * 1e-3) / 1e12, gbs=nbytes / (ms * 1e-3) / 1e9, copies=copies, wall_s=wall)
+    if ms_med is not None:
+        r["us_median"] = ms_med * 1e3
     if ms_kernel is not None:
         r["kernel_us"] = ms_kernel * 1e3
         r["kernel_tflops"] = flop / (ms_kernel * 1e-3) / 1e12
@@ -191,24 +203,70 @@ def bench_upload(hq, synth, reps=3):
                 gbs=round(blocks.nbytes / t / 1e9, 2))
 
 
+def cpu_topology():
+    """(physical cores, logical CPUs) of the CPUs this process may run on, from /proc/cpuinfo's
+    (physical id, core id) per processor; the physical count is None where the host does not
+    expose distinct core ids."""
+    allowed = os.sched_getaffinity(0)
+    seen, proc, phys, core = set(), None, None, None
+    try:
+        for line in list(open("/proc/cpuinfo")) + [""]:
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "processor":
+                proc = int(v)
+            elif k == "physical id":
+                phys = v
+            elif k == "core id":
+                core = v
+            elif not k:
+                if proc is not None and proc in allowed and core is not None:
+                    seen.add((phys, core))
+                proc, phys, core = None, None, None
+    except OSError:
+        pass
+    n = len(seen)
+    return (n if n > 1 or len(allowed) == 1 else None), len(allowed)
+
+
+def cpu_time(O, blocks, gtype, N, K, x, reps=3):
+    """Median of `reps` timings after one warm-up of the oracle matmul (seconds)."""
+    y = np.zeros((x.shape[0], N), np.float32)
+    O.matmul(blocks, gtype, N, K, x, y)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        O.matmul(blocks, gtype, N, K, x, y)
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
 def cpu_baseline(synth, gtype, N, K, M):
+    phys, logical = cpu_topology()  # before OpenMP binds this thread to one CPU
+    os.environ.setdefault("OMP_PROC_BIND", "close")  # read when the oracle's OpenMP runtime loads
     import oracle
     O = oracle.Oracle()
     blocks = synth.random_blocks(gtype, synth.Rng(4242 + gtype + N), N, K)
     x = O.f16_to_f32(synth.activations_f16(synth.Rng(99 + M), M, K))
-    y = np.zeros((M, N), np.float32)
-    O.matmul(blocks, gtype, N, K, x, y)  # warm-up
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        O.matmul(blocks, gtype, N, K, x, y)
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
-    cores = int(os.environ.get("OMP_NUM_THREADS") or len(os.sched_getaffinity(0)))
+    t = cpu_time(O, blocks, gtype, N, K, x)
+    gemv = []
+    for g, n, k in [(synth.Q8_0, 9728, 2560), (synth.Q4_K, 9728, 2560), (synth.Q4_K, 2560, 9728)]:
+        b = synth.random_blocks(g, synth.Rng(4242 + g + n), n, k)
+        x1 = O.f16_to_f32(synth.activations_f16(synth.Rng(100), 1, k))
+        t1 = cpu_time(O, b, g, n, k, x1)
+        gemv.append(dict(type="q8_0" if g == synth.Q8_0 else "q4_k", M=1, N=n, K=k, us=round(t1 * 1e6, 1),
+                         gbs=round(gemm_bytes(g, 1, n, k, 4) / t1 / 1e9, 3)))
+    threads = int(os.environ.get("OMP_NUM_THREADS") or logical)
+    cores = min(threads, phys) if phys else threads
     return dict(value=round(2.0 * M * N * K / t / 1e12, 6), unit="TFLOP/s", cores=cores, kind="port",
+                threads=threads, omp_proc_bind=os.environ.get("OMP_PROC_BIND"), cpu=cpu_model(),
                 sample=f"full headline GEMM (Q4_K M={M} N={N} K={K}), oracle restatement of cpu_backend.c "
                        f"matmul (-O2 -std=c11 -fopenmp), median of 3 after 1 warm-up: {t:.3f} s; "
-                       f"host CPU: {cpu_model()}")
+                       f"{threads} OpenMP threads (OMP_PROC_BIND={os.environ.get('OMP_PROC_BIND')}); the "
+                       f"process may run on {logical} logical CPUs, "
+                       + (f"{phys} physical cores" if phys else "physical cores not exposed by the host")
+                       + f"; CPU {cpu_model()}",
+                gemv=gemv)
 
 
 def cpu_model():
@@ -325,11 +383,13 @@ def main():
     kname = main_kernel_name(hq, gtype, M, N, K)
     roofline = dict(bound="mfma", achieved=round(kt, 3), peak=PEAK_TFLOPS, unit="TFLOP/s",
                     frac=round(kt / PEAK_TFLOPS, 4), traffic=read_traffic("q4_k_gemm_m512_k2560_n9728", kname),
-                    kernel=kname, kernel_us=round(head["kernel_us"], 3))
+                    kernel=kname, kernel_us=round(head["kernel_us"], 3),
+                    kernel_timing=f"median of {MEDIAN_REPS} HIP-graph replays of {MEDIAN_ITERS} launches")
     cpu = None if args.no_cpu else cpu_baseline(synth, gtype, N, K, M)
     line = {
         "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(head["us"] / 1e3, 6), "higher_is_better": True,
+        "warmup": args.warmup, "ms_per_step": round(head["us"] / 1e3, 6),
+        "us_median": round(head["us_median"], 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
         "config": {"workload": "q4_k_gemm_m512_k2560_n9728", "gtype": "Q4_K", "M": M, "N": N, "K": K,
                    "A": "fp16 N(0,1)", "C": "fp16 (fp32 accumulate)", "weight_copies": head["copies"],

@@ -3,6 +3,7 @@
 // the host before a kernel is launched, so no launch can read or write outside its buffers.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <thread>
@@ -787,40 +788,62 @@ extern "C" void hq_gemm_tiles(int ggml_type, int M, int N, int *rows_per_tile, i
 namespace {
 template <typename F>
 int time_graph(int iters, int reps, void *stream, float *ms, F launch) {
-    if (iters < 1 || reps < 1) return fail("hq_time: iters = %d, reps = %d", iters, reps);
+    if (iters < 1 || reps < 1 || reps > 64) return fail("hq_time: iters = %d, reps = %d (1 .. 64)", iters, reps);
     if (!stream) return fail("hq_time: needs a created stream (graph capture)");
     hipStream_t st = S(stream);
-    hipGraph_t g = nullptr;
-    hipGraphExec_t ge = nullptr;
-    HIPCK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-    int rc = 0;
-    for (int i = 0; i < iters && !rc; i++) rc = launch(i);
-    hipError_t e = hipStreamEndCapture(st, &g);
-    if (rc) {
-        if (g) (void)hipGraphDestroy(g);
-        return -1;
+    // replay r is its own graph of launches r * iters .. r * iters + iters - 1, so that launches keep
+    // rotating over the caller's buffers across replays
+    std::vector<hipGraph_t> g(reps, nullptr);
+    std::vector<hipGraphExec_t> ge(reps, nullptr);
+    std::vector<hipEvent_t> ev(reps + 1, nullptr);
+    auto cleanup = [&]() {
+        for (auto &x : ev)
+            if (x) (void)hipEventDestroy(x);
+        for (auto &x : ge)
+            if (x) (void)hipGraphExecDestroy(x);
+        for (auto &x : g)
+            if (x) (void)hipGraphDestroy(x);
+    };
+    for (int r = 0; r < reps; r++) {
+        hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
+        if (e != hipSuccess) {
+            cleanup();
+            return fail("hipStreamBeginCapture: %s", hipGetErrorString(e));
+        }
+        int rc = 0;
+        for (int i = 0; i < iters && !rc; i++) rc = launch(r * iters + i);
+        e = hipStreamEndCapture(st, &g[r]);
+        if (rc) {
+            cleanup();
+            return -1;
+        }
+        if (e == hipSuccess) e = hipGraphInstantiate(&ge[r], g[r], nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            cleanup();
+            return fail("graph capture: %s", hipGetErrorString(e));
+        }
     }
-    if (e != hipSuccess) return fail("hipStreamEndCapture: %s", hipGetErrorString(e));
-    e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
-    if (e != hipSuccess) {
-        (void)hipGraphDestroy(g);
-        return fail("hipGraphInstantiate: %s", hipGetErrorString(e));
+    // one event between consecutive replays: replay r's time is ev[r] .. ev[r + 1]; the result is the
+    // median over the replays of the time per launch
+    hipError_t e = hipSuccess;
+    for (auto &x : ev)
+        if (e == hipSuccess) e = hipEventCreate(&x);
+    if (e == hipSuccess) e = hipGraphLaunch(ge[reps - 1], st);  // warm-up
+    if (e == hipSuccess) e = hipEventRecord(ev[0], st);
+    for (int r = 0; r < reps && e == hipSuccess; r++) {
+        e = hipGraphLaunch(ge[r], st);
+        if (e == hipSuccess) e = hipEventRecord(ev[r + 1], st);
     }
-    hipEvent_t e0, e1;
-    HIPCK(hipEventCreate(&e0));
-    HIPCK(hipEventCreate(&e1));
-    HIPCK(hipGraphLaunch(ge, st));  // warm-up
-    HIPCK(hipEventRecord(e0, st));
-    for (int r = 0; r < reps; r++) HIPCK(hipGraphLaunch(ge, st));
-    HIPCK(hipEventRecord(e1, st));
-    HIPCK(hipEventSynchronize(e1));
-    float total = 0.f;
-    HIPCK(hipEventElapsedTime(&total, e0, e1));
-    *ms = total / (float)(iters * reps);
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
-    (void)hipGraphExecDestroy(ge);
-    (void)hipGraphDestroy(g);
+    if (e == hipSuccess) e = hipEventSynchronize(ev[reps]);
+    std::vector<float> per(reps);
+    for (int r = 0; r < reps && e == hipSuccess; r++) {
+        e = hipEventElapsedTime(&per[r], ev[r], ev[r + 1]);
+        per[r] /= (float)iters;
+    }
+    cleanup();
+    if (e != hipSuccess) return fail("hq_time: %s", hipGetErrorString(e));
+    std::sort(per.begin(), per.end());
+    *ms = reps % 2 ? per[reps / 2] : 0.5f * (per[reps / 2 - 1] + per[reps / 2]);
     return 0;
 }
 }  // namespace

@@ -82,7 +82,8 @@ int hq_llama_forward(const hq_llama_t *m, const uint32_t *tokens, size_t T, cons
         hq_internal_fail("forward: out of host memory");
         goto done;
     }
-    for (size_t i = 0; i < rot / 2; i++) w.inv_freq[i] = 1.0f / powf(m->rope_theta, (float)(2 * i) / (float)rot);
+    for (size_t i = 0; i < rot / 2; i++)
+        w.inv_freq[i] = m->rope_inv_freq ? m->rope_inv_freq[i] : 1.0f / powf(m->rope_theta, (float)(2 * i) / (float)rot);
 
     /* embedding rows, decoded on the device */
     const size_t out_off = (n_ids * sizeof(float) + 255) / 256 * 256, emb_bytes = T * H * sizeof(float);

@@ -46,7 +46,7 @@ class Llama(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in ("hidden", "n_layers", "intermediate", "vocab", "n_heads", "n_kv_heads",
                                           "head_dim", "rot_dim")] + [
         ("eps", C.c_float), ("rope_theta", C.c_float), ("embed", C.c_void_p), ("lm_head", C.c_void_p),
-        ("final_norm", C.c_void_p), ("layers", C.c_void_p)]
+        ("final_norm", C.c_void_p), ("layers", C.c_void_p), ("rope_inv_freq", C.c_void_p)]
 
 
 # Layout mirrors of the reference's config_t, layer_t, st_set_t, model_t and backend_t
@@ -487,6 +487,10 @@ class LlamaModel:
         self.st = Llama(H, c["n_layers"], I, V, c["n_heads"], c["n_kv_heads"], c["head_dim"], c["rot_dim"], c["eps"],
                         c["rope_theta"], up(model["embed"], V, H), up(model["lm_head"], V, H),
                         self.norms[0].ctypes.data, C.cast(self.layers, C.c_void_p).value)
+        if model.get("rope_inv_freq") is not None:
+            self.inv_freq = np.ascontiguousarray(model["rope_inv_freq"], np.float32)
+            assert self.inv_freq.shape == (c["rot_dim"] // 2,)
+            self.st.rope_inv_freq = self.inv_freq.ctypes.data
 
     def forward(self, tokens, ids):
         tokens = np.ascontiguousarray(tokens, np.uint32)

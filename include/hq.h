@@ -144,8 +144,10 @@ int hq_device_synchronize(void);
 
 /* Benchmark helpers: `iters` launches of hq_gemm (resp. hq_gather_dot_dev), launch i using
  * Ws[i % n_w] (and, for the gather, id set i % n_sets of n_sets consecutive [B*k] arrays at
- * ids_dev), captured in one HIP graph on `stream` and replayed `reps` times after one warm-up
- * replay; *ms = mean milliseconds per launch measured with HIP events on `stream`. */
+ * ids_dev), captured on `stream` in `reps` HIP graphs of `iters` launches each (graph r: launches
+ * r * iters .. r * iters + iters - 1; reps <= 64) and replayed in order after one warm-up replay of
+ * the last, a HIP event on `stream` between consecutive replays; *ms = the median over the replays
+ * of the replay's milliseconds per launch. */
 int hq_time_gemm(hq_mat *const *Ws, int n_w, const uint16_t *A, int M, void *C, int c_is_f32, int iters, int reps,
                  void *stream, float *ms);
 /* As hq_time_gemm, timing only the GEMM's main kernel (M >= 2): an activation pre-pass the

@@ -29,6 +29,10 @@ typedef struct {
     hq_mat *embed, *lm_head;
     const float *final_norm;
     const hq_llama_layer_t *layers;
+    /* Optional [rot_dim / 2] RoPE inverse frequencies, as the reference's model_t.rope_inv_freq
+     * (src/model.c:449-477: Llama 3.1 frequency scaling and GGUF rope_freqs divisors applied); NULL:
+     * 1 / powf(rope_theta, 2k / rot_dim), the unscaled table (src/model.c:453). */
+    const float *rope_inv_freq;
 } hq_llama_t;
 
 /* One prefill of T tokens from position 0; logits[i] for ids[i] at the last position.

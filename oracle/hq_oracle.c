@@ -246,8 +246,8 @@ static void attention(const or_llama_t *m, const or_layer_t *L, const float *h, 
     free(q), free(k), free(v);
 }
 
-/* src/cpu_backend.c:218-263 for a Llama model at position 0; RoPE frequencies from
- * src/model.c:450-454 (no Llama 3.1 scaling, no rope_freqs tensor). */
+/* src/cpu_backend.c:218-263 for a Llama model at position 0; RoPE frequencies the caller's table
+ * (model_t.rope_inv_freq, src/model.c:449-477) or, without one, src/model.c:453 (theta powers). */
 int or_llama_forward(const or_llama_t *m, const uint32_t *tokens, size_t T, const uint32_t *ids, uint32_t n_ids,
                      float *logits) {
     if (T == 0) return -1;
@@ -258,7 +258,7 @@ int or_llama_forward(const or_llama_t *m, const uint32_t *tokens, size_t T, cons
     const size_t H = m->hidden, I = m->intermediate, qw = (size_t)m->n_heads * m->head_dim;
     float *inv_freq = (float *)malloc(m->rot_dim / 2 * sizeof(float));
     for (uint32_t i = 0; i < m->rot_dim / 2; i++)
-        inv_freq[i] = 1.0f / powf(m->rope_theta, (float)(2 * i) / (float)m->rot_dim);
+        inv_freq[i] = m->rope_inv_freq ? m->rope_inv_freq[i] : 1.0f / powf(m->rope_theta, (float)(2 * i) / (float)m->rot_dim);
     float *x = (float *)malloc(T * H * sizeof *x), *h = (float *)malloc(T * H * sizeof *h);
     float *mix = (float *)malloc(T * qw * sizeof *mix);
     float *g = (float *)malloc(T * I * sizeof *g), *u = (float *)malloc(T * I * sizeof *u);

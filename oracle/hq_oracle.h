@@ -78,6 +78,7 @@ typedef struct {
     or_wmat_t embed, lm_head;
     const float *final_norm;
     const or_layer_t *layers;
+    const float *rope_inv_freq; /* optional [rot_dim / 2] table (model_t.rope_inv_freq); NULL: theta powers */
 } or_llama_t;
 
 /* One prefill from position 0 of T tokens; logits for ids at the last position.

@@ -29,7 +29,7 @@ class Llama(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in ("hidden", "n_layers", "intermediate", "vocab", "n_heads", "n_kv_heads",
                                           "head_dim", "rot_dim")] + [
         ("eps", C.c_float), ("rope_theta", C.c_float), ("embed", WMat), ("lm_head", WMat),
-        ("final_norm", C.c_void_p), ("layers", C.c_void_p)]
+        ("final_norm", C.c_void_p), ("layers", C.c_void_p), ("rope_inv_freq", C.c_void_p)]
 
 
 DT_GGML = 3
@@ -132,6 +132,11 @@ def llama_struct(model):
     st = Llama(H, c["n_layers"], I, c["vocab"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["rot_dim"],
                c["eps"], c["rope_theta"], wmat(model["embed"], 8, c["vocab"], H), wmat(model["lm_head"], 8, c["vocab"], H),
                model["final_norm"].ctypes.data, C.cast(layers, C.c_void_p).value)
+    if model.get("rope_inv_freq") is not None:
+        inv = np.ascontiguousarray(model["rope_inv_freq"], np.float32)
+        assert inv.shape == (c["rot_dim"] // 2,)
+        keep.append(inv)
+        st.rope_inv_freq = inv.ctypes.data
     return st, keep
 
 

@@ -76,4 +76,6 @@ def write_tiny_llama(path, model):
         t.append((f"blk.{li}.ffn_norm.weight", (H,), 0, L["post_norm"]))
         for key, (gn, ne0, ne1) in names.items():
             t.append((f"blk.{li}.{gn}.weight", (ne0, ne1), 8, L[key]))
+    if model.get("rope_freqs") is not None:  # per-frequency RoPE divisors (Llama 3.1 scaling in GGUF)
+        t.append(("rope_freqs.weight", (c["rot_dim"] // 2,), 0, np.ascontiguousarray(model["rope_freqs"], np.float32)))
     write(path, kv, t)

@@ -115,7 +115,8 @@ def test_gemm_kernel_names():
              (synth.Q4_K, 1, 9728, 256): "k_gemv_q4_k_s<16>", (synth.Q8_0, 1, 9728, 2560): "k_gemv_q8_0<2>",
              (synth.Q8_0, 1, 100, 512): "k_gemv_q8_0<1>",
              # special-scale cases: the narrow kernel at M = 16, the mid-M kernel with a 6-way K split
-             (synth.Q4_K, 16, 9728, 2560): "k_gemm_q4_k<2, 2>", (synth.Q4_K, 48, 9728, 2560): "k_gemm_q4_k_rb<1, 4, 3, 2>"}
+             (synth.Q4_K, 16, 9728, 2560): "k_gemm_q4_k<2, 2>", (synth.Q4_K, 48, 9728, 2560): "k_gemm_q4_k_rb<1, 4, 3, 2>",
+             (synth.Q4_K, 350, 9728, 512): "k_gemm_q4_k_wr<3>"}
     for (gtype, M, N, K), name in cases.items():
         assert hq.gemm_kernel(gtype, M, N, K) == name, (gtype, M, N, K)
 

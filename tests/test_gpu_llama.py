@@ -44,3 +44,28 @@ def test_tiny_llama_logits(hqlib, oracle, model):
     with pytest.raises(hqlib.HQError, match="out of range"):
         m.forward(t2, np.array([32000], np.uint32))
     m.free()
+
+
+def test_tiny_llama_rope_table(hqlib, oracle, model):
+    """A caller's RoPE table (model_t.rope_inv_freq; here the theta powers over per-frequency
+    divisors 1 .. 8, the Llama 3.1 scaling a GGUF file carries, the table test_oracle.py pins
+    bit-exact against the reference's model_load) reaches the HIP path's forward: it matches the
+    oracle under that table, whose logits differ from the unscaled table's."""
+    import synth as s
+    tokens, ids = s.tiny_llama_prompt(T=96)
+    c = model["cfg"]
+    half = c["rot_dim"] // 2
+    div = np.ones(half, np.float32)
+    div[half // 2:] = 8.0
+    div[half // 2 - 4:half // 2] = np.float32([1.5, 2.5, 4.0, 6.0])
+    inv = (hqlib.rope_inv_freq(c["rope_theta"], c["rot_dim"]) / div).astype(np.float32)
+    plain = oracle.llama_forward(model, tokens, ids)
+    scaled_model = dict(model, rope_inv_freq=inv)
+    m = hqlib.LlamaModel(scaled_model)
+    got = m.forward(tokens, ids)
+    m.free()
+    ref = oracle.llama_forward(scaled_model, tokens, ids)
+    print(f"[gpu] llama3 RoPE: max_abs {max_abs(got, ref):.2e} rel_l2 {rel_l2(got, ref):.2e}; "
+          f"vs unscaled {max_abs(ref, plain):.2e}", flush=True)
+    assert max_abs(got, ref) <= 1e-2 and rel_l2(got, ref) <= 1e-2
+    assert max_abs(ref, plain) > 1e-4

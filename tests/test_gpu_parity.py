@@ -235,10 +235,11 @@ def f64_reference(oracle, blocks, gtype, N, K, a16):
     return a @ w.T, np.abs(a) @ np.abs(w).T
 
 
-# the tile kernel (M = 350, 512 at N = 9728; M = 512 at N = 2560 with each tile's K split over 4
-# workgroups), the mid-M kernel (M = 48 at N = 9728: one workgroup per tile; M = 64 at N = 2560,
-# K = 9728: each tile's K split over 6, so every part restarts its accumulator units), the narrow
-# kernel (M = 16) and the GEMVs (M = 1)
+# the loader-wave tile kernel k_gemm_q4_k_wr (M = 350, 512 at N = 9728), the full-K tile kernel
+# k_gemm_q4_k_ws (M = 512 at N = 2560: each tile's K split over 4 workgroups), the mid-M kernel
+# k_gemm_q4_k_rb (M = 48 at N = 9728: one workgroup per tile; M = 64 at N = 2560, K = 9728: each
+# tile's K split over 6, so every part restarts its accumulator units), the narrow kernel
+# k_gemm_q4_k (M = 16) and the GEMVs (M = 1); test_abi.py pins these kernel names
 SPECIAL = [(9728, 512, 350), (9728, 2560, 512), (2560, 9728, 512), (9728, 2560, 48), (2560, 9728, 64),
            (9728, 2560, 16), (9728, 2560, 1), (2560, 9728, 1)]
 

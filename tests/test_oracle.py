@@ -337,6 +337,29 @@ def test_llama_forward_gqa_matches_reference(oracle, reference, tmp_path):
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+def test_llama_forward_rope_table_matches_reference(oracle, reference, tiny_model, tmp_path):
+    """A RoPE table: the GGUF carries per-frequency divisors (rope_freqs.weight: 1 for the short
+    wavelengths, 8 for the long ones, a ramp between, as Llama 3.1 files do), which the reference's
+    model_load divides its table by (src/model.c:470-476); the oracle forward given that table
+    (theta powers / divisors in float32) is bit-exact with it, and differs from the unscaled one."""
+    import gguf_writer
+    import hq
+    c = tiny_model["cfg"]
+    half = c["rot_dim"] // 2
+    div = np.ones(half, np.float32)
+    div[half // 2:] = 8.0
+    div[half // 2 - 4:half // 2] = np.float32([1.5, 2.5, 4.0, 6.0])
+    model = dict(tiny_model, rope_freqs=div)
+    path = str(tmp_path / "rope.gguf")
+    gguf_writer.write_tiny_llama(path, model)
+    tokens, ids = synth.tiny_llama_prompt(2, T=64)
+    inv = (hq.rope_inv_freq(c["rope_theta"], c["rot_dim"]) / div).astype(np.float32)
+    a = oracle.llama_forward(dict(tiny_model, rope_inv_freq=inv), tokens, ids)
+    b = reference.logits(path, tokens, ids)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert not np.array_equal(a, oracle.llama_forward(tiny_model, tokens, ids))
+
+
 def test_llama_forward_rejects_bad_ids(oracle, tiny_model):
     with pytest.raises(ValueError):
         oracle.llama_forward(tiny_model, np.array([32000], np.uint32), np.array([1], np.uint32))
