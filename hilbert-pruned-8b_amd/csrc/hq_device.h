@@ -110,6 +110,62 @@ DEV f4 buf_load16_sc1(rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, CPOL_SC1));
 }
 
+// sum of 8 products q*a: q four exact fp16 pairs, a four words of fp16 pairs (v_dot2_f32_f16: exact
+// products, fp32 sums)
+DEV float dot8(const h2 (&q)[4], const u4v a, float s) {
+    s = __builtin_amdgcn_fdot2(q[0], as_h2(a.x), s, false);
+    s = __builtin_amdgcn_fdot2(q[1], as_h2(a.y), s, false);
+    s = __builtin_amdgcn_fdot2(q[2], as_h2(a.z), s, false);
+    s = __builtin_amdgcn_fdot2(q[3], as_h2(a.w), s, false);
+    return s;
+}
+
+// sum of the 8 fp16 values of a (fp32)
+DEV float sum8(const u4v a, float s) {
+    const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    s = __builtin_amdgcn_fdot2(as_h2(a.x), one, s, false);
+    s = __builtin_amdgcn_fdot2(as_h2(a.y), one, s, false);
+    s = __builtin_amdgcn_fdot2(as_h2(a.z), one, s, false);
+    s = __builtin_amdgcn_fdot2(as_h2(a.w), one, s, false);
+    return s;
+}
+
+// One GEMV unit from LDS: 64 values of a weight row (32-byte quant group p of the super-block at
+// blk: low nibbles = sub-block 2p, high nibbles = sub-block 2p + 1) dotted with activations
+// [64 ku, 64 ku + 64) of sa, using the 32-value sums ss[2 ku], ss[2 ku + 1]. The quants become the
+// fp16 values 1024 + q (low) and 1024 + 16 q (high) under v_perm_b32, meet the activations in
+// v_dot2_f32_f16 (exact products, fp32 sums), and the 1024 bias comes off in fp32 through the sums:
+// d sc dot(q, a) - dmin m sum(a) per sub-block (ggml_quant.h:51-59 scale and min codes).
+DEV float gemv_unit_q4_k(const char *blk, int p, const char *sa, const float *ss, int ku) {
+    const u4v hd = *(const u4v *)blk;
+    const u4v q0 = *(const u4v *)(blk + 16 + 32 * p), q1 = *(const u4v *)(blk + 32 + 32 * p);
+    const u4v *const av = (const u4v *)(sa + 128 * ku);
+    const float s0 = ss[2 * ku], s1 = ss[2 * ku + 1];
+    uint32_t sw0, sw1, mw0, mw1;
+    q4k_scale_words(hd.y, hd.z, hd.w, sw0, sw1, mw0, mw1);
+    const uint32_t sh = 16u * (uint32_t)(p & 1);
+    const uint32_t sw = (p < 2 ? sw0 : sw1) >> sh, mw = (p < 2 ? mw0 : mw1) >> sh;
+    const float d = h2f((uint16_t)hd.x), dmin = h2f((uint16_t)(hd.x >> 16));
+    const float ds0 = d * (float)(sw & 0xffu), ds1 = d * (float)((sw >> 8) & 0xffu);
+    const float dm0 = dmin * (float)(mw & 0xffu), dm1 = dmin * (float)((mw >> 8) & 0xffu);
+    float part[4];
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        const u4v q = c ? q1 : q0;
+        const uint32_t wl[4] = {q.x & 0x0f0f0f0fu, q.y & 0x0f0f0f0fu, q.z & 0x0f0f0f0fu, q.w & 0x0f0f0f0fu};
+        const uint32_t wh[4] = {q.x & 0xf0f0f0f0u, q.y & 0xf0f0f0f0u, q.z & 0xf0f0f0f0u, q.w & 0xf0f0f0f0u};
+        const h2 l0[4] = {as_h2(perm_lo(wl[0])), as_h2(perm_hi(wl[0])), as_h2(perm_lo(wl[1])), as_h2(perm_hi(wl[1]))};
+        const h2 l1[4] = {as_h2(perm_lo(wl[2])), as_h2(perm_hi(wl[2])), as_h2(perm_lo(wl[3])), as_h2(perm_hi(wl[3]))};
+        const h2 g0[4] = {as_h2(perm_lo(wh[0])), as_h2(perm_hi(wh[0])), as_h2(perm_lo(wh[1])), as_h2(perm_hi(wh[1]))};
+        const h2 g1[4] = {as_h2(perm_lo(wh[2])), as_h2(perm_hi(wh[2])), as_h2(perm_lo(wh[3])), as_h2(perm_hi(wh[3]))};
+        part[c] = dot8(l1, av[2 * c + 1], dot8(l0, av[2 * c], 0.f));
+        part[2 + c] = dot8(g1, av[4 + 2 * c + 1], dot8(g0, av[4 + 2 * c], 0.f));
+    }
+    const float ql = (part[0] + part[1]) - 1024.0f * s0;  // dot(q, a), sub-block 2p
+    const float qh = (part[2] + part[3]) - 1024.0f * s1;  // 16 dot(q, a), sub-block 2p + 1
+    return (ds0 * ql - dm0 * s0) + (0.0625f * ds1 * qh - dm1 * s1);
+}
+
 DEV u4v buf_load16(rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
