@@ -26,16 +26,20 @@
 // and quants; each load has two stages to land) and the MFMA waves read the next stage's quant words.
 //
 // Arithmetic: as hq_gemm_ws.hip and hq_gemm_bt.hip (accumulators in units of c_u = d_u, weight operand
-// the exact integer s*q). The min term of super-block u (bf16 hi/lo S x Bmin, x = -dmin*m/c_u) is added
-// in its own units during stage p = 1, each row block four groups away from its own MFMAs; the row
-// blocks are rescaled by c_u / c_{u+1} right after their last MFMA of super-block u; at the end by
-// c_{U-1}. The per-column tables (scale words, Bmin, R, CL) depend on the weights only: they are
-// computed once at upload (k_q4k_tables) and moved into LDS with the loads.
+// the exact integer s*q). The row blocks are rescaled by c_u / c_{u+1} right after their last MFMA of
+// super-block u; at the end by c_{U-1}. The min term of super-block u (bf16 hi/lo S x Bmin) is added
+// one super-block late, in stage p = 1 of super-block u + 1 and in its units (x = -dmin*m/c_{u+1}),
+// each row block four groups away from its own MFMAs; the last super-block's after the loop, in its
+// own units. The activation sub-block sums S come from the loader waves: each stage's ring slot is
+// summed in LDS while the stage is being multiplied (no pass over A before the kernel), so S of
+// super-block u is whole one barrier after its last stage. The per-column tables (scale words, Bmin,
+// R, CL) depend on the weights only: they are computed once at upload (k_q4k_tables) and moved into
+// LDS with the loads.
 //
 // LDS (108 KB for NB = 3): A [4][128 rows][64 k] fp16 (16-byte slot p of row r at p ^ ((r >> 1) & 7));
 // quant groups [4][4 waves][16NB columns][32 B] (the two halves of column c swapped where
-// (c >> 3) & 1); S [2][128][16] bf16; per wave Bmin [16NB][32 B] and records [2][16NB][16 B]. The
-// output goes from the accumulators straight to C.
+// (c >> 3) & 1); S [2][128][hi x 8, lo x 8] bf16; per wave Bmin [16NB][32 B] and records
+// [2][16NB][16 B]. The output goes from the accumulators straight to C.
 #include "hq_device.h"
 #include "hq_kernels.h"
 
@@ -51,7 +55,6 @@ struct WrArgs {
     const uint8_t *W;  // Q4_K super-blocks, row n at n * row_bytes
     uint32_t row_bytes;
     const uint16_t *A;  // fp16 [M][K]
-    const uint16_t *S;  // activation sub-block sums [M][K/256][16] (k_asums, bf16 hi/lo)
     const uint8_t *tab; // per-super-block column tables (hq_launch_q4k_tables)
     int M, N, K;
     void *C;
@@ -107,7 +110,6 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
     const int role = wave >> 2, w4 = wave & 3;
     const rsrc_t ra = make_rsrc(g.A, (uint32_t)((size_t)M * K * 2));
     const rsrc_t rw = make_rsrc(g.W, (uint32_t)((size_t)N * g.row_bytes));
-    const rsrc_t rs = make_rsrc(g.S, (uint32_t)((size_t)M * U * 32));
     const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
     const int nw = n0 + WC * w4;  // first column of MFMA wave w4
 
@@ -135,22 +137,39 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
         const uint32_t so = (uint32_t)((s >> 2) * 144 + 16 + 32 * (s & 3));
         if (32 * k + 32 <= WC || lane < 2 * (WC - 32 * k)) dma16_so(rw, dst, q_voff[k], so);
     };
-    // S of super-block u into parity slot u & 1: wave w moves rows 32w .. + 32; lane i: row 32w + i/2
-    const uint32_t s_voff = (uint32_t)(m0 + 32 * w4 + (lane >> 1)) * (uint32_t)U * 32u + 16u * (uint32_t)(lane & 1);
-    auto dma_s = [&](int u) {
-        dma16_so(rs, lds0 + (uint32_t)(L::S + (u & 1) * L::S_BYTES + w4 * 1024), s_voff, (uint32_t)(u * 32));
+    // activation sub-block sums of stage s (sub-blocks 2p, 2p + 1 of super-block u; s = 4u + p) from
+    // its ring slot into S parity u & 1: lane i of loader wave w sums the 32 values of row
+    // r = 32w + i/2, sub-block 2p + i % 2 (fp32, the order of k_asums: the same bits); the lane pair
+    // swaps sums, then the even lane stores both bf16 hi parts and the odd lane both lo parts
+    const int s_row = 32 * w4 + (lane >> 1), s_h = lane & 1;
+    const uint32_t s_src = lds0 + (uint32_t)(L::A + s_row * 128), s_sw = (uint32_t)((s_row >> 1) & 7);
+    const uint32_t s_dst = lds0 + (uint32_t)(L::S + s_row * 32 + 16 * s_h);
+    auto sums = [&](int s) {
+        const uint32_t src = s_src + (uint32_t)((s & 3) * L::A_BYTES);
+        float v = 0.f;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+            v = sum8(*(const __attribute__((address_space(3))) u4v *)(uintptr_t)(src + 16u * ((uint32_t)(4 * s_h + t) ^ s_sw)), v);
+        const float o = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false));
+        const float v0 = s_h ? o : v, v1 = s_h ? v : o;
+        const __bf16 h0 = (__bf16)v0, h1 = (__bf16)v1;
+        const __bf16 e0 = s_h ? (__bf16)(v0 - (float)h0) : h0, e1 = s_h ? (__bf16)(v1 - (float)h1) : h1;
+        *(__attribute__((address_space(3))) uint32_t *)(uintptr_t)(s_dst + (uint32_t)(((s >> 2) & 1) * L::S_BYTES + 4 * (s & 3))) =
+            (uint32_t)__builtin_bit_cast(uint16_t, e0) | ((uint32_t)__builtin_bit_cast(uint16_t, e1) << 16);
     };
-    // tables of super-block u for MFMA wave w4's columns into its table area: Bmin (1536 bytes, two
-    // instructions) and the records (768 bytes, lanes < WC) in parity u & 1
+    // tables of MFMA wave w4's columns into its table area: Bmin of super-block u (1536 bytes, two
+    // instructions), the records of super-block u in parity u & 1 (768 bytes, lanes < WC)
     const rsrc_t rt = make_rsrc(g.tab, (uint32_t)((size_t)N * U * HQ_Q4K_TAB_BYTES));
     const uint32_t tw = lds0 + (uint32_t)(L::T + w4 * L::T_WAVE);
-    auto dma_t = [&](int u) {
-        const uint32_t so = (uint32_t)u * (uint32_t)N * HQ_Q4K_TAB_BYTES;
-        dma16_so(rt, tw + L::T_BM, 16u * (uint32_t)lane, so + (uint32_t)nw * 32u);
-        if (lane < WC * 2 - 64) dma16_so(rt, tw + L::T_BM + 1024, 16u * (uint32_t)lane, so + (uint32_t)nw * 32u + 1024u);
+    auto dma_bm = [&](int u) {
+        const uint32_t so = (uint32_t)u * (uint32_t)N * HQ_Q4K_TAB_BYTES + (uint32_t)nw * 32u;
+        dma16_so(rt, tw + L::T_BM, 16u * (uint32_t)lane, so);
+        if (lane < WC * 2 - 64) dma16_so(rt, tw + L::T_BM + 1024, 16u * (uint32_t)lane, so + 1024u);
+    };
+    auto dma_rec = [&](int u) {
         if (lane < WC)
             dma16_so(rt, tw + L::T_REC + (uint32_t)((u & 1) * WC * 16), 16u * (uint32_t)lane,
-                     so + (uint32_t)N * 32u + (uint32_t)nw * 16u);
+                     (uint32_t)u * (uint32_t)N * HQ_Q4K_TAB_BYTES + (uint32_t)N * 32u + (uint32_t)nw * 16u);
     };
 
     // ---- operand addresses. Activation fragment of row block i, k-step f, ring slot buf: lane (ln, lg)
@@ -205,14 +224,21 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
     const int u_last = U - 1;
     if (role == 1) {
         // ------------------------------------------------------------------------------ loaders
-        // prologue: stage 0 of activations and quants, S and tables of unit 0, then stage 1, which
-        // (as in every loader stage) is still in flight at the barrier
+        // prologue: stage 0 of activations and quants, the records of unit 0, then stage 1, which (as
+        // in every loader stage) is still in flight at the barrier. S parity 1 and Bmin are zeroed:
+        // the min step of unit 0 (the late one of unit -1) adds exact zeros
 #pragma unroll
         for (int q = 0; q < 4; q++) dma_a1(0, 0, q);
 #pragma unroll
         for (int k = 0; k < QI; k++) dma_q1(0, 0, k);
-        dma_s(0);
-        dma_t(0);
+        dma_rec(0);
+        {
+            using lds_u4 = __attribute__((address_space(3))) u4v;
+            const u4v z = {0u, 0u, 0u, 0u};
+            *(lds_u4 *)(uintptr_t)(lds0 + (uint32_t)(L::S + L::S_BYTES + w4 * 1024 + 16 * lane)) = z;
+            *(lds_u4 *)(uintptr_t)(tw + (uint32_t)(L::T_BM + 16 * lane)) = z;
+            if (lane < WC * 2 - 64) *(lds_u4 *)(uintptr_t)(tw + (uint32_t)(L::T_BM + 1024 + 16 * lane)) = z;
+        }
         {
             const int s1 = S2 > 1 ? 1 : 0;
 #pragma unroll
@@ -220,15 +246,16 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
 #pragma unroll
             for (int k = 0; k < QI; k++) dma_q1(s1, 1, k);
         }
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 + QI) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(4 + QI) : "memory");
         wr_barrier();
         // loader stage s = 4u + p runs between the MFMA waves' barriers of stages s - 1 and s (the
         // prologue's barrier counts as stage -1's), while they finish stage s - 1 and start stage s:
-        // the loads of stage s + 2 (ring slot (s + 2) % 4, last read in stage s - 2), at p = 0 S of unit
-        // u + 1, at p = 2 unit u + 1's tables (Bmin of unit u was read at p = 0, the records of unit
-        // u - 1 are done with); then wait for everything but this stage's loads (stage s + 1's land:
-        // each load has two stages) and meet the MFMA waves at their barrier. Past the last unit the
-        // S and table loads repeat it (same bytes).
+        // the loads of stage s + 2 (ring slot (s + 2) % 4, last read in stage s - 2), at p = 2 Bmin of
+        // unit u (unit u - 1's was read at p = 0) and the records of unit u + 1 (unit u - 1's are done
+        // with); the sums of stage s (landed by the last barrier); then wait for everything but this
+        // stage's loads (stage s + 1's land: each load has two stages) and for the sums' stores, and
+        // meet the MFMA waves at their barrier. Past the last unit the record loads repeat it (same
+        // bytes).
         for (int u = 0; u < U; u++) {
             const int u_next = u < u_last ? u + 1 : u_last;
 #pragma unroll
@@ -238,11 +265,10 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
                 for (int q = 0; q < 4; q++) dma_a1(s_src, ld, q);
 #pragma unroll
                 for (int k = 0; k < QI; k++) dma_q1(s_src, ld, k);
-                if (p == 0) dma_s(u_next);
-                if (p == 2) dma_t(u_next);
-                if (p == 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 + QI + 1) : "memory");
-                else if (p == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 + QI + 3) : "memory");
-                else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 + QI) : "memory");
+                if (p == 2) dma_bm(u), dma_rec(u_next);
+                sums(s);
+                if (p == 2) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(4 + QI + 3) : "memory");
+                else asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(4 + QI) : "memory");
                 wr_barrier();
             }
         }
@@ -270,14 +296,14 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
     h8 bm[NB], sa[3];
     f4 r[NB];
 #pragma unroll
-    for (int j = 0; j < NB; j++) bm[j] = rdbm(j), r[j] = f4{1.f, 1.f, 1.f, 1.f};
+    for (int j = 0; j < NB; j++) r[j] = f4{1.f, 1.f, 1.f, 1.f};
 
     // main loop: one super-block (4 stages) per iteration; stage s = 4u + p, ring slot s % 4. The
-    // super-block's min k-step (S x Bmin in units of c_u, tables read at p = 0) runs at p = 1: group g
-    // < 8 adds it to block row (g + 4) % 8, four groups away from that row's own MFMAs on either side.
-    // Rescale to the next super-block's units: block row i two groups after its last MFMA of the
-    // super-block (group 10 + i at p = 3; rows 6 and 7 in the next super-block's groups 0 and 1, ahead
-    // of their first MFMAs there).
+    // previous super-block's min k-step (S of unit u - 1 x its Bmin in units of c_u, read at p = 0)
+    // runs at p = 1: group g < 8 adds it to block row (g + 4) % 8, four groups away from that row's own
+    // MFMAs on either side. Rescale to the next super-block's units: block row i two groups after its
+    // last MFMA of the super-block (group 10 + i at p = 3; rows 6 and 7 in the next super-block's
+    // groups 0 and 1, ahead of their first MFMAs there).
     uint32_t swn[NB];  // the next stage's scale words
     h2 mul0[NB], add0[NB];  // and its k-step 0 multipliers and addends
     for (int u = 0; u < U; u++) {
@@ -299,11 +325,12 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
 #pragma unroll
                     for (int j = 0; j < NB; j++) acc[i][j] = mfma_bf16(bm[j], sa[gg % 3], acc[i][j]);
                 }
-                // sub-block sums of the row the min k-step reaches three groups later (p = 1, group g
-                // < 8: row (g + 4) % 8, read from group 13 of p = 0, after this group's use of the slot)
+                // unit u - 1's sub-block sums of the row the min k-step reaches three groups later (p = 1,
+                // group g < 8: row (g + 4) % 8, read from group 13 of p = 0, after this group's use of
+                // the slot)
                 if ((p == 0 && gg >= 13) || (p == 1 && gg < 5)) {
                     const int g = p == 0 ? gg - 13 : gg + 3;
-                    sa[g % 3] = rds(u & 1, (g + 4) & 7);
+                    sa[g % 3] = rds((u + 1) & 1, (g + 4) & 7);
                 }
                 // this stage's k-step 1 weights, half a column block per group
                 if (gg < 2 * NB) wr_dec_half(b1[gg / 2], qc[gg / 2], gg & 1, 0xf0f0f0f0u, muh[gg / 2], adh[gg / 2]);
@@ -323,8 +350,8 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
                     const int pn = (p + 1) & 3, un = p == 3 ? u + 1 : u;
 #pragma unroll
                     for (int j = 0; j < NB; j++) qc[j] = rdq(nxt, j), swn[j] = rdsw(pn, un, j);
-                    // this super-block's Bmin, before the loaders rewrite the table at p = 2; the
-                    // next one's R (its records land by this barrier at p = 3)
+                    // the previous super-block's Bmin, before the loaders rewrite the table at p = 2;
+                    // the next one's R (its records land by this barrier at p = 3)
                     if (p == 0)
 #pragma unroll
                         for (int j = 0; j < NB; j++) bm[j] = rdbm(j);
@@ -352,10 +379,19 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
             }
         }
     }
-    // ---- output: back to true units (the last super-block's c), then straight from the accumulators:
+    // ---- the last super-block's min k-step (its Bmin, in its own units, and its sums landed by the
+    // last barrier), then back to true units (its c) and straight from the accumulators:
     // lane (ln, lg) of block (i, j) holds row 16i + ln, columns 16j + 4lg .. + 3 of the wave's
     // columns (one 16-byte fp32 or 8-byte fp16 store; element by element at the matrix edge or where
     // N % 4 or C's alignment does not allow it)
+#pragma unroll
+    for (int j = 0; j < NB; j++) bm[j] = rdbm(j);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const h8 si = rds(u_last & 1, i);
+#pragma unroll
+        for (int j = 0; j < NB; j++) acc[i][j] = mfma_bf16(bm[j], si, acc[i][j]);
+    }
 #pragma unroll
     for (int j = 0; j < NB; j++) {
         const f4 cl = rdr(j, U - 1, 3);
@@ -404,9 +440,11 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
 }  // namespace
 
 // Per-column tables of every super-block of a Q4_K matrix (one thread per row, super-blocks in order):
-// for super-block v, Bmin [rows][32 B] = bf16 hi[8], lo[8] of x_i = -dmin * m_i / c_v at v * rows * 48,
-// then records [rows][16 B] = scale words sw0, sw1 (zero where d = 0), R = c_{v-1} / c_v (c_{-1} = 1),
-// CL = c_v; c_v = d_v, or 1 where d_v = 0 (-dmin * m_i is exact in fp32).
+// for super-block v, Bmin [rows][32 B] = bf16 hi[8], lo[8] of x_i = -dmin * m_i / c_{v+1} (the GEMM
+// adds super-block v's min term in the next one's units; the last super-block's in its own, c_v) at
+// v * rows * 48, then records [rows][16 B] = scale words sw0, sw1 (zero where d = 0),
+// R = c_{v-1} / c_v (c_{-1} = 1), CL = c_v; c_v = d_v, or 1 where d_v = 0 (-dmin * m_i is exact in
+// fp32).
 __global__ void __launch_bounds__(256) k_q4k_tables(const uint8_t *W, uint32_t rows, uint32_t nb, uint32_t row_bytes,
                                                     uint8_t *tab) {
     const uint32_t n = blockIdx.x * 256u + threadIdx.x;
@@ -418,7 +456,13 @@ __global__ void __launch_bounds__(256) k_q4k_tables(const uint8_t *W, uint32_t r
         q4k_scale_words(hm.y, hm.z, hm.w, sw0, sw1, mw0, mw1);
         const uint32_t nz = (hm.x & 0x7fffu) ? 0xffffffffu : 0u;
         const float d = h2f((uint16_t)hm.x), dmin = h2f((uint16_t)(hm.x >> 16));
-        const float c = d != 0.0f ? d : 1.0f, inv = 1.0f / c;
+        const float c = d != 0.0f ? d : 1.0f;
+        float cn = c;
+        if (v + 1 < nb) {
+            const float dn = h2f(*(const uint16_t *)(W + (size_t)n * row_bytes + (size_t)(v + 1) * 144));
+            cn = dn != 0.0f ? dn : 1.0f;
+        }
+        const float inv = 1.0f / cn;
         uint32_t bh[4], bl[4];
 #pragma unroll
         for (int q = 0; q < 4; q++) {
@@ -458,15 +502,16 @@ int hq_wr_choose(int M, int N, int n_cu, float *eff) {
 int hq_wr_fits(const hq_dev_mat *W, int M) {
     const size_t lim = (size_t)1 << 32, mr = (size_t)M + WR_BM;
     return W->type == HQ_TYPE_Q4_K && W->cols % 256 == 0 && M >= 1 && mr * W->cols * 2 < lim &&
-           mr * (W->cols / 256) * 32 < lim && ((size_t)W->rows + 64 * 3) * W->row_bytes < lim;
+           ((size_t)W->rows + 64 * 3) * (W->cols / 256) * HQ_Q4K_TAB_BYTES < lim &&
+           ((size_t)W->rows + 64 * 3) * W->row_bytes < lim;
 }
 
-hipError_t hq_launch_gemm_wr(const hq_dev_mat *W, const uint16_t *A, const uint16_t *S, int M, void *C, int c_f32,
-                             int accumulate, hipStream_t st) {
+hipError_t hq_launch_gemm_wr(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
+                             hipStream_t st) {
     if (!hq_wr_fits(W, M) || !W->tab) return hipErrorInvalidValue;  // (every uploaded Q4_K matrix has its tables)
     constexpr int NB = 3;
     WrArgs g;
-    g.W = W->qs, g.row_bytes = (uint32_t)W->row_bytes, g.A = A, g.S = S, g.tab = W->tab;
+    g.W = W->qs, g.row_bytes = (uint32_t)W->row_bytes, g.A = A, g.tab = W->tab;
     g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;
     g.mt = (M + WR_BM - 1) / WR_BM;
     g.nt = (g.N + 64 * NB - 1) / (64 * NB);

@@ -1325,17 +1325,18 @@ void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_by
         *partial_bytes = tiles * rparts * 64 * 64 * sizeof(float);
         *counter_bytes = tiles * sizeof(int);
     }
-    *sums_bytes = c.wide || c.rbm ? (size_t)M * (W->cols / KC) * 32 : 0;
+    *sums_bytes = (c.wide && !c.wr) || c.rbm ? (size_t)M * (W->cols / KC) * 32 : 0;  // (wr forms its own)
 }
 
-// Pre-pass of a GEMM (the wide Q4_K kernel's activation sub-block sums; nothing otherwise).
+// Pre-pass of a GEMM (the activation sub-block sums of the Q4_K kernels that read them from HBM;
+// nothing otherwise: the one-round tile kernel k_gemm_q4_k_wr forms its own).
 hipError_t hq_launch_gemm_pre(const hq_dev_mat *W, const uint16_t *A, int M, const HqGemmWork &wk, hipStream_t st) {
     const GemmCfg c = gemm_cfg(W, M, wk.n_cu);
     if (c.rbm) {
         const size_t nsub = (size_t)M * (W->cols / 32);
         k_asums<true, true><<<grid_for(nsub, 256, 16384), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
     }
-    if (c.wide) {
+    if (c.wide && !c.wr) {
         const size_t nsub = (size_t)M * (W->cols / 32);
         if (nsub >= ((size_t)1 << 31)) return hipErrorInvalidValue;
         if (c.ws_nb || c.bt) k_asums<true><<<grid_for(nsub, 256, 16384), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
@@ -1351,7 +1352,7 @@ hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, vo
     if (c.rbm) return hq_launch_gemm_rb(W, A, wk.sums, M, C, c_f32, accumulate, c.rbm, wk.partials, wk.counters, st);
     if (c.rb8) return hq_launch_gemm_rb8(W, A, M, C, c_f32, accumulate, c.rb8, wk.partials, wk.counters, st);
     if (c.bt) return hq_launch_gemm_bt(W, A, wk.sums, M, C, c_f32, accumulate, st);
-    if (c.wr) return hq_launch_gemm_wr(W, A, wk.sums, M, C, c_f32, accumulate, st);
+    if (c.wr) return hq_launch_gemm_wr(W, A, M, C, c_f32, accumulate, st);
     if (c.ws_nb)
         return hq_launch_gemm_ws(W, A, wk.sums, M, C, c_f32, accumulate, c.ws_nb, c.ws_parts, wk.partials, wk.counters, st);
     if (c.ws8_nb)

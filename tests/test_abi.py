@@ -87,8 +87,9 @@ def test_gemm_workspace_bytes():
     pb, cb, sb, fits = hq.gemm_workspace_bytes(synth.Q4_K, 4096, 2560, 9728)
     assert (pb, cb, fits) == (2 * 256 * 128 * 256 * 4, 32 * 10 * 4, True)
     assert hq.gemm_workspace_bytes(synth.Q4_K, 4096, 9728, 2560) == (0, 0, 4096 * 10 * 32, True)
-    # the 128 x 192 loader-wave kernel (M = 512, N = 9728): one round of tiles, the sub-block sums only
-    assert hq.gemm_workspace_bytes(synth.Q4_K, 512, 9728, 2560) == (0, 0, 512 * 10 * 32, True)
+    # the 128 x 192 loader-wave kernel (M = 512, N = 9728): one round of tiles; its loader waves form
+    # the sub-block sums in LDS, so no workspace at all
+    assert hq.gemm_workspace_bytes(synth.Q4_K, 512, 9728, 2560) == (0, 0, 0, True)
     assert hq.gemm_workspace_bytes(synth.Q8_0, 512, 9728, 2560) == (0, 0, 0, True)
     assert hq.gemm_workspace_bytes(synth.Q4_K, 16384, 2560, 9216)[3]
     assert not hq.gemm_workspace_bytes(synth.Q4_K, 131072, 256, 9216)[3]  # 151 MB of sub-block sums
