@@ -103,7 +103,10 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
     if (nt_i >= g.nt) return;
     const int m0 = mt_i * WR_BM, n0 = nt_i * BN;
     const int M = g.M, N = g.N, K = g.K, U = K / 256, S2 = 4 * U;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, ln = lane & 15, lg = lane >> 4;
+    // (the wave index through readfirstlane: the role and every LDS DMA address derived from it are
+    // then scalar values, not per-lane ones read back with a VALU instruction per DMA)
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, ln = lane & 15,
+              lg = lane >> 4;
     // roles: waves 0-3 multiply (wave w: columns 16NB w .. of the tile, all 128 rows); waves 4-7 load
     // (wave 4 + w: every load for MFMA wave w's columns and tables and a quarter of the shared
     // activation and S tiles)
@@ -138,24 +141,40 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
         if (32 * k + 32 <= WC || lane < 2 * (WC - 32 * k)) dma16_so(rw, dst, q_voff[k], so);
     };
     // activation sub-block sums of stage s (sub-blocks 2p, 2p + 1 of super-block u; s = 4u + p) from
-    // its ring slot into S parity u & 1: lane i of loader wave w sums the 32 values of row
-    // r = 32w + i/2, sub-block 2p + i % 2 (fp32, the order of k_asums: the same bits); the lane pair
-    // swaps sums, then the even lane stores both bf16 hi parts and the odd lane both lo parts
-    const int s_row = 32 * w4 + (lane >> 1), s_h = lane & 1;
-    const uint32_t s_src = lds0 + (uint32_t)(L::A + s_row * 128), s_sw = (uint32_t)((s_row >> 1) & 7);
-    const uint32_t s_dst = lds0 + (uint32_t)(L::S + s_row * 32 + 16 * s_h);
-    auto sums = [&](int s) {
-        const uint32_t src = s_src + (uint32_t)((s & 3) * L::A_BYTES);
-        float v = 0.f;
+    // its ring slot into S parity u & 1, on the matrix core (one VALU instruction on this SIMD costs
+    // the MFMA wave beside it as much as a quarter of an MFMA): loader wave w sums rows 32w + 16b + i
+    // (b = 0, 1) with two MFMAs per row block, activations as the B operand and a 0/1 A operand whose
+    // rows 0-7 select the stage's first sub-block and rows 8-15 the second. Lane (i, q) then holds the
+    // fp32 sum of row 32w + 16b + i, sub-block 2p + h for b = q & 1, h = q >> 1 (exact products, fp32
+    // sums) and stores its bf16 hi and lo parts
+    const int s_b = lg & 1, s_h = lg >> 1;
+    uint32_t s_src[2][2];
 #pragma unroll
-        for (int t = 0; t < 4; t++)
-            v = sum8(*(const __attribute__((address_space(3))) u4v *)(uintptr_t)(src + 16u * ((uint32_t)(4 * s_h + t) ^ s_sw)), v);
-        const float o = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false));
-        const float v0 = s_h ? o : v, v1 = s_h ? v : o;
-        const __bf16 h0 = (__bf16)v0, h1 = (__bf16)v1;
-        const __bf16 e0 = s_h ? (__bf16)(v0 - (float)h0) : h0, e1 = s_h ? (__bf16)(v1 - (float)h1) : h1;
-        *(__attribute__((address_space(3))) uint32_t *)(uintptr_t)(s_dst + (uint32_t)(((s >> 2) & 1) * L::S_BYTES + 4 * (s & 3))) =
-            (uint32_t)__builtin_bit_cast(uint16_t, e0) | ((uint32_t)__builtin_bit_cast(uint16_t, e1) << 16);
+    for (int b = 0; b < 2; b++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int row = 32 * w4 + 16 * b + ln;
+            s_src[b][h] = lds0 + (uint32_t)(L::A + row * 128) + 16u * ((uint32_t)(4 * h + lg) ^ (uint32_t)((row >> 1) & 7));
+        }
+    const uint32_t s_dst = lds0 + (uint32_t)(L::S + (32 * w4 + 16 * s_b + ln) * 32 + 2 * s_h);
+    const _Float16 one_lo = (_Float16)(ln < 8 ? 1.0f : 0.0f), one_hi = (_Float16)(ln < 8 ? 0.0f : 1.0f);
+    const h8 sel0 = {one_lo, one_lo, one_lo, one_lo, one_lo, one_lo, one_lo, one_lo};
+    const h8 sel1 = {one_hi, one_hi, one_hi, one_hi, one_hi, one_hi, one_hi, one_hi};
+    auto sums = [&](int s) {
+        using lds_h8 = const __attribute__((address_space(3))) h8;
+        const uint32_t so = (uint32_t)((s & 3) * L::A_BYTES);
+        f4 c[2];
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            const h8 x0 = *(lds_h8 *)(uintptr_t)(s_src[b][0] + so), x1 = *(lds_h8 *)(uintptr_t)(s_src[b][1] + so);
+            c[b] = mfma(sel1, x1, mfma(sel0, x0, f4{0.f, 0.f, 0.f, 0.f}));
+        }
+        const float v = s_b ? c[1][0] : c[0][0];
+        const __bf16 hi = (__bf16)v, lo = (__bf16)(v - (float)hi);
+        using lds_u16 = __attribute__((address_space(3))) uint16_t;
+        const uint32_t d = s_dst + (uint32_t)(((s >> 2) & 1) * L::S_BYTES + 4 * (s & 3));
+        *(lds_u16 *)(uintptr_t)d = __builtin_bit_cast(uint16_t, hi);
+        *(lds_u16 *)(uintptr_t)(d + 16) = __builtin_bit_cast(uint16_t, lo);
     };
     // tables of MFMA wave w4's columns into its table area: Bmin of super-block u (1536 bytes, two
     // instructions), the records of super-block u in parity u & 1 (768 bytes, lanes < WC)
