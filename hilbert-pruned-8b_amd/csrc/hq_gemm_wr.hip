@@ -69,15 +69,16 @@ struct WrLds {
     static constexpr int Q = WR_RING * A_BYTES, Q_WAVE = WC * 32;        // per wave and ring slot
     static constexpr int Q_BYTES = 4 * Q_WAVE;                           // per ring slot
     static constexpr int S = Q + WR_RING * Q_BYTES, S_BYTES = WR_BM * 32;  // per parity
-    static constexpr int T = S + 2 * S_BYTES;                            // per-wave tables
-    static constexpr int T_BM = 0, T_REC = WC * 32;                      // REC: 2 parities
-    static constexpr int T_WAVE = T_REC + 2 * WC * 16;
-    static constexpr int MAIN = T + 4 * T_WAVE;
-    static constexpr int TOTAL = MAIN;
+    static constexpr int T_BM = S + 2 * S_BYTES;                         // column tables: Bmin [BN][32 B],
+    static constexpr int T_REC = T_BM + BN * 32;                         // records [2][BN][16 B]
+    static constexpr int TOTAL = T_REC + 2 * BN * 16;
     static_assert(TOTAL <= 160 * 1024, "LDS budget");
 };
 
 DEV void wr_barrier() { asm volatile("s_barrier" ::: "memory"); }
+// a loader wave's wait before a barrier: every LDS DMA but the last n issued, and its LDS stores
+template <int n>
+DEV void wr_wait() { asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(n) : "memory"); }
 // keeps a computed operand in the group that computes it (the compiler would otherwise sink the work
 // to the operand's first use)
 DEV void wr_pin(h8 &x) { asm volatile("" : "+v"(x)); }
@@ -94,7 +95,8 @@ DEV void wr_dec_half(h8 &b, u2v q, int hf, uint32_t mask, h2 mul, h2 add) {
 template <int NB>
 __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
     using L = WrLds<NB>;
-    constexpr int BN = L::BN, WC = L::WC, QI = (WC + 31) / 32;  // quant DMA instructions per wave
+    constexpr int BN = L::BN, WC = L::WC;
+    static_assert(NB == 3, "the loaders' DMA schedule is written for 192-column tiles");
     __shared__ __attribute__((aligned(256))) char lds[L::TOTAL];
     // tile: XCD x = b % 8 takes N-tiles x, x + 8, ...; its slots run over the M-tiles of one N-tile
     // first (the weight slab is then fetched once per XCD)
@@ -108,13 +110,13 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, ln = lane & 15,
               lg = lane >> 4;
     // roles: waves 0-3 multiply (wave w: columns 16NB w .. of the tile, all 128 rows); waves 4-7 load
-    // (wave 4 + w: every load for MFMA wave w's columns and tables and a quarter of the shared
-    // activation and S tiles)
+    // (wave 4 + w: a quarter of the activation tile and of its sub-block sums, and a share of the quant
+    // groups and column tables)
     const int role = wave >> 2, w4 = wave & 3;
     const rsrc_t ra = make_rsrc(g.A, (uint32_t)((size_t)M * K * 2));
     const rsrc_t rw = make_rsrc(g.W, (uint32_t)((size_t)N * g.row_bytes));
     const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
-    const int nw = n0 + WC * w4;  // first column of MFMA wave w4
+    const int wc0 = WC * w4, nw = n0 + wc0;  // first column of MFMA wave w4 (in the tile, in W)
 
     // ---- loads. Activation DMA of stage s into ring slot buf: instruction q (0..3) of wave w fills rows
     // 8(4w + q) .. + 8; lane i: row r = 8(4w + q) + i/8, LDS slot i % 8, global chunk
@@ -127,18 +129,17 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
         dma16_so(ra, lds0 + (uint32_t)(L::A + buf * L::A_BYTES + w4 * 4096 + q * 1024), q & 1 ? a_voff1 : a_voff0,
                  (uint32_t)(q * 8 * K * 2 + s * WR_KS * 2));
     };
-    // quant DMA of stage s (the wave's own columns): instruction k, lane i: column c = 32k + i/2, LDS
-    // half i % 2 of the column's 32 bytes, holding the group's half (i % 2) ^ ((c >> 3) & 1)
-    uint32_t q_voff[QI];
-#pragma unroll
-    for (int k = 0; k < QI; k++) {
-        const int c = 32 * k + (lane >> 1), cc = c < WC ? c : WC - 1;
-        q_voff[k] = (uint32_t)(nw + cc) * g.row_bytes + 16u * (uint32_t)((lane & 1) ^ ((c >> 3) & 1));
-    }
-    auto dma_q1 = [&](int s, int buf, int k) {
-        const uint32_t dst = lds0 + (uint32_t)(L::Q + buf * L::Q_BYTES + w4 * L::Q_WAVE + k * 1024);
-        const uint32_t so = (uint32_t)((s >> 2) * 144 + 16 + 32 * (s & 3));
-        if (32 * k + 32 <= WC || lane < 2 * (WC - 32 * k)) dma16_so(rw, dst, q_voff[k], so);
+    // quant DMA of stage s, 32 of the tile's 192 columns per instruction: instruction k (wave w issues
+    // k = w, and k = 4 + w for w < 2), lane i: column c = 32k + i/2, LDS half i % 2 of the column's 32
+    // bytes, holding the group's half (i % 2) ^ ((c >> 3) & 1)
+    constexpr int QK = 2 * NB;
+    const int qw = w4 + 4 < QK ? 2 : 1;  // this wave's quant DMAs per stage
+    const uint32_t q_voff = (uint32_t)(n0 + (lane >> 1)) * g.row_bytes + 16u * (uint32_t)((lane & 1) ^ ((lane >> 4) & 1));
+    auto dma_q1 = [&](int s, int buf, int t) {
+        const int k = w4 + 4 * t;
+        const uint32_t dst = lds0 + (uint32_t)(L::Q + buf * L::Q_BYTES + k * 1024);
+        const uint32_t so = (uint32_t)((s >> 2) * 144 + 16 + 32 * (s & 3)) + (uint32_t)(32 * k) * g.row_bytes;
+        dma16_so(rw, dst, q_voff, so);
     };
     // activation sub-block sums of stage s (sub-blocks 2p, 2p + 1 of super-block u; s = 4u + p) from
     // its ring slot into S parity u & 1, on the matrix core (one VALU instruction on this SIMD costs
@@ -176,19 +177,17 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
         *(lds_u16 *)(uintptr_t)d = __builtin_bit_cast(uint16_t, hi);
         *(lds_u16 *)(uintptr_t)(d + 16) = __builtin_bit_cast(uint16_t, lo);
     };
-    // tables of MFMA wave w4's columns into its table area: Bmin of super-block u (1536 bytes, two
-    // instructions), the records of super-block u in parity u & 1 (768 bytes, lanes < WC)
+    // column tables of the tile, 1 KB per instruction: Bmin of super-block u, instruction k (0..5):
+    // columns 32k .. + 32; the records of super-block u in parity u & 1, instruction k (0..2): columns
+    // 64k .. + 64. Loader waves 2 and 3 issue them (they have one quant DMA per stage, waves 0 and 1 two)
     const rsrc_t rt = make_rsrc(g.tab, (uint32_t)((size_t)N * U * HQ_Q4K_TAB_BYTES));
-    const uint32_t tw = lds0 + (uint32_t)(L::T + w4 * L::T_WAVE);
-    auto dma_bm = [&](int u) {
-        const uint32_t so = (uint32_t)u * (uint32_t)N * HQ_Q4K_TAB_BYTES + (uint32_t)nw * 32u;
-        dma16_so(rt, tw + L::T_BM, 16u * (uint32_t)lane, so);
-        if (lane < WC * 2 - 64) dma16_so(rt, tw + L::T_BM + 1024, 16u * (uint32_t)lane, so + 1024u);
+    auto dma_bm = [&](int u, int k) {
+        dma16_so(rt, lds0 + (uint32_t)(L::T_BM + 1024 * k), 16u * (uint32_t)lane,
+                 (uint32_t)u * (uint32_t)N * HQ_Q4K_TAB_BYTES + (uint32_t)(n0 + 32 * k) * 32u);
     };
-    auto dma_rec = [&](int u) {
-        if (lane < WC)
-            dma16_so(rt, tw + L::T_REC + (uint32_t)((u & 1) * WC * 16), 16u * (uint32_t)lane,
-                     (uint32_t)u * (uint32_t)N * HQ_Q4K_TAB_BYTES + (uint32_t)N * 32u + (uint32_t)nw * 16u);
+    auto dma_rec = [&](int u, int k) {
+        dma16_so(rt, lds0 + (uint32_t)(L::T_REC + (u & 1) * BN * 16 + 1024 * k), 16u * (uint32_t)lane,
+                 (uint32_t)u * (uint32_t)N * HQ_Q4K_TAB_BYTES + (uint32_t)N * 32u + (uint32_t)(n0 + 64 * k) * 16u);
     };
 
     // ---- operand addresses. Activation fragment of row block i, k-step f, ring slot buf: lane (ln, lg)
@@ -206,8 +205,8 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
     };
     // scale word p / 2 of column block j in super-block v, shifted to sub-blocks 2p, 2p + 1 in its low bytes
     auto rdsw = [&](int p, int v, int j) {
-        return *(const __attribute__((address_space(3))) uint32_t *)(uintptr_t)(tw + (uint32_t)(L::T_REC + ((v & 1) * WC + 16 * j + ln) * 16 +
-                                                                                                 (p >> 1) * 4)) >>
+        return *(const __attribute__((address_space(3))) uint32_t *)(uintptr_t)(lds0 + (uint32_t)(L::T_REC + ((v & 1) * BN + wc0 + 16 * j + ln) * 16 +
+                                                                                                   (p >> 1) * 4)) >>
                ((p & 1) * 16);
     };
     const uint32_t s_lane = lds0 + (uint32_t)(L::S + ln * 32 + 16 * (lg & 1));
@@ -215,14 +214,14 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
         return *(const __attribute__((address_space(3))) h8 *)(uintptr_t)(s_lane + (uint32_t)(par * L::S_BYTES + i * 16 * 32));
     };
     auto rdbm = [&](int j) {
-        return *(const __attribute__((address_space(3))) h8 *)(uintptr_t)(tw + (uint32_t)(L::T_BM + (16 * j + ln) * 32 + 16 * (lg >> 1)));
+        return *(const __attribute__((address_space(3))) h8 *)(uintptr_t)(lds0 + (uint32_t)(L::T_BM + (wc0 + 16 * j + ln) * 32 + 16 * (lg >> 1)));
     };
     // field f (2: R, 3: CL) of the records of columns 16j + 4lg .. + 3 of super-block v
     auto rdr = [&](int j, int v, int f) {
         f4 r;
 #pragma unroll
         for (int c = 0; c < 4; c++)
-            r[c] = *(const __attribute__((address_space(3))) float *)(uintptr_t)(tw + (uint32_t)(L::T_REC + ((v & 1) * WC + 16 * j + 4 * lg + c) * 16 + 4 * f));
+            r[c] = *(const __attribute__((address_space(3))) float *)(uintptr_t)(lds0 + (uint32_t)(L::T_REC + ((v & 1) * BN + wc0 + 16 * j + 4 * lg + c) * 16 + 4 * f));
         return r;
     };
 
@@ -244,37 +243,36 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
     if (role == 1) {
         // ------------------------------------------------------------------------------ loaders
         // prologue: stage 0 of activations and quants, the records of unit 0, then stage 1, which (as
-        // in every loader stage) is still in flight at the barrier. S parity 1 and Bmin are zeroed:
-        // the min step of unit 0 (the late one of unit -1) adds exact zeros
+        // in every loader stage) is still in flight at the barrier. S parity 1 is zeroed: the min step
+        // of unit 0 (the late one of unit -1, with Bmin zero in the MFMA waves' registers) adds zeros
 #pragma unroll
         for (int q = 0; q < 4; q++) dma_a1(0, 0, q);
-#pragma unroll
-        for (int k = 0; k < QI; k++) dma_q1(0, 0, k);
-        dma_rec(0);
-        {
-            using lds_u4 = __attribute__((address_space(3))) u4v;
-            const u4v z = {0u, 0u, 0u, 0u};
-            *(lds_u4 *)(uintptr_t)(lds0 + (uint32_t)(L::S + L::S_BYTES + w4 * 1024 + 16 * lane)) = z;
-            *(lds_u4 *)(uintptr_t)(tw + (uint32_t)(L::T_BM + 16 * lane)) = z;
-            if (lane < WC * 2 - 64) *(lds_u4 *)(uintptr_t)(tw + (uint32_t)(L::T_BM + 1024 + 16 * lane)) = z;
-        }
+        dma_q1(0, 0, 0);
+        if (qw == 2) dma_q1(0, 0, 1);
+        if (w4 == 2) dma_rec(0, 0), dma_rec(0, 2);
+        if (w4 == 3) dma_rec(0, 1);
+        *(__attribute__((address_space(3))) u4v *)(uintptr_t)(lds0 + (uint32_t)(L::S + L::S_BYTES + w4 * 1024 + 16 * lane)) =
+            u4v{0u, 0u, 0u, 0u};
         {
             const int s1 = S2 > 1 ? 1 : 0;
 #pragma unroll
             for (int q = 0; q < 4; q++) dma_a1(s1, 1, q);
-#pragma unroll
-            for (int k = 0; k < QI; k++) dma_q1(s1, 1, k);
+            dma_q1(s1, 1, 0);
+            if (qw == 2) dma_q1(s1, 1, 1);
         }
-        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(4 + QI) : "memory");
+        if (qw == 2) wr_wait<6>();
+        else wr_wait<5>();
         wr_barrier();
         // loader stage s = 4u + p runs between the MFMA waves' barriers of stages s - 1 and s (the
         // prologue's barrier counts as stage -1's), while they finish stage s - 1 and start stage s:
-        // the loads of stage s + 2 (ring slot (s + 2) % 4, last read in stage s - 2), at p = 2 Bmin of
-        // unit u (unit u - 1's was read at p = 0) and the records of unit u + 1 (unit u - 1's are done
-        // with); the sums of stage s (landed by the last barrier); then wait for everything but this
-        // stage's loads (stage s + 1's land: each load has two stages) and for the sums' stores, and
-        // meet the MFMA waves at their barrier. Past the last unit the record loads repeat it (same
-        // bytes).
+        // the loads of stage s + 2 (ring slot (s + 2) % 4, last read in stage s - 2); the records of
+        // unit u + 1 at p = 0, 1 (parity (u + 1) & 1: unit u - 1's were last read in stage 4u - 2) and
+        // Bmin of unit u at p = 1, 2 (unit u - 1's was read in stage 4u - 1, it is read in stage 4u + 3);
+        // the sums of stage s (landed by the last barrier); then wait for everything but this stage's
+        // loads (stage s + 1's land: each load has two stages) and for the sums' stores, and meet the
+        // MFMA waves at their barrier. Per stage a loader wave issues 4 activation DMAs, 2 (waves 0, 1)
+        // or 1 (waves 2, 3) quant DMAs and, waves 2 and 3, 0 to 2 table DMAs. Past the last unit the
+        // record loads repeat it (same bytes).
         for (int u = 0; u < U; u++) {
             const int u_next = u < u_last ? u + 1 : u_last;
 #pragma unroll
@@ -282,12 +280,22 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
                 const int s = 4 * u + p, ld = (s + 2) & 3, s_src = s + 2 < S2 ? s + 2 : S2 - 1;
 #pragma unroll
                 for (int q = 0; q < 4; q++) dma_a1(s_src, ld, q);
-#pragma unroll
-                for (int k = 0; k < QI; k++) dma_q1(s_src, ld, k);
-                if (p == 2) dma_bm(u), dma_rec(u_next);
+                dma_q1(s_src, ld, 0);
+                if (qw == 2) dma_q1(s_src, ld, 1);
+                if (w4 == 2) {
+                    if (p == 0) dma_rec(u_next, 0);
+                    if (p == 1) dma_rec(u_next, 2);
+                    if (p == 2) dma_bm(u, 2), dma_bm(u, 3);
+                } else if (w4 == 3) {
+                    if (p == 0) dma_rec(u_next, 1);
+                    if (p == 1) dma_bm(u, 0), dma_bm(u, 1);
+                    if (p == 2) dma_bm(u, 4), dma_bm(u, 5);
+                }
                 sums(s);
-                if (p == 2) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(4 + QI + 3) : "memory");
-                else asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(4 + QI) : "memory");
+                if (qw == 2) wr_wait<6>();
+                else if (p == 3) wr_wait<5>();
+                else if (p == 0 || (p == 1 && w4 == 2)) wr_wait<6>();
+                else wr_wait<7>();
                 wr_barrier();
             }
         }
@@ -315,14 +323,14 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
     h8 bm[NB], sa[3];
     f4 r[NB];
 #pragma unroll
-    for (int j = 0; j < NB; j++) r[j] = f4{1.f, 1.f, 1.f, 1.f};
+    for (int j = 0; j < NB; j++) r[j] = f4{1.f, 1.f, 1.f, 1.f}, bm[j] = h8{};
 
     // main loop: one super-block (4 stages) per iteration; stage s = 4u + p, ring slot s % 4. The
-    // previous super-block's min k-step (S of unit u - 1 x its Bmin in units of c_u, read at p = 0)
-    // runs at p = 1: group g < 8 adds it to block row (g + 4) % 8, four groups away from that row's own
-    // MFMAs on either side. Rescale to the next super-block's units: block row i two groups after its
-    // last MFMA of the super-block (group 10 + i at p = 3; rows 6 and 7 in the next super-block's
-    // groups 0 and 1, ahead of their first MFMAs there).
+    // previous super-block's min k-step (S of unit u - 1 x its Bmin in units of c_u, read at p = 3 of
+    // unit u - 1) runs at p = 1: group g < 8 adds it to block row (g + 4) % 8, four groups away from
+    // that row's own MFMAs on either side. Rescale to the next super-block's units: block row i two
+    // groups after its last MFMA of the super-block (group 10 + i at p = 3; rows 6 and 7 in the next
+    // super-block's groups 0 and 1, ahead of their first MFMAs there).
     uint32_t swn[NB];  // the next stage's scale words
     h2 mul0[NB], add0[NB];  // and its k-step 0 multipliers and addends
     for (int u = 0; u < U; u++) {
@@ -369,14 +377,12 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
                     const int pn = (p + 1) & 3, un = p == 3 ? u + 1 : u;
 #pragma unroll
                     for (int j = 0; j < NB; j++) qc[j] = rdq(nxt, j), swn[j] = rdsw(pn, un, j);
-                    // the previous super-block's Bmin, before the loaders rewrite the table at p = 2;
-                    // the next one's R (its records land by this barrier at p = 3)
-                    if (p == 0)
-#pragma unroll
-                        for (int j = 0; j < NB; j++) bm[j] = rdbm(j);
+                    // at p = 3 this super-block's Bmin (landed by this barrier; the loaders rewrite it
+                    // from p = 1 of the next one) and the next one's R (its records have landed)
                     if (p == 3)
 #pragma unroll
                         for (int j = 0; j < NB; j++) {
+                            bm[j] = rdbm(j);
                             const f4 rn = rdr(j, u + 1, 2);
 #pragma unroll
                             for (int c = 0; c < 4; c++) r[j][c] = more ? rn[c] : 1.0f;
@@ -398,13 +404,11 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
             }
         }
     }
-    // ---- the last super-block's min k-step (its Bmin, in its own units, and its sums landed by the
-    // last barrier), then back to true units (its c) and straight from the accumulators:
+    // ---- the last super-block's min k-step (its Bmin, in its own units, read at p = 3, and its sums
+    // landed by the last barrier), then back to true units (its c) and straight from the accumulators:
     // lane (ln, lg) of block (i, j) holds row 16i + ln, columns 16j + 4lg .. + 3 of the wave's
     // columns (one 16-byte fp32 or 8-byte fp16 store; element by element at the matrix edge or where
     // N % 4 or C's alignment does not allow it)
-#pragma unroll
-    for (int j = 0; j < NB; j++) bm[j] = rdbm(j);
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const h8 si = rds(u_last & 1, i);
@@ -417,7 +421,10 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
 #pragma unroll
         for (int i = 0; i < 8; i++) acc[i][j] *= cl;
     }
+    // (vector stores write through to memory: SC1, measured faster than write-back here, where every
+    // tile stores its whole output at the end)
     const bool vec = (N & 3) == 0 && ((uintptr_t)g.C & (g.c_f32 ? 15u : 7u)) == 0;
+    const rsrc_t rc = make_rsrc(g.C, (uint32_t)((size_t)M * N * (g.c_f32 ? 4 : 2)));
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const int m = m0 + 16 * i + ln;
@@ -430,15 +437,15 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
             f4 v = acc[i][j];
             if (vec) {
                 if (g.c_f32) {
-                    f4 *q = (f4 *)((float *)g.C + idx);
-                    *q = g.accumulate ? *q + v : v;
+                    if (g.accumulate) v += *(const f4 *)((const float *)g.C + idx);
+                    buf_store16(rc, v, (uint32_t)(idx * 4), 0u);
                 } else {
-                    h4 *q = (h4 *)((_Float16 *)g.C + idx);
                     if (g.accumulate) {
-                        const h4 o = *q;
+                        const h4 o = *(const h4 *)((const _Float16 *)g.C + idx);
                         v += f4{(float)o[0], (float)o[1], (float)o[2], (float)o[3]};
                     }
-                    *q = h4{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+                    const h4 hv = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+                    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2v, hv), rc, (uint32_t)(idx * 2), 0u, CPOL_SC1);
                 }
             } else {
 #pragma unroll
@@ -517,10 +524,10 @@ int hq_wr_choose(int M, int N, int n_cu, float *eff) {
     return nb;
 }
 
-// every byte offset of the kernel (tile rows and columns past the matrix included) fits 32 bits
+// every byte offset of the kernel (tile rows and columns past the matrix included, C's) fits 32 bits
 int hq_wr_fits(const hq_dev_mat *W, int M) {
     const size_t lim = (size_t)1 << 32, mr = (size_t)M + WR_BM;
-    return W->type == HQ_TYPE_Q4_K && W->cols % 256 == 0 && M >= 1 && mr * W->cols * 2 < lim &&
+    return W->type == HQ_TYPE_Q4_K && W->cols % 256 == 0 && M >= 1 && mr * W->cols * 2 < lim && (size_t)M * W->rows * 4 < lim &&
            ((size_t)W->rows + 64 * 3) * (W->cols / 256) * HQ_Q4K_TAB_BYTES < lim &&
            ((size_t)W->rows + 64 * 3) * W->row_bytes < lim;
 }
