@@ -249,7 +249,7 @@ static int upload_rows(int type, uint32_t rows, uint32_t cols, F row_ptr, int de
     m->m.cols = cols;
     m->m.row_bytes = drb;
     m->m.ldd = type == HQ_GGML_Q8_0 ? (int)ldd : 0;
-    m->bytes = tab_bytes ? tab_at + tab_bytes : dev_bytes;
+    m->bytes = tab_bytes ? tab_at + tab_bytes + HQ_Q4K_TAB_PAD : dev_bytes;
     hipError_t e = hipMalloc(&m->alloc, m->bytes);
     if (e != hipSuccess) {
         free(m);
@@ -267,6 +267,8 @@ static int upload_rows(int type, uint32_t rows, uint32_t cols, F row_ptr, int de
         return fail("%s: %s", who, hipGetErrorString(err));
     };
     if (type == HQ_GGML_Q8_0 && (e = hipMemsetAsync(base, 0, dev_bytes, u->st)) != hipSuccess) return fail_free(e);
+    if (tab_bytes && (e = hipMemsetAsync(base + tab_at + tab_bytes, 0, HQ_Q4K_TAB_PAD, u->st)) != hipSuccess)
+        return fail_free(e);
     const uint32_t rows_per = (uint32_t)(UP_CHUNK / rb < rows ? UP_CHUNK / rb : rows);
     bool used[2] = {false, false};
     for (uint32_t r0 = 0, i = 0; r0 < rows; r0 += rows_per, i++) {

@@ -98,13 +98,15 @@ __global__ void __launch_bounds__(BT_NT) k_gemm_q4_k_bt(BtArgs g) {
     // ---- activation DMA: instruction q (0..3) of wave w fills rows 8(4w + q) .. + 8 of a buffer;
     // lane i: row r = 8(4w + q) + i/8, LDS slot i % 8, global 8-value chunk (i % 8) ^ ((r >> 1) & 7),
     // which is the q = 0 chunk ^ 4 for odd q
+    // (the row in the VGPR offset, the one a buffer load range-checks: rows past M read zeros and no
+    // load reads past the end of A)
     const int a_row0 = 32 * wave + (lane >> 3);
     const uint32_t a_ch = (uint32_t)((lane & 7) ^ ((a_row0 >> 1) & 7));
-    const uint32_t a_rowoff = (uint32_t)(m0 + a_row0) * (uint32_t)K * 2u;
-    const uint32_t a_voff0 = a_rowoff + 16u * a_ch, a_voff1 = a_rowoff + 16u * (a_ch ^ 4u);
+    uint32_t a_voff[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) a_voff[q] = (uint32_t)(m0 + a_row0 + 8 * q) * (uint32_t)K * 2u + 16u * (q & 1 ? a_ch ^ 4u : a_ch);
     auto dma_a1 = [&](int s, int buf, int q) {
-        dma16_so(ra, lds0 + (uint32_t)(L::A + buf * L::A_BYTES + wave * 4096 + q * 1024), q & 1 ? a_voff1 : a_voff0,
-                 (uint32_t)(q * 8 * K * 2 + s * BT_KS * 2));
+        dma16_so(ra, lds0 + (uint32_t)(L::A + buf * L::A_BYTES + wave * 4096 + q * 1024), a_voff[q], (uint32_t)(s * BT_KS * 2));
     };
     auto dma_a = [&](int s, int buf) {
 #pragma unroll

@@ -118,28 +118,32 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
     const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
     const int wc0 = WC * w4, nw = n0 + wc0;  // first column of MFMA wave w4 (in the tile, in W)
 
-    // ---- loads. Activation DMA of stage s into ring slot buf: instruction q (0..3) of wave w fills rows
+    // ---- loads. A buffer load checks only its VGPR offset against the buffer's size (the scalar offset
+    // is not range-checked), so every row and column index is in the VGPR offset: rows past M and
+    // columns past N read zeros, and no load reads past the end of A or W.
+    // Activation DMA of stage s into ring slot buf: instruction q (0..3) of wave w fills rows
     // 8(4w + q) .. + 8; lane i: row r = 8(4w + q) + i/8, LDS slot i % 8, global chunk
     // (i % 8) ^ ((r >> 1) & 7) (the q = 0 chunk ^ 4 for odd q)
     const int a_row0 = 32 * w4 + (lane >> 3);
     const uint32_t a_ch = (uint32_t)((lane & 7) ^ ((a_row0 >> 1) & 7));
-    const uint32_t a_rowoff = (uint32_t)(m0 + a_row0) * (uint32_t)K * 2u;
-    const uint32_t a_voff0 = a_rowoff + 16u * a_ch, a_voff1 = a_rowoff + 16u * (a_ch ^ 4u);
+    uint32_t a_voff[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) a_voff[q] = (uint32_t)(m0 + a_row0 + 8 * q) * (uint32_t)K * 2u + 16u * (q & 1 ? a_ch ^ 4u : a_ch);
     auto dma_a1 = [&](int s, int buf, int q) {
-        dma16_so(ra, lds0 + (uint32_t)(L::A + buf * L::A_BYTES + w4 * 4096 + q * 1024), q & 1 ? a_voff1 : a_voff0,
-                 (uint32_t)(q * 8 * K * 2 + s * WR_KS * 2));
+        dma16_so(ra, lds0 + (uint32_t)(L::A + buf * L::A_BYTES + w4 * 4096 + q * 1024), a_voff[q], (uint32_t)(s * WR_KS * 2));
     };
     // quant DMA of stage s, 32 of the tile's 192 columns per instruction: instruction k (wave w issues
     // k = w, and k = 4 + w for w < 2), lane i: column c = 32k + i/2, LDS half i % 2 of the column's 32
     // bytes, holding the group's half (i % 2) ^ ((c >> 3) & 1)
     constexpr int QK = 2 * NB;
     const int qw = w4 + 4 < QK ? 2 : 1;  // this wave's quant DMAs per stage
-    const uint32_t q_voff = (uint32_t)(n0 + (lane >> 1)) * g.row_bytes + 16u * (uint32_t)((lane & 1) ^ ((lane >> 4) & 1));
+    uint32_t q_voff[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+        q_voff[t] = (uint32_t)(n0 + 32 * (w4 + 4 * t) + (lane >> 1)) * g.row_bytes + 16u * (uint32_t)((lane & 1) ^ ((lane >> 4) & 1));
     auto dma_q1 = [&](int s, int buf, int t) {
-        const int k = w4 + 4 * t;
-        const uint32_t dst = lds0 + (uint32_t)(L::Q + buf * L::Q_BYTES + k * 1024);
-        const uint32_t so = (uint32_t)((s >> 2) * 144 + 16 + 32 * (s & 3)) + (uint32_t)(32 * k) * g.row_bytes;
-        dma16_so(rw, dst, q_voff, so);
+        const uint32_t dst = lds0 + (uint32_t)(L::Q + buf * L::Q_BYTES + (w4 + 4 * t) * 1024);
+        dma16_so(rw, dst, q_voff[t], (uint32_t)((s >> 2) * 144 + 16 + 32 * (s & 3)));
     };
     // activation sub-block sums of stage s (sub-blocks 2p, 2p + 1 of super-block u; s = 4u + p) from
     // its ring slot into S parity u & 1, on the matrix core (one VALU instruction on this SIMD costs
@@ -179,7 +183,9 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
     };
     // column tables of the tile, 1 KB per instruction: Bmin of super-block u, instruction k (0..5):
     // columns 32k .. + 32; the records of super-block u in parity u & 1, instruction k (0..2): columns
-    // 64k .. + 64. Loader waves 2 and 3 issue them (they have one quant DMA per stage, waves 0 and 1 two)
+    // 64k .. + 64. Loader waves 2 and 3 issue them (they have one quant DMA per stage, waves 0 and 1 two).
+    // Past column N these read other table bytes (the upload leaves HQ_Q4K_TAB_PAD zero bytes after the
+    // tables for the last tile's), used only for outputs that are not stored
     const rsrc_t rt = make_rsrc(g.tab, (uint32_t)((size_t)N * U * HQ_Q4K_TAB_BYTES));
     auto dma_bm = [&](int u, int k) {
         dma16_so(rt, lds0 + (uint32_t)(L::T_BM + 1024 * k), 16u * (uint32_t)lane,

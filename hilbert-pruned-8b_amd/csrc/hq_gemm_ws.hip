@@ -171,11 +171,12 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
         const int pt = tid - 256, xi = pt & 7;
         const rsrc_t rs = make_rsrc(Sb, (uint32_t)((size_t)M * UT * 32 - (size_t)u0 * 32));
         // activation DMA: instruction qq of wave pw fills rows 4(pw + 4qq) .. +4 (1 KB); lane l takes
-        // row 4(pw + 4qq) + l/16, LDS slot l % 16, global chunk (l % 16) ^ (row & 15)
+        // row 4(pw + 4qq) + l/16, LDS slot l % 16, global chunk (l % 16) ^ (row & 15) (the row in the
+        // VGPR offset, the one a buffer load range-checks: rows past M read zeros, none past A's end)
         const int arow = 4 * pw + (lane >> 4);
         const uint32_t a_voff = (uint32_t)(((m0 + arow) * K + 8 * ((lane & 15) ^ (arow & 15))) * 2);
         auto dma_a = [&](int s, int qq) {
-            dma16(ra, sA(s & 1) + (pw + 4 * qq) * 512, a_voff, (uint32_t)(qq * 16 * K * 2 + s * WS_KS * 2));
+            dma16(ra, sA(s & 1) + (pw + 4 * qq) * 512, a_voff + (uint32_t)(qq * 16 * K * 2), (uint32_t)(s * WS_KS * 2));
         };
         // S tile of unit u: 32 rows (1 KB) per wave; lane l: row 32pw + l/2, half l % 2
         const uint32_t s_voff = (uint32_t)(((m0 + 32 * pw + (lane >> 1)) * UT) * 32 + 16 * (lane & 1));
@@ -572,7 +573,7 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q8_0_ws(Ws8Args g) {
         const int arow = 4 * pw + (lane >> 4);
         const uint32_t a_voff = (uint32_t)(((m0 + arow) * K + 8 * ((lane & 15) ^ (arow & 15))) * 2);
         auto dma_a = [&](int s, int qq) {
-            dma16(ra, sA(s & 1) + (pw + 4 * qq) * 512, a_voff, (uint32_t)(qq * 16 * K * 2 + s * WS_KS * 2));
+            dma16(ra, sA(s & 1) + (pw + 4 * qq) * 512, a_voff + (uint32_t)(qq * 16 * K * 2), (uint32_t)(s * WS_KS * 2));
         };
         uint32_t q_voff[NB], d_voff[NB];
 #pragma unroll

@@ -21,6 +21,8 @@ typedef struct {
 
 // Q4_K column tables: HQ_Q4K_TAB_BYTES per row and super-block (Bmin hi / lo, scale words, R, CL)
 #define HQ_Q4K_TAB_BYTES 48u
+// zero bytes after a matrix's tables: the GEMM's table loads for the columns of its last tile past N
+#define HQ_Q4K_TAB_PAD 8192u
 hipError_t hq_launch_q4k_tables(const hq_dev_mat *W, uint8_t *tab, hipStream_t st);
 
 // The device view and device of a resident matrix (hq_api.hip), for the library's own host code.
