@@ -70,8 +70,8 @@ struct WrLds {
     static constexpr int Q_BYTES = 4 * Q_WAVE;                           // per ring slot
     static constexpr int S = Q + WR_RING * Q_BYTES, S_BYTES = WR_BM * 32;  // per parity
     static constexpr int T_BM = S + 2 * S_BYTES;                         // column tables: Bmin [BN][32 B],
-    static constexpr int T_REC = T_BM + BN * 32;                         // records [2][BN][16 B]
-    static constexpr int TOTAL = T_REC + 2 * BN * 16;
+    static constexpr int T_REC = T_BM + BN * 32;                         // records [3][BN][16 B]
+    static constexpr int TOTAL = T_REC + 3 * BN * 16;
     static_assert(TOTAL <= 160 * 1024, "LDS budget");
 };
 
@@ -182,7 +182,9 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
         *(lds_u16 *)(uintptr_t)(d + 16) = __builtin_bit_cast(uint16_t, lo);
     };
     // column tables of the tile, 1 KB per instruction: Bmin of super-block u, instruction k (0..5):
-    // columns 32k .. + 32; the records of super-block u in parity u & 1, instruction k (0..2): columns
+    // columns 32k .. + 32; the records of super-block u in record slot u % 3 (they stay until the
+    // super-block's rescale and the tile's end read them, two super-blocks after the next one's
+    // loads), instruction k (0..2): columns
     // 64k .. + 64. Loader waves 2 and 3 issue them (they have one quant DMA per stage, waves 0 and 1 two).
     // Past column N these read other table bytes (the upload leaves HQ_Q4K_TAB_PAD zero bytes after the
     // tables for the last tile's), used only for outputs that are not stored
@@ -191,8 +193,8 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
         dma16_so(rt, lds0 + (uint32_t)(L::T_BM + 1024 * k), 16u * (uint32_t)lane,
                  (uint32_t)u * (uint32_t)N * HQ_Q4K_TAB_BYTES + (uint32_t)(n0 + 32 * k) * 32u);
     };
-    auto dma_rec = [&](int u, int k) {
-        dma16_so(rt, lds0 + (uint32_t)(L::T_REC + (u & 1) * BN * 16 + 1024 * k), 16u * (uint32_t)lane,
+    auto dma_rec = [&](int u, int slot, int k) {
+        dma16_so(rt, lds0 + (uint32_t)(L::T_REC + slot * BN * 16 + 1024 * k), 16u * (uint32_t)lane,
                  (uint32_t)u * (uint32_t)N * HQ_Q4K_TAB_BYTES + (uint32_t)N * 32u + (uint32_t)(n0 + 64 * k) * 16u);
     };
 
@@ -209,9 +211,10 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
     auto rdq = [&](int buf, int j) {
         return *(const __attribute__((address_space(3))) u2v *)(uintptr_t)(q_lane + (uint32_t)(buf * L::Q_BYTES + j * 16 * 32));
     };
-    // scale word p / 2 of column block j in super-block v, shifted to sub-blocks 2p, 2p + 1 in its low bytes
+    // scale word p / 2 of column block j in record slot v, shifted to sub-blocks 2p, 2p + 1 in its low
+    // bytes
     auto rdsw = [&](int p, int v, int j) {
-        return *(const __attribute__((address_space(3))) uint32_t *)(uintptr_t)(lds0 + (uint32_t)(L::T_REC + ((v & 1) * BN + wc0 + 16 * j + ln) * 16 +
+        return *(const __attribute__((address_space(3))) uint32_t *)(uintptr_t)(lds0 + (uint32_t)(L::T_REC + (v * BN + wc0 + 16 * j + ln) * 16 +
                                                                                                    (p >> 1) * 4)) >>
                ((p & 1) * 16);
     };
@@ -222,12 +225,12 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
     auto rdbm = [&](int j) {
         return *(const __attribute__((address_space(3))) h8 *)(uintptr_t)(lds0 + (uint32_t)(L::T_BM + (wc0 + 16 * j + ln) * 32 + 16 * (lg >> 1)));
     };
-    // field f (2: R, 3: CL) of the records of columns 16j + 4lg .. + 3 of super-block v
+    // field f (2: F, 3: CN) of the records of columns 16j + 4lg .. + 3 in record slot v
     auto rdr = [&](int j, int v, int f) {
         f4 r;
 #pragma unroll
         for (int c = 0; c < 4; c++)
-            r[c] = *(const __attribute__((address_space(3))) float *)(uintptr_t)(lds0 + (uint32_t)(L::T_REC + ((v & 1) * BN + wc0 + 16 * j + 4 * lg + c) * 16 + 4 * f));
+            r[c] = *(const __attribute__((address_space(3))) float *)(uintptr_t)(lds0 + (uint32_t)(L::T_REC + (v * BN + wc0 + 16 * j + 4 * lg + c) * 16 + 4 * f));
         return r;
     };
 
@@ -255,8 +258,8 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
         for (int q = 0; q < 4; q++) dma_a1(0, 0, q);
         dma_q1(0, 0, 0);
         if (qw == 2) dma_q1(0, 0, 1);
-        if (w4 == 2) dma_rec(0, 0), dma_rec(0, 2);
-        if (w4 == 3) dma_rec(0, 1);
+        if (w4 == 2) dma_rec(0, 0, 0), dma_rec(0, 0, 2);
+        if (w4 == 3) dma_rec(0, 0, 1);
         *(__attribute__((address_space(3))) u4v *)(uintptr_t)(lds0 + (uint32_t)(L::S + L::S_BYTES + w4 * 1024 + 16 * lane)) =
             u4v{0u, 0u, 0u, 0u};
         {
@@ -279,8 +282,10 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
         // MFMA waves at their barrier. Per stage a loader wave issues 4 activation DMAs, 2 (waves 0, 1)
         // or 1 (waves 2, 3) quant DMAs and, waves 2 and 3, 0 to 2 table DMAs. Past the last unit the
         // record loads repeat it (same bytes).
+        int rs_next = 0;
         for (int u = 0; u < U; u++) {
             const int u_next = u < u_last ? u + 1 : u_last;
+            rs_next = u < u_last ? (rs_next == 2 ? 0 : rs_next + 1) : rs_next;  // u_next % 3
 #pragma unroll
             for (int p = 0; p < 4; p++) {
                 const int s = 4 * u + p, ld = (s + 2) & 3, s_src = s + 2 < S2 ? s + 2 : S2 - 1;
@@ -289,11 +294,11 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
                 dma_q1(s_src, ld, 0);
                 if (qw == 2) dma_q1(s_src, ld, 1);
                 if (w4 == 2) {
-                    if (p == 0) dma_rec(u_next, 0);
-                    if (p == 1) dma_rec(u_next, 2);
+                    if (p == 0) dma_rec(u_next, rs_next, 0);
+                    if (p == 1) dma_rec(u_next, rs_next, 2);
                     if (p == 2) dma_bm(u, 2), dma_bm(u, 3);
                 } else if (w4 == 3) {
-                    if (p == 0) dma_rec(u_next, 1);
+                    if (p == 0) dma_rec(u_next, rs_next, 1);
                     if (p == 1) dma_bm(u, 0), dma_bm(u, 1);
                     if (p == 2) dma_bm(u, 4), dma_bm(u, 5);
                 }
@@ -322,7 +327,7 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
     for (int j = 0; j < NB; j++) {
         qc[j] = rdq(0, j);
         h2 mu, ad;
-        scales(rdsw(0, 0, j), mu, ad);
+        scales(rdsw(0, 0, j), mu, ad);  // (super-block 0's records: slot 0)
         muh[j] = h2{mu.y, mu.y}, adh[j] = h2{ad.y, ad.y};
         b0[j] = decode8<false>(qc[j], h2{mu.x, mu.x}, h2{ad.x, ad.x});
     }
@@ -339,8 +344,9 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
     // super-block's groups 0 and 1, ahead of their first MFMAs there).
     uint32_t swn[NB];  // the next stage's scale words
     h2 mul0[NB], add0[NB];  // and its k-step 0 multipliers and addends
+    int rs = 0;  // record slot of super-block u (u % 3)
     for (int u = 0; u < U; u++) {
-        const bool more = u + 1 < U;
+        const int rsn = rs == 2 ? 0 : rs + 1;  // record slot of the next super-block
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             const int s = 4 * u + p, cur = s & 3, nxt = (s + 1) & 3;
@@ -380,18 +386,16 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
                     // quants; after it they refill the slot of stage s - 1, whose reads have all been
                     // consumed (this stage's quants are decoded, so qc is free)
                     wr_barrier();
-                    const int pn = (p + 1) & 3, un = p == 3 ? u + 1 : u;
+                    const int pn = (p + 1) & 3, un = p == 3 ? rsn : rs;
 #pragma unroll
                     for (int j = 0; j < NB; j++) qc[j] = rdq(nxt, j), swn[j] = rdsw(pn, un, j);
                     // at p = 3 this super-block's Bmin (landed by this barrier; the loaders rewrite it
-                    // from p = 1 of the next one) and the next one's R (its records have landed)
+                    // from p = 1 of the next one) and its rescale factor F = c_u / c_{u+1}
                     if (p == 3)
 #pragma unroll
                         for (int j = 0; j < NB; j++) {
                             bm[j] = rdbm(j);
-                            const f4 rn = rdr(j, u + 1, 2);
-#pragma unroll
-                            for (int c = 0; c < 4; c++) r[j][c] = more ? rn[c] : 1.0f;
+                            r[j] = rdr(j, rs, 2);
                         }
                 }
                 // the next stage's scales and k-step 0 weights (b0 is free after group 7), half a
@@ -409,9 +413,11 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
+        rs = rsn;
     }
     // ---- the last super-block's min k-step (its Bmin, in its own units, read at p = 3, and its sums
-    // landed by the last barrier), then back to true units (its c) and straight from the accumulators:
+    // landed by the last barrier; its F is 1, so rows 6 and 7 need no rescale), then back to true units
+    // (its c) and straight from the accumulators:
     // lane (ln, lg) of block (i, j) holds row 16i + ln, columns 16j + 4lg .. + 3 of the wave's
     // columns (one 16-byte fp32 or 8-byte fp16 store; element by element at the matrix edge or where
     // N % 4 or C's alignment does not allow it)
@@ -423,7 +429,7 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
     }
 #pragma unroll
     for (int j = 0; j < NB; j++) {
-        const f4 cl = rdr(j, U - 1, 3);
+        const f4 cl = rdr(j, u_last % 3, 3);
 #pragma unroll
         for (int i = 0; i < 8; i++) acc[i][j] *= cl;
     }
@@ -472,16 +478,16 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
 }  // namespace
 
 // Per-column tables of every super-block of a Q4_K matrix (one thread per row, super-blocks in order):
-// for super-block v, Bmin [rows][32 B] = bf16 hi[8], lo[8] of x_i = -dmin * m_i / c_{v+1} (the GEMM
-// adds super-block v's min term in the next one's units; the last super-block's in its own, c_v) at
+// for super-block v, Bmin [rows][32 B] = bf16 hi[8], lo[8] of x_i = -dmin * m_i / c_{v+1} at
 // v * rows * 48, then records [rows][16 B] = scale words sw0, sw1 (zero where d = 0),
-// R = c_{v-1} / c_v (c_{-1} = 1), CL = c_v; c_v = d_v, or 1 where d_v = 0 (-dmin * m_i is exact in
+// F = c_v / c_{v+1}, CN = c_{v+1}; c_v = d_v, or 1 where d_v = 0, and c_{v+1} reads c_v for the last
+// super-block (F = 1). The GEMM accumulates super-block v in units of c_v, rescales by F after it and
+// adds its min term in the next units (the last super-block's in its own; -dmin * m_i is exact in
 // fp32).
 __global__ void __launch_bounds__(256) k_q4k_tables(const uint8_t *W, uint32_t rows, uint32_t nb, uint32_t row_bytes,
                                                     uint8_t *tab) {
     const uint32_t n = blockIdx.x * 256u + threadIdx.x;
     if (n >= rows) return;
-    float c_prev = 1.0f;
     for (uint32_t v = 0; v < nb; v++) {
         const u4v hm = *(const u4v *)(W + (size_t)n * row_bytes + (size_t)v * 144);
         uint32_t sw0, sw1, mw0, mw1;
@@ -510,8 +516,7 @@ __global__ void __launch_bounds__(256) k_q4k_tables(const uint8_t *W, uint32_t r
         *(u4v *)(t + (size_t)n * 32) = u4v{bh[0], bh[1], bh[2], bh[3]};
         *(u4v *)(t + (size_t)n * 32 + 16) = u4v{bl[0], bl[1], bl[2], bl[3]};
         *(u4v *)(t + (size_t)rows * 32 + (size_t)n * 16) =
-            u4v{sw0 & nz, sw1 & nz, __builtin_bit_cast(uint32_t, c_prev / c), __builtin_bit_cast(uint32_t, c)};
-        c_prev = c;
+            u4v{sw0 & nz, sw1 & nz, __builtin_bit_cast(uint32_t, c / cn), __builtin_bit_cast(uint32_t, cn)};
     }
 }
 

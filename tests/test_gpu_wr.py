@@ -1,14 +1,14 @@
 """GPU parity of the one-round Q4_K tile kernel with loader waves (k_gemm_q4_k_wr<3>: 128 x 192
-tiles over the whole of K, 4 MFMA waves and 4 loader waves; the headline shape M = 512, N = 9728,
-K = 2560), through the C ABI, against the CPU oracle.
+tiles, 4 MFMA waves and 4 loader waves; the headline shape M = 512, N = 9728, K = 2560), through the
+C ABI, against the CPU oracle.
 
-Shapes: M = 350 (two whole 128-row tiles and a ragged one of 94 rows) and 512; N = 9672 (50 whole
-192-column tiles and a ragged one of 72: one MFMA wave's columns whole, the next one's half, two
+Shapes: M = 256, 350 (two whole 128-row tiles and a ragged one of 94 rows) and 512; N = 9672 (50
+whole 192-column tiles and a ragged one of 72: one MFMA wave's columns whole, the next one's half, two
 waves with none) or 9674 (N not a multiple of 4: the element-wise store path); K = 256 (one
-super-block: no rescale between super-blocks), 512, 1024 and 4096. The per-super-block column
-tables come from the upload (k_q4k_tables), so every test also checks them. Bars as in
-test_gpu_parity.py: rel-L2 <= 1e-3 and max-abs <= 2e-3 (Q4_K); against the float64 product,
-2^-13 |W| @ |a| per output.
+super-block: no rescale between super-blocks), 512, 1024, 2560 and 4096 (the record ring of three
+slots wraps). The per-super-block column tables come from the upload (k_q4k_tables), so every test
+also checks them. Bars as in test_gpu_parity.py: rel-L2 <= 1e-3 and max-abs <= 2e-3
+(Q4_K); against the float64 product, 2^-13 |W| @ |a| per output.
 """
 import numpy as np
 import pytest
@@ -45,7 +45,7 @@ def run(hqlib, blocks, a, N, K, what, c_f32=True, c_init=None):
     return got
 
 
-@pytest.mark.parametrize("N,K", [(9672, 512), (9674, 256)])
+@pytest.mark.parametrize("N,K", [(9672, 512), (9674, 256), (9674, 2560)])
 def test_wr_special_scales_ragged(hqlib, oracle, N, K):
     """Weights with zero, negative, subnormal and widely varying super-block scales (and one all-zero
     row, one min-term-only row); ragged last row and column tiles; N % 4 != 0 at N = 9674."""
@@ -62,9 +62,9 @@ def test_wr_special_scales_ragged(hqlib, oracle, N, K):
     assert np.all(np.isfinite(got))
 
 
-@pytest.mark.parametrize("N", [9728, 9674])
-def test_wr_accumulate_and_fp16_output(hqlib, oracle, N):
-    M, K = 512, 1024
+@pytest.mark.parametrize("N,K", [(9728, 1024), (9674, 1024), (9728, 2560), (9674, 2560)])
+def test_wr_accumulate_and_fp16_output(hqlib, oracle, N, K):
+    M = 512
     blocks = synth.random_blocks(synth.Q4_K, synth.Rng(181 + N), N, K)
     rng = synth.Rng(182)
     a = synth.activations_f16(rng, M, K)
@@ -122,6 +122,19 @@ def test_wr_long_k_repeatable(hqlib, oracle):
     cols = sample_cols(N)
     ref = oracle.matmul(np.ascontiguousarray(blocks[cols]), synth.Q4_K, len(cols), K, oracle.f16_to_f32(a[rows]))
     check(got[0][np.ix_(rows, cols)], ref, f"wr long K ({len(rows)} rows x {len(cols)} columns)")
+
+
+def test_wr_two_row_tiles(hqlib, oracle):
+    """M = 256 (two row tiles per column tile, no ragged rows), K = 2560: sampled parity; the
+    workspace query reports none (the loader waves form the sub-block sums)."""
+    M, N, K = 256, 9728, 2560
+    assert hqlib.gemm_workspace_bytes(synth.Q4_K, M, N, K) == (0, 0, 0, True)
+    blocks = synth.random_blocks(synth.Q4_K, synth.Rng(221), N, K)
+    a = synth.activations_f16(synth.Rng(222), M, K)
+    got = run(hqlib, blocks, a, N, K, "wr two row tiles")
+    rows = sample_rows(M, per_tile=4)
+    ref = oracle.matmul(blocks, synth.Q4_K, N, K, oracle.f16_to_f32(a[rows]))
+    check(got[rows], ref, f"wr two row tiles ({len(rows)} rows)")
 
 
 def test_wr_download_round_trip(hqlib):
