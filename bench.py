@@ -159,22 +159,23 @@ def bench_gather(hq, synth, k, stream, reps=3):
                 tflops=2.0 * B * k * K / (ms * 1e-3) / 1e12, id_sets=n_sets)
 
 
-def bench_swiglu(hq, synth, gtype, stream, M=512, I=9728, K=2560, steps=20):
+def bench_swiglu(hq, synth, gtype, stream, M=512, I=9728, K=2560):
     """The SwiGLU FFN input silu(A gate^T) * (A up^T) of config 3's up/gate shape as one pair GEMM
     (hq_gemm_swiglu; the epilogue in the tile kernel) against the unfused sequence's two GEMMs alone
-    (hq_gemm on gate and on up, fp16 outputs; the reference adds a k_swiglu pass on top)."""
+    (hq_gemm on gate and on up, fp16 outputs; the reference adds a k_swiglu pass on top); both as
+    the median per-launch time of HIP-graph replays (MEDIAN_REPS graphs of MEDIAN_ITERS calls)."""
     gb = synth.random_blocks(gtype, synth.Rng(4242 + gtype + I), I, K)
     rb = synth.row_bytes(gtype, K)
     copies = max(2, -(-ROTATE_BYTES // (2 * I * rb)))
     pairs = [hq.PairMat(gb, gb, gtype, I, K) for _ in range(copies)]
     A = hq.DevBuf.from_array(synth.activations_f16(synth.Rng(99 + M), M, K))
     out = hq.DevBuf(M * I * 2)
-    ms = hq.time_gemm_swiglu(pairs, A, M, out, steps, 1, stream)
+    ms = hq.time_gemm_swiglu(pairs, A, M, out, MEDIAN_ITERS, MEDIAN_REPS, stream)
     for p in pairs:
         p.free()
     mats = [hq.Mat(gb, gtype, I, K) for _ in range(2 * copies)]
     C = hq.DevBuf(M * I * 2)
-    ms2 = hq.time_gemm(mats, A, M, C, False, 2 * steps, 1, stream) * 2
+    ms2 = hq.time_gemm(mats, A, M, C, False, MEDIAN_ITERS, MEDIAN_REPS, stream) * 2
     for m in mats:
         m.free()
     A.free(), out.free(), C.free()
