@@ -33,13 +33,13 @@
 // own units. The activation sub-block sums S come from the loader waves: each stage's ring slot is
 // summed in LDS while the stage is being multiplied (no pass over A before the kernel), so S of
 // super-block u is whole one barrier after its last stage. The per-column tables (scale words, Bmin,
-// R, CL) depend on the weights only: they are computed once at upload (k_q4k_tables) and moved into
-// LDS with the loads.
+// F = c_u / c_{u+1}, CN = c_{u+1}) depend on the weights only: they are computed once at upload
+// (k_q4k_tables) and moved into LDS with the loads.
 //
-// LDS (108 KB for NB = 3): A [4][128 rows][64 k] fp16 (16-byte slot p of row r at p ^ ((r >> 1) & 7));
-// quant groups [4][4 waves][16NB columns][32 B] (the two halves of column c swapped where
-// (c >> 3) & 1); S [2][128][hi x 8, lo x 8] bf16; per wave Bmin [16NB][32 B] and records
-// [2][16NB][16 B]. The output goes from the accumulators straight to C.
+// LDS (111 KB for NB = 3): A [4][128 rows][64 k] fp16 (16-byte slot p of row r at p ^ ((r >> 1) & 7));
+// quant groups [4][64NB columns][32 B] (the two halves of column c swapped where (c >> 3) & 1);
+// S [2][128][hi x 8, lo x 8] bf16; the tile's Bmin [64NB][32 B] and records [3][64NB][16 B]. The
+// output goes from the accumulators straight to C.
 #include "hq_device.h"
 #include "hq_kernels.h"
 
