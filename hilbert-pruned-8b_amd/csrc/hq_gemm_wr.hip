@@ -526,15 +526,6 @@ hipError_t hq_launch_q4k_tables(const hq_dev_mat *W, uint8_t *tab, hipStream_t s
     return hipGetLastError();
 }
 
-// tiles of 128 x 64nb: the number of tile rounds on n_cu CUs and the fraction of CU time they fill
-int hq_wr_choose(int M, int N, int n_cu, float *eff) {
-    const int mt = (M + WR_BM - 1) / WR_BM, nb = 3;
-    const int nt = (N + 64 * nb - 1) / (64 * nb);
-    const long tiles = (long)mt * nt, rounds = (tiles + n_cu - 1) / n_cu;
-    if (eff) *eff = (float)((double)M * N / ((double)rounds * n_cu * WR_BM * 64.0 * nb));
-    return nb;
-}
-
 // every byte offset of the kernel (tile rows and columns past the matrix included, C's) fits 32 bits
 int hq_wr_fits(const hq_dev_mat *W, int M) {
     const size_t lim = (size_t)1 << 32, mr = (size_t)M + WR_BM;

@@ -78,9 +78,8 @@ hipError_t hq_launch_gemm_bt(const hq_dev_mat *W, const uint16_t *A, const uint1
                              int accumulate, hipStream_t st);
 // Prefill Q4_K GEMM of one tile round (hq_gemm_wr.hip): 128 x 192 tiles over the whole of K, 4 waves
 // that each decode their own 48 columns and 4 loader waves (which also form the activation sub-block
-// sums: no pre-pass, no workspace); the tile width chooser, whether a shape's byte offsets suit it,
-// and the launch (c_f32: 1 fp32 C, 0 fp16 C).
-int hq_wr_choose(int M, int N, int n_cu, float *eff);
+// sums: no pre-pass, no workspace); whether a shape's byte offsets suit it, and the launch (c_f32:
+// 1 fp32 C, 0 fp16 C).
 int hq_wr_fits(const hq_dev_mat *W, int M);
 hipError_t hq_launch_gemm_wr(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
                              hipStream_t st);
