@@ -8,6 +8,7 @@
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2v __attribute__((ext_vector_type(2)));
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
@@ -204,6 +205,29 @@ DEV h2 bytes_f16(uint32_t w, bool hi_pair) {
 // pair matrix, fp16 (see tile_finish).
 constexpr int HQ_OUT_SWIGLU = 2;
 
+// SwiGLU output from accumulators in the MFMA layout of the register-decode kernels (lane (ln, lg) of
+// block (i, j): row 16i + ln, columns 16j + 4lg .. + 3 of the wave's columns). Each 16-column block of
+// a gate/up pair matrix is 8 gate columns and the 8 matching up columns, so lanes 32 apart hold
+// matching gate (lg = 0, 1) and up (lg = 2, 3) values of the same 4 pair columns 4 (lg & 1) .. + 3.
+// The two lanes split them: each sends its partner the two values the partner lacks (all 64 lanes
+// take part, so this comes before any per-lane bounds check) and returns silu(gate) * up of pair
+// columns 4 (lg & 1) + 2 (lg >> 1) and + 1 of the block, as two fp16 in a word. silu(g) =
+// g / (1 + e^-g) with the hardware exp2 and reciprocal (about 1 ulp of fp32 each, far below the
+// fp16 rounding of the result; e^-g overflowing to inf gives -0 for very negative g).
+DEV uint32_t swiglu_pair2(const f4 &v, int lg) {
+    const bool gate = lg < 2;
+    h2 y;
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const float own = gate ? v[k] : v[2 + k];
+        const float got = __shfl_xor(gate ? v[2 + k] : v[k], 32, 64);
+        const float gv = gate ? own : got, uv = gate ? got : own;
+        const float silu = gv * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gv * -1.4426950408889634f));
+        y[k] = (_Float16)(silu * uv);
+    }
+    return __builtin_bit_cast(uint32_t, y);
+}
+
 // End of a full-K tile kernel's tile, held in LDS as fp32 rows of LD floats (BM x BN, NT threads).
 // parts == 1: stored to C. parts > 1 (a K split, at most MAXP parts): every part stores its tile to
 // partials[tile][part] with device-scope (sc1) 16-byte stores, waits for them and counts itself in
@@ -359,7 +383,6 @@ DEV f4 quad_transpose(f4 x) {
 // register e of lane (ln, lg). A quad transpose gives lane (4c + k, lg) row 4lg + k, columns
 // 4c .. 4c + 3, stored as one 8-byte (fp16) or 16-byte (fp32) access when N % 4 == 0, else
 // element by element (the same values and roundings either way).
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 template <int MB, int NB>
 DEV void store_tile(void *C, const f4 (&acc)[MB][NB], int M, int N, int m0, int nw, int ln, int lg, int c_f32,
                     int accumulate) {

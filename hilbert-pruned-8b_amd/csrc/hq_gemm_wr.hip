@@ -59,7 +59,7 @@ struct WrArgs {
     int M, N, K;
     void *C;
     int c_f32, accumulate;
-    int mt, nt;
+    int mt, nt0, nt;  // M-tiles; this launch's column tiles nt0 .. nt - 1
 };
 
 template <int NB>
@@ -101,7 +101,7 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
     // tile: XCD x = b % 8 takes N-tiles x, x + 8, ...; its slots run over the M-tiles of one N-tile
     // first (the weight slab is then fetched once per XCD)
     const int b = blockIdx.x, x = b & 7, j8 = b >> 3;
-    const int nt_i = x + 8 * (j8 / g.mt), mt_i = j8 % g.mt;
+    const int nt_i = g.nt0 + x + 8 * (j8 / g.mt), mt_i = j8 % g.mt;
     if (nt_i >= g.nt) return;
     const int m0 = mt_i * WR_BM, n0 = nt_i * BN;
     const int M = g.M, N = g.N, K = g.K, U = K / 256, S2 = 4 * U;
@@ -435,6 +435,24 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
     }
     // (vector stores write through to memory: SC1, measured faster than write-back here, where every
     // tile stores its whole output at the end)
+    if (g.c_f32 == HQ_OUT_SWIGLU) {
+        // gate/up pair matrix: C is fp16 [M, N / 2] and takes silu(gate) * up (N a multiple of 16)
+        const int Nh = N / 2;
+        const rsrc_t ro = make_rsrc(g.C, (uint32_t)((size_t)M * Nh * 2));
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int m = m0 + 16 * i + ln;
+#pragma unroll
+            for (int j = 0; j < NB; j++) {
+                const uint32_t y = swiglu_pair2(acc[i][j], lg);
+                const int n = nw + 16 * j;
+                if (m < M && n < N)
+                    __builtin_amdgcn_raw_buffer_store_b32(y, ro, (uint32_t)(((size_t)m * Nh + n / 2 + 4 * (lg & 1) + 2 * (lg >> 1)) * 2),
+                                                          0u, CPOL_SC1);
+            }
+        }
+        return;
+    }
     const bool vec = (N & 3) == 0 && ((uintptr_t)g.C & (g.c_f32 ? 15u : 7u)) == 0;
     const rsrc_t rc = make_rsrc(g.C, (uint32_t)((size_t)M * N * (g.c_f32 ? 4 : 2)));
 #pragma unroll
@@ -535,16 +553,19 @@ int hq_wr_fits(const hq_dev_mat *W, int M) {
 }
 
 hipError_t hq_launch_gemm_wr(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
-                             hipStream_t st) {
+                             int nt0, int nt1, hipStream_t st) {
     if (!hq_wr_fits(W, M) || !W->tab) return hipErrorInvalidValue;  // (every uploaded Q4_K matrix has its tables)
     constexpr int NB = 3;
     WrArgs g;
     g.W = W->qs, g.row_bytes = (uint32_t)W->row_bytes, g.A = A, g.tab = W->tab;
     g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;
     g.mt = (M + WR_BM - 1) / WR_BM;
-    g.nt = (g.N + 64 * NB - 1) / (64 * NB);
-    if (c_f32 != 0 && c_f32 != 1) return hipErrorInvalidValue;  // (fp32 or fp16 C)
-    const unsigned grid = (unsigned)(8 * ((g.nt + 7) / 8) * g.mt);
+    const int nt_all = (g.N + 64 * NB - 1) / (64 * NB);
+    g.nt0 = nt0, g.nt = nt1 < 0 || nt1 > nt_all ? nt_all : nt1;
+    if (nt0 < 0 || nt0 >= g.nt) return hipErrorInvalidValue;
+    // fp32 or fp16 C, or the SwiGLU output of a gate/up pair matrix (N a multiple of 16, no accumulate)
+    if (c_f32 != 0 && c_f32 != 1 && !(c_f32 == HQ_OUT_SWIGLU && W->rows % 16 == 0 && !accumulate)) return hipErrorInvalidValue;
+    const unsigned grid = (unsigned)(8 * ((g.nt - g.nt0 + 7) / 8) * g.mt);
     k_gemm_q4_k_wr<NB><<<grid, WR_NT, 0, st>>>(g);
     return hipGetLastError();
 }

@@ -79,10 +79,15 @@ hipError_t hq_launch_gemm_bt(const hq_dev_mat *W, const uint16_t *A, const uint1
 // Prefill Q4_K GEMM of one tile round (hq_gemm_wr.hip): 128 x 192 tiles over the whole of K, 4 waves
 // that each decode their own 48 columns and 4 loader waves (which also form the activation sub-block
 // sums: no pre-pass, no workspace); whether a shape's byte offsets suit it, and the launch (c_f32:
-// 1 fp32 C, 0 fp16 C).
+// 1 fp32 C, 0 fp16 C, HQ_OUT_SWIGLU fp16 silu(gate) * up of a gate/up pair matrix) of the column
+// tiles nt0 .. nt1 - 1 (nt1 < 0: to the last).
 int hq_wr_fits(const hq_dev_mat *W, int M);
 hipError_t hq_launch_gemm_wr(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
-                             hipStream_t st);
+                             int nt0, int nt1, hipStream_t st);
+// The same tile shape for Q8_0 (hq_gemm_wr8.hip; K a multiple of 256, no workspace).
+int hq_wr8_fits(const hq_dev_mat *W, int M);
+hipError_t hq_launch_gemm_wr8(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
+                              int nt0, int nt1, hipStream_t st);
 // Mid-M Q4_K GEMM (hq_gemm_rb.hip): whether M, K suit it (33 <= M <= 64, K a multiple of 512,
 // 32-bit offsets), its workgroups per tile for a shape, and the launch (S = k_asums output for A in
 // the (hi, lo) pair layout; partials / counters as for the other K splits when parts > 1).

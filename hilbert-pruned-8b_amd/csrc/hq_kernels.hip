@@ -26,6 +26,8 @@
 #include <stdint.h>
 #include <cstdio>
 
+#include <algorithm>
+
 #include "hq_device.h"
 #include "hq_kernels.h"
 
@@ -1185,6 +1187,7 @@ struct GemmCfg {
     int rb8;        // Q8_0 M <= 64: workgroups per tile of k_gemm_q8_0_rb (hq_gemm_rb.hip); 0: not used
     bool bt;        // Q4_K large M: the 256 x 256 tile kernel k_gemm_q4_k_bt (hq_gemm_bt.hip)
     bool wr;        // Q4_K, one round of full-K tiles: the 128 x 192 tile kernel k_gemm_q4_k_wr (hq_gemm_wr.hip)
+    bool wr8;       // Q8_0, the same: k_gemm_q8_0_wr (hq_gemm_wr8.hip)
 };
 
 // Q4_K with M > 64 runs the full-K tile kernel when its tiles fit in one round on the CUs and fill
@@ -1256,6 +1259,13 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
                     }
                 }
     }
+    // Q8_0 full-K tiles without a K split, when the 128 x 192 tiles fit in one round and fill at least
+    // 70 % of the CUs (M = 512, N = 9728: 204 tiles)
+    c.wr8 = false;
+    if (c.ws8_nb && c.ws8_parts == 1 && hq_wr8_fits(W, M)) {
+        const long t = (long)((M + 127) / 128) * (((long)W->rows + 191) / 192);
+        c.wr8 = t <= n_cu && 10 * t >= 7L * n_cu;
+    }
     return c;
 }
 
@@ -1269,9 +1279,10 @@ void hq_gemm_tile_shape(int type, int M, int N, int K, int n_cu, int *rows, int 
     W.type = type;
     W.rows = (uint32_t)N;
     W.cols = (uint32_t)K;
+    W.ldd = type == HQ_TYPE_Q8_0 ? (K / 32 + 7) / 8 * 8 : 0;
     const GemmCfg c = gemm_cfg(&W, M, n_cu);
-    *rows = c.bt ? 256 : c.wr ? 128 : c.rbm ? 64 : c.rb8 ? (M <= 16 ? 16 : M <= 32 ? 32 : 64) : c.ws_nb || c.ws8_nb ? 128 : 16 * c.mb;
-    *cols = c.bt ? 256 : c.wr ? 192 : c.rbm || c.rb8 ? 64 : c.ws_nb ? 32 * c.ws_nb : c.ws8_nb ? 32 * c.ws8_nb : 16 * c.nb * c.waves;
+    *rows = c.bt ? 256 : c.wr || c.wr8 ? 128 : c.rbm ? 64 : c.rb8 ? (M <= 16 ? 16 : M <= 32 ? 32 : 64) : c.ws_nb || c.ws8_nb ? 128 : 16 * c.mb;
+    *cols = c.bt ? 256 : c.wr || c.wr8 ? 192 : c.rbm || c.rb8 ? 64 : c.ws_nb ? 32 * c.ws_nb : c.ws8_nb ? 32 * c.ws8_nb : 16 * c.nb * c.waves;
 }
 
 // Name of the kernel that does the work of an M x N x K hq_gemm call (the main kernel for GEMMs
@@ -1281,6 +1292,7 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
     W.type = type;
     W.rows = (uint32_t)N;
     W.cols = (uint32_t)K;
+    W.ldd = type == HQ_TYPE_Q8_0 ? (K / 32 + 7) / 8 * 8 : 0;
     W.row_bytes = type == HQ_TYPE_Q4_K ? (size_t)K / 256 * 144 : type == HQ_TYPE_Q6_K ? (size_t)K / 256 * 224 : (size_t)K;
     if (M == 1 && type == HQ_TYPE_Q6_K) {
         snprintf(buf, n, "k_gemv_q6_k");
@@ -1298,6 +1310,7 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
     else if (c.rb8) snprintf(buf, n, "k_gemm_q8_0_rb<%d, 3, 2>", M <= 16 ? 1 : M <= 32 ? 2 : 4);
     else if (c.bt) snprintf(buf, n, "k_gemm_q4_k_bt");
     else if (c.wr) snprintf(buf, n, "k_gemm_q4_k_wr<3>");
+    else if (c.wr8) snprintf(buf, n, "k_gemm_q8_0_wr");
     else if (c.ws_nb) snprintf(buf, n, "k_gemm_q4_k_ws<%d>", c.ws_nb);
     else if (c.ws8_nb) snprintf(buf, n, "k_gemm_q8_0_ws<%d>", c.ws8_nb);
     else if (c.wide) snprintf(buf, n, "k_gemm_q4_k_w<%d>", c.mb);  // template argument: row blocks
@@ -1352,7 +1365,8 @@ hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, vo
     if (c.rbm) return hq_launch_gemm_rb(W, A, wk.sums, M, C, c_f32, accumulate, c.rbm, wk.partials, wk.counters, st);
     if (c.rb8) return hq_launch_gemm_rb8(W, A, M, C, c_f32, accumulate, c.rb8, wk.partials, wk.counters, st);
     if (c.bt) return hq_launch_gemm_bt(W, A, wk.sums, M, C, c_f32, accumulate, st);
-    if (c.wr) return hq_launch_gemm_wr(W, A, M, C, c_f32, accumulate, st);
+    if (c.wr) return hq_launch_gemm_wr(W, A, M, C, c_f32, accumulate, 0, -1, st);
+    if (c.wr8) return hq_launch_gemm_wr8(W, A, M, C, c_f32, accumulate, 0, -1, st);
     if (c.ws_nb)
         return hq_launch_gemm_ws(W, A, wk.sums, M, C, c_f32, accumulate, c.ws_nb, c.ws_parts, wk.partials, wk.counters, st);
     if (c.ws8_nb)
@@ -1392,6 +1406,24 @@ hipError_t hq_launch_gemm_swiglu(const hq_dev_mat *W, const uint16_t *A, int M, 
     *fused = 0;
     const int N = (int)W->rows, K = (int)W->cols;
     if (M <= 64 || (size_t)M * K * 2 >= ((size_t)1 << 32) || N % 16) return hipSuccess;
+    // the register-decode tile kernels (128 x 192 tiles) when their tiles fill at least 70 % of the CUs
+    // in rounds of launches of at most one round each (M = 512, pair matrix of I = 9728: 4 x 102
+    // tiles as two launches of 4 x 51, each like the one-round GEMM of a single 9728-row matrix;
+    // measured faster than one launch of two rounds); the Q4_K one needs its upload-time column tables
+    const int nt = (N + 191) / 192, mt = (M + 127) / 128;
+    const int per = std::max(1, std::min(nt, wk.n_cu / mt));  // column tiles per launch
+    const int launches = (nt + per - 1) / per, span = (nt + launches - 1) / launches;
+    const bool wr_fill = (long)mt * span <= wk.n_cu && 10L * mt * nt >= 7L * launches * wk.n_cu;
+    const bool wr8 = W->type == HQ_TYPE_Q8_0 && hq_wr8_fits(W, M), wr4 = W->type == HQ_TYPE_Q4_K && W->tab && hq_wr_fits(W, M);
+    if (wr_fill && (wr8 || wr4)) {
+        *fused = 1;
+        for (int t0 = 0; t0 < nt; t0 += span) {
+            const hipError_t e = wr8 ? hq_launch_gemm_wr8(W, A, M, out, HQ_OUT_SWIGLU, 0, t0, t0 + span, st)
+                                     : hq_launch_gemm_wr(W, A, M, out, HQ_OUT_SWIGLU, 0, t0, t0 + span, st);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     float eff = 0.f;
     const int nb = hq_ws_choose(M, N, wk.n_cu, &eff);
     if (W->type == HQ_TYPE_Q4_K && wk.sums) {

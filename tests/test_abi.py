@@ -99,7 +99,7 @@ def test_gemm_workspace_bytes():
 
 def test_gemm_kernel_names():
     """hq_gemm_kernel names the kernel the launch plan picks (the names rocprofv3 lists)."""
-    cases = {(synth.Q4_K, 512, 9728, 2560): "k_gemm_q4_k_wr<3>", (synth.Q4_K, 256, 9728, 2560): "k_gemm_q4_k_wr<3>", (synth.Q8_0, 512, 9728, 2560): "k_gemm_q8_0_ws<5>",
+    cases = {(synth.Q4_K, 512, 9728, 2560): "k_gemm_q4_k_wr<3>", (synth.Q4_K, 256, 9728, 2560): "k_gemm_q4_k_wr<3>", (synth.Q8_0, 512, 9728, 2560): "k_gemm_q8_0_wr",
              (synth.Q8_0, 2048, 9728, 2560): "k_gemm_q8_0_ws<5>", (synth.Q8_0, 128, 9728, 2560): "k_gemm_q8_0_ws<2>",
              (synth.Q8_0, 65, 9728, 2560): "k_gemm_q8_0<8, 2>",
              (synth.Q4_K, 4096, 9728, 2560): "k_gemm_q4_k_bt", (synth.Q4_K, 16384, 2560, 9216): "k_gemm_q4_k_bt",
@@ -137,8 +137,9 @@ def test_gemm_tile_selection():
                 assert (r, c) in ((128, 256), (256, 256), (128, 192)) or (r == 128 and c in (64, 96, 128, 160))
             elif gtype == synth.Q8_0 and M > 64:
                 # Q8_0 above M = 64: full-K tiles of 128 x 32NB when they fill >= 50 % of the CU
-                # time (any number of rounds), else the narrow Stream-K kernel
-                assert c == 128 or (r == 128 and c in (64, 96, 128, 160))
+                # time (any number of rounds; 128 x 192 with loader waves when one round of them fills
+                # >= 70 % of the CUs), else the narrow Stream-K kernel
+                assert c == 128 or (r == 128 and c in (64, 96, 128, 160, 192))
             elif gtype == synth.Q8_0:
                 # Q8_0 up to M = 64 at N >= 8192: the mid-M kernel's full-K tiles of 16/32/64 x 64
                 assert (r, c) == (16 if M <= 16 else 32 if M <= 32 else 64, 64)
@@ -148,8 +149,9 @@ def test_gemm_tile_selection():
     assert hq.gemm_tiles(synth.Q8_0, 65, 9728) == (128, 128)
     assert hq.gemm_tiles(synth.Q8_0, 128, 9728) == (128, 64)
     assert hq.gemm_tiles(synth.Q4_K, 2, 9728) == (32, 128)
-    # Q8_0 full-K tiles: 4 x 61 tiles of 128 x 160 at M = 512, 16 x 61 (four rounds) at M = 2048
-    assert hq.gemm_tiles(synth.Q8_0, 512, 9728) == (128, 160)
+    # Q8_0 full-K tiles: 4 x 51 tiles of 128 x 192 (one round, loader waves) at M = 512, 16 x 61 of
+    # 128 x 160 (four rounds) at M = 2048
+    assert hq.gemm_tiles(synth.Q8_0, 512, 9728) == (128, 192)
     assert hq.gemm_tiles(synth.Q8_0, 2048, 9728) == (128, 160)
     assert hq.gemm_tiles(synth.Q4_K, 65, 9728) == (128, 256)
     # full-K tiles: 4 x 51 tiles of 128 x 192 on 256 CUs; more tiles than CUs: Stream-K, or at large

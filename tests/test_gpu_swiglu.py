@@ -2,7 +2,9 @@
 gate/up pair matrix (hq_mat_upload_pair + hq_gemm_swiglu), through the C ABI, against the oracle's
 gate and up matmuls: silu(g) * u in float64, the GPU's fp16 output within half an ulp of |y| on top
 of the 1e-2 bar. M > 64 runs the fused epilogue of the full-K tile kernels (the product never
-leaves the tile); other M run one GEMM for both halves and a separate epilogue pass."""
+leaves the tile: the register-decode kernels k_gemm_q4_k_wr / k_gemm_q8_0_wr where their 128 x 192
+tiles fill the CUs, e.g. M = 512 at I = 9728, else the LDS-decode kernels); other M run one GEMM for
+both halves and a separate epilogue pass."""
 import numpy as np
 import pytest
 
@@ -18,7 +20,11 @@ def say(*a):
 CASES = [(synth.Q4_K, 9728, 2560, M) for M in (1, 16, 64, 65, 512)] + \
         [(synth.Q8_0, 9728, 2560, M) for M in (1, 33, 128, 512)] + \
         [(synth.Q4_K, 1000, 512, 200), (synth.Q8_0, 1000, 512, 131), (synth.Q6_K, 1024, 512, 100),
-         (synth.Q4_K, 2560, 9728, 300)]
+         (synth.Q4_K, 2560, 9728, 300)] + \
+        [(synth.Q4_K, 9728, 1024, 448), (synth.Q8_0, 9728, 1024, 500), (synth.Q4_K, 9720, 512, 512),
+         (synth.Q8_0, 9720, 512, 512)]
+# (the last four: the register-decode tile kernels' epilogue over two rounds of 128 x 192 tiles, with
+# a ragged last row tile, and with a ragged last column tile: 2 x 9720 = 101 x 192 + 48)
 
 
 @pytest.mark.parametrize("gtype,I,K,M", CASES)
