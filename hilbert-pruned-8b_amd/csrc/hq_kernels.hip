@@ -1173,6 +1173,48 @@ static SkPlan hq_sk_plan(int M, int N, int K, int bm, int bn, int n_cu) {
 }
 
 namespace {
+// Launch plan of the register-decode tile kernels (128 x 192 full-K tiles, one workgroup per CU):
+// launches of row_tiles x col_tiles tiles, each at most one round on every XCD. A launch deals its
+// column tiles to the 8 XCDs in turn (all row tiles of a column tile on one XCD, which then fetches
+// the weight slab once), so an XCD gets row_tiles x ceil(col_tiles / 8) tiles; more than its CUs
+// would leave a second round on that XCD (measured: M = 640, 5 x 51 tiles in one launch, 59 us
+// against 30 at M = 512). Chunks of rows come first (each launch reads all the weights, which stay
+// in the last-level cache, and a slice of A), then chunks of columns. `fill` when the launches'
+// tiles fill at least 70 % of the CU time.
+struct WrPlan {
+    int row_tiles, col_tiles, launches;
+    bool fill;
+};
+WrPlan wr_plan(int M, int N, int n_cu) {
+    WrPlan w;
+    const int mt = (M + 127) / 128, nt = (N + 191) / 192, per_xcd = std::max(1, n_cu / 8), ncx = (nt + 7) / 8;
+    if (mt * ncx <= per_xcd) {
+        w.row_tiles = mt, w.col_tiles = nt;
+    } else if (ncx <= per_xcd) {
+        w.row_tiles = per_xcd / ncx, w.col_tiles = nt;
+    } else {
+        w.row_tiles = std::min(mt, per_xcd), w.col_tiles = 8 * std::max(1, per_xcd / w.row_tiles);
+    }
+    w.launches = ((mt + w.row_tiles - 1) / w.row_tiles) * ((nt + w.col_tiles - 1) / w.col_tiles);
+    w.fill = 10L * mt * nt >= 7L * w.launches * n_cu;
+    return w;
+}
+// the plan's launches: launch(m0, rows, t0, t1) for row chunk m0 .. m0 + rows - 1 and column tiles
+// t0 .. t1 - 1
+template <class F>
+hipError_t wr_launches(const WrPlan &pl, int M, int N, F &&launch) {
+    const int mt = (M + 127) / 128, nt = (N + 191) / 192;
+    for (int r = 0; r < mt; r += pl.row_tiles)
+        for (int t = 0; t < nt; t += pl.col_tiles) {
+            const int m0 = 128 * r;
+            const hipError_t e = launch(m0, std::min(M - m0, 128 * pl.row_tiles), t, std::min(nt, t + pl.col_tiles));
+            if (e != hipSuccess) return e;
+        }
+    return hipSuccess;
+}
+}  // namespace
+
+namespace {
 // Kernel choice for M >= 2: MB (16-row blocks of M per tile) grows with M up to 8 (Q4_K: at least 2);
 // NB = 2 16-column blocks per wave. Q4_K with M > 64 uses the wide 8-wave kernel (tile 128 x 256).
 // Stream-K removes the wave-quantization cost, so the tile only sets the operand reuse.
@@ -1259,13 +1301,10 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
                     }
                 }
     }
-    // Q8_0 full-K tiles without a K split, when the 128 x 192 tiles fit in one round and fill at least
-    // 70 % of the CUs (M = 512, N = 9728: 204 tiles)
-    c.wr8 = false;
-    if (c.ws8_nb && c.ws8_parts == 1 && hq_wr8_fits(W, M)) {
-        const long t = (long)((M + 127) / 128) * (((long)W->rows + 191) / 192);
-        c.wr8 = t <= n_cu && 10 * t >= 7L * n_cu;
-    }
+    // Q8_0 with M > 64: the register-decode tile kernel (128 x 192 full-K tiles) where its launches of
+    // at most one round each fill at least 70 % of the CU time (M = 512, N = 9728: one launch of 204
+    // tiles; M = 2048: four launches of 16 x 13 tiles)
+    c.wr8 = W->type == HQ_TYPE_Q8_0 && M > 64 && hq_wr8_fits(W, M) && wr_plan(M, (int)W->rows, n_cu).fill;
     return c;
 }
 
@@ -1339,6 +1378,7 @@ void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_by
         *counter_bytes = tiles * sizeof(int);
     }
     *sums_bytes = (c.wide && !c.wr) || c.rbm ? (size_t)M * (W->cols / KC) * 32 : 0;  // (wr forms its own)
+    if (c.wr8) *partial_bytes = *counter_bytes = 0;  // (no K split)
 }
 
 // Pre-pass of a GEMM (the activation sub-block sums of the Q4_K kernels that read them from HBM;
@@ -1366,7 +1406,12 @@ hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, vo
     if (c.rb8) return hq_launch_gemm_rb8(W, A, M, C, c_f32, accumulate, c.rb8, wk.partials, wk.counters, st);
     if (c.bt) return hq_launch_gemm_bt(W, A, wk.sums, M, C, c_f32, accumulate, st);
     if (c.wr) return hq_launch_gemm_wr(W, A, M, C, c_f32, accumulate, 0, -1, st);
-    if (c.wr8) return hq_launch_gemm_wr8(W, A, M, C, c_f32, accumulate, 0, -1, st);
+    if (c.wr8) {
+        const size_t K = W->cols, N = W->rows, esize = c_f32 ? 4 : 2;
+        return wr_launches(wr_plan(M, (int)N, wk.n_cu), M, (int)N, [&](int m0, int rows, int t0, int t1) {
+            return hq_launch_gemm_wr8(W, A + (size_t)m0 * K, rows, (char *)C + (size_t)m0 * N * esize, c_f32, accumulate, t0, t1, st);
+        });
+    }
     if (c.ws_nb)
         return hq_launch_gemm_ws(W, A, wk.sums, M, C, c_f32, accumulate, c.ws_nb, c.ws_parts, wk.partials, wk.counters, st);
     if (c.ws8_nb)
@@ -1406,23 +1451,20 @@ hipError_t hq_launch_gemm_swiglu(const hq_dev_mat *W, const uint16_t *A, int M, 
     *fused = 0;
     const int N = (int)W->rows, K = (int)W->cols;
     if (M <= 64 || (size_t)M * K * 2 >= ((size_t)1 << 32) || N % 16) return hipSuccess;
-    // the register-decode tile kernels (128 x 192 tiles) when their tiles fill at least 70 % of the CUs
-    // in rounds of launches of at most one round each (M = 512, pair matrix of I = 9728: 4 x 102
-    // tiles as two launches of 4 x 51, each like the one-round GEMM of a single 9728-row matrix;
-    // measured faster than one launch of two rounds); the Q4_K one needs its upload-time column tables
-    const int nt = (N + 191) / 192, mt = (M + 127) / 128;
-    const int per = std::max(1, std::min(nt, wk.n_cu / mt));  // column tiles per launch
-    const int launches = (nt + per - 1) / per, span = (nt + launches - 1) / launches;
-    const bool wr_fill = (long)mt * span <= wk.n_cu && 10L * mt * nt >= 7L * launches * wk.n_cu;
+    // the register-decode tile kernels (128 x 192 tiles) where their launches of at most one round
+    // fill at least 70 % of the CU time (M = 512, pair matrix of I = 9728: 4 x 102 tiles as two
+    // launches; measured faster than one launch of two rounds); the Q4_K one needs its upload-time
+    // column tables
     const bool wr8 = W->type == HQ_TYPE_Q8_0 && hq_wr8_fits(W, M), wr4 = W->type == HQ_TYPE_Q4_K && W->tab && hq_wr_fits(W, M);
-    if (wr_fill && (wr8 || wr4)) {
+    const WrPlan pl = wr_plan(M, N, wk.n_cu);
+    if (pl.fill && (wr8 || wr4)) {
         *fused = 1;
-        for (int t0 = 0; t0 < nt; t0 += span) {
-            const hipError_t e = wr8 ? hq_launch_gemm_wr8(W, A, M, out, HQ_OUT_SWIGLU, 0, t0, t0 + span, st)
-                                     : hq_launch_gemm_wr(W, A, M, out, HQ_OUT_SWIGLU, 0, t0, t0 + span, st);
-            if (e != hipSuccess) return e;
-        }
-        return hipSuccess;
+        return wr_launches(pl, M, N, [&](int m0, int rows, int t0, int t1) {
+            const uint16_t *Am = A + (size_t)m0 * K;
+            uint16_t *om = out + (size_t)m0 * (N / 2);
+            return wr8 ? hq_launch_gemm_wr8(W, Am, rows, om, HQ_OUT_SWIGLU, 0, t0, t1, st)
+                       : hq_launch_gemm_wr(W, Am, rows, om, HQ_OUT_SWIGLU, 0, t0, t1, st);
+        });
     }
     float eff = 0.f;
     const int nb = hq_ws_choose(M, N, wk.n_cu, &eff);

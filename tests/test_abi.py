@@ -100,7 +100,7 @@ def test_gemm_workspace_bytes():
 def test_gemm_kernel_names():
     """hq_gemm_kernel names the kernel the launch plan picks (the names rocprofv3 lists)."""
     cases = {(synth.Q4_K, 512, 9728, 2560): "k_gemm_q4_k_wr<3>", (synth.Q4_K, 256, 9728, 2560): "k_gemm_q4_k_wr<3>", (synth.Q8_0, 512, 9728, 2560): "k_gemm_q8_0_wr",
-             (synth.Q8_0, 2048, 9728, 2560): "k_gemm_q8_0_ws<5>", (synth.Q8_0, 128, 9728, 2560): "k_gemm_q8_0_ws<2>",
+             (synth.Q8_0, 2048, 9728, 2560): "k_gemm_q8_0_wr", (synth.Q8_0, 128, 9728, 2560): "k_gemm_q8_0_ws<2>",
              (synth.Q8_0, 65, 9728, 2560): "k_gemm_q8_0<8, 2>",
              (synth.Q4_K, 4096, 9728, 2560): "k_gemm_q4_k_bt", (synth.Q4_K, 16384, 2560, 9216): "k_gemm_q4_k_bt",
              (synth.Q4_K, 16384, 1024, 2560): "k_gemm_q4_k_bt", (synth.Q4_K, 2048, 9728, 2560): "k_gemm_q4_k_w<8>",
@@ -149,10 +149,12 @@ def test_gemm_tile_selection():
     assert hq.gemm_tiles(synth.Q8_0, 65, 9728) == (128, 128)
     assert hq.gemm_tiles(synth.Q8_0, 128, 9728) == (128, 64)
     assert hq.gemm_tiles(synth.Q4_K, 2, 9728) == (32, 128)
-    # Q8_0 full-K tiles: 4 x 51 tiles of 128 x 192 (one round, loader waves) at M = 512, 16 x 61 of
-    # 128 x 160 (four rounds) at M = 2048
+    # Q8_0 full-K tiles of 128 x 192 (loader waves, register decode): 4 x 51 in one launch at M = 512,
+    # 16 x 51 as four launches of at most one round at M = 2048; 128 x 96 at M = 256 (102 of the
+    # larger tiles would fill only 40 % of the CUs)
     assert hq.gemm_tiles(synth.Q8_0, 512, 9728) == (128, 192)
-    assert hq.gemm_tiles(synth.Q8_0, 2048, 9728) == (128, 160)
+    assert hq.gemm_tiles(synth.Q8_0, 2048, 9728) == (128, 192)
+    assert hq.gemm_tiles(synth.Q8_0, 256, 9728) == (128, 96)
     assert hq.gemm_tiles(synth.Q4_K, 65, 9728) == (128, 256)
     # full-K tiles: 4 x 51 tiles of 128 x 192 on 256 CUs; more tiles than CUs: Stream-K, or at large
     # M the 256 x 256 tiles when their rounds fill >= 3/4 of the CU time (M = 4096: 608 tiles in 3

@@ -159,3 +159,16 @@ def test_wr8_workspace_none(hqlib):
     """The kernel needs no workspace (its loads go straight to LDS, its output straight to C)."""
     assert hqlib.gemm_workspace_bytes(synth.Q8_0, 512, 9728, 2560) == (0, 0, 0, True)
     assert hqlib.gemm_tiles(synth.Q8_0, 512, 9728) == (128, 192)
+
+
+@pytest.mark.parametrize("M,N,K", [(1000, 9672, 512), (2048, 2560, 1024)])
+def test_wr8_several_launches(hqlib, oracle, M, N, K):
+    """Many tiles: the GEMM as launches of at most one round of tiles each (M = 1000: two launches of
+    26 and 25 column tiles x 8 row tiles, the last row tile ragged; M = 2048 at N = 2560: one launch
+    of 16 x 14 tiles)."""
+    blocks = synth.random_blocks(synth.Q8_0, synth.Rng(271 + M), N, K)
+    a = synth.activations_f16(synth.Rng(272 + M), M, K)
+    got = run(hqlib, blocks, a, N, K, "wr8 launches")
+    rows = sample_rows(M, per_tile=4)
+    ref = oracle.matmul(blocks, synth.Q8_0, N, K, oracle.f16_to_f32(a[rows]))
+    check(got[rows], ref, f"wr8 launches ({len(rows)} rows)")
