@@ -1,6 +1,7 @@
-// hq_gemm_wr8.hip - Q8_0 GEMM for prefill shapes of one tile round (M = 512 at N ~ 10k; also the
-// gate/up pair GEMM with the SwiGLU epilogue, one launch per round) on gfx950: 128 x 192 output tiles;
-// 4 MFMA waves that each own all 128 rows and 48 columns, and 4 loader waves.
+// hq_gemm_wr8.hip - Q8_0 GEMM for prefill shapes (M = 512 at N ~ 10k in one launch; larger M and the
+// gate/up pair GEMM with the SwiGLU epilogue as launches of one round each, planned by the caller) on
+// gfx950: 128 x 192 output tiles; 4 MFMA waves that each own all 128 rows and 48 columns, and 4
+// loader waves.
 //
 // C[M,N] (+)= A[M,K] . W^T with A fp16 and W GGUF Q8_0 blocks resident in HBM (reference arithmetic:
 // cleanroom-transformer/src/ggml_quant.h:42-49; matmul src/cpu_backend.c:38-54).

@@ -163,9 +163,9 @@ def test_wr8_workspace_none(hqlib):
 
 @pytest.mark.parametrize("M,N,K", [(1000, 9672, 512), (2048, 2560, 1024)])
 def test_wr8_several_launches(hqlib, oracle, M, N, K):
-    """Many tiles: the GEMM as launches of at most one round of tiles each (M = 1000: two launches of
-    26 and 25 column tiles x 8 row tiles, the last row tile ragged; M = 2048 at N = 2560: one launch
-    of 16 x 14 tiles)."""
+    """Many tiles: the GEMM as launches of at most one round of tiles per XCD (M = 1000: two launches
+    of 512 and 488 rows, the second's last row tile ragged, x 51 column tiles; M = 2048 at N = 2560:
+    one launch of 16 x 14 tiles, 32 on each of the XCDs that get two column tiles)."""
     blocks = synth.random_blocks(synth.Q8_0, synth.Rng(271 + M), N, K)
     a = synth.activations_f16(synth.Rng(272 + M), M, K)
     got = run(hqlib, blocks, a, N, K, "wr8 launches")
