@@ -60,6 +60,12 @@ struct WrArgs {
     void *C;
     int c_f32, accumulate;
     int mt, nt0, nt;  // M-tiles; this launch's column tiles nt0 .. nt - 1
+    // K split: each tile's super-blocks cut into `parts` contiguous ranges, one workgroup each, whose
+    // fp32 tiles meet in partials (tile_finish: the last to arrive adds them in part order); 1: whole K
+    int parts;
+    float *partials;
+    int *counters;
+    int ntiles;  // mt * nt (the counter and partial-tile index range)
 };
 
 template <int NB>
@@ -92,19 +98,31 @@ DEV void wr_dec_half(h8 &b, u2v q, int hf, uint32_t mask, h2 mul, h2 add) {
 }
 
 
-template <int NB>
-__global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
+// The tile body; KS: with the K split (parts > 1; the split-only work is compiled out of the whole-K
+// kernel, which is the headline's)
+template <int NB, bool KS>
+DEV void wr_tile(const WrArgs &g) {
     using L = WrLds<NB>;
     constexpr int BN = L::BN, WC = L::WC;
     static_assert(NB == 3, "the loaders' DMA schedule is written for 192-column tiles");
     __shared__ __attribute__((aligned(256))) char lds[L::TOTAL];
-    // tile: XCD x = b % 8 takes N-tiles x, x + 8, ...; its slots run over the M-tiles of one N-tile
-    // first (the weight slab is then fetched once per XCD)
+    // tile and K part: XCD x = b % 8 takes column units x, x + 8, ... (unit = N-tile x parts + part);
+    // its slots run over the M-tiles of one unit first (the unit's weight slab is then fetched once
+    // per XCD)
     const int b = blockIdx.x, x = b & 7, j8 = b >> 3;
-    const int nt_i = g.nt0 + x + 8 * (j8 / g.mt), mt_i = j8 % g.mt;
+    const int parts = KS ? g.parts : 1;
+    const int cu = g.nt0 * parts + x + 8 * (j8 / g.mt), mt_i = j8 % g.mt;
+    const int nt_i = KS ? cu / parts : cu, part = KS ? cu - nt_i * parts : 0;
     if (nt_i >= g.nt) return;
     const int m0 = mt_i * WR_BM, n0 = nt_i * BN;
-    const int M = g.M, N = g.N, K = g.K, U = K / 256, S2 = 4 * U;
+    const int M = g.M, N = g.N, K = g.K, Ut = K / 256;
+    // this part's super-blocks u0 .. u0 + U - 1: the operand bases move to u0 (row strides stay), so
+    // the body below counts super-blocks and stages from 0 (the column tables are global: F and c of
+    // a part's last super-block look at the next part's first)
+    const int u0 = KS ? part * Ut / parts : 0, U = KS ? (part + 1) * Ut / parts - u0 : Ut, S2 = 4 * U;
+    const uint16_t *const Ab = g.A + (size_t)u0 * 256;
+    const uint8_t *const Wb = g.W + (size_t)u0 * 144;
+    const uint8_t *const Tb = g.tab + (size_t)u0 * N * HQ_Q4K_TAB_BYTES;
     // (the wave index through readfirstlane: the role and every LDS DMA address derived from it are
     // then scalar values, not per-lane ones read back with a VALU instruction per DMA)
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, ln = lane & 15,
@@ -113,8 +131,8 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
     // (wave 4 + w: a quarter of the activation tile and of its sub-block sums, and a share of the quant
     // groups and column tables)
     const int role = wave >> 2, w4 = wave & 3;
-    const rsrc_t ra = make_rsrc(g.A, (uint32_t)((size_t)M * K * 2));
-    const rsrc_t rw = make_rsrc(g.W, (uint32_t)((size_t)N * g.row_bytes));
+    const rsrc_t ra = make_rsrc(Ab, (uint32_t)((size_t)M * K * 2 - (size_t)u0 * 512));
+    const rsrc_t rw = make_rsrc(Wb, (uint32_t)((size_t)N * g.row_bytes - (size_t)u0 * 144));
     const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
     const int wc0 = WC * w4, nw = n0 + wc0;  // first column of MFMA wave w4 (in the tile, in W)
 
@@ -188,7 +206,7 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
     // 64k .. + 64. Loader waves 2 and 3 issue them (they have one quant DMA per stage, waves 0 and 1 two).
     // Past column N these read other table bytes (the upload leaves HQ_Q4K_TAB_PAD zero bytes after the
     // tables for the last tile's), used only for outputs that are not stored
-    const rsrc_t rt = make_rsrc(g.tab, (uint32_t)((size_t)N * U * HQ_Q4K_TAB_BYTES));
+    const rsrc_t rt = make_rsrc(Tb, (uint32_t)((size_t)N * U * HQ_Q4K_TAB_BYTES));
     auto dma_bm = [&](int u, int k) {
         dma16_so(rt, lds0 + (uint32_t)(L::T_BM + 1024 * k), 16u * (uint32_t)lane,
                  (uint32_t)u * (uint32_t)N * HQ_Q4K_TAB_BYTES + (uint32_t)(n0 + 32 * k) * 32u);
@@ -311,6 +329,13 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
             }
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last (clamped, unused) loads
+        if constexpr (KS) {
+            // meet the MFMA waves once they are done with the rings and tables and once their tile is
+            // in LDS, then store or reduce it with them
+            wr_barrier();
+            wr_barrier();
+            tile_finish<WR_BM, BN, WR_NT, 4>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::T_REC));
+        }
         return;
     }
 
@@ -415,12 +440,17 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
         }
         rs = rsn;
     }
-    // ---- the last super-block's min k-step (its Bmin, in its own units, read at p = 3, and its sums
-    // landed by the last barrier; its F is 1, so rows 6 and 7 need no rescale), then back to true units
-    // (its c) and straight from the accumulators:
+    // ---- rows 6 and 7 to the units of the next super-block (rows 0-5 were rescaled in the last stage;
+    // F is 1 for the matrix's last super-block, c_u / c_{u+1} where a K part ends before it), the last
+    // super-block's min k-step (its Bmin, in those units, read at p = 3, and its sums landed by the
+    // last barrier), then back to true units (c_{u+1}, or the last super-block's c) and straight from
+    // the accumulators (or, with a K split, through LDS to tile_finish):
     // lane (ln, lg) of block (i, j) holds row 16i + ln, columns 16j + 4lg .. + 3 of the wave's
     // columns (one 16-byte fp32 or 8-byte fp16 store; element by element at the matrix edge or where
     // N % 4 or C's alignment does not allow it)
+    if constexpr (KS)
+#pragma unroll
+        for (int j = 0; j < NB; j++) acc[6][j] *= r[j], acc[7][j] *= r[j];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const h8 si = rds(u_last & 1, i);
@@ -432,6 +462,19 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
         const f4 cl = rdr(j, u_last % 3, 3);
 #pragma unroll
         for (int i = 0; i < 8; i++) acc[i][j] *= cl;
+    }
+    if constexpr (KS) {
+        constexpr int LD = BN + 4;  // tile_finish's row stride in floats
+        wr_barrier();               // every wave is done with the rings and tables
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+#pragma unroll
+            for (int j = 0; j < NB; j++)
+                *(f4 *)(lds + ((16 * i + ln) * LD + wc0 + 16 * j + 4 * lg) * 4) = acc[i][j];
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        wr_barrier();
+        tile_finish<WR_BM, BN, WR_NT, 4>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::T_REC));
+        return;
     }
     // (vector stores write through to memory: SC1, measured faster than write-back here, where every
     // tile stores its whole output at the end)
@@ -493,6 +536,15 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
         }
     }
 }
+
+template <int NB>
+__global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
+    wr_tile<NB, false>(g);
+}
+template <int NB>
+__global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr_ks(WrArgs g) {
+    wr_tile<NB, true>(g);
+}
 }  // namespace
 
 // Per-column tables of every super-block of a Q4_K matrix (one thread per row, super-blocks in order):
@@ -553,7 +605,7 @@ int hq_wr_fits(const hq_dev_mat *W, int M) {
 }
 
 hipError_t hq_launch_gemm_wr(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
-                             int nt0, int nt1, hipStream_t st) {
+                             int nt0, int nt1, int parts, float *partials, int *counters, hipStream_t st) {
     if (!hq_wr_fits(W, M) || !W->tab) return hipErrorInvalidValue;  // (every uploaded Q4_K matrix has its tables)
     constexpr int NB = 3;
     WrArgs g;
@@ -563,9 +615,17 @@ hipError_t hq_launch_gemm_wr(const hq_dev_mat *W, const uint16_t *A, int M, void
     const int nt_all = (g.N + 64 * NB - 1) / (64 * NB);
     g.nt0 = nt0, g.nt = nt1 < 0 || nt1 > nt_all ? nt_all : nt1;
     if (nt0 < 0 || nt0 >= g.nt) return hipErrorInvalidValue;
+    // K split: whole super-blocks per part, the full column range, a workspace of one fp32 tile per
+    // (tile, part) and a zeroed counter per tile, 32-bit offsets
+    g.parts = parts, g.partials = partials, g.counters = counters, g.ntiles = g.mt * g.nt;
+    if (parts < 1 || parts > 4 || parts > g.K / 256) return hipErrorInvalidValue;
+    if (parts > 1 && (!partials || !counters || nt0 != 0 || c_f32 == HQ_OUT_SWIGLU ||
+                      (size_t)g.ntiles * parts * WR_BM * 64 * NB * 4 >= ((size_t)1 << 32)))
+        return hipErrorInvalidValue;
     // fp32 or fp16 C, or the SwiGLU output of a gate/up pair matrix (N a multiple of 16, no accumulate)
     if (c_f32 != 0 && c_f32 != 1 && !(c_f32 == HQ_OUT_SWIGLU && W->rows % 16 == 0 && !accumulate)) return hipErrorInvalidValue;
-    const unsigned grid = (unsigned)(8 * ((g.nt - g.nt0 + 7) / 8) * g.mt);
-    k_gemm_q4_k_wr<NB><<<grid, WR_NT, 0, st>>>(g);
+    const unsigned grid = (unsigned)(8 * (((g.nt - g.nt0) * parts + 7) / 8) * g.mt);
+    if (parts > 1) k_gemm_q4_k_wr_ks<NB><<<grid, WR_NT, 0, st>>>(g);
+    else k_gemm_q4_k_wr<NB><<<grid, WR_NT, 0, st>>>(g);
     return hipGetLastError();
 }

@@ -80,10 +80,11 @@ hipError_t hq_launch_gemm_bt(const hq_dev_mat *W, const uint16_t *A, const uint1
 // that each decode their own 48 columns and 4 loader waves (which also form the activation sub-block
 // sums: no pre-pass, no workspace); whether a shape's byte offsets suit it, and the launch (c_f32:
 // 1 fp32 C, 0 fp16 C, HQ_OUT_SWIGLU fp16 silu(gate) * up of a gate/up pair matrix) of the column
-// tiles nt0 .. nt1 - 1 (nt1 < 0: to the last).
+// tiles nt0 .. nt1 - 1 (nt1 < 0: to the last); the Q4_K one also with each tile's K split over
+// `parts` workgroups (partials / counters as for the other K splits).
 int hq_wr_fits(const hq_dev_mat *W, int M);
 hipError_t hq_launch_gemm_wr(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
-                             int nt0, int nt1, hipStream_t st);
+                             int nt0, int nt1, int parts, float *partials, int *counters, hipStream_t st);
 // The same tile shape for Q8_0 (hq_gemm_wr8.hip; K a multiple of 256, no workspace).
 int hq_wr8_fits(const hq_dev_mat *W, int M);
 hipError_t hq_launch_gemm_wr8(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,

@@ -1229,6 +1229,7 @@ struct GemmCfg {
     int rb8;        // Q8_0 M <= 64: workgroups per tile of k_gemm_q8_0_rb (hq_gemm_rb.hip); 0: not used
     bool bt;        // Q4_K large M: the 256 x 256 tile kernel k_gemm_q4_k_bt (hq_gemm_bt.hip)
     bool wr;        // Q4_K, one round of full-K tiles: the 128 x 192 tile kernel k_gemm_q4_k_wr (hq_gemm_wr.hip)
+    int wr_parts;   // with wr: workgroups per tile (K split), 1: whole K
     bool wr8;       // Q8_0, the same: k_gemm_q8_0_wr (hq_gemm_wr8.hip)
 };
 
@@ -1269,6 +1270,20 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
     // Q4_K full-K tiles without a K split: the 128 x 192 tile kernel, whose waves decode their own
     // columns (M = 512, N = 9728: 204 tiles)
     c.wr = c.ws_nb && c.ws_parts == 1 && hq_wr_fits(W, M);
+    c.wr_parts = 1;
+    // few tiles over a long K, where the LDS-decode kernel splits K (M = 512, N = 2560, K = 9728): the
+    // register-decode kernel with each tile's K split over 4 or 2 workgroups of >= 8 super-blocks,
+    // when its tiles x parts fit one round on every XCD and fill >= 70 % of the CUs (4 x 14 x 4 = 224)
+    if (!c.wr && c.ws_nb && c.ws_parts > 1 && hq_wr_fits(W, M)) {
+        const int mt = (M + 127) / 128, nt = ((int)W->rows + 191) / 192, per_xcd = std::max(1, n_cu / 8);
+        for (int parts = 4; !c.wr && parts >= 2; parts /= 2) {
+            const int units = nt * parts;
+            if (mt * ((units + 7) / 8) <= per_xcd && 10L * mt * units >= 7L * n_cu && (int)(W->cols / 256) >= 8 * parts) {
+                c.wr = true;
+                c.wr_parts = parts;
+            }
+        }
+    }
     // Q4_K where the Stream-K wide kernel would run: the 256 x 256 tile kernel when its rounds of
     // tiles fill at least 3/4 of the CU time (M = 16384, N = 9728: 2432 tiles in 9.5 rounds)
     c.bt = false;
@@ -1348,7 +1363,7 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
     if (c.rbm) snprintf(buf, n, "k_gemm_q4_k_rb<1, 4, 3, 2>");
     else if (c.rb8) snprintf(buf, n, "k_gemm_q8_0_rb<%d, 3, 2>", M <= 16 ? 1 : M <= 32 ? 2 : 4);
     else if (c.bt) snprintf(buf, n, "k_gemm_q4_k_bt");
-    else if (c.wr) snprintf(buf, n, "k_gemm_q4_k_wr<3>");
+    else if (c.wr) snprintf(buf, n, c.wr_parts > 1 ? "k_gemm_q4_k_wr_ks<3>" : "k_gemm_q4_k_wr<3>");
     else if (c.wr8) snprintf(buf, n, "k_gemm_q8_0_wr");
     else if (c.ws_nb) snprintf(buf, n, "k_gemm_q4_k_ws<%d>", c.ws_nb);
     else if (c.ws8_nb) snprintf(buf, n, "k_gemm_q8_0_ws<%d>", c.ws8_nb);
@@ -1379,6 +1394,11 @@ void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_by
     }
     *sums_bytes = (c.wide && !c.wr) || c.rbm ? (size_t)M * (W->cols / KC) * 32 : 0;  // (wr forms its own)
     if (c.wr8) *partial_bytes = *counter_bytes = 0;  // (no K split)
+    if (c.wr) {  // K split: one fp32 128 x 192 tile per (tile, part)
+        const size_t tiles = (size_t)((M + 127) / 128) * ((W->rows + 191) / 192);
+        *partial_bytes = c.wr_parts > 1 ? tiles * c.wr_parts * 128 * 192 * sizeof(float) : 0;
+        *counter_bytes = c.wr_parts > 1 ? tiles * sizeof(int) : 0;
+    }
 }
 
 // Pre-pass of a GEMM (the activation sub-block sums of the Q4_K kernels that read them from HBM;
@@ -1405,7 +1425,7 @@ hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, vo
     if (c.rbm) return hq_launch_gemm_rb(W, A, wk.sums, M, C, c_f32, accumulate, c.rbm, wk.partials, wk.counters, st);
     if (c.rb8) return hq_launch_gemm_rb8(W, A, M, C, c_f32, accumulate, c.rb8, wk.partials, wk.counters, st);
     if (c.bt) return hq_launch_gemm_bt(W, A, wk.sums, M, C, c_f32, accumulate, st);
-    if (c.wr) return hq_launch_gemm_wr(W, A, M, C, c_f32, accumulate, 0, -1, st);
+    if (c.wr) return hq_launch_gemm_wr(W, A, M, C, c_f32, accumulate, 0, -1, c.wr_parts, wk.partials, wk.counters, st);
     if (c.wr8) {
         const size_t K = W->cols, N = W->rows, esize = c_f32 ? 4 : 2;
         return wr_launches(wr_plan(M, (int)N, wk.n_cu), M, (int)N, [&](int m0, int rows, int t0, int t1) {
@@ -1463,7 +1483,7 @@ hipError_t hq_launch_gemm_swiglu(const hq_dev_mat *W, const uint16_t *A, int M, 
             const uint16_t *Am = A + (size_t)m0 * K;
             uint16_t *om = out + (size_t)m0 * (N / 2);
             return wr8 ? hq_launch_gemm_wr8(W, Am, rows, om, HQ_OUT_SWIGLU, 0, t0, t1, st)
-                       : hq_launch_gemm_wr(W, Am, rows, om, HQ_OUT_SWIGLU, 0, t0, t1, st);
+                       : hq_launch_gemm_wr(W, Am, rows, om, HQ_OUT_SWIGLU, 0, t0, t1, 1, nullptr, nullptr, st);
         });
     }
     float eff = 0.f;
