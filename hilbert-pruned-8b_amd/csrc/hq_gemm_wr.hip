@@ -1,6 +1,7 @@
-// hq_gemm_wr.hip - Q4_K GEMM for prefill shapes of one tile round (M = 128 .. ~512 at N ~ 10k) on
-// gfx950: 128 x 64NB output tiles; 4 MFMA waves that each own all 128 rows and 16NB columns, and 4
-// loader waves.
+// hq_gemm_wr.hip - Q4_K GEMM for prefill shapes of one tile round (M = 128 .. ~512 at N ~ 10k; with
+// each tile's K split over workgroups for few tiles over a long K, k_gemm_q4_k_wr_ks; the gate/up pair
+// GEMM with the SwiGLU epilogue) on gfx950: 128 x 64NB output tiles; 4 MFMA waves that each own all
+// 128 rows and 16NB columns, and 4 loader waves.
 //
 // C[M,N] (+)= A[M,K] . W^T with A fp16 and W GGUF Q4_K super-blocks resident in HBM (reference
 // arithmetic: cleanroom-transformer/src/ggml_quant.h:51-59, :135-150; matmul src/cpu_backend.c:38-54).
