@@ -80,7 +80,7 @@ def main_kernel_name(hq, gtype, M, N, K):
 
 
 def bench_gemm(hq, synth, gtype, N, K, M, c_f32, steps, warmup, stream, eager_warmup=True, kernel_time=False,
-               rotate=True, settle_s=0.0):
+               rotate=True, settle_s=0.0, reps=1):
     rb = synth.row_bytes(gtype, K)
     blocks = synth.random_blocks(gtype, synth.Rng(4242 + gtype + N), N, K)
     copies = max(2, -(-ROTATE_BYTES // (N * rb))) if rotate else 2
@@ -99,7 +99,7 @@ def bench_gemm(hq, synth, gtype, N, K, M, c_f32, steps, warmup, stream, eager_wa
                 i += 1
             stream.sync()
     t0 = time.perf_counter()
-    ms = hq.time_gemm(mats, A, M, C, c_f32, steps, 1, stream)
+    ms = hq.time_gemm(mats, A, M, C, c_f32, steps, reps, stream)
     wall = time.perf_counter() - t0
     ms_med = hq.time_gemm(mats, A, M, C, c_f32, MEDIAN_ITERS, MEDIAN_REPS, stream) if kernel_time else None
     ms_kernel = (hq.time_gemm_kernel(mats, A, M, C, c_f32, MEDIAN_ITERS, MEDIAN_REPS, stream)
@@ -356,8 +356,10 @@ def main():
         shapes = [(synth.Q8_0, 9728, 2560, m) for m in (1, 16, 128, 512, 2048)] + \
                  [(synth.Q4_K, 9728, 2560, m) for m in (1, 64, 512, 4096)] + \
                  [(synth.Q4_K, 2560, 9728, m) for m in (1, 64, 512, 4096)]
+        # each shape: 0.1 s of untimed calls (clocks at their loaded level), then the median of
+        # MEDIAN_REPS graph replays of 20 calls (a single replay ran up to a third slow at M = 2048)
         for g, n, k, m in shapes:
-            r = bench_gemm(hq, synth, g, n, k, m, False, 20, 2, stream)
+            r = bench_gemm(hq, synth, g, n, k, m, False, 20, 2, stream, settle_s=0.1, reps=MEDIAN_REPS)
             bound = "hbm" if (2.0 * m * n * k) / gemm_bytes(g, m, n, k, 2) < 312.5 else "mfma"
             r["bound"] = bound
             r["frac"] = round(r["gbs"] / PEAK_GBS if bound == "hbm" else r["tflops"] / PEAK_TFLOPS, 4)
