@@ -786,7 +786,8 @@ __global__ void __launch_bounds__(256) k_gemm_q4_k(GemmArgs g) {
 constexpr int WNW = 8;  // waves per workgroup
 
 // A tile DMA: instruction q = w + 8qq (rows 2q, 2q + 1) of wave w; r & 15 = (2w + (lane >> 5)) & 15
-// is the same for every qq, so one per-lane base serves all of them.
+// is the same for every qq, so one per-lane base serves all of them. The row step and k0 go into the
+// VGPR offset (the one a buffer load range-checks), so rows past M read zeros.
 DEV uint32_t adma_w_base(int K, int m0) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, p = lane & 31;
     const int r0 = 2 * wave + (lane >> 5);
@@ -800,15 +801,15 @@ DEV void dma_a_w(_Float16 *buf, rsrc_t ra, uint32_t base, int K, int k0) {
     const int wave = threadIdx.x >> 6;
 #pragma unroll
     for (int qq = 0; qq < PER_WAVE; qq++)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, lds_ptr(buf + (wave + WNW * qq) * 512), 16, base,
-                                                 (uint32_t)(qq * 16 * K * 2 + 2 * k0), 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, lds_ptr(buf + (wave + WNW * qq) * 512), 16,
+                                                 base + (uint32_t)(qq * 16 * K * 2 + 2 * k0), 0, 0, 0);
 }
 
 // Instruction qq of dma_a_w alone (the wide kernel spreads them over a unit's k-steps).
 DEV void dma_a_w1(_Float16 *buf, rsrc_t ra, uint32_t base, int K, int k0, int qq) {
     const int wave = threadIdx.x >> 6;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, lds_ptr(buf + (wave + WNW * qq) * 512), 16, base,
-                                             (uint32_t)(qq * 16 * K * 2 + 2 * k0), 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, lds_ptr(buf + (wave + WNW * qq) * 512), 16,
+                                             base + (uint32_t)(qq * 16 * K * 2 + 2 * k0), 0, 0, 0);
 }
 
 // S tile of unit u: 16*MB rows x 32 bytes, one 1 KB instruction (32 rows) per wave w < 16*MB/32.

@@ -43,7 +43,9 @@ constexpr int KC = 256;
 
 // Activation tile DMA: instruction qq of wave w moves rows r = 8qq + 2w + (lane >> 5) (two 256-half
 // rows per 64-lane instruction) into LDS slots (r, lane & 31). The per-lane byte offset is
-// a_base[qq & 1] (row and swizzled chunk) plus the uniform qq * 16 * K + 2 * k0 in soffset.
+// a_base[qq & 1] (row and swizzled chunk) plus qq * 16 * K + 2 * k0, all of it in the VGPR offset:
+// a buffer load range-checks only that offset (not soffset), so rows at or past M, and the tail of
+// the last row past K, read zeros instead of memory beyond A.
 struct ADma {
     uint32_t base[2];
 };
@@ -69,8 +71,8 @@ DEV void dma_a(_Float16 *buf, rsrc_t ra, const ADma &d, int K, int k0) {
     for (int qq = 0; qq < (INSTR + 3) / 4; qq++) {
         const int q = 4 * qq + wave;
         if (INSTR % 4 == 0 || q < INSTR)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, lds_ptr(buf + q * 512), 16, d.base[qq & 1],
-                                                     (uint32_t)(qq * 16 * K + 2 * k0), 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, lds_ptr(buf + q * 512), 16,
+                                                     d.base[qq & 1] + (uint32_t)(qq * 16 * K + 2 * k0), 0, 0, 0);
     }
 }
 
