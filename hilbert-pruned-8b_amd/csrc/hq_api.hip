@@ -95,6 +95,16 @@ static uint32_t block_bytes(int t) {
     return t == HQ_GGML_Q8_0 ? 34u : t == HQ_GGML_Q4_K ? 144u : t == HQ_GGML_Q6_K ? 210u : 0u;
 }
 constexpr size_t Q6K_SLOT = 224;  // device bytes of one Q6_K super-block (210 GGUF bytes + zero padding)
+static const char SUPPORTED[] = "Q8_0 = 8, Q4_K = 12, Q6_K = 14";
+
+extern "C" int hq_internal_block_shape(int ggml_type, uint32_t *values, uint32_t *bytes) {
+    if (!block_values(ggml_type)) return -1;
+    *values = block_values(ggml_type);
+    *bytes = block_bytes(ggml_type);
+    return 0;
+}
+
+extern "C" const char *hq_internal_supported_types(void) { return SUPPORTED; }
 
 // Storage row of Hugging Face row r (llama.cpp q/k interleave; reference src/model.c:283-289).
 static uint32_t storage_row(uint32_t rows, uint32_t perm_heads, uint32_t r) {
@@ -211,7 +221,7 @@ static int check_wmat(const hq_wmat_t *w, const char *who, size_t *rb) {
     if (!w || !w->data) return fail("%s: no matrix", who);
     if (w->dtype != HQ_DT_GGML) return fail("%s: dtype %d is not a GGUF block type", who, w->dtype);
     const uint32_t per = block_values(w->ggml_type);
-    if (!per) return fail("%s: ggml type %d is not supported (Q8_0 = 8, Q4_K = 12, Q6_K = 14)", who, w->ggml_type);
+    if (!per) return fail("%s: ggml type %d is not supported (%s)", who, w->ggml_type, SUPPORTED);
     if (w->rows == 0 || w->cols == 0 || w->cols % per)
         return fail("%s: shape [%u, %u] is not a whole number of %u-value blocks per row", who, w->rows, w->cols, per);
     if (w->rows > (1u << 30) || w->cols > (1u << 24)) return fail("%s: shape [%u, %u] too large", who, w->rows, w->cols);

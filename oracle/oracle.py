@@ -162,6 +162,8 @@ class Reference:
         L.ref_gguf_tensor.restype = C.c_int
         L.ref_gguf_tensor.argtypes = [C.c_char_p, C.c_char_p, C.POINTER(C.c_int), C.POINTER(C.c_uint64), C.c_void_p,
                                       C.c_size_t, C.POINTER(C.c_size_t)]
+        L.ref_gguf_open_ok.restype = C.c_int
+        L.ref_gguf_open_ok.argtypes = [C.c_char_p]
         L.ref_logits.restype = C.c_int
         L.ref_logits.argtypes = [C.c_char_p, _u32p, C.c_size_t, _u32p, C.c_uint32, _f32p, C.c_void_p]
 
@@ -188,6 +190,10 @@ class Reference:
         if self.lib.ref_gguf_tensor(str(path).encode(), name.encode(), C.byref(t), ne, buf.ctypes.data, cap, C.byref(n)):
             raise RuntimeError("reference: " + (self.lib.ref_last_error() or b"?").decode())
         return t.value, tuple(ne), buf[:n.value].copy()
+
+    def gguf_accepts(self, path):
+        """Whether the reference's GGUF reader opens the file (header, metadata, tensor table)."""
+        return self.lib.ref_gguf_open_ok(str(path).encode()) == 0
 
     def logits(self, gguf_path, tokens, ids):
         out = np.empty(len(ids), dtype=np.float32)

@@ -4,7 +4,8 @@
  * /root/reference/cleanroom-transformer/src, into oracle/_ref/libref.so. The reference source
  * is included, not copied: this file only adds exported wrappers around functions that the
  * reference declares static (src/cpu_backend.c:28, :39; src/ops_common.h:32;
- * src/ggml_quant.h:51, :63) and a one-call model + CPU-forward driver (as src/main.c:351-387).
+ * src/ggml_quant.h:51, :63), a one-call model + CPU-forward driver (as src/main.c:351-387) and
+ * two probes of the reference GGUF reader (src/gguf.c).
  * Used only by tests/ to pin the oracle restatement (oracle/hq_oracle.c) bit for bit.
  */
 #include "cpu_backend.c"
@@ -58,4 +59,13 @@ int ref_gguf_tensor(const char *path, const char *name, int *type, uint64_t ne[4
     if (n <= cap) memcpy(out, p, n);
     gguf_close(g);
     return n <= cap ? 0 : -1;
+}
+
+/* gguf_open alone (src/gguf.c:134-219): 0 when the reference reader accepts the file's header,
+ * metadata and tensor table, else -1 (ref_last_error). */
+int ref_gguf_open_ok(const char *path) {
+    gguf_t *g;
+    if (gguf_open(path, &g)) return -1;
+    gguf_close(g);
+    return 0;
 }
