@@ -184,8 +184,16 @@ void gather_rows(F row_ptr, size_t rb, uint32_t r0, uint32_t n, uint8_t *dst) {
         work(0);
         return;
     }
+    // a thread that cannot be created (std::system_error under thread limits) leaves its share to
+    // this thread, so the upload still completes instead of terminating the process
     std::vector<std::thread> th;
-    for (int t = 1; t < nthr; t++) th.emplace_back(work, t);
+    int t = 1;
+    try {
+        th.reserve(nthr - 1);
+        for (; t < nthr; t++) th.emplace_back(work, t);
+    } catch (const std::exception &) {
+    }
+    for (int u = t; u < nthr; u++) work(u);
     work(0);
     for (auto &x : th) x.join();
 }

@@ -7,6 +7,9 @@ Block layouts (GGUF, little-endian; reference cleanroom-transformer/src/ggml_qua
   Q8_0  34 B / 32 values : fp16 d, int8 q[32]                          (ggml_quant.h:95-99)
   Q4_K 144 B / 256 values: fp16 d, fp16 dmin, u8 scales[12], u8 qs[128] (ggml_quant.h:135-150)
   Q6_K 210 B / 256 values: u8 ql[128], u8 qh[64], int8 scales[16], fp16 d (ggml_quant.h:151-169)
+  Q2_K  84 B / 256 values: u8 scales[16], u8 qs[64], fp16 d, fp16 dmin  (ggml_quant.h:100-111)
+  Q3_K 110 B / 256 values: u8 hmask[32], u8 qs[64], u8 scales[12], fp16 d (ggml_quant.h:112-134)
+  Q5_K 176 B / 256 values: fp16 d, fp16 dmin, u8 scales[12], u8 qh[32], u8 qs[128] (:135-150)
 
 Workloads:
   config 2  Q8_0 9728x2560, q uniform in [-127, 127], d = fp16(|N(0,1)| * 2e-4)
@@ -18,9 +21,11 @@ Activations are fp16(N(0,1)), returned as uint16 bit patterns.
 """
 import numpy as np
 
-Q8_0, Q4_K, Q6_K = 8, 12, 14
-BLOCK_VALUES = {Q8_0: 32, Q4_K: 256, Q6_K: 256}
-BLOCK_BYTES = {Q8_0: 34, Q4_K: 144, Q6_K: 210}
+Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 8, 10, 11, 12, 13, 14
+KQUANTS = (Q2_K, Q3_K, Q4_K, Q5_K, Q6_K)
+BLOCK_VALUES = {Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+BLOCK_BYTES = {Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+TYPE_NAMES = {Q8_0: "Q8_0", Q2_K: "Q2_K", Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
 
 _M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
 
@@ -124,10 +129,35 @@ def q6_k_blocks(rng, rows, cols, scale=2e-5):
     return blk.reshape(rows, row_bytes(Q6_K, cols))
 
 
+def _kquant_blocks(gtype, rng, rows, cols, fp16_at, scale):
+    """Super-blocks of `gtype` with every byte uniform except the fp16 scales at byte offsets
+    `fp16_at`, which are fp16(|N(0,1)| * scale)."""
+    nb = rows * (cols // 256)
+    blk = rng.bytes(nb * BLOCK_BYTES[gtype]).reshape(nb, BLOCK_BYTES[gtype])
+    for o in fp16_at:
+        blk[:, o:o + 2] = f16_bits(np.abs(rng.normal(nb)) * scale).view(np.uint8).reshape(nb, 2)
+    return blk.reshape(rows, row_bytes(gtype, cols))
+
+
+def q2_k_blocks(rng, rows, cols, scale=1e-2):
+    """Q2_K super-blocks: scales and qs uniform bytes, d and dmin = fp16(|N(0,1)| * scale)."""
+    return _kquant_blocks(Q2_K, rng, rows, cols, (80, 82), scale)
+
+
+def q3_k_blocks(rng, rows, cols, scale=5e-4):
+    """Q3_K super-blocks: hmask, qs and the packed scales uniform bytes, d = fp16(|N(0,1)| * scale)."""
+    return _kquant_blocks(Q3_K, rng, rows, cols, (108,), scale)
+
+
+def q5_k_blocks(rng, rows, cols, scale=5e-4):
+    """Q5_K super-blocks: scales, qh and qs uniform bytes, d and dmin = fp16(|N(0,1)| * scale)."""
+    return _kquant_blocks(Q5_K, rng, rows, cols, (0, 2), scale)
+
+
 def random_blocks(gtype, rng, rows, cols):
-    if gtype == Q6_K:
-        return q6_k_blocks(rng, rows, cols)
-    return q8_0_blocks(rng, rows, cols) if gtype == Q8_0 else q4_k_blocks(rng, rows, cols)
+    gen = {Q8_0: q8_0_blocks, Q2_K: q2_k_blocks, Q3_K: q3_k_blocks, Q4_K: q4_k_blocks, Q5_K: q5_k_blocks,
+           Q6_K: q6_k_blocks}
+    return gen[gtype](rng, rows, cols)
 
 
 def quantize_q8_0(w):

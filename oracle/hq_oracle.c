@@ -37,10 +37,22 @@ void or_f16_to_f32_array(const uint16_t *in, float *out, size_t n) {
 
 /* src/ggml_quant.h:22-47 (the formats on this path; 0 = unsupported) */
 uint32_t or_block_values(int type) {
-    return type == OR_GGML_Q8_0 ? 32u : type == OR_GGML_Q4_K || type == OR_GGML_Q6_K ? 256u : 0u;
+    switch (type) {
+    case OR_GGML_Q8_0: return 32u;
+    case OR_GGML_Q2_K: case OR_GGML_Q3_K: case OR_GGML_Q4_K: case OR_GGML_Q5_K: case OR_GGML_Q6_K: return 256u;
+    default: return 0u;
+    }
 }
 uint32_t or_block_bytes(int type) {
-    return type == OR_GGML_Q8_0 ? 34u : type == OR_GGML_Q4_K ? 144u : type == OR_GGML_Q6_K ? 210u : 0u;
+    switch (type) {
+    case OR_GGML_Q8_0: return 34u;
+    case OR_GGML_Q2_K: return 84u;
+    case OR_GGML_Q3_K: return 110u;
+    case OR_GGML_Q4_K: return 144u;
+    case OR_GGML_Q5_K: return 176u;
+    case OR_GGML_Q6_K: return 210u;
+    default: return 0u;
+    }
 }
 
 /* src/gguf.c:54-57 */
@@ -66,24 +78,68 @@ void or_scale_min_k4(int j, const uint8_t *q, uint8_t *s, uint8_t *m) {
     *m = (uint8_t)((lo >> 4) | ((q[j] >> 6) << 4));
 }
 
+/* Q3_K 6-bit scale e (0..15) from the 12 packed bytes at sc (src/ggml_quant.h:118-128): the low
+ * nibble of scale 4g + i (g = 0..3, i = 0..3) is nibble g / 2 of byte 4 (g % 2) + i, its top two
+ * bits are bits 2g, 2g + 1 of byte 8 + i. */
+static int q3k_scale(const uint8_t *sc, int e) {
+    const int g = e >> 2, i = e & 3;
+    const int lo = (sc[4 * (g & 1) + i] >> (4 * (g >> 1))) & 0x0f, hi = (sc[8 + i] >> (2 * g)) & 3;
+    return lo | (hi << 4);
+}
+
 /* Sub-block `sub` (32 values) of one block.
  * Q8_0 (src/ggml_quant.h:95-99): {fp16 d; int8 q[32]}, y = q * d (exact in float).
- * Q4_K (src/ggml_quant.h:135-150): {fp16 d, fp16 dmin, u8 scales[12], u8 qs[128]}; sub-block j
- * reads nibble (j odd: high, even: low) of qs[32*(j/2) + l]; y = (d*s)*q - dmin*m, where the
- * two products are exact in float and only the subtraction rounds. */
+ * Q4_K / Q5_K (src/ggml_quant.h:135-150): {fp16 d, fp16 dmin, u8 scales[12], [Q5_K: u8 qh[32],]
+ * u8 qs[128]}; sub-block j reads nibble (j odd: high, even: low) of qs[32*(j/2) + l], Q5_K adds
+ * 16 where bit j of qh[l] is set; y = (d*s)*q - dmin*m, where the two products are exact in float
+ * and only the subtraction rounds. */
 void or_dequant_sub32(int type, const uint8_t *b, int sub, float *y) {
     if (type == OR_GGML_Q8_0) {
         const float d = le_f16(b);
         for (int l = 0; l < 32; l++) y[l] = (float)(int8_t)b[2 + l] * d;
         return;
     }
-    if (type == OR_GGML_Q4_K) {
+    if (type == OR_GGML_Q4_K || type == OR_GGML_Q5_K) {
+        const int five = type == OR_GGML_Q5_K;
         uint8_t s, m;
         or_scale_min_k4(sub, b + 4, &s, &m);
         const float ds = le_f16(b) * (float)s, dm = le_f16(b + 2) * (float)m;
-        const uint8_t *qs = b + 16 + 32 * (sub >> 1);
+        const uint8_t *qs = b + (five ? 48 : 16) + 32 * (sub >> 1), *qh = b + 16;
         const int shift = (sub & 1) ? 4 : 0;
-        for (int l = 0; l < 32; l++) y[l] = ds * (float)((qs[l] >> shift) & 0x0f) - dm;
+        for (int l = 0; l < 32; l++) {
+            const int q = ((qs[l] >> shift) & 0x0f) + (five ? 16 * ((qh[l] >> sub) & 1) : 0);
+            y[l] = ds * (float)q - dm;
+        }
+        return;
+    }
+    if (type == OR_GGML_Q2_K) {
+        /* Q2_K (src/ggml_quant.h:100-111): {u8 scales[16], u8 qs[64], fp16 d, fp16 dmin}. Value
+         * 128h + 32j + l (h = 0, 1; j = 0..3) is bits 2j, 2j + 1 of qs[32h + l]; each 16 values have
+         * their own byte scales[8h + 2j + l/16]: low nibble s, high nibble m;
+         * y = (d*s)*q - dmin*m (both products exact in float, the subtraction rounds). */
+        const int h = sub >> 2, j = sub & 3;
+        const uint8_t *qs = b + 16 + 32 * h;
+        const float d = le_f16(b + 80), dmin = le_f16(b + 82);
+        for (int l = 0; l < 32; l++) {
+            const uint8_t sm = b[8 * h + 2 * j + (l >> 4)];
+            const float ds = d * (float)(sm & 0x0f), dm = dmin * (float)(sm >> 4);
+            y[l] = ds * (float)((qs[l] >> (2 * j)) & 3) - dm;
+        }
+        return;
+    }
+    if (type == OR_GGML_Q3_K) {
+        /* Q3_K (src/ggml_quant.h:112-134): {u8 hmask[32], u8 qs[64], u8 scales[12], fp16 d}. Value
+         * 128h + 32j + l is bits 2j, 2j + 1 of qs[32h + l] minus 4 unless bit 4h + j of hmask[l] is
+         * set; 16 values share the 6-bit scale 8h + 2j + l/16 (q3k_scale), offset by -32;
+         * y = (d * (sc - 32)) * q, both products exact in float. */
+        const int h = sub >> 2, j = sub & 3;
+        const uint8_t *qs = b + 32 + 32 * h;
+        const float d = le_f16(b + 108);
+        for (int l = 0; l < 32; l++) {
+            const float dl = d * (float)(q3k_scale(b + 96, 8 * h + 2 * j + (l >> 4)) - 32);
+            const int q = ((qs[l] >> (2 * j)) & 3) - ((b[l] >> (4 * h + j)) & 1 ? 0 : 4);
+            y[l] = dl * (float)q;
+        }
         return;
     }
     if (type == OR_GGML_Q6_K) {

@@ -10,7 +10,9 @@
  *   src/gguf.c:54-57            bytes per row                     or_row_bytes
  *   src/ggml_quant.h:51-59      6-bit scale/min unpack (k-quants) or_scale_min_k4
  *   src/ggml_quant.h:95-99      Q8_0 32-value block decode        or_dequant_sub32 (Q8_0)
- *   src/ggml_quant.h:135-150    Q4_K sub-block decode             or_dequant_sub32 (Q4_K)
+ *   src/ggml_quant.h:100-111    Q2_K sub-block decode             or_dequant_sub32 (Q2_K)
+ *   src/ggml_quant.h:112-134    Q3_K sub-block decode             or_dequant_sub32 (Q3_K), q3k_scale
+ *   src/ggml_quant.h:135-150    Q4_K / Q5_K sub-block decode      or_dequant_sub32 (Q4_K, Q5_K)
  *   src/ggml_quant.h:151-169    Q6_K sub-block decode             or_dequant_sub32 (Q6_K)
  *   src/gguf.c:59-73            row decode                        or_dequantize_row
  *   src/model.c:283-307         q/k row un-permute, row widen     or_src_row, or_wmat_row_f32
@@ -35,7 +37,7 @@
 extern "C" {
 #endif
 
-enum { OR_GGML_Q8_0 = 8, OR_GGML_Q4_K = 12, OR_GGML_Q6_K = 14 };
+enum { OR_GGML_Q8_0 = 8, OR_GGML_Q2_K = 10, OR_GGML_Q3_K = 11, OR_GGML_Q4_K = 12, OR_GGML_Q5_K = 13, OR_GGML_Q6_K = 14 };
 
 /* Same field order and types as the reference wmat_t (src/transformer.h:293-300). dtype is
  * always 3 (DT_GGML) here; only block-quantized matrices are on this path. */

@@ -11,6 +11,10 @@ Inputs are synthetic (hilbert-pruned-8b_amd/synth.py), so only inputs and output
                                        blocks, x, y0 -> y = matmul(W, x, accumulate) (cpu_backend.c:39)
   tiny_llama.npz                       config-1 prompt -> logits (model_load + cpu backend forward),
                                        with the sha256 of synth.tiny_llama(1) to catch generator drift
+  dequant_q{2,3,5}_k.npz / matmul_q{2,3,5}_k.npz
+                                       the same two fixtures for Q2_K, Q3_K and Q5_K
+
+`python tests/golden/make_golden.py kquants` writes only the Q2_K / Q3_K / Q5_K fixtures.
 """
 import hashlib
 import os
@@ -27,7 +31,8 @@ sys.path[:0] = [os.path.join(ROOT, "hilbert-pruned-8b_amd"), os.path.join(ROOT, 
 import gguf_writer  # noqa: E402
 import oracle  # noqa: E402
 import synth  # noqa: E402
-from test_oracle import special_q4_k_blocks, special_q6_k_blocks, special_q8_0_blocks  # noqa: E402
+from test_oracle import (special_kquant_blocks, special_q4_k_blocks, special_q6_k_blocks,  # noqa: E402
+                         special_q8_0_blocks)
 
 
 def digest(model):
@@ -94,5 +99,30 @@ def main():
     print("golden fixtures written:", logits)
 
 
+def kquants():
+    """Q2_K, Q3_K, Q5_K: dequant of special + random blocks (perm_heads 2) and a matmul with
+    accumulate (N = 40, K = 512, M = 5, the reference selftest's quant shape)."""
+    ref = oracle.Reference()
+    for gtype in (synth.Q2_K, synth.Q3_K, synth.Q5_K):
+        name = synth.TYPE_NAMES[gtype].lower()
+        rng = synth.Rng(7000 + gtype)
+        sp = special_kquant_blocks(gtype)  # 2 rows x 1024 values
+        blocks = np.ascontiguousarray(np.concatenate([sp, synth.random_blocks(gtype, rng, 6, 1024)]))
+        vals = ref.dequantize(blocks, gtype, 8, 1024, perm_heads=2)
+        np.savez_compressed(os.path.join(HERE, f"dequant_{name}.npz"), blocks=blocks, values=vals, gtype=gtype, rows=8,
+                            cols=1024, perm_heads=2)
+        blocks = synth.random_blocks(gtype, rng, 40, 512)
+        x = synth.activations_f16(rng, 5, 512).view(np.float16).astype(np.float32)
+        y0 = rng.normal(5 * 40).astype(np.float32).reshape(5, 40)
+        y = ref.matmul(blocks, gtype, 40, 512, x, y0.copy(), True)
+        np.savez_compressed(os.path.join(HERE, f"matmul_{name}.npz"), blocks=blocks, x=x, y0=y0, y=y, gtype=gtype,
+                            rows=40, cols=512, accumulate=True)
+    print("k-quant fixtures written")
+
+
 if __name__ == "__main__":
-    main()
+    if sys.argv[1:] == ["kquants"]:
+        kquants()
+    else:
+        main()
+        kquants()

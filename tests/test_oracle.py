@@ -123,11 +123,34 @@ def special_q6_k_blocks():
     return blk.reshape(2, -1)
 
 
+def special_kquant_blocks(gtype):
+    """Q2_K / Q3_K / Q5_K super-blocks whose fp16 scales are 0, +-1, the smallest subnormal, the
+    largest finite value, inf, NaN and a typical value; one block with every other byte 0 and one
+    with every other byte 0xFF (all quants and scale codes at their extremes)."""
+    fp16_at = {synth.Q2_K: (80, 82), synth.Q3_K: (108,), synth.Q5_K: (0, 2)}[gtype]
+    nbytes = synth.BLOCK_BYTES[gtype]
+    rng = synth.Rng(60 + gtype)
+    ds = [0x0000, 0x3C00, 0xBC00, 0x0001, 0x7BFF, 0x7C00, 0x7E00, 0x1400]
+    blk = rng.bytes(len(ds) * nbytes).reshape(len(ds), nbytes)
+    keep = np.ones(nbytes, bool)
+    for o in fp16_at:
+        keep[o:o + 2] = False
+    blk[1, keep] = 0
+    blk[2, keep] = 0xFF
+    for i, d in enumerate(ds):
+        for j, o in enumerate(fp16_at):
+            v = d if j == 0 else ds[(i + 3) % len(ds)]
+            blk[i, o:o + 2] = [v & 0xFF, v >> 8]
+    return blk.reshape(2, -1)
+
+
 SPECIAL_BLOCKS = {synth.Q8_0: lambda: special_q8_0_blocks(), synth.Q4_K: lambda: special_q4_k_blocks(),
-                  synth.Q6_K: lambda: special_q6_k_blocks()}
+                  synth.Q6_K: lambda: special_q6_k_blocks(), synth.Q2_K: lambda: special_kquant_blocks(synth.Q2_K),
+                  synth.Q3_K: lambda: special_kquant_blocks(synth.Q3_K),
+                  synth.Q5_K: lambda: special_kquant_blocks(synth.Q5_K)}
 
 
-@pytest.mark.parametrize("gtype", [synth.Q8_0, synth.Q4_K, synth.Q6_K])
+@pytest.mark.parametrize("gtype", [synth.Q8_0, synth.Q2_K, synth.Q3_K, synth.Q4_K, synth.Q5_K, synth.Q6_K])
 def test_dequant_matches_reference(oracle, reference, gtype):
     rng = synth.Rng(31)
     rows, cols = 24, 1024
@@ -207,6 +230,96 @@ def test_dequant_q4_k_closed_form(oracle):
         assert np.array_equal(got[:, 32 * sub:32 * sub + 32], want.astype(np.float32)), sub
 
 
+def test_dequant_q5_k_closed_form(oracle):
+    """Every (scale, min) code pair, every 5-bit code: y = d*s*(lo + 16 hb) - dmin*m in float64,
+    rounded once to float32 (both products are exact in float32). lo is the nibble of qs[32 (j/2) +
+    l] (j odd: high), hb bit j of qh[l]."""
+    rng = synth.Rng(43)
+    n_blocks = 64 * 8
+    blk = rng.bytes(n_blocks * 176).reshape(n_blocks, 176)
+    codes_s = np.zeros((n_blocks, 8), np.int64)
+    codes_m = np.zeros((n_blocks, 8), np.int64)
+    for b in range(n_blocks):
+        codes_s[b] = [(b * 8 + j) % 64 for j in range(8)]
+        codes_m[b] = [((b * 8 + j) // 64) % 64 for j in range(8)]
+        blk[b, 4:16] = pack_scale_min(list(codes_s[b]), list(codes_m[b]))
+    d = synth.f16_bits(np.abs(rng.normal(n_blocks)) * 1e-3)
+    dm = synth.f16_bits(np.abs(rng.normal(n_blocks)) * 1e-3)
+    blk[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+    blk[:, 2:4] = dm.view(np.uint8).reshape(-1, 2)
+    got = oracle.dequantize(blk.reshape(8, -1), synth.Q5_K, 8, 64 * 256).reshape(n_blocks, 256)
+    dv, dmv = d.view(np.float16).astype(np.float64), dm.view(np.float16).astype(np.float64)
+    qh, qs = blk[:, 16:48].astype(np.int64), blk[:, 48:].astype(np.int64)
+    codes = set()
+    for sub in range(8):
+        byte = qs[:, 32 * (sub // 2):32 * (sub // 2) + 32]
+        q = ((byte >> 4) if sub % 2 else (byte & 0xF)) + 16 * ((qh >> sub) & 1)
+        codes.update(np.unique(q).tolist())
+        want = (dv[:, None] * codes_s[:, sub:sub + 1]) * q - (dmv[:, None] * codes_m[:, sub:sub + 1])
+        assert np.array_equal(got[:, 32 * sub:32 * sub + 32], want.astype(np.float32)), sub
+    assert codes == set(range(32))
+
+
+def test_dequant_q2_k_closed_form(oracle):
+    """Every (scale, min) nibble pair in every scale slot, every 2-bit code: y = d*s*q - dmin*m in
+    float64 rounded once to float32. Value 128 h + 32 j + l takes bits 2j of qs[32 h + l] and the
+    scale byte 8 h + 2 j + l / 16."""
+    rng = synth.Rng(47)
+    n_blocks = 256
+    blk = rng.bytes(n_blocks * 84).reshape(n_blocks, 84)
+    blk[:, :16] = (np.arange(n_blocks * 16).reshape(n_blocks, 16) % 256).astype(np.uint8)  # every byte value
+    d = synth.f16_bits(np.abs(rng.normal(n_blocks)) * 1e-2)
+    dm = synth.f16_bits(np.abs(rng.normal(n_blocks)) * 1e-2)
+    blk[:, 80:82] = d.view(np.uint8).reshape(-1, 2)
+    blk[:, 82:84] = dm.view(np.uint8).reshape(-1, 2)
+    got = oracle.dequantize(blk.reshape(8, -1), synth.Q2_K, 8, 32 * 256).reshape(n_blocks, 256)
+    dv, dmv = d.view(np.float16).astype(np.float64), dm.view(np.float16).astype(np.float64)
+    sc, qs = blk[:, :16].astype(np.int64), blk[:, 16:80].astype(np.int64)
+    for v in range(256):
+        h, j, l = v // 128, (v % 128) // 32, v % 32
+        q = (qs[:, 32 * h + l] >> (2 * j)) & 3
+        b = sc[:, 8 * h + 2 * j + l // 16]
+        want = dv * (b & 15) * q - dmv * (b >> 4)
+        assert np.array_equal(got[:, v], want.astype(np.float32)), v
+
+
+def pack_q3_k_scales(s):
+    """16 six-bit Q3_K scale codes -> the 12 packed bytes (the inverse of the unpacking the oracle
+    restates, written from the layout: low nibbles of codes 0-7 in bytes 0-7, of codes 8-15 in the
+    high nibbles of bytes 0-7, top two bits of code 4g + i in bits 2g of byte 8 + i)."""
+    out = np.zeros(12, np.uint8)
+    for e, c in enumerate(s):
+        g, i = divmod(e, 4)
+        out[4 * (g & 1) + i] |= (c & 15) << (4 * (g >> 1))
+        out[8 + i] |= (c >> 4) << (2 * g)
+    return out
+
+
+def test_dequant_q3_k_closed_form(oracle):
+    """Every 6-bit scale code in every slot, every 3-bit code: y = d*(sc - 32)*q exactly (at most
+    20 significant bits), with q = (2-bit field) - 4 unless the hmask bit is set."""
+    rng = synth.Rng(49)
+    n_blocks = 64
+    blk = rng.bytes(n_blocks * 110).reshape(n_blocks, 110)
+    codes = (np.arange(n_blocks * 16).reshape(n_blocks, 16) + np.arange(n_blocks)[:, None] * 5) % 64
+    for b in range(n_blocks):
+        blk[b, 96:108] = pack_q3_k_scales(codes[b])
+    d = synth.f16_bits(np.abs(rng.normal(n_blocks)) * 1e-3)
+    blk[:, 108:110] = d.view(np.uint8).reshape(-1, 2)
+    got = oracle.dequantize(blk.reshape(8, -1), synth.Q3_K, 8, 8 * 256).reshape(n_blocks, 256)
+    dv = d.view(np.float16).astype(np.float64)
+    hm, qs = blk[:, :32].astype(np.int64), blk[:, 32:96].astype(np.int64)
+    seen = set()
+    for v in range(256):
+        h, j, l = v // 128, (v % 128) // 32, v % 32
+        q = ((qs[:, 32 * h + l] >> (2 * j)) & 3) - 4 * (1 - ((hm[:, l] >> (4 * h + j)) & 1))
+        seen.update(q.tolist())
+        want = dv * (codes[:, 8 * h + 2 * j + l // 16] - 32) * q
+        assert np.array_equal(got[:, v].astype(np.float64), want), v
+    assert seen == set(range(-4, 4))
+    assert set(codes.ravel().tolist()) == set(range(64))
+
+
 def test_src_row_is_llama_cpp_interleave(oracle):
     """Storage row 2i+j of a head holds HF row j*(hd/2)+i: check the permutation inverts that."""
     import ctypes as C
@@ -236,7 +349,8 @@ def test_src_row_matches_reference(oracle, reference):
 # 256-value chunk (K = 1408, the config-1 FFN width) and a perm_heads matrix
 MATMUL_CASES = [(synth.Q8_0, 40, 512, 5), (synth.Q8_0, 40, 512, 40), (synth.Q4_K, 40, 512, 5),
                 (synth.Q4_K, 40, 512, 40), (synth.Q8_0, 33, 1408, 7), (synth.Q4_K, 130, 2560, 3),
-                (synth.Q6_K, 40, 512, 5), (synth.Q6_K, 130, 2560, 3)]
+                (synth.Q6_K, 40, 512, 5), (synth.Q6_K, 130, 2560, 3), (synth.Q2_K, 40, 512, 5),
+                (synth.Q3_K, 40, 512, 5), (synth.Q5_K, 40, 512, 5), (synth.Q5_K, 130, 2560, 3)]
 
 
 @pytest.mark.parametrize("gtype,N,K,T", MATMUL_CASES)
@@ -375,14 +489,16 @@ def load_golden(name):
     return np.load(path, allow_pickle=False)
 
 
-@pytest.mark.parametrize("name", ["dequant_q8_0.npz", "dequant_q4_k.npz", "dequant_q6_k.npz"])
+@pytest.mark.parametrize("name", ["dequant_q8_0.npz", "dequant_q4_k.npz", "dequant_q6_k.npz", "dequant_q2_k.npz",
+                                  "dequant_q3_k.npz", "dequant_q5_k.npz"])
 def test_golden_dequant(oracle, name):
     g = load_golden(name)
     got = oracle.dequantize(g["blocks"], int(g["gtype"]), int(g["rows"]), int(g["cols"]), int(g["perm_heads"]))
     assert same_bits_nan_aware(got, g["values"])
 
 
-@pytest.mark.parametrize("name", ["matmul_q8_0.npz", "matmul_q4_k.npz", "matmul_q6_k.npz"])
+@pytest.mark.parametrize("name", ["matmul_q8_0.npz", "matmul_q4_k.npz", "matmul_q6_k.npz", "matmul_q2_k.npz",
+                                  "matmul_q3_k.npz", "matmul_q5_k.npz"])
 def test_golden_matmul(oracle, name):
     g = load_golden(name)
     got = oracle.matmul(g["blocks"], int(g["gtype"]), int(g["rows"]), int(g["cols"]), g["x"], g["y0"].copy(),
