@@ -89,13 +89,27 @@ extern "C" int hq_device_init(int device) {
 
 // ------------------------------------------------------------------------------------ residency
 static uint32_t block_values(int t) {
-    return t == HQ_GGML_Q8_0 ? 32u : t == HQ_GGML_Q4_K || t == HQ_GGML_Q6_K ? 256u : 0u;
+    switch (t) {
+    case HQ_GGML_Q8_0: return 32u;
+    case HQ_GGML_Q2_K: case HQ_GGML_Q3_K: case HQ_GGML_Q4_K: case HQ_GGML_Q5_K: case HQ_GGML_Q6_K: return 256u;
+    default: return 0u;
+    }
 }
 static uint32_t block_bytes(int t) {
-    return t == HQ_GGML_Q8_0 ? 34u : t == HQ_GGML_Q4_K ? 144u : t == HQ_GGML_Q6_K ? 210u : 0u;
+    switch (t) {
+    case HQ_GGML_Q8_0: return 34u;
+    case HQ_GGML_Q2_K: return 84u;
+    case HQ_GGML_Q3_K: return 110u;
+    case HQ_GGML_Q4_K: return 144u;
+    case HQ_GGML_Q5_K: return 176u;
+    case HQ_GGML_Q6_K: return 210u;
+    default: return 0u;
+    }
 }
-constexpr size_t Q6K_SLOT = 224;  // device bytes of one Q6_K super-block (210 GGUF bytes + zero padding)
-static const char SUPPORTED[] = "Q8_0 = 8, Q4_K = 12, Q6_K = 14";
+// Device bytes of one super-block where the GGUF block is padded into an aligned slot (the GGUF
+// bytes, then zeros; every 16-byte load of a row aligned); 0 where the bytes are kept as they are.
+static size_t slot_bytes(int t) { return t == HQ_GGML_Q2_K ? 96 : t == HQ_GGML_Q3_K ? 112 : t == HQ_GGML_Q6_K ? 224 : 0; }
+static const char SUPPORTED[] = "Q8_0 = 8, Q2_K = 10, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14";
 
 extern "C" int hq_internal_block_shape(int ggml_type, uint32_t *values, uint32_t *bytes) {
     if (!block_values(ggml_type)) return -1;
@@ -212,11 +226,12 @@ __global__ void k_repack_q8_0(const uint8_t *__restrict__ raw, uint32_t n, uint3
     }
 }
 
-// GGUF Q6_K rows (210-byte super-blocks, 2-byte aligned) -> 224-byte slots (the tail zeroed)
-__global__ void k_repack_q6_k(const uint16_t *__restrict__ raw, size_t nblk, uint16_t *dst) {
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < nblk * 112; i += (size_t)gridDim.x * blockDim.x) {
-        const size_t b = i / 112, h = i % 112;
-        dst[i] = h < 105 ? raw[b * 105 + h] : (uint16_t)0;
+// GGUF k-quant rows (super-blocks of `in` halves, 2-byte aligned) -> slots of `out` halves (the tail
+// zeroed): Q2_K 42 -> 48, Q3_K 55 -> 56, Q6_K 105 -> 112
+__global__ void k_repack_slots(const uint16_t *__restrict__ raw, size_t nblk, uint32_t in, uint32_t out, uint16_t *dst) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < nblk * out; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t b = i / out, h = i % out;
+        dst[i] = h < in ? raw[b * in + h] : (uint16_t)0;
     }
 }
 
@@ -248,7 +263,7 @@ static int upload_rows(int type, uint32_t rows, uint32_t cols, F row_ptr, int de
     const size_t rb = (size_t)(cols / per) * block_bytes(type);
     // the kernels address a matrix through 32-bit buffer ranges: its device bytes stay below 4 GiB
     const size_t K = cols, nb = K / per, ldd = round_up(K / 32, 8), qbytes = round_up((size_t)rows * K, 256);
-    const size_t drb = type == HQ_GGML_Q6_K ? nb * Q6K_SLOT : rb;
+    const size_t drb = slot_bytes(type) ? nb * slot_bytes(type) : rb;
     const size_t dev_bytes = type == HQ_GGML_Q8_0 ? qbytes + (size_t)rows * ldd * 2 : drb * rows;
     if (dev_bytes >= ((size_t)1 << 32))
         return fail("%s: shape [%u, %u] needs %zu device bytes; one matrix is limited to 4 GiB (split its rows)", who, rows,
@@ -295,7 +310,7 @@ static int upload_rows(int type, uint32_t rows, uint32_t cols, F row_ptr, int de
         if (used[b] && (e = hipEventSynchronize(u->ev[b])) != hipSuccess) return fail_free(e);
         gather_rows(row_ptr, rb, r0, n, (uint8_t *)u->pinned[b]);
         const size_t bytes = (size_t)n * rb;
-        if (type == HQ_GGML_Q4_K) {
+        if (!slot_bytes(type) && type != HQ_GGML_Q8_0) {  // Q4_K, Q5_K: the GGUF bytes in place
             e = hipMemcpyAsync(base + (size_t)r0 * rb, u->pinned[b], bytes, hipMemcpyHostToDevice, u->st);
         } else {
             e = hipMemcpyAsync(u->raw[b], u->pinned[b], bytes, hipMemcpyHostToDevice, u->st);
@@ -305,8 +320,9 @@ static int upload_rows(int type, uint32_t rows, uint32_t cols, F row_ptr, int de
                                                                           (uint16_t *)(base + qbytes) + (size_t)r0 * ldd);
                 e = hipGetLastError();
             } else if (e == hipSuccess) {
-                k_repack_q6_k<<<up_grid((size_t)n * nb * 112), 256, 0, u->st>>>((const uint16_t *)u->raw[b], (size_t)n * nb,
-                                                                                (uint16_t *)(base + (size_t)r0 * drb));
+                const uint32_t in = block_bytes(type) / 2, outh = (uint32_t)(slot_bytes(type) / 2);
+                k_repack_slots<<<up_grid((size_t)n * nb * outh), 256, 0, u->st>>>((const uint16_t *)u->raw[b], (size_t)n * nb, in,
+                                                                                  outh, (uint16_t *)(base + (size_t)r0 * drb));
                 e = hipGetLastError();
             }
         }
@@ -373,19 +389,20 @@ extern "C" int hq_mat_download(const hq_mat *m, void *out, size_t nbytes) {
     const size_t rb = (size_t)(m->m.cols / block_values(m->m.type)) * block_bytes(m->m.type), total = rb * m->m.rows;
     if (nbytes < total) return fail("hq_mat_download: need %zu bytes, got %zu", total, nbytes);
     if (use_device(m->device)) return -1;
-    const size_t copy = m->m.type == HQ_GGML_Q4_K ? total : m->bytes;  // (not the Q4_K column tables)
+    const bool in_place = m->m.type != HQ_GGML_Q8_0 && !slot_bytes(m->m.type);
+    const size_t copy = in_place ? total : m->bytes;  // (not the Q4_K column tables)
     std::vector<uint8_t> host(copy);
     HIPCK(hipMemcpy(host.data(), m->alloc, copy, hipMemcpyDeviceToHost));
     uint8_t *dst = (uint8_t *)out;
-    if (m->m.type == HQ_GGML_Q4_K) {
+    if (in_place) {
         memcpy(dst, host.data(), total);
         return 0;
     }
-    if (m->m.type == HQ_GGML_Q6_K) {
-        const size_t nb = m->m.cols / 256;
+    if (slot_bytes(m->m.type)) {
+        const size_t nb = m->m.cols / 256, bb = block_bytes(m->m.type), sb = slot_bytes(m->m.type);
         for (uint32_t r = 0; r < m->m.rows; r++)
             for (size_t b = 0; b < nb; b++)
-                memcpy(dst + (size_t)r * rb + 210 * b, host.data() + (size_t)r * m->m.row_bytes + b * Q6K_SLOT, 210);
+                memcpy(dst + (size_t)r * rb + bb * b, host.data() + (size_t)r * m->m.row_bytes + b * sb, bb);
         return 0;
     }
     const size_t K = m->m.cols, nb = K / 32, ldd = (size_t)m->m.ldd;

@@ -33,6 +33,7 @@
 #include "hq_device.h"
 #include "hq_internal.h"
 #include "hq_kernels.h"
+#include "hq_kquant.h"
 
 namespace {
 
@@ -48,9 +49,14 @@ constexpr int MAX_IDS = 4096;  // readout ids per forward
 
 // ------------------------------------------------------------------------------------ kernels
 // Eight consecutive weights 8g .. 8g + 7 of row r as fp32, bit-identical to the reference decoder
-// (src/ggml_quant.h:95-99 Q8_0, :135-150 Q4_K, :151-169 Q6_K; device layouts as in hq_kernels.hip
-// and hq_q6k.hip).
+// (src/ggml_quant.h:95-99 Q8_0, :100-134 Q2_K / Q3_K, :135-150 Q4_K / Q5_K, :151-169 Q6_K; device
+// layouts as in hq_kernels.hip, hq_kquant.h and hq_q6k.hip).
 DEV void deq8(const hq_dev_mat &W, size_t r, int g, float (&w)[8]) {
+    if (hq_is_kq(W.type)) {
+        const uint8_t *b = W.qs + r * W.row_bytes + (size_t)(8 * g / 256) * kq_slot(W.type);
+        kq_deq8_any(W.type, b, (8 * g) % 256, w);
+        return;
+    }
     if (W.type == HQ_TYPE_Q8_0) {
         const u2v q = *(const u2v *)(W.qs + r * W.cols + 8 * (size_t)g);
         const float d = h2f(W.d[r * (size_t)W.ldd + g / 4]);

@@ -6,16 +6,17 @@
 #include <stddef.h>
 #include <stdint.h>
 
-enum { HQ_TYPE_Q8_0 = 8, HQ_TYPE_Q4_K = 12, HQ_TYPE_Q6_K = 14 };
+enum { HQ_TYPE_Q8_0 = 8, HQ_TYPE_Q2_K = 10, HQ_TYPE_Q3_K = 11, HQ_TYPE_Q4_K = 12, HQ_TYPE_Q5_K = 13, HQ_TYPE_Q6_K = 14 };
 
 // A weight matrix resident in HBM, rows in Hugging Face order (see hq_kernels.hip for layouts).
 typedef struct {
     int type;
     uint32_t rows, cols;
-    const uint8_t *qs;   // Q8_0: biased quant plane [rows][cols]; Q4_K / Q6_K: super-blocks [rows][row_bytes]
+    const uint8_t *qs;   // Q8_0: biased quant plane [rows][cols]; k-quants: super-blocks [rows][row_bytes]
     const uint16_t *d;   // Q8_0: fp16 scale plane [rows][ldd]; Q4_K: unused
     int ldd;             // Q8_0 scale-plane row stride in halves (cols/32 rounded up to 8)
-    size_t row_bytes;    // Q8_0 / Q4_K: GGUF bytes per row; Q6_K: device bytes per row (224 per super-block)
+    size_t row_bytes;    // Q8_0 / Q4_K / Q5_K: GGUF bytes per row; Q2_K / Q3_K / Q6_K: device bytes per row
+                         // (96 / 112 / 224 per super-block)
     const uint8_t *tab;  // Q4_K: per-super-block column tables of the GEMM kernels (hq_launch_q4k_tables)
 } hq_dev_mat;
 
@@ -112,5 +113,14 @@ hipError_t hq_launch_gemv_q6k(const hq_dev_mat *W, const uint16_t *a, void *C, i
 hipError_t hq_launch_gather_q6k(const hq_dev_mat *W, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
                                 hipStream_t st);
 hipError_t hq_launch_gemm_q6k(const GemmArgs &g, int mb, hipStream_t st);
+
+// Q2_K, Q3_K, Q5_K (hq_kquant.hip)
+hipError_t hq_launch_dequant_kq(const hq_dev_mat *W, uint32_t row0, const uint32_t *ids, uint32_t nrows, float *out,
+                                hipStream_t st);
+hipError_t hq_launch_gemv_kq(const hq_dev_mat *W, const uint16_t *a, void *C, int c_f32, int accumulate, hipStream_t st);
+hipError_t hq_launch_gather_kq(const hq_dev_mat *W, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
+                               hipStream_t st);
+hipError_t hq_launch_gemm_kq(int type, const GemmArgs &g, int mb, hipStream_t st);
+constexpr bool hq_is_kq(int type) { return type == HQ_TYPE_Q2_K || type == HQ_TYPE_Q3_K || type == HQ_TYPE_Q5_K; }
 
 #endif

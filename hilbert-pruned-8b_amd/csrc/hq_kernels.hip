@@ -1052,6 +1052,7 @@ static unsigned grid_for(size_t n, unsigned per, unsigned cap) {
 hipError_t hq_launch_dequant(const hq_dev_mat *W, uint32_t row0, const uint32_t *ids, uint32_t nrows, float *out,
                              hipStream_t st) {
     if (W->type == HQ_TYPE_Q6_K) return hq_launch_dequant_q6k(W, row0, ids, nrows, out, st);
+    if (hq_is_kq(W->type)) return hq_launch_dequant_kq(W, row0, ids, nrows, out, st);
     if (W->type == HQ_TYPE_Q8_0) {
         const size_t n = (size_t)nrows * W->cols / 4;
         k_dequant_q8_0<<<grid_for(n, 256, 65536), 256, 0, st>>>(W->qs, W->d, W->cols, W->ldd, row0, ids, nrows, out);
@@ -1112,6 +1113,7 @@ static GemvPlan gemv_plan(const hq_dev_mat *W) {
 
 hipError_t hq_launch_gemv(const hq_dev_mat *W, const uint16_t *a, void *C, int c_f32, int accumulate, hipStream_t st) {
     if (W->type == HQ_TYPE_Q6_K) return hq_launch_gemv_q6k(W, a, C, c_f32, accumulate, st);
+    if (hq_is_kq(W->type)) return hq_launch_gemv_kq(W, a, C, c_f32, accumulate, st);
     const GemvPlan pl = gemv_plan(W);
     const int N = (int)W->rows, K = (int)W->cols;
     const uint32_t rb = (uint32_t)W->row_bytes;
@@ -1151,6 +1153,7 @@ static void launch_gather_t(const hq_dev_mat *W, const uint16_t *H, const uint32
 hipError_t hq_launch_gather(const hq_dev_mat *W, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
                             hipStream_t st) {
     if (W->type == HQ_TYPE_Q6_K) return hq_launch_gather_q6k(W, H, ids, B, k, out, st);
+    if (hq_is_kq(W->type)) return hq_launch_gather_kq(W, H, ids, B, k, out, st);
     switch (lanes_per_row((long)B * k)) {
     case 16: launch_gather_t<16>(W, H, ids, B, k, out, st); break;
     case 32: launch_gather_t<32>(W, H, ids, B, k, out, st); break;
@@ -1242,7 +1245,7 @@ struct GemmCfg {
 GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
     GemmCfg c;
     c.mb = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
-    if (W->type == HQ_TYPE_Q6_K && c.mb > 4) c.mb = 4;  // Q6_K: the narrow kernel with up to 64-row tiles
+    if ((W->type == HQ_TYPE_Q6_K || hq_is_kq(W->type)) && c.mb > 4) c.mb = 4;  // the narrow kernel, up to 64-row tiles
     c.nb = 2;
     if (W->type == HQ_TYPE_Q4_K && c.mb == 1) c.mb = 2;
     c.wide = W->type == HQ_TYPE_Q4_K && M > 64;
@@ -1349,8 +1352,15 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
     W.cols = (uint32_t)K;
     W.ldd = type == HQ_TYPE_Q8_0 ? (K / 32 + 7) / 8 * 8 : 0;
     W.row_bytes = type == HQ_TYPE_Q4_K ? (size_t)K / 256 * 144 : type == HQ_TYPE_Q6_K ? (size_t)K / 256 * 224 : (size_t)K;
+    const char *kq = type == HQ_TYPE_Q2_K ? "10" : type == HQ_TYPE_Q3_K ? "11" : type == HQ_TYPE_Q5_K ? "13" : nullptr;
     if (M == 1 && type == HQ_TYPE_Q6_K) {
         snprintf(buf, n, "k_gemv_q6_k");
+        return;
+    }
+    if (kq) {  // template argument: the ggml type
+        const int mb = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+        if (M == 1) snprintf(buf, n, "k_gemv_kq<%s>", kq);
+        else snprintf(buf, n, "k_gemm_kq<%s, %d, 2>", kq, mb);
         return;
     }
     if (M == 1) {
@@ -1453,6 +1463,7 @@ hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, vo
         return hipGetLastError();
     }
     if (W->type == HQ_TYPE_Q6_K) return hq_launch_gemm_q6k(g, c.mb, st);
+    if (hq_is_kq(W->type)) return hq_launch_gemm_kq(W->type, g, c.mb, st);
 #define CASE(a)                                                                                 \
     if (c.mb == a) {                                                                            \
         if (W->type == HQ_TYPE_Q8_0) k_gemm_q8_0<a, 2><<<g.plan.G, 256, 0, st>>>(g);            \

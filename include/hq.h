@@ -10,8 +10,9 @@
  *     (src/cpu_backend.c:38-54, src/cuda_backend.cu:701-715);
  *   - every fallible call returns 0, or -1 after recording a message for hq_last_error()
  *     (the reference's set_error/last_error convention, src/transformer.h:17-21, src/base.c:11-21).
- * Supported block types: Q8_0 (ggml type 8), Q4_K (12) and Q6_K (14) (src/ggml_quant.h:16-19); K must
- * be a multiple of the block (32 / 256 / 256), as src/gguf.c:331-335 enforces for GGUF tensors.
+ * Supported block types: Q8_0 (ggml type 8) and the k-quants Q2_K (10), Q3_K (11), Q4_K (12), Q5_K (13)
+ * and Q6_K (14) (src/ggml_quant.h:16-19); K must be a multiple of the block (32 for Q8_0, 256 for the
+ * k-quants), as src/gguf.c:331-335 enforces for GGUF tensors.
  * Not thread-safe across concurrent calls that share a matrix's device (as the reference engine,
  * which is single threaded: src/transformer.h:18-19).
  */
@@ -27,7 +28,8 @@ extern "C" {
 #endif
 
 enum { HQ_DT_GGML = 3 };                     /* dtype_t DT_GGML (src/transformer.h:214) */
-enum { HQ_GGML_Q8_0 = 8, HQ_GGML_Q4_K = 12, HQ_GGML_Q6_K = 14 }; /* src/ggml_quant.h:16-19 */
+enum { HQ_GGML_Q8_0 = 8, HQ_GGML_Q2_K = 10, HQ_GGML_Q3_K = 11, HQ_GGML_Q4_K = 12, HQ_GGML_Q5_K = 13,
+       HQ_GGML_Q6_K = 14 }; /* src/ggml_quant.h:16-19 */
 
 /* Host matrix descriptor, field for field the reference wmat_t (src/transformer.h:293-300):
  * data points at GGUF blocks (typically into the model's mmap), rows in storage order;
@@ -56,7 +58,8 @@ int hq_device_name(int device, char *name, size_t name_len, char *arch, size_t a
 /* Weight residency. Replaces upload_mat (src/cuda_backend.cu:677-699) for GGUF-quantized
  * matrices: the blocks are copied to `device` with rows reordered into Hugging Face order
  * (perm_heads, as src/cuda_backend.cu:689-696). Q4_K blocks are kept byte-identical; Q8_0 is
- * repacked losslessly into a quant plane and a scale plane, Q6_K into 224-byte aligned slots
+ * repacked losslessly into a quant plane and a scale plane, Q2_K / Q3_K / Q6_K into 96- / 112- /
+ * 224-byte aligned slots (Q5_K keeps its bytes)
  * (hq_mat_download restores the bytes).
  * There is no bf16 fallback: non-GGML dtypes and other block types are rejected. */
 int hq_mat_upload(const hq_wmat_t *w, int device, hq_mat **out);
