@@ -3,12 +3,14 @@
 Headline workload (the BASELINE north-star target): Q4_K GEMM, M = 512, K = 2560, N = 9728
 (config 3, up/gate shape), fp16 activations, fp32 accumulation, fp16 output. A "step" is one GEMM
 launch over one batch; weights rotate over enough distinct device copies (> 512 MB) that every
-launch streams its weights from HBM, not from the 256 MB Infinity Cache. The timed steps are one
-HIP-graph replay of exactly `steps` launches, timed with HIP events on the launch stream, after
-`warmup` eager launches and one untimed replay of the same graph (`ms_per_step`, `value`). The
-median over >= 50 launches is reported beside it (`us_median` of the headline and the roofline's
-`kernel_us`): five replays of 20-launch graphs that continue the rotation, a HIP event between
-replays, median of the five per-launch times.
+launch streams its weights from HBM, not from the 256 MB Infinity Cache. The timed steps are HIP-graph
+replays of exactly `steps` launches, timed with HIP events on the launch stream, after `warmup`
+eager launches, 0.3 s of untimed launches and one untimed replay: five such replays, each graph
+continuing the weight rotation, a HIP event between replays; `ms_per_step` and `value` come from the
+median of the five per-launch times (`us_first_replay` is the first replay alone). `us_median` and
+the roofline's `kernel_us` are the same median over five replays of 20-launch graphs. The headline
+is also timed with fp32 C (`headline_fp32_c`), the output mode the parity bar covers and the
+reference's output type.
 
 Also reported (key "sweep"): the config 2 / 3 M sweeps and the config 5 option readout, each as
 achieved TFLOP/s and GB/s of algorithmic bytes (W blocks once + A + C) and their roofline fractions,
@@ -101,6 +103,7 @@ def bench_gemm(hq, synth, gtype, N, K, M, c_f32, steps, warmup, stream, eager_wa
     t0 = time.perf_counter()
     ms = hq.time_gemm(mats, A, M, C, c_f32, steps, reps, stream)
     wall = time.perf_counter() - t0
+    ms_first = hq.time_gemm(mats, A, M, C, c_f32, steps, 1, stream) if reps > 1 and kernel_time else None
     ms_med = hq.time_gemm(mats, A, M, C, c_f32, MEDIAN_ITERS, MEDIAN_REPS, stream) if kernel_time else None
     ms_kernel = (hq.time_gemm_kernel(mats, A, M, C, c_f32, MEDIAN_ITERS, MEDIAN_REPS, stream)
                  if (kernel_time and M > 1) else None)
@@ -109,10 +112,12 @@ def bench_gemm(hq, synth, gtype, N, K, M, c_f32, steps, warmup, stream, eager_wa
     A.free(), C.free()
     flop = 2.0 * M * N * K
     nbytes = gemm_bytes(gtype, M, N, K, 4 if c_f32 else 2)
-    r = dict(type="q8_0" if gtype == synth.Q8_0 else "q4_k", M=M, N=N, K=K, us=ms * 1e3,
+    r = dict(type=synth.TYPE_NAMES[gtype].lower(), M=M, N=N, K=K, us=ms * 1e3,
              tflops=flop / (ms * 1e-3) / 1e12, gbs=nbytes / (ms * 1e-3) / 1e9, copies=copies, wall_s=wall)
     if ms_med is not None:
         r["us_median"] = ms_med * 1e3
+    if ms_first is not None:
+        r["us_first_replay"] = ms_first * 1e3
     if ms_kernel is not None:
         r["kernel_us"] = ms_kernel * 1e3
         r["kernel_tflops"] = flop / (ms_kernel * 1e-3) / 1e12
@@ -180,7 +185,7 @@ def bench_swiglu(hq, synth, gtype, stream, M=512, I=9728, K=2560):
         m.free()
     A.free(), out.free(), C.free()
     flop = 2.0 * 2 * M * I * K
-    return dict(type=("q4_k" if gtype == synth.Q4_K else "q8_0") + "_gate_up_swiglu", M=M, I=I, K=K,
+    return dict(type=synth.TYPE_NAMES[gtype].lower() + "_gate_up_swiglu", M=M, I=I, K=K,
                 us=round(ms * 1e3, 2), tflops=round(flop / (ms * 1e-3) / 1e12, 1),
                 unfused_two_gemms_us=round(ms2 * 1e3, 2), copies=copies)
 
@@ -299,7 +304,7 @@ def main():
     ap.add_argument("--gemv-only", action="store_true",
                     help="only time the three M = 1 GEMV shapes of the sweep (for profiling) and exit")
     ap.add_argument("--shape", default="", metavar="TYPE:M:N:K",
-                    help="only time this one GEMM shape (TYPE q8_0 or q4_k; for profiling) and exit")
+                    help="only time this one GEMM shape (TYPE q8_0, q2_k .. q6_k; for profiling) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); the quantized matmul "
@@ -323,7 +328,7 @@ def main():
     stream = hq.Stream()
     if args.shape:
         t, m, n, k = args.shape.split(":")
-        g = {"q8_0": synth.Q8_0, "q4_k": synth.Q4_K}[t]
+        g = {v.lower(): k for k, v in synth.TYPE_NAMES.items()}[t]
         r = bench_gemm(hq, synth, g, int(n), int(k), int(m), False, args.steps, args.warmup, stream, settle_s=0.2)
         log("shape", main_kernel_name(hq, g, int(m), int(n), int(k)), r)
         return
@@ -347,15 +352,19 @@ def main():
 
     gtype, N, K, M = synth.Q4_K, 9728, 2560, 512
     head = bench_gemm(hq, synth, gtype, N, K, M, False, args.steps, args.warmup, stream, kernel_time=True,
-                      settle_s=0.3)
+                      settle_s=0.3, reps=MEDIAN_REPS)
     log("headline", head)
     value = head["tflops"]
+    head32 = bench_gemm(hq, synth, gtype, N, K, M, True, args.steps, args.warmup, stream, kernel_time=True,
+                        settle_s=0.3, reps=MEDIAN_REPS)
+    log("headline fp32 C", head32)
 
     sweep = []
     if not args.no_sweep:
         shapes = [(synth.Q8_0, 9728, 2560, m) for m in (1, 16, 128, 512, 2048)] + \
                  [(synth.Q4_K, 9728, 2560, m) for m in (1, 64, 512, 4096)] + \
-                 [(synth.Q4_K, 2560, 9728, m) for m in (1, 64, 512, 4096)]
+                 [(synth.Q4_K, 2560, 9728, m) for m in (1, 64, 512, 4096)] + \
+                 [(g, 9728, 2560, m) for g in (synth.Q2_K, synth.Q3_K, synth.Q5_K, synth.Q6_K) for m in (1, 64, 512)]
         # each shape: 0.1 s of untimed calls (clocks at their loaded level), then the median of
         # MEDIAN_REPS graph replays of 20 calls (a single replay ran up to a third slow at M = 2048)
         for g, n, k, m in shapes:
@@ -392,12 +401,17 @@ def main():
     line = {
         "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(head["us"] / 1e3, 6),
-        "us_median": round(head["us_median"], 3), "higher_is_better": True,
+        "us_median": round(head["us_median"], 3), "us_first_replay": round(head["us_first_replay"], 3),
+        "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
         "config": {"workload": "q4_k_gemm_m512_k2560_n9728", "gtype": "Q4_K", "M": M, "N": N, "K": K,
                    "A": "fp16 N(0,1)", "C": "fp16 (fp32 accumulate)", "weight_copies": head["copies"],
                    "device": f"{name} ({arch})"},
         "roofline": roofline,
+        "headline_fp32_c": {"C": "fp32", "us": round(head32["us"], 3), "tflops": round(head32["tflops"], 3),
+                            "frac": round(head32["tflops"] / PEAK_TFLOPS, 4), "kernel_us": round(head32["kernel_us"], 3),
+                            "kernel_tflops": round(head32["kernel_tflops"], 3),
+                            "timing": f"median of {MEDIAN_REPS} HIP-graph replays of {args.steps} launches"},
         "cpu_baseline": cpu,
         "sweep": sweep,
     }
