@@ -185,9 +185,45 @@ def bench_swiglu(hq, synth, gtype, stream, M=512, I=9728, K=2560):
         m.free()
     A.free(), out.free(), C.free()
     flop = 2.0 * 2 * M * I * K
-    return dict(type=synth.TYPE_NAMES[gtype].lower() + "_gate_up_swiglu", M=M, I=I, K=K,
-                us=round(ms * 1e3, 2), tflops=round(flop / (ms * 1e-3) / 1e12, 1),
-                unfused_two_gemms_us=round(ms2 * 1e3, 2), copies=copies)
+    r = dict(type=synth.TYPE_NAMES[gtype].lower() + "_gate_up_swiglu", M=M, I=I, K=K,
+             us=round(ms * 1e3, 2), tflops=round(flop / (ms * 1e-3) / 1e12, 1),
+             unfused_two_gemms_us=round(ms2 * 1e3, 2), copies=copies)
+    if M == 1:  # HBM-bound: bytes of both matrices once, the activation row and the fp16 output
+        nbytes = 2 * I * rb + K * 2 + I * 2
+        r["gbs"], r["frac"], r["bound"] = round(nbytes / (ms * 1e-3) / 1e9, 1), round(nbytes / (ms * 1e-3) / 1e9 / PEAK_GBS, 4), "hbm"
+    return r
+
+
+def bench_prefill(hq, synth, T=2048, reps=5):
+    """Config 1 (the tiny Llama, Q8_0) through the backend_t vtable (hip_backend_create), as the
+    reference's selftest times it (src/cuda_backend.cu:1447-1457): a T-token prefill with two readout
+    ids, median of `reps` timed passes after one warm-up (each pass resets the position; forward is
+    synchronous), and one-token decode steps after a 128-token prompt. Every projection runs through
+    hq_gemm / hq_gemm_swiglu; host wall-clock per forward call."""
+    view = hq.RefModelView(synth.tiny_llama(1))
+    be = hq.HipBackend(view, T)
+    tokens, ids = synth.tiny_llama_prompt(2, T=T)
+    ids2 = ids[:2]
+    be.forward(tokens, ids2)
+    times = []
+    for _ in range(reps):
+        be.reset()
+        t0 = time.perf_counter()
+        be.forward(tokens, ids2)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    be.reset()
+    be.forward(tokens[:128])
+    steps = []
+    for i in range(32):
+        t0 = time.perf_counter()
+        be.forward(tokens[128 + i:129 + i], ids2)
+        steps.append(time.perf_counter() - t0)
+    be.destroy()
+    ts = statistics.median(steps)
+    return dict(type="config1_tiny_llama_vtable", T=T, prefill_ms=round(t * 1e3, 3), prefill_tokens_s=round(T / t, 1),
+                decode_step_ms=round(ts * 1e3, 4), decode_tokens_s=round(1.0 / ts, 1),
+                timing=f"prefill: median of {reps} after a warm-up; decode: median of 32 steps after 128 tokens")
 
 
 def bench_upload(hq, synth, reps=3):
@@ -299,6 +335,8 @@ def main():
                     help="only time config 4 (both readings of its shape list) and exit")
     ap.add_argument("--swiglu-only", action="store_true",
                     help="only time the fused gate/up+SwiGLU pair GEMM against two GEMMs and exit")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only time config 1's prefill and decode steps through the backend vtable and exit")
     ap.add_argument("--upload-only", action="store_true",
                     help="only time the upload of the 413 MB config-5 head and exit")
     ap.add_argument("--gemv-only", action="store_true",
@@ -343,6 +381,9 @@ def main():
     if args.upload_only:
         log("upload", bench_upload(hq, synth))
         return
+    if args.prefill_only:
+        log("prefill", bench_prefill(hq, synth))
+        return
     if args.gemv_only:
         for g, n, k in [(synth.Q8_0, 9728, 2560), (synth.Q4_K, 9728, 2560), (synth.Q4_K, 2560, 9728)]:
             r = bench_gemm(hq, synth, g, n, k, 1, False, args.steps, args.warmup, stream, settle_s=0.2)
@@ -384,9 +425,13 @@ def main():
             log("sweep", r)
             sweep.append(r)
         for g in (synth.Q4_K, synth.Q8_0):
-            r = bench_swiglu(hq, synth, g, stream)
-            log("sweep", r)
-            sweep.append(r)
+            for m in (512, 1):
+                r = bench_swiglu(hq, synth, g, stream, M=m)
+                log("sweep", r)
+                sweep.append(r)
+        r = bench_prefill(hq, synth)
+        log("sweep", r)
+        sweep.append(r)
         r = bench_upload(hq, synth)
         log("sweep", r)
         sweep.append(r)

@@ -12,8 +12,12 @@
 //                      (k_attention)
 //   x += hq_gemm(o, ob)                               (accumulate into the residual)
 //   hb = RMSNorm(x) fp16
-//   T = 1: fb = silu(gate . hb) * (up . hb) fp16 in one pass over both matrices (k_gateup_swiglu)
-//   else:  g, u = hq_gemm(gate|up, hb); fb = silu(g) * u fp16 (k_swiglu)
+//   fb = silu(gate . hb) * (up . hb) fp16: where gate and up share a block type and shape they are
+//        resident as one gate/up pair matrix (hq_mat_upload_pair) and fb comes from hq_gemm_swiglu
+//        (any T: the SwiGLU epilogue inside the GEMM's tiles for prefill shapes, the tuned GEMV over
+//        both halves at T = 1); otherwise (a Q4_K gate with a Q6_K up, as Q4_K_M files pair them)
+//        T = 1 runs k_gateup_swiglu (one pass over both matrices) and larger T two hq_gemm calls and
+//        k_swiglu
 //   x += hq_gemm(down, fb)
 // then, with readout ids, one kernel normalises the last position (final RMSNorm, fp32) and dots it
 // with each id's lm_head row decoded from its blocks (k_norm_readout; src/cuda_backend.cu:561-592).
@@ -293,6 +297,7 @@ unsigned blocks_for(size_t n, unsigned per) { return (unsigned)((n + per - 1) / 
 // ------------------------------------------------------------------------------------ backend
 struct DevLayer {
     hq_mat *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr, *gate = nullptr, *up = nullptr, *down = nullptr;
+    hq_mat *pair = nullptr;  // gate and up as one pair matrix (then gate and up are null)
     float *in_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
     float *kc = nullptr, *vc = nullptr;  // [max_seq, kvw] fp32
 };
@@ -343,7 +348,7 @@ void release(HipBackend *b) {
     (void)hipSetDevice(b->device);
     if (b->st) (void)hipStreamSynchronize(b->st);
     for (DevLayer &l : b->L)
-        for (hq_mat *m : {l.q, l.k, l.v, l.o, l.gate, l.up, l.down}) hq_mat_free(m);
+        for (hq_mat *m : {l.q, l.k, l.v, l.o, l.gate, l.up, l.down, l.pair}) hq_mat_free(m);
     if (b->lm_head != b->embed) hq_mat_free(b->lm_head);
     hq_mat_free(b->embed);
     for (void *p : b->allocs) (void)hipFree(p);
@@ -406,7 +411,9 @@ int run_layers(HipBackend *b, int T, int pos0) {
         if (gemm(b, L.o, b->ob, T, b->x, true)) return -1;
         k_rmsnorm<_Float16><<<T, 256, 0, st>>>(b->x, L.post_norm, off, eps, b->hb, H);
         BCK(hipGetLastError());
-        if (T == 1) {
+        if (L.pair) {
+            if (hq_gemm_swiglu(L.pair, (const uint16_t *)b->hb, T, (uint16_t *)b->fb, st)) return -1;
+        } else if (T == 1) {
             k_gateup_swiglu<<<(I + 3) / 4, 256, 0, st>>>(*hq_mat_dev(L.gate), *hq_mat_dev(L.up), b->hb, b->fb, I, H);
             BCK(hipGetLastError());
         } else {
@@ -509,9 +516,20 @@ int init(HipBackend *b, const hq_ref_model_t *m, size_t max_seq) {
         snprintf(what, sizeof what, "layer %u", l);
         if (upload_vec(b, &d.in_norm, s.in_norm, H) || upload_vec(b, &d.post_norm, s.post_norm, H) ||
             upload_mat(b, &d.q, &s.q, what) || upload_mat(b, &d.k, &s.k, what) || upload_mat(b, &d.v, &s.v, what) ||
-            upload_mat(b, &d.o, &s.o, what) || upload_mat(b, &d.gate, &s.gate, what) ||
-            upload_mat(b, &d.up, &s.up, what) || upload_mat(b, &d.down, &s.down, what))
+            upload_mat(b, &d.o, &s.o, what) || upload_mat(b, &d.down, &s.down, what))
             return -1;
+        // gate and up of one block type and shape (rows a multiple of 8): one pair matrix
+        const bool pair = s.gate.dtype == HQ_DT_GGML && s.up.dtype == HQ_DT_GGML && s.gate.ggml_type == s.up.ggml_type &&
+                          s.gate.rows == s.up.rows && s.gate.cols == s.up.cols && s.gate.rows % 8 == 0;
+        if (pair) {
+            if (hq_mat_upload_pair(&s.gate, &s.up, b->device, &d.pair)) {
+                char msg[512];
+                snprintf(msg, sizeof msg, "%s", hq_last_error());
+                return hq_internal_fail("hip backend: %s gate/up: %s", what, msg);
+            }
+        } else if (upload_mat(b, &d.gate, &s.gate, what) || upload_mat(b, &d.up, &s.up, what)) {
+            return -1;
+        }
         if (c.qk_norm && (upload_vec(b, &d.q_norm, s.q_norm, hd) || upload_vec(b, &d.k_norm, s.k_norm, hd))) return -1;
         if (dalloc(b, (void **)&d.kc, max_seq * kvw * sizeof(float)) || dalloc(b, (void **)&d.vc, max_seq * kvw * sizeof(float)))
             return -1;
@@ -538,8 +556,9 @@ int init(HipBackend *b, const hq_ref_model_t *m, size_t max_seq) {
         } want[] = {{d.q, (uint32_t)qw, (uint32_t)H, "q"},        {d.k, (uint32_t)kvw, (uint32_t)H, "k"},
                     {d.v, (uint32_t)kvw, (uint32_t)H, "v"},        {d.o, (uint32_t)H, (uint32_t)ow, "o"},
                     {d.gate, (uint32_t)I, (uint32_t)H, "gate"},   {d.up, (uint32_t)I, (uint32_t)H, "up"},
-                    {d.down, (uint32_t)H, (uint32_t)I, "down"}};
+                    {d.pair, 2 * (uint32_t)I, (uint32_t)H, "gate/up"}, {d.down, (uint32_t)H, (uint32_t)I, "down"}};
         for (auto &w : want) {
+            if (!w.w) continue;  // (gate and up, or their pair)
             if (hq_mat_shape(w.w, &r, &k, nullptr)) return -1;
             if (r != w.rows || k != w.cols)
                 return hq_internal_fail("hip backend: layer %u %s is [%u, %u], the config needs [%u, %u]", l, w.name, r, k,
@@ -615,6 +634,66 @@ int selftest_gemm(const hq_mat *W, const char *name, int verbose, int *failed, h
         if (!ok) (*failed)++;
         if (verbose || !ok)
             printf("  gemm %-8s M=%-4d N=%-6u K=%-6u rel-L2 %.2e max-abs %.2e  %s\n", name, M, N, K, rel, worst, ok ? "ok" : "FAIL");
+    }
+    return 0;
+}
+
+// hq_gemm_swiglu on a gate/up pair matrix at several M against silu(g) * u in float64 from the
+// decoded gate and up rows (hq_dequant_f32) on up to 64 sampled output columns; the output is fp16,
+// so half an ulp of |y| is allowed on top of the 1e-2 bar.
+int selftest_swiglu(const hq_mat *P, int verbose, int *failed, hipStream_t st) {
+    uint32_t N2, K;
+    if (hq_mat_shape(P, &N2, &K, nullptr)) return -1;
+    const uint32_t I = N2 / 2;
+    const int Ms[] = {1, 5, 64, 200};
+    uint64_t seed = 17 + I + K;
+    const int ncol = I < 64 ? (int)I : 64;
+    std::vector<uint32_t> cols(ncol);
+    for (int j = 0; j < ncol; j++) cols[j] = (uint32_t)((uint64_t)j * I / ncol);
+    std::vector<float> wg((size_t)ncol * K), wu((size_t)ncol * K);
+    float *dw;
+    BCK(hipMalloc(&dw, (size_t)K * 4));
+    for (int j = 0; j < ncol; j++) {
+        const uint32_t i = cols[j], rg = 16 * (i / 8) + i % 8;  // pair rows of gate i and up i
+        if (hq_dequant_f32(P, rg, 1, dw, st)) return -1;
+        BCK(hipMemcpyAsync(wg.data() + (size_t)j * K, dw, (size_t)K * 4, hipMemcpyDeviceToHost, st));
+        if (hq_dequant_f32(P, rg + 8, 1, dw, st)) return -1;
+        BCK(hipMemcpyAsync(wu.data() + (size_t)j * K, dw, (size_t)K * 4, hipMemcpyDeviceToHost, st));
+        BCK(hipStreamSynchronize(st));
+    }
+    BCK(hipFree(dw));
+    for (int M : Ms) {
+        std::vector<uint16_t> A((size_t)M * K), O((size_t)M * I);
+        for (auto &a : A) a = to_f16((float)((double)lcg(&seed) / (double)(1ull << 31) * 2.0 - 1.0));
+        void *dA, *dO;
+        BCK(hipMalloc(&dA, A.size() * 2));
+        BCK(hipMalloc(&dO, O.size() * 2));
+        BCK(hipMemcpy(dA, A.data(), A.size() * 2, hipMemcpyHostToDevice));
+        if (hq_gemm_swiglu(P, (const uint16_t *)dA, M, (uint16_t *)dO, st)) return -1;
+        BCK(hipMemcpyAsync(O.data(), dO, O.size() * 2, hipMemcpyDeviceToHost, st));
+        BCK(hipStreamSynchronize(st));
+        BCK(hipFree(dA));
+        BCK(hipFree(dO));
+        double worst = 0, num = 0, den = 0;
+        bool ok = true;
+        for (int m = 0; m < M; m++)
+            for (int j = 0; j < ncol; j++) {
+                double g = 0, u = 0;
+                for (uint32_t k = 0; k < K; k++) {
+                    const double a = from_f16(A[(size_t)m * K + k]);
+                    g += a * wg[(size_t)j * K + k], u += a * wu[(size_t)j * K + k];
+                }
+                const double want = g / (1.0 + exp(-g)) * u, got = from_f16(O[(size_t)m * I + cols[j]]);
+                const double err = fabs(want - got);
+                ok = ok && err <= 1e-2 + fabs(want) * 0x1p-11;
+                worst = err > worst ? err : worst;
+                num += err * err, den += want * want;
+            }
+        const double rel = den > 0 ? sqrt(num / den) : sqrt(num);
+        ok = ok && rel <= 1e-3;
+        if (!ok) (*failed)++;
+        if (verbose || !ok)
+            printf("  gate/up+SwiGLU M=%-4d I=%-6u K=%-6u rel-L2 %.2e max-abs %.2e  %s\n", M, I, K, rel, worst, ok ? "ok" : "FAIL");
     }
     return 0;
 }
@@ -724,19 +803,26 @@ extern "C" int hip_selftest(const hq_ref_model_t *m, int device, size_t n_tokens
     int failed = 0, rc = 0;
     printf("hq_gemm on the model's matrices vs a float64 host product of the decoded weights:\n");
     const DevLayer &L0 = b->L[0];
-    rc = selftest_gemm(L0.q, "q", verbose, &failed, b->st) || selftest_gemm(L0.gate, "gate", verbose, &failed, b->st) ||
-         selftest_gemm(L0.down, "down", verbose, &failed, b->st);
-    printf("fused single-token kernel vs the unfused kernels:\n");
-    rc = rc || selftest_fused(b, verbose, &failed);
+    rc = selftest_gemm(L0.q, "q", verbose, &failed, b->st) || selftest_gemm(L0.down, "down", verbose, &failed, b->st) ||
+         (!L0.pair && selftest_gemm(L0.gate, "gate", verbose, &failed, b->st));
+    if (L0.pair) {
+        printf("hq_gemm_swiglu on the gate/up pair vs silu(g) * u from the decoded weights in float64:\n");
+        rc = rc || selftest_swiglu(L0.pair, verbose, &failed, b->st);
+    } else {
+        printf("fused single-token kernel vs the unfused kernels:\n");
+        rc = rc || selftest_fused(b, verbose, &failed);
+    }
     uint64_t seed = 7;
     std::vector<uint32_t> tok(n_tokens), ids(16);
     for (auto &t : tok) t = (uint32_t)(lcg(&seed) % c.vocab);
     for (auto &i : ids) i = (uint32_t)(lcg(&seed) % c.vocab);
     float full[16], split[16], step[16], ref[16];
+    std::vector<float> hg(c.hidden), hc(c.hidden);
     const size_t half = n_tokens / 2;
     double t0 = now_s();
     rc = rc || gpu->reset(gpu) || gpu->forward(gpu, tok.data(), n_tokens, ids.data(), 16, full);
     const double gpu_s = now_s() - t0;
+    rc = rc || gpu->last_hidden(gpu, hg.data());  // after the full prefill
     rc = rc || gpu->reset(gpu) || gpu->forward(gpu, tok.data(), half, nullptr, 0, nullptr) || gpu->snapshot(gpu) ||
          gpu->forward(gpu, tok.data() + half, n_tokens - half, ids.data(), 16, split) || gpu->restore(gpu) ||
          gpu->forward(gpu, tok.data() + half, n_tokens - half, ids.data(), 16, split);
@@ -748,16 +834,35 @@ extern "C" int hip_selftest(const hq_ref_model_t *m, int device, size_t n_tokens
         compare("prefill + 1-token step vs full prefill", full, step, 16, 1e-3, &failed);
         if (cpu_backend_create) {
             hq_ref_backend_t *cpu = cpu_backend_create(m, n_tokens);
-            if (!cpu || cpu->reset(cpu) || cpu->forward(cpu, tok.data(), n_tokens, ids.data(), 16, ref)) {
+            if (!cpu || cpu->reset(cpu) || cpu->forward(cpu, tok.data(), n_tokens, ids.data(), 16, ref) ||
+                cpu->last_hidden(cpu, hc.data())) {
                 if (cpu) cpu->destroy(cpu);
                 rc = hq_internal_fail("hip_selftest: the CPU reference forward failed");
             } else {
                 cpu->destroy(cpu);
                 compare("hip vs cpu (full prefill)", ref, full, 16, 1e-2, &failed);
+                // the reference's direction check of the final hidden state (src/cuda_backend.cu:1440-1446)
+                double dot = 0, nc = 0, ng = 0;
+                for (uint32_t k = 0; k < c.hidden; k++)
+                    dot += (double)hc[k] * hg[k], nc += (double)hc[k] * hc[k], ng += (double)hg[k] * hg[k];
+                const double cosine = nc > 0 && ng > 0 ? dot / sqrt(nc * ng) : 0;
+                const bool ok = cosine >= 0.999;
+                if (!ok) failed++;
+                printf("  %-40s cosine %.6f  %s\n", "hip vs cpu final hidden state", cosine, ok ? "ok" : "FAIL");
             }
         } else {
             printf("  (no cpu_backend_create in this program: the CPU comparison is left to the caller)\n");
         }
+        // prefill throughput at a realistic prompt length (src/cuda_backend.cu:1447-1457): one warm-up
+        // pass, then the timed one
+        const size_t bench = ctx < 2048 ? ctx : 2048;
+        std::vector<uint32_t> bt(bench);
+        for (size_t t = 0; t < bench; t++) bt[t] = tok[t % n_tokens];
+        rc = gpu->reset(gpu) || gpu->forward(gpu, bt.data(), bench, ids.data(), 2, full);
+        t0 = now_s();
+        rc = rc || gpu->reset(gpu) || gpu->forward(gpu, bt.data(), bench, ids.data(), 2, full);
+        const double dt = now_s() - t0;
+        if (!rc) printf("  hip prefill %zu tokens: %.2f ms (%.0f tokens/s)\n", bench, dt * 1e3, (double)bench / dt);
     }
     gpu->destroy(gpu);
     if (rc) return -1;

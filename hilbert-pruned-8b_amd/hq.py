@@ -522,7 +522,8 @@ class RefModelView:
     """A reference model_t (layout mirror RefModel) over a synth.tiny_llama()-style dict of Q8_0 /
     Q4_K block arrays, as the reference's model_load would fill it for a GGUF Llama model: q/k in
     llama.cpp storage order with perm_heads, every layer LAYER_FULL, RMSNorm offset 0. Keeps the
-    arrays alive while the view exists."""
+    arrays alive while the view exists. model["types"] may give other ggml types for the layer
+    matrices by name (e.g. {"gate": Q4_K, "up": Q6_K}, as Q4_K_M files mix them)."""
 
     def __init__(self, model, gtype=Q8_0):
         c = model["cfg"]
@@ -530,10 +531,12 @@ class RefModelView:
         H, I, V = c["hidden"], c["intermediate"], c["vocab"]
         qw, kvw = c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
 
-        def wm(blocks, rows, cols, perm=0):
+        types = model.get("types", {})
+
+        def wm(blocks, rows, cols, perm=0, name=None):
             blocks = np.ascontiguousarray(blocks, np.uint8)
             self.keep.append(blocks)
-            return WMat(DT_GGML, rows, cols, blocks.ctypes.data, gtype, perm)
+            return WMat(DT_GGML, rows, cols, blocks.ctypes.data, types.get(name, gtype), perm)
 
         def vec(v):
             v = np.ascontiguousarray(v, np.float32)
@@ -555,7 +558,8 @@ class RefModelView:
             d.q = wm(L["q"], qw, H, c["n_heads"])
             d.k = wm(L["k"], kvw, H, c["n_kv_heads"])
             d.v, d.o = wm(L["v"], kvw, H), wm(L["o"], H, qw)
-            d.gate, d.up, d.down = wm(L["gate"], I, H), wm(L["up"], I, H), wm(L["down"], H, I)
+            d.gate, d.up = wm(L["gate"], I, H, name="gate"), wm(L["up"], I, H, name="up")
+            d.down = wm(L["down"], H, I, name="down")
         self.m = RefModel()
         self.m.cfg = cfg
         self.m.embed, self.m.lm_head = wm(model["embed"], V, H), wm(model["lm_head"], V, H)

@@ -95,12 +95,14 @@ struct hq_ref_backend {
 hq_ref_backend_t *hip_backend_create(const hq_ref_model_t *m, size_t max_seq, int device, bool keep_quantized);
 
 /* cuda_selftest (src/cuda_backend.cu:1392-1466), for this backend: every GEMM path of hq_gemm on
- * the model's own matrices against a float64 host product of the decoded weights; the fused
- * single-token gate/up+SwiGLU kernel against the unfused kernels; then a forward pass of n_tokens
- * (>= 2) seeded tokens three ways (full prefill; prefix + snapshot + suffix + restore + suffix;
- * prefill of n - 1 tokens + one step) whose logits must agree, and against the reference CPU
- * backend when the program provides cpu_backend_create. Prints a report; returns 0 when every check
- * passes, else -1. */
+ * the model's own matrices against a float64 host product of the decoded weights; the gate/up +
+ * SwiGLU path (hq_gemm_swiglu on the pair matrix at M = 1 .. 200 against float64, or the fused
+ * single-token kernel against the unfused kernels where gate and up differ in type); then a forward
+ * pass of n_tokens (>= 2) seeded tokens three ways (full prefill; prefix + snapshot + suffix +
+ * restore + suffix; prefill of n - 1 tokens + one step) whose logits must agree, and against the
+ * reference CPU backend when the program provides cpu_backend_create (logits, and the final hidden
+ * state by cosine >= 0.999 as the reference checks it); last, a timed prefill of 2048 tokens
+ * (tokens/s printed). Prints a report; returns 0 when every check passes, else -1. */
 int hip_selftest(const hq_ref_model_t *m, int device, size_t n_tokens, int verbose);
 
 #ifdef __cplusplus

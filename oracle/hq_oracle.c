@@ -303,9 +303,11 @@ static void attention(const or_llama_t *m, const or_layer_t *L, const float *h, 
 }
 
 /* src/cpu_backend.c:218-263 for a Llama model at position 0; RoPE frequencies the caller's table
- * (model_t.rope_inv_freq, src/model.c:449-477) or, without one, src/model.c:453 (theta powers). */
-int or_llama_forward(const or_llama_t *m, const uint32_t *tokens, size_t T, const uint32_t *ids, uint32_t n_ids,
-                     float *logits) {
+ * (model_t.rope_inv_freq, src/model.c:449-477) or, without one, src/model.c:453 (theta powers).
+ * hidden (optional, H floats): the final-normalised last position, the CPU backend's last_hidden
+ * (src/cpu_backend.c:253-254, :294-298). */
+int or_llama_forward_h(const or_llama_t *m, const uint32_t *tokens, size_t T, const uint32_t *ids, uint32_t n_ids,
+                       float *logits, float *hidden) {
     if (T == 0) return -1;
     for (size_t t = 0; t < T; t++)
         if (tokens[t] >= m->vocab) return -1;
@@ -331,6 +333,7 @@ int or_llama_forward(const or_llama_t *m, const uint32_t *tokens, size_t T, cons
         or_matmul(&L->down, g, T, x, 1);
     }
     rms_norm(x + (T - 1) * H, m->final_norm, h, H, m->eps);
+    if (hidden) memcpy(hidden, h, H * sizeof *hidden);
     float *row = (float *)malloc(H * sizeof *row);
     for (uint32_t i = 0; i < n_ids; i++) {
         or_wmat_row_f32(&m->lm_head, ids[i], row);
@@ -338,4 +341,9 @@ int or_llama_forward(const or_llama_t *m, const uint32_t *tokens, size_t T, cons
     }
     free(row), free(x), free(h), free(mix), free(g), free(u), free(inv_freq);
     return 0;
+}
+
+int or_llama_forward(const or_llama_t *m, const uint32_t *tokens, size_t T, const uint32_t *ids, uint32_t n_ids,
+                     float *logits) {
+    return or_llama_forward_h(m, tokens, T, ids, n_ids, logits, NULL);
 }

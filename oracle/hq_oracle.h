@@ -87,6 +87,10 @@ typedef struct {
  * Returns 0, or -1 on an empty prompt or an out-of-range token / id. */
 int or_llama_forward(const or_llama_t *m, const uint32_t *tokens, size_t T, const uint32_t *ids, uint32_t n_ids,
                      float *logits);
+/* The same, also writing the final-normalised last position (the CPU backend's last_hidden) to
+ * hidden [hidden floats] when it is not NULL. */
+int or_llama_forward_h(const or_llama_t *m, const uint32_t *tokens, size_t T, const uint32_t *ids, uint32_t n_ids,
+                       float *logits, float *hidden);
 
 #ifdef __cplusplus
 }

@@ -66,6 +66,8 @@ class Oracle:
         L.or_f16_to_f32_array.argtypes = [_u16p, _f32p, C.c_size_t]
         L.or_llama_forward.restype = C.c_int
         L.or_llama_forward.argtypes = [C.POINTER(Llama), _u32p, C.c_size_t, _u32p, C.c_uint32, _f32p]
+        L.or_llama_forward_h.restype = C.c_int
+        L.or_llama_forward_h.argtypes = [C.POINTER(Llama), _u32p, C.c_size_t, _u32p, C.c_uint32, _f32p, _f32p]
 
     def f16_to_f32(self, bits):
         bits = np.ascontiguousarray(bits, dtype=np.uint16)
@@ -102,20 +104,23 @@ class Oracle:
         self.lib.or_gather_dot(C.byref(w), h.reshape(-1), ids.reshape(-1), B, k, out.reshape(-1))
         return out
 
-    def llama_forward(self, model, tokens, ids):
-        """model: synth.tiny_llama() dict (blocks in llama.cpp storage order)."""
+    def llama_forward(self, model, tokens, ids, hidden=False):
+        """model: synth.tiny_llama() dict (blocks in llama.cpp storage order). With hidden=True also
+        returns the final-normalised last position (the CPU backend's last_hidden)."""
         st, keep = llama_struct(model)
         logits = np.empty(len(ids), dtype=np.float32)
-        rc = self.lib.or_llama_forward(C.byref(st), np.ascontiguousarray(tokens, np.uint32), len(tokens),
-                                       np.ascontiguousarray(ids, np.uint32), len(ids), logits)
+        h = np.empty(model["cfg"]["hidden"], dtype=np.float32)
+        rc = self.lib.or_llama_forward_h(C.byref(st), np.ascontiguousarray(tokens, np.uint32), len(tokens),
+                                         np.ascontiguousarray(ids, np.uint32), len(ids), logits, h)
         del keep
         if rc:
             raise ValueError("or_llama_forward: bad tokens or ids")
-        return logits
+        return (logits, h) if hidden else logits
 
 
 def llama_struct(model):
-    """Llama struct over a synth.tiny_llama() dict; returns (struct, objects to keep alive)."""
+    """Llama struct over a synth.tiny_llama() dict; returns (struct, objects to keep alive). Layer
+    matrices are Q8_0 unless model["types"] names another ggml type for them (e.g. {"up": Q6_K})."""
     c = model["cfg"]
     H, I = c["hidden"], c["intermediate"]
     qw, kvw = c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
@@ -125,7 +130,7 @@ def llama_struct(model):
               "gate": (I, H, 0), "up": (I, H, 0), "down": (H, I, 0)}
     for li, L in enumerate(model["layers"]):
         for name, (r, k, perm) in shapes.items():
-            setattr(layers[li], name, wmat(L[name], 8, r, k, perm))
+            setattr(layers[li], name, wmat(L[name], model.get("types", {}).get(name, 8), r, k, perm))
         layers[li].in_norm = L["in_norm"].ctypes.data
         layers[li].post_norm = L["post_norm"].ctypes.data
     keep.append(layers)
@@ -195,10 +200,13 @@ class Reference:
         """Whether the reference's GGUF reader opens the file (header, metadata, tensor table)."""
         return self.lib.ref_gguf_open_ok(str(path).encode()) == 0
 
-    def logits(self, gguf_path, tokens, ids):
+    def logits(self, gguf_path, tokens, ids, hidden_size=0):
+        """Option logits of the reference CPU backend; with hidden_size > 0 also its last_hidden."""
         out = np.empty(len(ids), dtype=np.float32)
+        h = np.empty(max(hidden_size, 1), dtype=np.float32)
         rc = self.lib.ref_logits(gguf_path.encode(), np.ascontiguousarray(tokens, np.uint32), len(tokens),
-                                 np.ascontiguousarray(ids, np.uint32), len(ids), out, None)
+                                 np.ascontiguousarray(ids, np.uint32), len(ids), out,
+                                 h.ctypes.data if hidden_size else None)
         if rc:
             raise RuntimeError("reference: " + (self.lib.ref_last_error() or b"?").decode())
-        return out
+        return (out, h) if hidden_size else out

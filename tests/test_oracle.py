@@ -427,9 +427,10 @@ def test_llama_forward_matches_reference(oracle, reference, tiny_model, tmp_path
     path = str(tmp_path / "tiny.gguf")
     gguf_writer.write_tiny_llama(path, tiny_model)
     tokens, ids = synth.tiny_llama_prompt(2)
-    a = oracle.llama_forward(tiny_model, tokens, ids)
-    b = reference.logits(path, tokens, ids)
+    a, ha = oracle.llama_forward(tiny_model, tokens, ids, hidden=True)
+    b, hb = reference.logits(path, tokens, ids, hidden_size=tiny_model["cfg"]["hidden"])
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.array_equal(ha.view(np.uint32), hb.view(np.uint32))  # last_hidden, bit for bit
     # a second prompt: shorter, repeated ids
     t2 = tokens[:17]
     i2 = np.array([5, 5, 31999, 0], np.uint32)
