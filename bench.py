@@ -376,7 +376,8 @@ def main():
         return
     if args.swiglu_only:
         for g in (synth.Q4_K, synth.Q8_0):
-            log("swiglu", bench_swiglu(hq, synth, g, stream))
+            for m in (512, 1):
+                log("swiglu", bench_swiglu(hq, synth, g, stream, M=m))
         return
     if args.upload_only:
         log("upload", bench_upload(hq, synth))
