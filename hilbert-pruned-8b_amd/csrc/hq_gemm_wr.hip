@@ -69,16 +69,31 @@ struct WrArgs {
     int ntiles;  // mt * nt (the counter and partial-tile index range)
 };
 
-template <int NB>
+// Tile geometry. TW = 192: MFMA wave w owns column blocks 3w .. 3w + 2 for all 8 row blocks. TW = 160
+// (10 column blocks; 4 x 61 = 244 tiles at N = 9728 instead of 4 x 51 = 204 of 192 columns): wave w owns
+// blocks 2w and 2w + 1 for all rows and the half (row blocks 4h .. 4h + 3, h = w % 2) of block
+// 8 + w / 2, so every wave issues the same 40 MFMAs per stage (48 at TW = 192).
+template <int TW>
+struct WrGeo {
+    static_assert(TW == 192 || TW == 160, "tile width");
+    static constexpr bool SPLIT = TW == 160;
+    static constexpr int BN = TW, QK = TW / 32;  // quant (and Bmin) DMA instructions: 32 columns each
+    static constexpr int RC = 192;               // record slot width in columns (TW = 160 over-fetches)
+    // column block of the wave's operand j, and whether it covers processing row i (TW = 160 rotates
+    // a wave's row blocks by 4 h, so its half block is always processing rows 0 .. 3)
+    DEV int cb(int w, int j) { return SPLIT ? (j < 2 ? 2 * w + j : 8 + (w >> 1)) : 3 * w + j; }
+    static constexpr bool has(int i, int j) { return !SPLIT || j < 2 || i < 4; }
+};
+
+template <int TW>
 struct WrLds {
-    static constexpr int BN = 64 * NB, WC = 16 * NB;
+    static constexpr int BN = TW;
     static constexpr int A = 0, A_BYTES = WR_BM * WR_KS * 2;            // per ring slot
-    static constexpr int Q = WR_RING * A_BYTES, Q_WAVE = WC * 32;        // per wave and ring slot
-    static constexpr int Q_BYTES = 4 * Q_WAVE;                           // per ring slot
+    static constexpr int Q = WR_RING * A_BYTES, Q_BYTES = BN * 32;       // quant groups per ring slot
     static constexpr int S = Q + WR_RING * Q_BYTES, S_BYTES = WR_BM * 32;  // per parity
     static constexpr int T_BM = S + 2 * S_BYTES;                         // column tables: Bmin [BN][32 B],
-    static constexpr int T_REC = T_BM + BN * 32;                         // records [3][BN][16 B]
-    static constexpr int TOTAL = T_REC + 3 * BN * 16;
+    static constexpr int T_REC = T_BM + BN * 32;                         // records [3][192][16 B]
+    static constexpr int TOTAL = T_REC + 3 * WrGeo<TW>::RC * 16;
     static_assert(TOTAL <= 160 * 1024, "LDS budget");
 };
 
@@ -100,12 +115,13 @@ DEV void wr_dec_half(h8 &b, u2v q, int hf, uint32_t mask, h2 mul, h2 add) {
 
 
 // The tile body; KS: with the K split (parts > 1; the split-only work is compiled out of the whole-K
-// kernel, which is the headline's)
-template <int NB, bool KS>
+// kernels, which are the headline's); TW: the tile width (192 or 160 columns)
+template <bool KS, int TW>
 DEV void wr_tile(const WrArgs &g) {
-    using L = WrLds<NB>;
-    constexpr int BN = L::BN, WC = L::WC;
-    static_assert(NB == 3, "the loaders' DMA schedule is written for 192-column tiles");
+    using L = WrLds<TW>;
+    using G = WrGeo<TW>;
+    constexpr int NB = 3, BN = L::BN;
+    static_assert(!(KS && G::SPLIT), "the K split runs 192-column tiles");
     __shared__ __attribute__((aligned(256))) char lds[L::TOTAL];
     // tile and K part: XCD x = b % 8 takes column units x, x + 8, ... (unit = N-tile x parts + part);
     // its slots run over the M-tiles of one unit first (the unit's weight slab is then fetched once
@@ -135,7 +151,13 @@ DEV void wr_tile(const WrArgs &g) {
     const rsrc_t ra = make_rsrc(Ab, (uint32_t)((size_t)M * K * 2 - (size_t)u0 * 512));
     const rsrc_t rw = make_rsrc(Wb, (uint32_t)((size_t)N * g.row_bytes - (size_t)u0 * 144));
     const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
-    const int wc0 = WC * w4, nw = n0 + wc0;  // first column of MFMA wave w4 (in the tile, in W)
+    // tile-relative first column of the wave's operand j; TW = 160: the wave's row blocks are processed
+    // rotated by 4 hr (processing row i is row block (i + 4 hr) % 8), so its half block's rows come first
+    int c0[NB];
+#pragma unroll
+    for (int j = 0; j < NB; j++) c0[j] = 16 * G::cb(w4, j);
+    const int hr = G::SPLIT ? (w4 & 1) : 0;
+    auto rb_of = [&](int i) { return (i + 4 * hr) & 7; };  // row block of processing row i
 
     // ---- loads. A buffer load checks only its VGPR offset against the buffer's size (the scalar offset
     // is not range-checked), so every row and column index is in the VGPR offset: rows past M and
@@ -154,7 +176,7 @@ DEV void wr_tile(const WrArgs &g) {
     // quant DMA of stage s, 32 of the tile's 192 columns per instruction: instruction k (wave w issues
     // k = w, and k = 4 + w for w < 2), lane i: column c = 32k + i/2, LDS half i % 2 of the column's 32
     // bytes, holding the group's half (i % 2) ^ ((c >> 3) & 1)
-    constexpr int QK = 2 * NB;
+    constexpr int QK = G::QK;
     const int qw = w4 + 4 < QK ? 2 : 1;  // this wave's quant DMAs per stage
     uint32_t q_voff[2];
 #pragma unroll
@@ -200,56 +222,61 @@ DEV void wr_tile(const WrArgs &g) {
         *(lds_u16 *)(uintptr_t)d = __builtin_bit_cast(uint16_t, hi);
         *(lds_u16 *)(uintptr_t)(d + 16) = __builtin_bit_cast(uint16_t, lo);
     };
-    // column tables of the tile, 1 KB per instruction: Bmin of super-block u, instruction k (0..5):
+    // column tables of the tile, 1 KB per instruction: Bmin of super-block u, instruction k (0 .. QK - 1):
     // columns 32k .. + 32; the records of super-block u in record slot u % 3 (they stay until the
     // super-block's rescale and the tile's end read them, two super-blocks after the next one's
-    // loads), instruction k (0..2): columns
-    // 64k .. + 64. Loader waves 2 and 3 issue them (they have one quant DMA per stage, waves 0 and 1 two).
-    // Past column N these read other table bytes (the upload leaves HQ_Q4K_TAB_PAD zero bytes after the
-    // tables for the last tile's), used only for outputs that are not stored
+    // loads), instruction k (0..2): columns 64k .. + 64 (for TW = 160 the last 32 are the next tile's,
+    // never read). The loader waves with one quant DMA per stage issue them. Past column N these read
+    // other table bytes (the upload leaves HQ_Q4K_TAB_PAD zero bytes after the tables for the last
+    // tile's), used only for outputs that are not stored
     const rsrc_t rt = make_rsrc(Tb, (uint32_t)((size_t)N * U * HQ_Q4K_TAB_BYTES));
     auto dma_bm = [&](int u, int k) {
         dma16_so(rt, lds0 + (uint32_t)(L::T_BM + 1024 * k), 16u * (uint32_t)lane,
                  (uint32_t)u * (uint32_t)N * HQ_Q4K_TAB_BYTES + (uint32_t)(n0 + 32 * k) * 32u);
     };
     auto dma_rec = [&](int u, int slot, int k) {
-        dma16_so(rt, lds0 + (uint32_t)(L::T_REC + slot * BN * 16 + 1024 * k), 16u * (uint32_t)lane,
+        dma16_so(rt, lds0 + (uint32_t)(L::T_REC + slot * G::RC * 16 + 1024 * k), 16u * (uint32_t)lane,
                  (uint32_t)u * (uint32_t)N * HQ_Q4K_TAB_BYTES + (uint32_t)N * 32u + (uint32_t)(n0 + 64 * k) * 16u);
     };
 
     // ---- operand addresses. Activation fragment of row block i, k-step f, ring slot buf: lane (ln, lg)
     // reads row 16i + ln, slot (4f + lg) ^ ((ln >> 1) & 7)
+    // (processing rows 0 .. 3 and 4 .. 7 have their own bases, which differ by the rotation)
     const uint32_t a_lane = lds0 + (uint32_t)(L::A + ln * 128) + 16u * ((uint32_t)lg ^ (uint32_t)((ln >> 1) & 7));
+    const uint32_t a_lo = a_lane + (uint32_t)(4 * hr * 16 * 128), a_hi = a_lane - (uint32_t)(4 * hr * 16 * 128);
     auto rd = [&](int buf, int gg) {
-        return *(const __attribute__((address_space(3))) h8 *)(uintptr_t)(((a_lane ^ (64u * (uint32_t)(gg >> 3))) +
+        return *(const __attribute__((address_space(3))) h8 *)(uintptr_t)(((((gg & 7) < 4 ? a_lo : a_hi) ^ (64u * (uint32_t)(gg >> 3))) +
                                                                            (uint32_t)(buf * L::A_BYTES)) +
                                                                           (uint32_t)((gg & 7) * 16 * 128));
     };
-    // quant words of column block j (column 16j + ln of the wave, bytes 8lg .. + 7 of the group)
-    const uint32_t q_lane = lds0 + (uint32_t)(L::Q + w4 * L::Q_WAVE + ln * 32 + 16 * ((lg >> 1) ^ ((ln >> 3) & 1)) + 8 * (lg & 1));
+    // quant words of operand j (column c0[j] + ln of the tile, bytes 8lg .. + 7 of the group)
+    uint32_t q_lane[NB];
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+        q_lane[j] = lds0 + (uint32_t)(L::Q + (c0[j] + ln) * 32 + 16 * ((lg >> 1) ^ ((ln >> 3) & 1)) + 8 * (lg & 1));
     auto rdq = [&](int buf, int j) {
-        return *(const __attribute__((address_space(3))) u2v *)(uintptr_t)(q_lane + (uint32_t)(buf * L::Q_BYTES + j * 16 * 32));
+        return *(const __attribute__((address_space(3))) u2v *)(uintptr_t)(q_lane[j] + (uint32_t)(buf * L::Q_BYTES));
     };
-    // scale word p / 2 of column block j in record slot v, shifted to sub-blocks 2p, 2p + 1 in its low
-    // bytes
+    // scale word p / 2 of operand j in record slot v, shifted to sub-blocks 2p, 2p + 1 in its low bytes
     auto rdsw = [&](int p, int v, int j) {
-        return *(const __attribute__((address_space(3))) uint32_t *)(uintptr_t)(lds0 + (uint32_t)(L::T_REC + (v * BN + wc0 + 16 * j + ln) * 16 +
+        return *(const __attribute__((address_space(3))) uint32_t *)(uintptr_t)(lds0 + (uint32_t)(L::T_REC + (v * G::RC + c0[j] + ln) * 16 +
                                                                                                    (p >> 1) * 4)) >>
                ((p & 1) * 16);
     };
     const uint32_t s_lane = lds0 + (uint32_t)(L::S + ln * 32 + 16 * (lg & 1));
-    auto rds = [&](int par, int i) {
-        return *(const __attribute__((address_space(3))) h8 *)(uintptr_t)(s_lane + (uint32_t)(par * L::S_BYTES + i * 16 * 32));
+    const uint32_t s_lo = s_lane + (uint32_t)(4 * hr * 16 * 32), s_hi = s_lane - (uint32_t)(4 * hr * 16 * 32);
+    auto rds = [&](int par, int i) {  // processing row i
+        return *(const __attribute__((address_space(3))) h8 *)(uintptr_t)((i < 4 ? s_lo : s_hi) + (uint32_t)(par * L::S_BYTES + i * 16 * 32));
     };
     auto rdbm = [&](int j) {
-        return *(const __attribute__((address_space(3))) h8 *)(uintptr_t)(lds0 + (uint32_t)(L::T_BM + (wc0 + 16 * j + ln) * 32 + 16 * (lg >> 1)));
+        return *(const __attribute__((address_space(3))) h8 *)(uintptr_t)(lds0 + (uint32_t)(L::T_BM + (c0[j] + ln) * 32 + 16 * (lg >> 1)));
     };
-    // field f (2: F, 3: CN) of the records of columns 16j + 4lg .. + 3 in record slot v
+    // field f (2: F, 3: CN) of the records of columns c0[j] + 4lg .. + 3 in record slot v
     auto rdr = [&](int j, int v, int f) {
         f4 r;
 #pragma unroll
         for (int c = 0; c < 4; c++)
-            r[c] = *(const __attribute__((address_space(3))) float *)(uintptr_t)(lds0 + (uint32_t)(L::T_REC + (v * BN + wc0 + 16 * j + 4 * lg + c) * 16 + 4 * f));
+            r[c] = *(const __attribute__((address_space(3))) float *)(uintptr_t)(lds0 + (uint32_t)(L::T_REC + (v * G::RC + c0[j] + 4 * lg + c) * 16 + 4 * f));
         return r;
     };
 
@@ -277,8 +304,12 @@ DEV void wr_tile(const WrArgs &g) {
         for (int q = 0; q < 4; q++) dma_a1(0, 0, q);
         dma_q1(0, 0, 0);
         if (qw == 2) dma_q1(0, 0, 1);
-        if (w4 == 2) dma_rec(0, 0, 0), dma_rec(0, 0, 2);
-        if (w4 == 3) dma_rec(0, 0, 1);
+        if constexpr (G::SPLIT) {
+            if (w4 >= 1) dma_rec(0, 0, w4 - 1);
+        } else {
+            if (w4 == 2) dma_rec(0, 0, 0), dma_rec(0, 0, 2);
+            if (w4 == 3) dma_rec(0, 0, 1);
+        }
         *(__attribute__((address_space(3))) u4v *)(uintptr_t)(lds0 + (uint32_t)(L::S + L::S_BYTES + w4 * 1024 + 16 * lane)) =
             u4v{0u, 0u, 0u, 0u};
         {
@@ -300,7 +331,8 @@ DEV void wr_tile(const WrArgs &g) {
         // loads (stage s + 1's land: each load has two stages) and for the sums' stores, and meet the
         // MFMA waves at their barrier. Per stage a loader wave issues 4 activation DMAs, 2 (waves 0, 1)
         // or 1 (waves 2, 3) quant DMAs and, waves 2 and 3, 0 to 2 table DMAs. Past the last unit the
-        // record loads repeat it (same bytes).
+        // record loads repeat it (same bytes). TW = 160: waves 1-3 issue record instruction w - 1 at
+        // p = 0 and Bmin instructions w - 1, w + 2 (up to 4) at p = 1 and p = 2.
         int rs_next = 0;
         for (int u = 0; u < U; u++) {
             const int u_next = u < u_last ? u + 1 : u_last;
@@ -312,7 +344,13 @@ DEV void wr_tile(const WrArgs &g) {
                 for (int q = 0; q < 4; q++) dma_a1(s_src, ld, q);
                 dma_q1(s_src, ld, 0);
                 if (qw == 2) dma_q1(s_src, ld, 1);
-                if (w4 == 2) {
+                if constexpr (G::SPLIT) {
+                    if (w4 >= 1) {
+                        if (p == 0) dma_rec(u_next, rs_next, w4 - 1);
+                        if (p == 1) dma_bm(u, w4 - 1);
+                        if (p == 2 && w4 + 2 < QK) dma_bm(u, w4 + 2);
+                    }
+                } else if (w4 == 2) {
                     if (p == 0) dma_rec(u_next, rs_next, 0);
                     if (p == 1) dma_rec(u_next, rs_next, 2);
                     if (p == 2) dma_bm(u, 2), dma_bm(u, 3);
@@ -322,10 +360,16 @@ DEV void wr_tile(const WrArgs &g) {
                     if (p == 2) dma_bm(u, 4), dma_bm(u, 5);
                 }
                 sums(s);
-                if (qw == 2) wr_wait<6>();
-                else if (p == 3) wr_wait<5>();
-                else if (p == 0 || (p == 1 && w4 == 2)) wr_wait<6>();
-                else wr_wait<7>();
+                // wait for all but this stage's DMAs (4 activation, qw quant, and the table ones)
+                if constexpr (G::SPLIT) {
+                    if (qw == 2 || p < 2 || (p == 2 && w4 + 2 < QK)) wr_wait<6>();
+                    else wr_wait<5>();
+                } else {
+                    if (qw == 2) wr_wait<6>();
+                    else if (p == 3) wr_wait<5>();
+                    else if (p == 0 || (p == 1 && w4 == 2)) wr_wait<6>();
+                    else wr_wait<7>();
+                }
                 wr_barrier();
             }
         }
@@ -384,11 +428,13 @@ DEV void wr_tile(const WrArgs &g) {
                 if (gg + WR_AD < 16) af[(gg + WR_AD) % WR_AF] = rd(cur, gg + WR_AD);
                 else af[(gg + WR_AD) % WR_AF] = rd(nxt, gg + WR_AD - 16);
 #pragma unroll
-                for (int j = 0; j < NB; j++) acc[gg & 7][j] = mfma(gg < 8 ? b0[j] : b1[j], af[gg % WR_AF], acc[gg & 7][j]);
+                for (int j = 0; j < NB; j++)
+                    if (G::has(gg & 7, j)) acc[gg & 7][j] = mfma(gg < 8 ? b0[j] : b1[j], af[gg % WR_AF], acc[gg & 7][j]);
                 if (p == 1 && gg < 8) {
                     const int i = (gg + 4) & 7;
 #pragma unroll
-                    for (int j = 0; j < NB; j++) acc[i][j] = mfma_bf16(bm[j], sa[gg % 3], acc[i][j]);
+                    for (int j = 0; j < NB; j++)
+                        if (G::has(i, j)) acc[i][j] = mfma_bf16(bm[j], sa[gg % 3], acc[i][j]);
                 }
                 // unit u - 1's sub-block sums of the row the min k-step reaches three groups later (p = 1,
                 // group g < 8: row (g + 4) % 8, read from group 13 of p = 0, after this group's use of
@@ -402,11 +448,13 @@ DEV void wr_tile(const WrArgs &g) {
                 if (p == 3 && gg >= 10) {
                     const int i = gg - 10;
 #pragma unroll
-                    for (int j = 0; j < NB; j++) acc[i][j] *= r[j];
+                    for (int j = 0; j < NB; j++)
+                        if (G::has(i, j)) acc[i][j] *= r[j];
                 }
                 if (p == 0 && gg < 2)
 #pragma unroll
-                    for (int j = 0; j < NB; j++) acc[6 + gg][j] *= r[j];
+                    for (int j = 0; j < NB; j++)
+                        if (G::has(6 + gg, j)) acc[6 + gg][j] *= r[j];
                 if (gg == 6) {
                     // the loaders' wait before the barrier lands the next stage's activations and
                     // quants; after it they refill the slot of stage s - 1, whose reads have all been
@@ -456,13 +504,15 @@ DEV void wr_tile(const WrArgs &g) {
     for (int i = 0; i < 8; i++) {
         const h8 si = rds(u_last & 1, i);
 #pragma unroll
-        for (int j = 0; j < NB; j++) acc[i][j] = mfma_bf16(bm[j], si, acc[i][j]);
+        for (int j = 0; j < NB; j++)
+            if (G::has(i, j)) acc[i][j] = mfma_bf16(bm[j], si, acc[i][j]);
     }
 #pragma unroll
     for (int j = 0; j < NB; j++) {
         const f4 cl = rdr(j, u_last % 3, 3);
 #pragma unroll
-        for (int i = 0; i < 8; i++) acc[i][j] *= cl;
+        for (int i = 0; i < 8; i++)
+            if (G::has(i, j)) acc[i][j] *= cl;
     }
     if constexpr (KS) {
         constexpr int LD = BN + 4;  // tile_finish's row stride in floats
@@ -471,7 +521,7 @@ DEV void wr_tile(const WrArgs &g) {
         for (int i = 0; i < 8; i++)
 #pragma unroll
             for (int j = 0; j < NB; j++)
-                *(f4 *)(lds + ((16 * i + ln) * LD + wc0 + 16 * j + 4 * lg) * 4) = acc[i][j];
+                *(f4 *)(lds + ((16 * i + ln) * LD + c0[j] + 4 * lg) * 4) = acc[i][j];  // (KS: TW = 192, no rotation)
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         wr_barrier();
         tile_finish<WR_BM, BN, WR_NT, 4>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::T_REC));
@@ -485,11 +535,12 @@ DEV void wr_tile(const WrArgs &g) {
         const rsrc_t ro = make_rsrc(g.C, (uint32_t)((size_t)M * Nh * 2));
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const int m = m0 + 16 * i + ln;
+            const int m = m0 + 16 * rb_of(i) + ln;
 #pragma unroll
             for (int j = 0; j < NB; j++) {
+                if (!G::has(i, j)) continue;
                 const uint32_t y = swiglu_pair2(acc[i][j], lg);
-                const int n = nw + 16 * j;
+                const int n = n0 + c0[j];
                 if (m < M && n < N)
                     __builtin_amdgcn_raw_buffer_store_b32(y, ro, (uint32_t)(((size_t)m * Nh + n / 2 + 4 * (lg & 1) + 2 * (lg >> 1)) * 2),
                                                           0u, CPOL_SC1);
@@ -501,12 +552,12 @@ DEV void wr_tile(const WrArgs &g) {
     const rsrc_t rc = make_rsrc(g.C, (uint32_t)((size_t)M * N * (g.c_f32 ? 4 : 2)));
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const int m = m0 + 16 * i + ln;
-        if (m >= M) break;
+        const int m = m0 + 16 * rb_of(i) + ln;
+        if (m >= M) continue;
 #pragma unroll
         for (int j = 0; j < NB; j++) {
-            const int n = nw + 16 * j + 4 * lg;
-            if (n >= N) continue;
+            const int n = n0 + c0[j] + 4 * lg;
+            if (!G::has(i, j) || n >= N) continue;
             const size_t idx = (size_t)m * N + n;
             f4 v = acc[i][j];
             if (vec) {
@@ -540,11 +591,13 @@ DEV void wr_tile(const WrArgs &g) {
 
 template <int NB>
 __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr(WrArgs g) {
-    wr_tile<NB, false>(g);
+    wr_tile<false, 64 * NB>(g);
 }
+// the same for 160-column tiles (more tiles in one round where 192-column ones leave CUs idle)
+__global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr160(WrArgs g) { wr_tile<false, 160>(g); }
 template <int NB>
 __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr_ks(WrArgs g) {
-    wr_tile<NB, true>(g);
+    wr_tile<true, 64 * NB>(g);
 }
 }  // namespace
 
@@ -606,14 +659,15 @@ int hq_wr_fits(const hq_dev_mat *W, int M) {
 }
 
 hipError_t hq_launch_gemm_wr(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
-                             int nt0, int nt1, int parts, float *partials, int *counters, hipStream_t st) {
+                             int nt0, int nt1, int parts, float *partials, int *counters, hipStream_t st, int tw) {
     if (!hq_wr_fits(W, M) || !W->tab) return hipErrorInvalidValue;  // (every uploaded Q4_K matrix has its tables)
+    if (tw != 192 && !(tw == 160 && parts == 1)) return hipErrorInvalidValue;
     constexpr int NB = 3;
     WrArgs g;
     g.W = W->qs, g.row_bytes = (uint32_t)W->row_bytes, g.A = A, g.tab = W->tab;
     g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;
     g.mt = (M + WR_BM - 1) / WR_BM;
-    const int nt_all = (g.N + 64 * NB - 1) / (64 * NB);
+    const int nt_all = (g.N + tw - 1) / tw;
     g.nt0 = nt0, g.nt = nt1 < 0 || nt1 > nt_all ? nt_all : nt1;
     if (nt0 < 0 || nt0 >= g.nt) return hipErrorInvalidValue;
     // K split: whole super-blocks per part, the full column range, a workspace of one fp32 tile per
@@ -627,6 +681,7 @@ hipError_t hq_launch_gemm_wr(const hq_dev_mat *W, const uint16_t *A, int M, void
     if (c_f32 != 0 && c_f32 != 1 && !(c_f32 == HQ_OUT_SWIGLU && W->rows % 16 == 0 && !accumulate)) return hipErrorInvalidValue;
     const unsigned grid = (unsigned)(8 * (((g.nt - g.nt0) * parts + 7) / 8) * g.mt);
     if (parts > 1) k_gemm_q4_k_wr_ks<NB><<<grid, WR_NT, 0, st>>>(g);
+    else if (tw == 160) k_gemm_q4_k_wr160<<<grid, WR_NT, 0, st>>>(g);
     else k_gemm_q4_k_wr<NB><<<grid, WR_NT, 0, st>>>(g);
     return hipGetLastError();
 }

@@ -85,7 +85,7 @@ hipError_t hq_launch_gemm_bt(const hq_dev_mat *W, const uint16_t *A, const uint1
 // `parts` workgroups (partials / counters as for the other K splits).
 int hq_wr_fits(const hq_dev_mat *W, int M);
 hipError_t hq_launch_gemm_wr(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
-                             int nt0, int nt1, int parts, float *partials, int *counters, hipStream_t st);
+                             int nt0, int nt1, int parts, float *partials, int *counters, hipStream_t st, int tw = 192);
 // The same tile shape for Q8_0 (hq_gemm_wr8.hip; K a multiple of 256, no workspace).
 int hq_wr8_fits(const hq_dev_mat *W, int M);
 hipError_t hq_launch_gemm_wr8(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,

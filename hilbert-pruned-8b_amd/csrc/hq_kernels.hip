@@ -1234,6 +1234,7 @@ struct GemmCfg {
     bool bt;        // Q4_K large M: the 256 x 256 tile kernel k_gemm_q4_k_bt (hq_gemm_bt.hip)
     bool wr;        // Q4_K, one round of full-K tiles: the 128 x 192 tile kernel k_gemm_q4_k_wr (hq_gemm_wr.hip)
     int wr_parts;   // with wr: workgroups per tile (K split), 1: whole K
+    int wr_tw;      // with wr: tile width, 192 or 160 columns (k_gemm_q4_k_wr160)
     bool wr8;       // Q8_0, the same: k_gemm_q8_0_wr (hq_gemm_wr8.hip)
 };
 
@@ -1275,6 +1276,15 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
     // columns (M = 512, N = 9728: 204 tiles)
     c.wr = c.ws_nb && c.ws_parts == 1 && hq_wr_fits(W, M);
     c.wr_parts = 1;
+    // 160-column tiles where they still make one round on every XCD and are more tiles than the
+    // 192-column ones (M = 512, N = 9728: 244 tiles instead of 204 on 256 CUs); each wave issues
+    // 40 MFMAs per stage instead of 48
+    c.wr_tw = 192;
+    if (c.wr) {
+        const int mt = (M + 127) / 128, per_xcd = std::max(1, n_cu / 8);
+        const int n192 = ((int)W->rows + 191) / 192, n160 = ((int)W->rows + 159) / 160;
+        if (mt * ((n160 + 7) / 8) <= per_xcd && n160 > n192) c.wr_tw = 160;
+    }
     // few tiles over a long K, where the LDS-decode kernel splits K (M = 512, N = 2560, K = 9728): the
     // register-decode kernel with each tile's K split over 4 or 2 workgroups of >= 8 super-blocks,
     // when its tiles x parts fit one round on every XCD and fill >= 70 % of the CUs (4 x 14 x 4 = 224)
@@ -1340,7 +1350,7 @@ void hq_gemm_tile_shape(int type, int M, int N, int K, int n_cu, int *rows, int 
     W.ldd = type == HQ_TYPE_Q8_0 ? (K / 32 + 7) / 8 * 8 : 0;
     const GemmCfg c = gemm_cfg(&W, M, n_cu);
     *rows = c.bt ? 256 : c.wr || c.wr8 ? 128 : c.rbm ? 64 : c.rb8 ? (M <= 16 ? 16 : M <= 32 ? 32 : 64) : c.ws_nb || c.ws8_nb ? 128 : 16 * c.mb;
-    *cols = c.bt ? 256 : c.wr || c.wr8 ? 192 : c.rbm || c.rb8 ? 64 : c.ws_nb ? 32 * c.ws_nb : c.ws8_nb ? 32 * c.ws8_nb : 16 * c.nb * c.waves;
+    *cols = c.bt ? 256 : c.wr ? c.wr_tw : c.wr8 ? 192 : c.rbm || c.rb8 ? 64 : c.ws_nb ? 32 * c.ws_nb : c.ws8_nb ? 32 * c.ws8_nb : 16 * c.nb * c.waves;
 }
 
 // Name of the kernel that does the work of an M x N x K hq_gemm call (the main kernel for GEMMs
@@ -1374,7 +1384,7 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
     if (c.rbm) snprintf(buf, n, "k_gemm_q4_k_rb<1, 4, 3, 2>");
     else if (c.rb8) snprintf(buf, n, "k_gemm_q8_0_rb<%d, 3, 2>", M <= 16 ? 1 : M <= 32 ? 2 : 4);
     else if (c.bt) snprintf(buf, n, "k_gemm_q4_k_bt");
-    else if (c.wr) snprintf(buf, n, c.wr_parts > 1 ? "k_gemm_q4_k_wr_ks<3>" : "k_gemm_q4_k_wr<3>");
+    else if (c.wr) snprintf(buf, n, c.wr_parts > 1 ? "k_gemm_q4_k_wr_ks<3>" : c.wr_tw == 160 ? "k_gemm_q4_k_wr160" : "k_gemm_q4_k_wr<3>");
     else if (c.wr8) snprintf(buf, n, "k_gemm_q8_0_wr");
     else if (c.ws_nb) snprintf(buf, n, "k_gemm_q4_k_ws<%d>", c.ws_nb);
     else if (c.ws8_nb) snprintf(buf, n, "k_gemm_q8_0_ws<%d>", c.ws8_nb);
@@ -1436,7 +1446,7 @@ hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, vo
     if (c.rbm) return hq_launch_gemm_rb(W, A, wk.sums, M, C, c_f32, accumulate, c.rbm, wk.partials, wk.counters, st);
     if (c.rb8) return hq_launch_gemm_rb8(W, A, M, C, c_f32, accumulate, c.rb8, wk.partials, wk.counters, st);
     if (c.bt) return hq_launch_gemm_bt(W, A, wk.sums, M, C, c_f32, accumulate, st);
-    if (c.wr) return hq_launch_gemm_wr(W, A, M, C, c_f32, accumulate, 0, -1, c.wr_parts, wk.partials, wk.counters, st);
+    if (c.wr) return hq_launch_gemm_wr(W, A, M, C, c_f32, accumulate, 0, -1, c.wr_parts, wk.partials, wk.counters, st, c.wr_tw);
     if (c.wr8) {
         const size_t K = W->cols, N = W->rows, esize = c_f32 ? 4 : 2;
         return wr_launches(wr_plan(M, (int)N, wk.n_cu), M, (int)N, [&](int m0, int rows, int t0, int t1) {

@@ -101,7 +101,8 @@ def test_gemm_workspace_bytes():
 
 def test_gemm_kernel_names():
     """hq_gemm_kernel names the kernel the launch plan picks (the names rocprofv3 lists)."""
-    cases = {(synth.Q4_K, 512, 9728, 2560): "k_gemm_q4_k_wr<3>", (synth.Q4_K, 256, 9728, 2560): "k_gemm_q4_k_wr<3>", (synth.Q8_0, 512, 9728, 2560): "k_gemm_q8_0_wr",
+    cases = {(synth.Q4_K, 512, 9728, 2560): "k_gemm_q4_k_wr160", (synth.Q4_K, 256, 9728, 2560): "k_gemm_q4_k_wr160",
+             (synth.Q4_K, 384, 13000, 2560): "k_gemm_q4_k_wr<3>", (synth.Q8_0, 512, 9728, 2560): "k_gemm_q8_0_wr",
              (synth.Q8_0, 2048, 9728, 2560): "k_gemm_q8_0_wr", (synth.Q8_0, 128, 9728, 2560): "k_gemm_q8_0_ws<2>",
              (synth.Q8_0, 65, 9728, 2560): "k_gemm_q8_0<8, 2>",
              (synth.Q4_K, 4096, 9728, 2560): "k_gemm_q4_k_bt", (synth.Q4_K, 16384, 2560, 9216): "k_gemm_q4_k_bt",
@@ -119,7 +120,7 @@ def test_gemm_kernel_names():
              (synth.Q8_0, 1, 100, 512): "k_gemv_q8_0<1>",
              # special-scale cases: the narrow kernel at M = 16, the mid-M kernel with a 6-way K split
              (synth.Q4_K, 16, 9728, 2560): "k_gemm_q4_k<2, 2>", (synth.Q4_K, 48, 9728, 2560): "k_gemm_q4_k_rb<1, 4, 3, 2>",
-             (synth.Q4_K, 350, 9728, 512): "k_gemm_q4_k_wr<3>"}
+             (synth.Q4_K, 350, 9728, 512): "k_gemm_q4_k_wr160"}
     for (gtype, M, N, K), name in cases.items():
         assert hq.gemm_kernel(gtype, M, N, K) == name, (gtype, M, N, K)
 
@@ -158,10 +159,10 @@ def test_gemm_tile_selection():
     assert hq.gemm_tiles(synth.Q8_0, 2048, 9728) == (128, 192)
     assert hq.gemm_tiles(synth.Q8_0, 256, 9728) == (128, 96)
     assert hq.gemm_tiles(synth.Q4_K, 65, 9728) == (128, 256)
-    # full-K tiles: 4 x 51 tiles of 128 x 192 on 256 CUs; more tiles than CUs: Stream-K, or at large
+    # full-K tiles: 4 x 61 tiles of 128 x 160 on 256 CUs; more tiles than CUs: Stream-K, or at large
     # M the 256 x 256 tiles when their rounds fill >= 3/4 of the CU time (M = 4096: 608 tiles in 3
     # rounds; M = 2048: 304 tiles in 2 rounds, 59 %)
-    assert hq.gemm_tiles(synth.Q4_K, 512, 9728) == (128, 192)
+    assert hq.gemm_tiles(synth.Q4_K, 512, 9728) == (128, 160)  # k_gemm_q4_k_wr160: 244 tiles in one round
     assert hq.gemm_tiles(synth.Q4_K, 2048, 9728) == (128, 256)
     assert hq.gemm_tiles(synth.Q4_K, 4096, 9728) == (256, 256)
 

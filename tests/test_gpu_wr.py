@@ -1,14 +1,16 @@
-"""GPU parity of the one-round Q4_K tile kernel with loader waves (k_gemm_q4_k_wr<3>: 128 x 192
-tiles, 4 MFMA waves and 4 loader waves; the headline shape M = 512, N = 9728, K = 2560), through the
-C ABI, against the CPU oracle.
+"""GPU parity of the one-round Q4_K tile kernels with loader waves, through the C ABI, against the
+CPU oracle: k_gemm_q4_k_wr160 (128 x 160 tiles; the headline shape M = 512, N = 9728, K = 2560: 244
+tiles) and k_gemm_q4_k_wr<3> (128 x 192 tiles, where 160-column tiles would not fit one round:
+M = 300 .. 384 at N ~ 13000), both with 4 MFMA waves and 4 loader waves.
 
-Shapes: M = 256, 350 (two whole 128-row tiles and a ragged one of 94 rows) and 512; N = 9672 (50
-whole 192-column tiles and a ragged one of 72: one MFMA wave's columns whole, the next one's half, two
-waves with none) or 9674 (N not a multiple of 4: the element-wise store path); K = 256 (one
-super-block: no rescale between super-blocks), 512, 1024, 2560 and 4096 (the record ring of three
-slots wraps). The per-super-block column tables come from the upload (k_q4k_tables), so every test
-also checks them. Bars as in test_gpu_parity.py: rel-L2 <= 1e-3 and max-abs <= 2e-3
-(Q4_K); against the float64 product, 2^-13 |W| @ |a| per output.
+Shapes: M = 256, 300, 350 (two whole 128-row tiles and a ragged one of 94 rows), 384 and 512;
+N = 9672 (60 whole 160-column tiles and a ragged one of 72: wave 0's and wave 1's full blocks whole,
+wave 2's first half valid, the rest and both half blocks past N) or 9674 (N not a multiple of 4: the
+element-wise store path); N = 13000 / 12996 for the 192-column kernel (67 whole tiles and a ragged one
+of 136 / 132 columns); K = 256 (one super-block: no rescale between super-blocks), 512, 1024, 2560
+and 4096 (the record ring of three slots wraps). The per-super-block column tables come from the
+upload (k_q4k_tables), so every test also checks them. Bars as in test_gpu_parity.py: rel-L2 <= 1e-3
+and max-abs <= 2e-3 (Q4_K); against the float64 product, 2^-13 |W| @ |a| per output.
 """
 import numpy as np
 import pytest
@@ -21,7 +23,7 @@ from test_gpu_parity import f64_reference, special_q4_k_weights
 pytestmark = pytest.mark.gpu
 
 REL_L2, Q4K_MAX_ABS = 1e-3, 2e-3
-KERNEL = "k_gemm_q4_k_wr<3>"
+KERNELS = ("k_gemm_q4_k_wr160", "k_gemm_q4_k_wr<3>")
 
 
 def say(*a):
@@ -38,18 +40,19 @@ def run(hqlib, blocks, a, N, K, what, c_f32=True, c_init=None):
     M = a.shape[0]
     name = hqlib.gemm_kernel(synth.Q4_K, M, N, K)
     say(f"{what}: M={M} N={N} K={K} kernel={name}")
-    assert name == KERNEL
+    assert name in KERNELS
     W = hqlib.Mat(blocks, synth.Q4_K, N, K)
     got = hqlib.gemm_np(W, a, c_f32=c_f32, c_init=c_init)
     W.free()
     return got
 
 
-@pytest.mark.parametrize("N,K", [(9672, 512), (9674, 256), (9674, 2560)])
-def test_wr_special_scales_ragged(hqlib, oracle, N, K):
+@pytest.mark.parametrize("M,N,K", [(350, 9672, 512), (350, 9674, 256), (350, 9674, 2560), (300, 13000, 512),
+                                   (300, 12996, 2560)])
+def test_wr_special_scales_ragged(hqlib, oracle, M, N, K):
     """Weights with zero, negative, subnormal and widely varying super-block scales (and one all-zero
-    row, one min-term-only row); ragged last row and column tiles; N % 4 != 0 at N = 9674."""
-    M = 350
+    row, one min-term-only row); ragged last row and column tiles; N % 4 != 0 at N = 9674; both tile
+    widths."""
     blocks = special_q4_k_weights(171 + N, N, K)
     a = synth.activations_f16(synth.Rng(172 + N), M, K)
     got = run(hqlib, blocks, a, N, K, "wr special scales")
@@ -62,9 +65,9 @@ def test_wr_special_scales_ragged(hqlib, oracle, N, K):
     assert np.all(np.isfinite(got))
 
 
-@pytest.mark.parametrize("N,K", [(9728, 1024), (9674, 1024), (9728, 2560), (9674, 2560)])
-def test_wr_accumulate_and_fp16_output(hqlib, oracle, N, K):
-    M = 512
+@pytest.mark.parametrize("M,N,K", [(512, 9728, 1024), (512, 9674, 1024), (512, 9728, 2560), (512, 9674, 2560),
+                                   (384, 13000, 1024)])
+def test_wr_accumulate_and_fp16_output(hqlib, oracle, M, N, K):
     blocks = synth.random_blocks(synth.Q4_K, synth.Rng(181 + N), N, K)
     rng = synth.Rng(182)
     a = synth.activations_f16(rng, M, K)
@@ -103,17 +106,18 @@ def test_wr_positive_activations(hqlib, oracle):
     assert np.all(np.abs(got[rows] - r64) <= 2.0 ** -13 * bound)
 
 
-def test_wr_long_k_repeatable(hqlib, oracle):
+@pytest.mark.parametrize("M,N", [(350, 9672), (300, 13000)])
+def test_wr_long_k_repeatable(hqlib, oracle, M, N):
     """K = 4096 (16 super-blocks, 64 stages through the 4-slot LDS ring and the double-buffered table
     records): sampled parity, and three calls give the same bits (each output is one workgroup's
     fixed sequence of MFMAs, so any difference would come from a race between the loader waves'
-    DMA and the MFMA waves' reads)."""
-    M, N, K = 350, 9672, 4096
+    DMA and the MFMA waves' reads); both tile widths."""
+    K = 4096
     blocks = synth.random_blocks(synth.Q4_K, synth.Rng(201), N, K)
     a = synth.activations_f16(synth.Rng(202), M, K)
     name = hqlib.gemm_kernel(synth.Q4_K, M, N, K)
     say(f"wr long K: M={M} N={N} K={K} kernel={name}")
-    assert name == KERNEL
+    assert name in KERNELS
     W = hqlib.Mat(blocks, synth.Q4_K, N, K)
     got = [hqlib.gemm_np(W, a) for _ in range(3)]
     W.free()
