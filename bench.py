@@ -226,6 +226,23 @@ def bench_prefill(hq, synth, T=2048, reps=5):
                 timing=f"prefill: median of {reps} after a warm-up; decode: median of 32 steps after 128 tokens")
 
 
+def bench_read_floor(hq, synth, stream, iters=20):
+    """The floor of one HBM-bound dispatch: a pure streaming read (hq_time_read) of the GEMVs' weight
+    bytes (Q4_K 9728 x 2560: 14,008,320 B; Q8_0: 26,460,160 B), over rotated buffers (> 512 MB in all,
+    as the GEMV timings), for several grid sizes; median of MEDIAN_REPS graph replays."""
+    out = []
+    for nbytes in (14008320, 26460160):
+        copies = max(2, -(-ROTATE_BYTES // nbytes))
+        bufs = [hq.DevBuf(nbytes) for _ in range(copies)]
+        for grid in (1024, 2048, 4096):
+            ms = hq.time_read(bufs, nbytes, grid, iters, MEDIAN_REPS, stream)
+            out.append(dict(type="stream_read", bytes=nbytes, grid=grid, us=round(ms * 1e3, 3),
+                            gbs=round(nbytes / (ms * 1e-3) / 1e9, 1), frac=round(nbytes / (ms * 1e-3) / 1e9 / PEAK_GBS, 4)))
+        for b in bufs:
+            b.free()
+    return out
+
+
 def bench_upload(hq, synth, reps=3):
     """hq_mat_upload of the config-5 lm_head (151936 x 2560 Q8_0, 413 MB of GGUF blocks) from host
     memory: rows through the pinned staging buffers, asynchronous copies, device-side plane repack.
@@ -340,9 +357,12 @@ def main():
     ap.add_argument("--upload-only", action="store_true",
                     help="only time the upload of the 413 MB config-5 head and exit")
     ap.add_argument("--gemv-only", action="store_true",
-                    help="only time the three M = 1 GEMV shapes of the sweep (for profiling) and exit")
-    ap.add_argument("--shape", default="", metavar="TYPE:M:N:K",
-                    help="only time this one GEMM shape (TYPE q8_0, q2_k .. q6_k; for profiling) and exit")
+                    help="only time the three M = 1 GEMV shapes of the sweep and the streaming-read floor of "
+                         "their byte counts (for profiling) and exit")
+    ap.add_argument("--gather-only", action="store_true",
+                    help="only time the config-5 option readout at k = 2, 8, 32 (for profiling) and exit")
+    ap.add_argument("--shape", default="", metavar="TYPE:M:N:K[,TYPE:M:N:K...]",
+                    help="only time these GEMM shapes (TYPE q8_0, q2_k .. q6_k; for profiling) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); the quantized matmul "
@@ -365,10 +385,17 @@ def main():
     log("device", name, arch)
     stream = hq.Stream()
     if args.shape:
-        t, m, n, k = args.shape.split(":")
-        g = {v.lower(): k for k, v in synth.TYPE_NAMES.items()}[t]
-        r = bench_gemm(hq, synth, g, int(n), int(k), int(m), False, args.steps, args.warmup, stream, settle_s=0.2)
-        log("shape", main_kernel_name(hq, g, int(m), int(n), int(k)), r)
+        for shape in args.shape.split(","):
+            t, m, n, k = shape.split(":")
+            g = {v.lower(): k for k, v in synth.TYPE_NAMES.items()}[t]
+            r = bench_gemm(hq, synth, g, int(n), int(k), int(m), False, args.steps, args.warmup, stream, settle_s=0.2)
+            log("shape", main_kernel_name(hq, g, int(m), int(n), int(k)), r)
+        return
+    if args.gather_only:
+        for k in (2, 8, 32):
+            r = bench_gather(hq, synth, k, stream)
+            r["frac"] = round(r["gbs"] / PEAK_GBS, 4)
+            log("gather", r)
         return
     if args.config4_only:
         for reading in ("baseline", "layer_weights"):
@@ -390,6 +417,8 @@ def main():
             r = bench_gemm(hq, synth, g, n, k, 1, False, args.steps, args.warmup, stream, settle_s=0.2)
             r["frac_hbm"] = round(r["gbs"] / PEAK_GBS, 4)
             log("gemv", r)
+        for r in bench_read_floor(hq, synth, stream, args.steps):
+            log("read floor", r)
         return
 
     gtype, N, K, M = synth.Q4_K, 9728, 2560, 512

@@ -935,6 +935,23 @@ extern "C" int hq_time_gemm_swiglu(hq_mat *const *pairs, int n_w, const uint16_t
     return time_graph(iters, reps, stream, ms, [&](int i) { return hq_gemm_swiglu(pairs[i % n_w], A, M, out, stream); });
 }
 
+extern "C" int hq_time_read(void *const *bufs, int n_bufs, size_t bytes, int grid, int iters, int reps, void *stream,
+                            float *ms) {
+    if (!bufs || n_bufs < 1 || bytes == 0 || bytes % 16) return fail("hq_time_read: %d buffers of %zu bytes", n_bufs, bytes);
+    if (grid < 1 || grid > (1 << 20)) return fail("hq_time_read: grid %d", grid);
+    for (int i = 0; i < n_bufs; i++)
+        if (!bufs[i] || !aligned(bufs[i], 16)) return fail("hq_time_read: buffer %d missing or not 16-byte aligned", i);
+    int dev;
+    HIPCK(hipGetDevice(&dev));
+    void *out;
+    if (staging(dev, stream, 3, (size_t)grid * 16, &out)) return -1;  // (outside the capture)
+    HIPCK(hipStreamSynchronize(S(stream)));
+    return time_graph(iters, reps, stream, ms, [&](int i) {
+        const hipError_t e = hq_launch_stream_read(bufs[i % n_bufs], bytes, (uint32_t *)out, (unsigned)grid, S(stream));
+        return e == hipSuccess ? 0 : fail("hq_time_read: %s", hipGetErrorString(e));
+    });
+}
+
 extern "C" int hq_time_gather(hq_mat *const *Ws, int n_w, const uint16_t *H, const uint32_t *ids_dev, int n_sets,
                               int B, int k, float *out, int iters, int reps, void *stream, float *ms) {
     if (!Ws || n_w < 1) return fail("hq_time_gather: no matrices");

@@ -56,6 +56,8 @@ hipError_t hq_launch_gemm(const hq_dev_mat *W, const uint16_t *A, int M, void *C
 hipError_t hq_launch_gather(const hq_dev_mat *W, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
                             hipStream_t st);
 hipError_t hq_launch_f32_to_f16(const float *in, uint16_t *out, size_t n, hipStream_t st);
+// diagnostic streaming read of `bytes` (a multiple of 16) by `grid` workgroups; out[4 * grid] words
+hipError_t hq_launch_stream_read(const void *p, size_t bytes, uint32_t *out, unsigned grid, hipStream_t st);
 // gate/up pair matrices (rows 16k .. 16k + 7 of gate, 16k + 8 .. + 15 of up): the GEMM with the SwiGLU
 // epilogue fused into the tile kernels (*fused = 0 when the shape does not run them), and the
 // epilogue as a separate pass over an fp32 [M, 2I] product (n_out = M * I)

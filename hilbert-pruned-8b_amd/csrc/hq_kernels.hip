@@ -1043,6 +1043,31 @@ __global__ void __launch_bounds__(256) k_f32_to_f16(const float *__restrict__ in
         out[i] = __builtin_bit_cast(uint16_t, (_Float16)in[i]);
 }
 
+// Diagnostic: a pure streaming read of n16 16-byte words (grid-stride, four loads in flight per lane),
+// folded into one word per wave so nothing is dead: the floor one dispatch of that many bytes
+// reaches, measured beside the HBM-bound GEMVs.
+__global__ void __launch_bounds__(256) k_stream_read(const u4v *__restrict__ p, size_t n16, uint32_t *__restrict__ out) {
+    const size_t stride = (size_t)gridDim.x * 256;
+    uint32_t acc = 0;
+    size_t i = blockIdx.x * (size_t)256 + threadIdx.x;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        const u4v a = p[i], b = p[i + stride], c = p[i + 2 * stride], d = p[i + 3 * stride];
+        acc ^= (a.x ^ a.y ^ a.z ^ a.w) ^ (b.x ^ b.y ^ b.z ^ b.w) ^ (c.x ^ c.y ^ c.z ^ c.w) ^ (d.x ^ d.y ^ d.z ^ d.w);
+    }
+    for (; i < n16; i += stride) {
+        const u4v a = p[i];
+        acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, o, 64);
+    if ((threadIdx.x & 63) == 0) out[blockIdx.x * 4 + (threadIdx.x >> 6)] = acc;
+}
+
+hipError_t hq_launch_stream_read(const void *p, size_t bytes, uint32_t *out, unsigned grid, hipStream_t st) {
+    k_stream_read<<<grid, 256, 0, st>>>((const u4v *)p, bytes / 16, out);
+    return hipGetLastError();
+}
+
 // ============================================================================ launchers
 static unsigned grid_for(size_t n, unsigned per, unsigned cap) {
     size_t g = (n + per - 1) / per;

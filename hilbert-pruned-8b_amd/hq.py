@@ -25,7 +25,7 @@ EXPORTS = (
     "hq_device_synchronize", "hq_time_gemm", "hq_time_gemm_kernel", "hq_time_gather", "hq_gemm_tiles", "hq_llama_forward",
     "hq_embed_f32", "hq_gemm_kernel", "hq_gemm_noalloc", "hq_gemm_workspace_bytes", "hq_gemv_swiglu",
     "hq_gguf_open", "hq_gguf_close", "hq_gguf_n_tensors", "hq_gguf_tensor_info", "hq_gguf_find", "hq_gguf_get_uint",
-    "hq_gguf_wmat", "hq_mat_upload_pair", "hq_gemm_swiglu", "hq_time_gemm_swiglu",
+    "hq_gguf_wmat", "hq_mat_upload_pair", "hq_gemm_swiglu", "hq_time_gemm_swiglu", "hq_time_read",
 )
 # include/hq_backend.h (no hq_ prefix: the names of the reference entry points they replace)
 BACKEND_EXPORTS = ("hip_backend_create", "hip_selftest")
@@ -135,6 +135,7 @@ def load(path=LIB_PATH):
         "hq_time_gemm": (i, [C.POINTER(vp), i, vp, i, vp, i, i, i, vp, C.POINTER(C.c_float)]),
         "hq_time_gemm_kernel": (i, [C.POINTER(vp), i, vp, i, vp, i, i, i, vp, C.POINTER(C.c_float)]),
         "hq_time_gather": (i, [C.POINTER(vp), i, vp, vp, i, i, i, vp, i, i, vp, C.POINTER(C.c_float)]),
+        "hq_time_read": (i, [C.POINTER(vp), i, sz, i, i, i, vp, C.POINTER(C.c_float)]),
         "hq_gemm_tiles": (None, [i, i, i, C.POINTER(i), C.POINTER(i)]),
         "hq_gemm_kernel": (None, [i, i, i, i, C.c_char_p, i]),
         "hq_llama_forward": (i, [C.POINTER(Llama), vp, sz, vp, u32, vp]),
@@ -430,6 +431,14 @@ class Stream:
         if self.ptr:
             _check(_lib.hq_stream_destroy(self.ptr))
             self.ptr = None
+
+
+def time_read(bufs, nbytes, grid, iters, reps, stream):
+    """hq_time_read: ms per launch of a pure streaming read of nbytes from bufs[i % len(bufs)]."""
+    arr = (C.c_void_p * len(bufs))(*[b.ptr for b in bufs])
+    ms = C.c_float()
+    _check(_lib.hq_time_read(arr, len(bufs), nbytes, grid, iters, reps, stream.ptr, C.byref(ms)))
+    return ms.value
 
 
 def time_gemm(mats, A, M, C_buf, c_f32, iters, reps, stream):

@@ -162,6 +162,9 @@ int hq_time_gemm_swiglu(hq_mat *const *pairs, int n_w, const uint16_t *A, int M,
                         void *stream, float *ms);
 int hq_time_gather(hq_mat *const *Ws, int n_w, const uint16_t *H, const uint32_t *ids_dev, int n_sets, int B, int k,
                    float *out, int iters, int reps, void *stream, float *ms);
+/* Diagnostic floor for the HBM-bound kernels: a pure streaming read of `bytes` (a multiple of 16)
+ * from bufs[i % n_bufs] by `grid` workgroups of 256 threads, timed as hq_time_gemm times its calls. */
+int hq_time_read(void *const *bufs, int n_bufs, size_t bytes, int grid, int iters, int reps, void *stream, float *ms);
 
 /* The output tile hq_gemm uses for an M x N problem of the given ggml type on a 256-CU MI355X
  * (diagnostics; the launch itself sizes for the device's CU count). */
