@@ -111,12 +111,9 @@ hipError_t hq_launch_gemm_ws8(const hq_dev_mat *W, const uint16_t *A, int M, voi
 struct GemmArgs;
 hipError_t hq_launch_dequant_q6k(const hq_dev_mat *W, uint32_t row0, const uint32_t *ids, uint32_t nrows, float *out,
                                  hipStream_t st);
-hipError_t hq_launch_gemv_q6k(const hq_dev_mat *W, const uint16_t *a, void *C, int c_f32, int accumulate, hipStream_t st);
-hipError_t hq_launch_gather_q6k(const hq_dev_mat *W, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
-                                hipStream_t st);
 hipError_t hq_launch_gemm_q6k(const GemmArgs &g, int mb, hipStream_t st);
 
-// Q2_K, Q3_K, Q5_K (hq_kquant.hip)
+// Q2_K, Q3_K, Q5_K (hq_kquant.hip); the GEMV and gather launchers also take Q6_K
 hipError_t hq_launch_dequant_kq(const hq_dev_mat *W, uint32_t row0, const uint32_t *ids, uint32_t nrows, float *out,
                                 hipStream_t st);
 hipError_t hq_launch_gemv_kq(const hq_dev_mat *W, const uint16_t *a, void *C, int c_f32, int accumulate, hipStream_t st);

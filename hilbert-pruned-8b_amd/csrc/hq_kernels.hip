@@ -1137,8 +1137,7 @@ static GemvPlan gemv_plan(const hq_dev_mat *W) {
 }
 
 hipError_t hq_launch_gemv(const hq_dev_mat *W, const uint16_t *a, void *C, int c_f32, int accumulate, hipStream_t st) {
-    if (W->type == HQ_TYPE_Q6_K) return hq_launch_gemv_q6k(W, a, C, c_f32, accumulate, st);
-    if (hq_is_kq(W->type)) return hq_launch_gemv_kq(W, a, C, c_f32, accumulate, st);
+    if (W->type == HQ_TYPE_Q6_K || hq_is_kq(W->type)) return hq_launch_gemv_kq(W, a, C, c_f32, accumulate, st);
     const GemvPlan pl = gemv_plan(W);
     const int N = (int)W->rows, K = (int)W->cols;
     const uint32_t rb = (uint32_t)W->row_bytes;
@@ -1177,8 +1176,7 @@ static void launch_gather_t(const hq_dev_mat *W, const uint16_t *H, const uint32
 
 hipError_t hq_launch_gather(const hq_dev_mat *W, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
                             hipStream_t st) {
-    if (W->type == HQ_TYPE_Q6_K) return hq_launch_gather_q6k(W, H, ids, B, k, out, st);
-    if (hq_is_kq(W->type)) return hq_launch_gather_kq(W, H, ids, B, k, out, st);
+    if (W->type == HQ_TYPE_Q6_K || hq_is_kq(W->type)) return hq_launch_gather_kq(W, H, ids, B, k, out, st);
     switch (lanes_per_row((long)B * k)) {
     case 16: launch_gather_t<16>(W, H, ids, B, k, out, st); break;
     case 32: launch_gather_t<32>(W, H, ids, B, k, out, st); break;
@@ -1388,14 +1386,14 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
     W.ldd = type == HQ_TYPE_Q8_0 ? (K / 32 + 7) / 8 * 8 : 0;
     W.row_bytes = type == HQ_TYPE_Q4_K ? (size_t)K / 256 * 144 : type == HQ_TYPE_Q6_K ? (size_t)K / 256 * 224 : (size_t)K;
     const char *kq = type == HQ_TYPE_Q2_K ? "10" : type == HQ_TYPE_Q3_K ? "11" : type == HQ_TYPE_Q5_K ? "13" : nullptr;
-    if (M == 1 && type == HQ_TYPE_Q6_K) {
-        snprintf(buf, n, "k_gemv_q6_k");
+    if (M == 1 && (kq || type == HQ_TYPE_Q6_K)) {  // template arguments: the ggml type, rows per wave
+        const int nsb = K / 256, r = nsb % 8 == 0 ? 1 : nsb % 4 == 0 ? 2 : nsb % 2 == 0 ? 4 : 8;
+        snprintf(buf, n, "k_gemv_sb<%d, %d, false>", type, r);
         return;
     }
     if (kq) {  // template argument: the ggml type
         const int mb = M <= 16 ? 1 : M <= 32 ? 2 : 4;
-        if (M == 1) snprintf(buf, n, "k_gemv_kq<%s>", kq);
-        else snprintf(buf, n, "k_gemm_kq<%s, %d, 2>", kq, mb);
+        snprintf(buf, n, "k_gemm_kq<%s, %d, 2>", kq, mb);
         return;
     }
     if (M == 1) {

@@ -18,13 +18,17 @@
 // Device layout (hq_mat_upload): Q5_K keeps the GGUF bytes (176 = 11 x 16, so every field sits at a
 // 16-byte boundary); Q2_K and Q3_K super-blocks are stored in 96- and 112-byte slots (the GGUF
 // bytes, then zeros), so that every 16-byte load of a row is aligned. Fields keep their GGUF offsets.
+// (Q6_K, whose kernels live in hq_q6k.hip, uses 224-byte slots the same way; kq_slot covers it for
+// the GEMV of hq_kquant.hip.)
 #ifndef HQ_KQUANT_H
 #define HQ_KQUANT_H
 
 #include "hq_device.h"
 #include "hq_kernels.h"
 
-constexpr int kq_slot(int type) { return type == HQ_TYPE_Q2_K ? 96 : type == HQ_TYPE_Q3_K ? 112 : 176; }
+constexpr int kq_slot(int type) {
+    return type == HQ_TYPE_Q2_K ? 96 : type == HQ_TYPE_Q3_K ? 112 : type == HQ_TYPE_Q6_K ? 224 : 176;
+}
 
 // 6-bit Q3_K scale e (0..15) from the 12 packed bytes: low nibble from byte 4 (g % 2) + i (high
 // nibble when g >= 2), top two bits from bits 2g, 2g + 1 of byte 8 + i, for e = 4g + i.

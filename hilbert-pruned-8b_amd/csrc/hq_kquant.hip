@@ -1,11 +1,11 @@
 // hq_kquant.hip - GGUF Q2_K, Q3_K and Q5_K matrices on gfx950: decode, GEMV (M = 1), option-row gather
-// and the MFMA GEMM (M >= 2). Formats, device slots and the exact decode are in hq_kquant.h.
+// and the MFMA GEMM (M >= 2); the GEMV and gather also serve Q6_K. Formats, device slots and the exact
+// decode are in hq_kquant.h.
 //
-// Kernels (one template per kernel, instantiated for the three types)
+// Kernels (one template per kernel, instantiated per type)
 //   k_dequant_kq  rows -> fp32, bit-identical to the reference decoder.
-//   k_gemv_kq     M = 1: one wave per output row, lanes over 16-value chunks, exact fp32 weights,
-//                 fp32 sums (HBM-bound).
-//   k_gather_kq   option-row readout: the GEMV loop over (state, id) pairs.
+//   k_gemv_sb     M = 1 and the option-row gather (Q2_K, Q3_K, Q5_K, Q6_K): lane tasks of one eighth
+//                 of a super-block, exact fp16 integers in v_dot2_f32_f16, R rows per wave (HBM-bound).
 //   k_gemm_kq     M >= 2: the Stream-K MFMA kernel of hq_sk.h (tile 16 MB x 128, K-units of one
 //                 super-block). No weight is rounded to 16 bits: each weight is d * B1 - dmin * B2
 //                 with B1, B2 exact fp16 integers per 8 consecutive k of a lane:
@@ -42,46 +42,196 @@ __global__ void __launch_bounds__(256) k_dequant_kq(const uint8_t *__restrict__ 
     }
 }
 
-// dot of one row with fp16 activations a [K]: lane j of 64 takes 16-value chunks j, j + 64, ...
+// ------------------------------------------------------------------ GEMV / gather by super-block eighths
+// A lane task is one eighth of a super-block of one row: 32 values, read with its own 8- or 16-byte
+// loads (the eight lanes of a super-block are neighbours, so a super-block's bytes arrive as whole
+// lines and its scale bytes as one broadcast load). The quantized integers become exact fp16 values
+// (fp16 1024 + u from v_perm_b32, minus 1024 + bias) and meet the fp16 activations in v_dot2_f32_f16
+// (exact products, fp32 sums); the scale, and for Q2_K / Q5_K the min against the activations' fp32
+// sum, are applied per 8 or 16 values in fp32. A wave holds RW rows, 64 / RW lanes each: eight per
+// super-block and S = 8 / RW super-blocks side by side, so a lane walks K / 256 / S super-blocks of its
+// row with the next one's loads in flight while it computes the current one.
+
+// 8 values: the bytes of w0, w1 (exact integers u <= 63), minus kb - 1024, dotted with the 8 fp16 a
+DEV float dotu8(uint32_t w0, uint32_t w1, const u4v a, h2 kb, float s) {
+    const h2 q[4] = {as_h2(perm_lo(w0)) - kb, as_h2(perm_hi(w0)) - kb, as_h2(perm_lo(w1)) - kb, as_h2(perm_hi(w1)) - kb};
+    return dot8(q, a, s);
+}
+
+DEV h2 splat2(float x) { return h2{(_Float16)x, (_Float16)x}; }
+
+// The loaded bytes of one lane task: up to three weight pieces and four 8-value activation vectors.
+struct SbRaw {
+    u4v w0, w1, w2;
+    u4v a[4];
+};
+
+// Loads of eighth p of the super-block at blk (device slot) and of its 256 activations a.
+//   Q2_K, Q3_K, Q6_K: values 128 h + 32 j + l0 .. + 7 for j = 0 .. 3 (h = p / 4, l0 = 8 (p % 4)).
+//   Q5_K: values 16 (p % 2) .. + 15 of sub-blocks 2 (p / 2) and 2 (p / 2) + 1.
 template <int T>
-DEV float kq_row_dot(const uint8_t *__restrict__ row, const uint16_t *__restrict__ a, int K, int j) {
+DEV SbRaw sb_load(const uint8_t *__restrict__ blk, const uint16_t *__restrict__ a, int p) {
+    SbRaw x;
+    if constexpr (T == HQ_TYPE_Q5_K) {
+        const int sp = p >> 1, l0 = 16 * (p & 1);
+        x.w0 = *(const u4v *)blk;                          // d, dmin, scales[12]
+        x.w1 = *(const u4v *)(blk + 48 + 32 * sp + l0);    // qs
+        x.w2 = *(const u4v *)(blk + 16 + l0);              // qh
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            x.a[2 * t] = *(const u4v *)(a + 32 * (2 * sp + t) + l0);
+            x.a[2 * t + 1] = *(const u4v *)(a + 32 * (2 * sp + t) + l0 + 8);
+        }
+    } else {
+        const int h = p >> 2, l0 = 8 * (p & 3);
+        if constexpr (T == HQ_TYPE_Q2_K) {
+            x.w0 = *(const u4v *)blk;  // scales[16]
+            const u2v qs = *(const u2v *)(blk + 16 + 32 * h + l0);
+            x.w1 = u4v{qs.x, qs.y, *(const uint32_t *)(blk + 80), 0u};  // qs, {d, dmin}
+        } else if constexpr (T == HQ_TYPE_Q3_K) {
+            x.w0 = *(const u4v *)(blk + 96);  // scales[12], d
+            const u2v qs = *(const u2v *)(blk + 32 + 32 * h + l0), hm = *(const u2v *)(blk + l0);
+            x.w1 = u4v{qs.x, qs.y, hm.x, hm.y};
+        } else {
+            static_assert(T == HQ_TYPE_Q6_K, "k-quant type");
+            x.w0 = *(const u4v *)(blk + 192);  // int8 scales[16]
+            const u2v q0 = *(const u2v *)(blk + 64 * h + l0), q1 = *(const u2v *)(blk + 64 * h + 32 + l0);
+            const u2v qh = *(const u2v *)(blk + 128 + 32 * h + l0);
+            x.w1 = u4v{q0.x, q0.y, q1.x, q1.y};
+            x.w2 = u4v{qh.x, qh.y, (uint32_t)*(const uint16_t *)(blk + 208), 0u};  // qh, d
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) x.a[j] = *(const u4v *)(a + 128 * h + 32 * j + l0);
+    }
+    return x;
+}
+
+// The lane task's dot product from its loaded bytes. For Q2_K, Q3_K, Q6_K the scale of group j is
+// number 8 h + 2 j + (l0 >> 4): word 2 h + (j >> 1), byte 2 (j & 1) + (l0 >> 4) of the scale vector.
+template <int T>
+DEV float sb_dot(const SbRaw &x, int p) {
+    float r = 0.f;
+    if constexpr (T == HQ_TYPE_Q5_K) {
+        // sub-block j = 2 sp + t: nibble t of the qs bytes, qh bit j; q = u (0 .. 31)
+        const int sp = p >> 1;
+        uint32_t sw0, sw1, mw0, mw1;
+        q4k_scale_words(x.w0.y, x.w0.z, x.w0.w, sw0, sw1, mw0, mw1);
+        const float d = h2f((uint16_t)x.w0.x), dm = h2f((uint16_t)(x.w0.x >> 16));
+        const h2 kb = splat2(1024.0f);
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int j = 2 * sp + t;
+            uint32_t u[4];
+#pragma unroll
+            for (int w = 0; w < 4; w++) u[w] = ((x.w1[w] >> (4 * t)) & 0x0f0f0f0fu) | (((x.w2[w] >> j) & 0x01010101u) << 4);
+            const float dq = dotu8(u[2], u[3], x.a[2 * t + 1], kb, dotu8(u[0], u[1], x.a[2 * t], kb, 0.f));
+            const float sa = sum8(x.a[2 * t + 1], sum8(x.a[2 * t], 0.f));
+            const uint32_t s = byte_of(j < 4 ? sw0 : sw1, j & 3), m = byte_of(j < 4 ? mw0 : mw1, j & 3);
+            r += d * (float)s * dq - dm * (float)m * sa;
+        }
+    } else {
+        const int h = p >> 2, hl = (p & 3) >> 1;  // hl = l0 >> 4
+        if constexpr (T == HQ_TYPE_Q2_K) {
+            // q = u (0 .. 3); scale byte sm: d (sm & 15), min dmin (sm >> 4)
+            const float d = h2f((uint16_t)x.w1.z), dm = h2f((uint16_t)(x.w1.z >> 16));
+            const h2 kb = splat2(1024.0f);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t sm = byte_of(x.w0[2 * h + (j >> 1)], 2 * (j & 1) + hl);
+                const float dq = dotu8((x.w1.x >> (2 * j)) & 0x03030303u, (x.w1.y >> (2 * j)) & 0x03030303u, x.a[j], kb, 0.f);
+                r += d * (float)(sm & 15u) * dq - dm * (float)(sm >> 4) * sum8(x.a[j], 0.f);
+            }
+        } else if constexpr (T == HQ_TYPE_Q3_K) {
+            // u = q2 + 4 hb (0 .. 7), q = u - 4; the 6-bit scale codes as in q3k_code (e = 4 g + i)
+            const float d = h2f((uint16_t)x.w0.w);
+            const h2 kb = splat2(1028.0f);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int g = 2 * h + (j >> 1), i = 2 * (j & 1) + hl;
+                const int s = (int)(((byte_of(g & 1 ? x.w0.y : x.w0.x, i) >> (4 * (g >> 1))) & 15u) |
+                                    (((byte_of(x.w0.z, i) >> (2 * g)) & 3u) << 4)) - 32;
+                const uint32_t u0 = ((x.w1.x >> (2 * j)) & 0x03030303u) | (((x.w1.z >> (4 * h + j)) & 0x01010101u) << 2);
+                const uint32_t u1 = ((x.w1.y >> (2 * j)) & 0x03030303u) | (((x.w1.w >> (4 * h + j)) & 0x01010101u) << 2);
+                r += d * (float)s * dotu8(u0, u1, x.a[j], kb, 0.f);
+            }
+        } else {
+            // j: low (j < 2) or high nibble of ql[64 h + 32 (j & 1) + l], bits 2 j, 2 j + 1 of
+            // qh[32 h + l]; u = nibble | bits << 4 (0 .. 63), q = u - 32; signed 8-bit scales
+            const float d = h2f((uint16_t)x.w2.z);
+            const h2 kb = splat2(1056.0f);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t q0 = (j & 1) ? x.w1.z : x.w1.x, q1 = (j & 1) ? x.w1.w : x.w1.y;
+                const int sh = j >= 2 ? 4 : 0;
+                const uint32_t u0 = ((q0 >> sh) & 0x0f0f0f0fu) | (((x.w2.x >> (2 * j)) & 0x03030303u) << 4);
+                const uint32_t u1 = ((q1 >> sh) & 0x0f0f0f0fu) | (((x.w2.y >> (2 * j)) & 0x03030303u) << 4);
+                const int s = (int)(int8_t)byte_of(x.w0[2 * h + (j >> 1)], 2 * (j & 1) + hl);
+                r += d * (float)s * dotu8(u0, u1, x.a[j], kb, 0.f);
+            }
+        }
+    }
+    return r;
+}
+
+// GATHER = false: C[o] = dot(W[o], a) for o < n_out = N (store_out modes). GATHER = true:
+// out[o] = dot(W[ids[o]], a + (o / k_opts) K) for o < n_out = B k; an id >= rows stores NaN (its lanes
+// read row 0). Rows of a wave past n_out compute row n_out - 1 and store nothing.
+template <int T, int RW, bool GATHER>
+__global__ void __launch_bounds__(256) k_gemv_sb(const uint8_t *__restrict__ W, size_t row_bytes,
+                                                 const uint16_t *__restrict__ a, const uint32_t *__restrict__ ids,
+                                                 int n_out, int k_opts, int K, uint32_t rows, void *C, int c_f32,
+                                                 int accumulate) {
+    constexpr int S = 8 / RW, G = 8 * S;  // super-blocks side by side, lanes per row
+    const int lane = threadIdx.x & 63, o0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RW;
+    if (o0 >= n_out) return;
+    const int p = lane & 7, s = (lane >> 3) & (S - 1), o = o0 + lane / G, oc = min(o, n_out - 1);
+    uint32_t row = (uint32_t)oc;
+    const uint16_t *av = a;
+    if constexpr (GATHER) {
+        const uint32_t id = ids[oc];
+        row = id < rows ? id : 0u;
+        av = a + (size_t)(oc / k_opts) * K;
+    }
+    const int nsb = K >> 8;
+    const uint8_t *base = W + (size_t)row * row_bytes;
     float acc = 0.f;
-    for (int c = j; c < K / 16; c += 64) {
-        const uint8_t *blk = row + (size_t)(c >> 4) * kq_slot(T);
-        const h8 a0 = *(const h8 *)(a + 16 * c), a1 = *(const h8 *)(a + 16 * c + 8);
-        float w[8];
-        kq_deq8<T>(blk, (c & 15) * 16, w);
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc = fmaf(w[e], (float)a0[e], acc);
-        kq_deq8<T>(blk, (c & 15) * 16 + 8, w);
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc = fmaf(w[e], (float)a1[e], acc);
+    int u = min(s, nsb - 1);
+    SbRaw x = sb_load<T>(base + (size_t)u * kq_slot(T), av + 256 * u, p);
+    for (u = s; u < nsb; u += S) {
+        const int un = min(u + S, nsb - 1);  // the next super-block (the last one again at the end)
+        const SbRaw y = sb_load<T>(base + (size_t)un * kq_slot(T), av + 256 * un, p);
+        acc += sb_dot<T>(x, p);
+        x = y;
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-    return acc;
+    for (int off = G / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if ((lane & (G - 1)) == 0 && o < n_out) {
+        if constexpr (GATHER) ((float *)C)[o] = ids[o] < rows ? acc : __builtin_nanf("");
+        else store_out(C, (size_t)o, acc, c_f32, accumulate);
+    }
 }
 
-// M = 1: one wave per output row
-template <int T>
-__global__ void __launch_bounds__(256) k_gemv_kq(const uint8_t *__restrict__ W, size_t row_bytes, const uint16_t *__restrict__ a,
-                                                 int N, int K, void *C, int c_f32, int accumulate) {
-    const int n = blockIdx.x * 4 + (threadIdx.x >> 6), j = threadIdx.x & 63;
-    if (n >= N) return;
-    const float v = kq_row_dot<T>(W + (size_t)n * row_bytes, a, K, j);
-    if (j == 0) store_out(C, (size_t)n, v, c_f32, accumulate);
+// rows per wave of k_gemv_sb: enough waves to keep the weight stream's loads in flight, few enough
+// super-blocks per lane to stay short
+int sb_rows(int n_out, int nsb) {
+    (void)nsb;
+    return n_out >= 8192 ? 2 : 1;
 }
 
-// out[i] = dot(H[i / k], W[ids[i]]); an id >= rows stores NaN and reads row 0 instead
-template <int T>
-__global__ void __launch_bounds__(256) k_gather_kq(const uint8_t *__restrict__ W, size_t row_bytes, const uint16_t *__restrict__ H,
-                                                   const uint32_t *__restrict__ ids, int pairs, int k, int K, uint32_t rows,
-                                                   float *__restrict__ out) {
-    const int i = blockIdx.x * 4 + (threadIdx.x >> 6), j = threadIdx.x & 63;
-    if (i >= pairs) return;
-    const uint32_t id = ids[i];
-    const float v = kq_row_dot<T>(W + (size_t)(id < rows ? id : 0) * row_bytes, H + (size_t)(i / k) * K, K, j);
-    if (j == 0) out[i] = id < rows ? v : __builtin_nanf("");
+template <int T, bool GATHER>
+hipError_t launch_sb(const hq_dev_mat *W, const uint16_t *a, const uint32_t *ids, int n_out, int k_opts, void *C, int c_f32,
+                     int accumulate, hipStream_t st) {
+    const int R = sb_rows(n_out, (int)W->cols / 256);
+    const unsigned grid = (unsigned)(((n_out + R - 1) / R + 3) / 4);
+#define SB(r) k_gemv_sb<T, r, GATHER><<<grid, 256, 0, st>>>(W->qs, W->row_bytes, a, ids, n_out, k_opts, (int)W->cols, W->rows, C, c_f32, accumulate)
+    switch (R) {
+    case 1: SB(1); break;
+    case 2: SB(2); break;
+    case 4: SB(4); break;
+    default: SB(8); break;
+    }
+#undef SB
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------------------- GEMM
@@ -306,19 +456,26 @@ hipError_t hq_launch_dequant_kq(const hq_dev_mat *W, uint32_t row0, const uint32
 }
 
 hipError_t hq_launch_gemv_kq(const hq_dev_mat *W, const uint16_t *a, void *C, int c_f32, int accumulate, hipStream_t st) {
-#define GV(t) k_gemv_kq<t><<<(W->rows + 3) / 4, 256, 0, st>>>(W->qs, W->row_bytes, a, (int)W->rows, (int)W->cols, C, c_f32, accumulate)
-    KQ_SWITCH(W->type, GV)
-#undef GV
-    return hipGetLastError();
+    const int n = (int)W->rows;
+    switch (W->type) {
+    case HQ_TYPE_Q2_K: return launch_sb<HQ_TYPE_Q2_K, false>(W, a, nullptr, n, 1, C, c_f32, accumulate, st);
+    case HQ_TYPE_Q3_K: return launch_sb<HQ_TYPE_Q3_K, false>(W, a, nullptr, n, 1, C, c_f32, accumulate, st);
+    case HQ_TYPE_Q5_K: return launch_sb<HQ_TYPE_Q5_K, false>(W, a, nullptr, n, 1, C, c_f32, accumulate, st);
+    case HQ_TYPE_Q6_K: return launch_sb<HQ_TYPE_Q6_K, false>(W, a, nullptr, n, 1, C, c_f32, accumulate, st);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t hq_launch_gather_kq(const hq_dev_mat *W, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
                                hipStream_t st) {
     const int pairs = B * k;
-#define GA(t) k_gather_kq<t><<<(pairs + 3) / 4, 256, 0, st>>>(W->qs, W->row_bytes, H, ids, pairs, k, (int)W->cols, W->rows, out)
-    KQ_SWITCH(W->type, GA)
-#undef GA
-    return hipGetLastError();
+    switch (W->type) {
+    case HQ_TYPE_Q2_K: return launch_sb<HQ_TYPE_Q2_K, true>(W, H, ids, pairs, k, out, 1, 0, st);
+    case HQ_TYPE_Q3_K: return launch_sb<HQ_TYPE_Q3_K, true>(W, H, ids, pairs, k, out, 1, 0, st);
+    case HQ_TYPE_Q5_K: return launch_sb<HQ_TYPE_Q5_K, true>(W, H, ids, pairs, k, out, 1, 0, st);
+    case HQ_TYPE_Q6_K: return launch_sb<HQ_TYPE_Q6_K, true>(W, H, ids, pairs, k, out, 1, 0, st);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t hq_launch_gemm_kq(int type, const GemmArgs &g, int mb, hipStream_t st) {

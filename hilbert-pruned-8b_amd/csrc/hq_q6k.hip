@@ -1,4 +1,4 @@
-// hq_q6k.hip - GGUF Q6_K matrices on gfx950: decode, GEMV (M = 1), option-row gather and the MFMA GEMM.
+// hq_q6k.hip - GGUF Q6_K matrices on gfx950: decode and the MFMA GEMM.
 //
 // Reference arithmetic (cleanroom-transformer/src/ggml_quant.h:151-169): a super-block of 256 values
 // {u8 ql[128], u8 qh[64], int8 scales[16], fp16 d}; value 128h + 32r + l (half h, lane r = 0..3,
@@ -12,8 +12,7 @@
 //
 // Kernels
 //   k_dequant_q6_k  rows -> fp32, bit-identical to the reference decoder ((d * sc) * q in fp32).
-//   k_gemv_q6_k     M = 1: lanes over 16-value chunks, exact fp32 weights, fp32 sums (HBM-bound).
-//   k_gather_q6_k   option-row readout: the GEMV loop over (state, id) pairs.
+//   (M = 1 and the option-row gather: k_gemv_sb in hq_kquant.hip)
 //   k_gemm_q6_k     M >= 2: the Stream-K MFMA kernel of hq_sk.h (tile 16 MB x 128, K-units of one
 //                   super-block). No weight is rounded to 16 bits: with q = lo + 16 hb - 32 (lo the
 //                   4-bit part, hb the 2-bit part), W / d = sc * lo + 16 sc * (hb - 2), and both terms
@@ -60,45 +59,6 @@ __global__ void __launch_bounds__(256) k_dequant_q6_k(const uint8_t *__restrict_
 #pragma unroll
         for (int q = 0; q < 4; q++) o[q] = float4{w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]};
     }
-}
-
-// dot of row `row` with fp16 activations a [K]: lane j of LPR takes chunks j, j + LPR, ...
-template <int LPR>
-DEV float q6k_row_dot(const uint8_t *__restrict__ row, const uint16_t *__restrict__ a, int K, int j) {
-    float acc = 0.f;
-    for (int c = j; c < K / 16; c += LPR) {
-        float w[16];
-        q6k_deq16(row + (size_t)(c >> 4) * Q6_SLOT, (c & 15) * 16, w);
-        const h8 a0 = *(const h8 *)(a + 16 * c), a1 = *(const h8 *)(a + 16 * c + 8);
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc = fmaf(w[e], (float)a0[e], acc);
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc = fmaf(w[8 + e], (float)a1[e], acc);
-    }
-#pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, LPR);
-    return acc;
-}
-
-// M = 1: one wave per output row
-__global__ void __launch_bounds__(256) k_gemv_q6_k(const uint8_t *__restrict__ W, size_t row_bytes,
-                                                   const uint16_t *__restrict__ a, int N, int K, void *C, int c_f32,
-                                                   int accumulate) {
-    const int n = blockIdx.x * 4 + (threadIdx.x >> 6), j = threadIdx.x & 63;
-    if (n >= N) return;
-    const float v = q6k_row_dot<64>(W + (size_t)n * row_bytes, a, K, j);
-    if (j == 0) store_out(C, (size_t)n, v, c_f32, accumulate);
-}
-
-// out[i] = dot(H[i / k], W[ids[i]]); an id >= rows stores NaN and reads no row
-__global__ void __launch_bounds__(256) k_gather_q6_k(const uint8_t *__restrict__ W, size_t row_bytes,
-                                                     const uint16_t *__restrict__ H, const uint32_t *__restrict__ ids,
-                                                     int pairs, int k, int K, uint32_t rows, float *__restrict__ out) {
-    const int i = blockIdx.x * 4 + (threadIdx.x >> 6), j = threadIdx.x & 63;
-    if (i >= pairs) return;
-    const uint32_t id = ids[i];
-    const float v = q6k_row_dot<64>(W + (size_t)(id < rows ? id : 0) * row_bytes, H + (size_t)(i / k) * K, K, j);
-    if (j == 0) out[i] = id < rows ? v : __builtin_nanf("");
 }
 
 // The two exact fp16 B terms of 8 weights: bytes 8e .. 8e + 7 of the lane's ql / qh vectors, nibble
@@ -241,18 +201,6 @@ hipError_t hq_launch_dequant_q6k(const hq_dev_mat *W, uint32_t row0, const uint3
                                  hipStream_t st) {
     const size_t n = (size_t)nrows * (W->cols / 16);
     k_dequant_q6_k<<<grid_cap(n, 256, 65536), 256, 0, st>>>(W->qs, W->row_bytes, (int)W->cols, row0, ids, nrows, out);
-    return hipGetLastError();
-}
-
-hipError_t hq_launch_gemv_q6k(const hq_dev_mat *W, const uint16_t *a, void *C, int c_f32, int accumulate, hipStream_t st) {
-    k_gemv_q6_k<<<(W->rows + 3) / 4, 256, 0, st>>>(W->qs, W->row_bytes, a, (int)W->rows, (int)W->cols, C, c_f32, accumulate);
-    return hipGetLastError();
-}
-
-hipError_t hq_launch_gather_q6k(const hq_dev_mat *W, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
-                                hipStream_t st) {
-    const int pairs = B * k;
-    k_gather_q6_k<<<(pairs + 3) / 4, 256, 0, st>>>(W->qs, W->row_bytes, H, ids, pairs, k, (int)W->cols, W->rows, out);
     return hipGetLastError();
 }
 

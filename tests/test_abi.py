@@ -118,6 +118,9 @@ def test_gemm_kernel_names():
              (synth.Q4_K, 1, 2560, 9728): "k_gemv_q4_k_s<4>", (synth.Q4_K, 1, 100, 512): "k_gemv_q4_k_s<1>",
              (synth.Q4_K, 1, 9728, 256): "k_gemv_q4_k_s<16>", (synth.Q8_0, 1, 9728, 2560): "k_gemv_q8_0<2>",
              (synth.Q8_0, 1, 100, 512): "k_gemv_q8_0<1>",
+             # k-quant GEMVs: rows per wave = 8 / gcd(K / 256, 8)
+             (synth.Q6_K, 1, 9728, 2560): "k_gemv_sb<14, 4, false>", (synth.Q3_K, 1, 2560, 9728): "k_gemv_sb<11, 4, false>",
+             (synth.Q5_K, 1, 100, 2048): "k_gemv_sb<13, 1, false>", (synth.Q2_K, 1, 100, 768): "k_gemv_sb<10, 8, false>",
              # special-scale cases: the narrow kernel at M = 16, the mid-M kernel with a 6-way K split
              (synth.Q4_K, 16, 9728, 2560): "k_gemm_q4_k<2, 2>", (synth.Q4_K, 48, 9728, 2560): "k_gemm_q4_k_rb<1, 4, 3, 2>",
              (synth.Q4_K, 350, 9728, 512): "k_gemm_q4_k_wr160"}
