@@ -538,6 +538,88 @@ DEV void decode16_q8_0(const u4v q, h2 d2, h8 &lo, h8 &hi) {
     hi = h8{v[4].x, v[4].y, v[5].x, v[5].y, v[6].x, v[6].y, v[7].x, v[7].y};
 }
 
+// Consumers of the LDS-decode kernels whose B tile holds the weights themselves (Q8_0 and the
+// k-quants of k_gemm_kq_ws: no min term, no rescale): the k-step stream of k_gemm_q4_k_ws without
+// its min k-step, 4 main k-steps per 128-K stage, each reading the next k-step's operands while its
+// MFMAs run, the stage barrier inside a stage's last k-step. S2 stages; prefetch(s) warms L2 with the
+// weights of stages s and s + 1 (issued every second stage, four stages ahead). Ends with the fp32
+// tile in LDS and a barrier, for tile_finish.
+template <int NB, class L, class Pf>
+DEV void ws_plain_consumers(char *lds, int wave, int lane, int S2, Pf &prefetch) {
+    constexpr int BN = 32 * NB;
+    _Float16 *const sA0 = (_Float16 *)(lds + L::A);
+    _Float16 *const sB0 = (_Float16 *)(lds + L::B);
+    const int wm = wave & 1, wn = wave >> 1, ln = lane & 15, lg = lane >> 4;
+    const uint32_t sw0 = 16u * ((uint32_t)lg ^ (uint32_t)ln);
+    const uint32_t a_lane = (uint32_t)(uintptr_t)sA0 + (uint32_t)((64 * wm + ln) * WS_KS * 2) + sw0;
+    const uint32_t b_lane = (uint32_t)(uintptr_t)sB0 + (uint32_t)(((BN / 2) * wn + ln) * WS_KS * 2) + sw0;
+    using lds_h8 = const __attribute__((address_space(3))) h8;
+    auto lds_at = [](uint32_t byte) { return *(lds_h8 *)(uintptr_t)byte; };
+    auto ldA = [&](int src, int i, int f) -> h8 {
+        return lds_at((a_lane ^ (64u * f)) + src * L::A_BYTES + i * 16 * WS_KS * 2);
+    };
+    auto ldB = [&](int src, int j, int f) -> h8 {
+        return lds_at((b_lane ^ (64u * f)) + src * L::B_BYTES + j * 16 * WS_KS * 2);
+    };
+    f4 acc[4][NB];
+    h8 fa[2][4], fb[NB];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < NB; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+    constexpr int JB = NB >= 3 ? 2 : 1;
+    auto kstep = [&](auto cfg) {
+        using C = decltype(cfg);
+        constexpr int P = C::P;
+        auto read_next_a = [&]() {
+#pragma unroll
+            for (int i = 0; i < 4; i++) fa[P ^ 1][i] = ldA(C::NSRC, i, C::NF);
+        };
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            if (!C::BAR && j == 0) read_next_a();
+            if (C::BAR && j == JB) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                wg_barrier();
+                read_next_a();
+#pragma unroll
+                for (int jj = 0; jj < JB; jj++) fb[jj] = ldB(C::NSRC, jj, C::NF);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i][j] = mfma(fb[j], fa[P][i], acc[i][j]);
+            if (!(C::BAR && j < JB)) fb[j] = ldB(C::NSRC, j, C::NF);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    wg_barrier();  // stage 0 is in LDS
+#pragma unroll
+    for (int i = 0; i < 4; i++) fa[0][i] = ldA(0, i, 0);
+#pragma unroll
+    for (int j = 0; j < NB; j++) fb[j] = ldB(0, j, 0);
+    int t = 0;
+    for (; t + 2 <= S2; t += 2) {
+        if (t + 5 < S2) prefetch(t + 4);
+        kstep(WsStep<0, 0, 0, false, 0, 1>{});
+        kstep(WsStep<1, 0, 1, false, 0, 2>{});
+        kstep(WsStep<0, 0, 2, false, 0, 3>{});
+        kstep(WsStep<1, 0, 3, true, 1, 0>{});
+        kstep(WsStep<0, 1, 0, false, 1, 1>{});
+        kstep(WsStep<1, 1, 1, false, 1, 2>{});
+        kstep(WsStep<0, 1, 2, false, 1, 3>{});
+        kstep(WsStep<1, 1, 3, true, 0, 0>{});
+    }
+    if (t < S2) {  // odd stage count: the last stage sits in buffer 0
+        kstep(WsStep<0, 0, 0, false, 0, 1>{});
+        kstep(WsStep<1, 0, 1, false, 0, 2>{});
+        kstep(WsStep<0, 0, 2, false, 0, 3>{});
+        kstep(WsStep<1, 0, 3, true, 1, 0>{});
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the prefetches
+    ws_tile_to_lds<NB>(lds, acc, wm, wn, ln, lg);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    wg_barrier();
+}
+
 template <int NB>
 __global__ void __launch_bounds__(WS_NT) k_gemm_q8_0_ws(Ws8Args g) {
     constexpr int BN = 32 * NB;
@@ -649,57 +731,8 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q8_0_ws(Ws8Args g) {
     }
 
     // ---------------------------------------------------------------------- consumers
-    // k-step stream as in k_gemm_q4_k_ws: 4 main k-steps per stage, each reading the next k-step's
-    // operands while its MFMAs run; the stage barrier inside a stage's last k-step.
-    const int wm = wave & 1, wn = wave >> 1, ln = lane & 15, lg = lane >> 4;
-    const uint32_t sw0 = 16u * ((uint32_t)lg ^ (uint32_t)ln);
-    const uint32_t a_lane = (uint32_t)(uintptr_t)sA(0) + (uint32_t)((64 * wm + ln) * WS_KS * 2) + sw0;
-    const uint32_t b_lane = (uint32_t)(uintptr_t)sB(0) + (uint32_t)(((BN / 2) * wn + ln) * WS_KS * 2) + sw0;
-    using lds_h8 = const __attribute__((address_space(3))) h8;
-    auto lds_at = [](uint32_t byte) { return *(lds_h8 *)(uintptr_t)byte; };
-    auto ldA = [&](int src, int i, int f) -> h8 {
-        return lds_at((a_lane ^ (64u * f)) + src * L::A_BYTES + i * 16 * WS_KS * 2);
-    };
-    auto ldB = [&](int src, int j, int f) -> h8 {
-        return lds_at((b_lane ^ (64u * f)) + src * L::B_BYTES + j * 16 * WS_KS * 2);
-    };
-    f4 acc[4][NB];
-    h8 fa[2][4], fb[NB];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < NB; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
-    constexpr int JB = NB >= 3 ? 2 : 1;
-    auto kstep = [&](auto cfg) {
-        using C = decltype(cfg);
-        constexpr int P = C::P;
-        auto read_next_a = [&]() {
-#pragma unroll
-            for (int i = 0; i < 4; i++) fa[P ^ 1][i] = ldA(C::NSRC, i, C::NF);
-        };
-#pragma unroll
-        for (int j = 0; j < NB; j++) {
-            if (!C::BAR && j == 0) read_next_a();
-            if (C::BAR && j == JB) {
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                wg_barrier();
-                read_next_a();
-#pragma unroll
-                for (int jj = 0; jj < JB; jj++) fb[jj] = ldB(C::NSRC, jj, C::NF);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc[i][j] = mfma(fb[j], fa[P][i], acc[i][j]);
-            if (!(C::BAR && j < JB)) fb[j] = ldB(C::NSRC, j, C::NF);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-    wg_barrier();  // stage 0 is in LDS
-#pragma unroll
-    for (int i = 0; i < 4; i++) fa[0][i] = ldA(0, i, 0);
-#pragma unroll
-    for (int j = 0; j < NB; j++) fb[j] = ldB(0, j, 0);
-    // L2 warm-up of the quants of stages t + 4, t + 5 at stage t (one 128-byte line per column and
-    // stage; the mt workgroups of an N-tile split the columns), as in k_gemm_q4_k_ws
+    // L2 warm-up of the quants of stages s, s + 1 (one 128-byte line per column and stage; the mt
+    // workgroups of an N-tile split the columns), as in k_gemm_q4_k_ws
     const int pf_cols = (BN - mt_i + g.mt - 1) / g.mt, pf_lanes = 2 * pf_cols;
     const uint32_t pf_lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds + L::PF) + 256u * (uint32_t)wave);
     auto prefetch = [&](int s) {
@@ -710,29 +743,220 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q8_0_ws(Ws8Args g) {
             l2_touch(rq, voff, pf_lds);
         }
     };
-    int t = 0;
-    for (; t + 2 <= S2; t += 2) {
-        if (t + 5 < S2) prefetch(t + 4);
-        kstep(WsStep<0, 0, 0, false, 0, 1>{});
-        kstep(WsStep<1, 0, 1, false, 0, 2>{});
-        kstep(WsStep<0, 0, 2, false, 0, 3>{});
-        kstep(WsStep<1, 0, 3, true, 1, 0>{});
-        kstep(WsStep<0, 1, 0, false, 1, 1>{});
-        kstep(WsStep<1, 1, 1, false, 1, 2>{});
-        kstep(WsStep<0, 1, 2, false, 1, 3>{});
-        kstep(WsStep<1, 1, 3, true, 0, 0>{});
-    }
-    if (t < S2) {  // odd stage count: the last stage sits in buffer 0
-        kstep(WsStep<0, 0, 0, false, 0, 1>{});
-        kstep(WsStep<1, 0, 1, false, 0, 2>{});
-        kstep(WsStep<0, 0, 2, false, 0, 3>{});
-        kstep(WsStep<1, 0, 3, true, 1, 0>{});
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the prefetches
-    ws_tile_to_lds<NB>(lds, acc, wm, wn, ln, lg);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    wg_barrier();
+    ws_plain_consumers<NB, L>(lds, wave, lane, S2, prefetch);
     tile_finish<WS_BM, 32 * NB, WS_NT, 4>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::PF));
+}
+
+// ---------------------------------------------------------------------------------------------
+// Q6_K and Q3_K tile kernel: the Q8_0 kernel's decomposition, roles and consumers, with producers
+// that decode the k-quant super-blocks (device slots of hq_kquant.h / hq_q6k.hip). A 128-K stage is
+// half h of a super-block; producer thread (column c = pt / 8 + 32 i, xi = pt % 8) takes the values
+// 32 j + 8 lq .. + 7 of the stage for j = jp and jp + 2 (jp = xi / 4, lq = xi % 4): for both types
+// these share the thread's quant bytes (Q6_K: low and high nibbles of the same ql bytes; Q3_K: bit
+// pairs of the same qs bytes), and each 8 of them share one scale. B = fp16((q) * fp16(d * s)): q
+// exact, d * s exact in fp32 and rounded to fp16, then one rounding of the product (two roundings of
+// the exact weight, each at most 2^-11 relative; the fp16 range bounds |w| < 65504 as for Q8_0).
+//   Q6_K (:151-169)  q = (ql nibble | 2 bits of qh << 4) - 32, s = int8 scales[8h + 2j + l/16]
+//   Q3_K (:112-134)  q = (2 bits of qs | hmask bit 4h + j << 2) - 4, s = 6-bit code 8h + 2j + l/16 - 32
+struct KqwsArgs {
+    const uint8_t *W;  // device slots, row n at n * row_bytes
+    uint32_t row_bytes;
+    const uint16_t *A;
+    int M, N, K;
+    void *C;
+    int c_f32, accumulate;
+    int mt, nt;
+    int parts;  // K split as in WsArgs (ranges of whole super-blocks)
+    float *partials;
+    int *counters;
+    int ntiles;
+};
+
+// one producer thread's loaded bytes of one column and stage
+struct KqwsRaw {
+    u2v q0, q1;  // Q6_K: ql, qh; Q3_K: qs, hmask (8 bytes each, the thread's l range)
+    u4v sc;      // Q6_K: scales 8h .. 8h + 7, d; Q3_K: the 12 scale bytes and d
+};
+
+template <int T>
+struct KqwsSrc {
+    static_assert(T == HQ_TYPE_Q6_K || T == HQ_TYPE_Q3_K, "k-quant tile kernel types");
+    static constexpr int SLOT = T == HQ_TYPE_Q6_K ? 224 : 112;
+    static constexpr int NLD = T == HQ_TYPE_Q6_K ? 4 : 3;  // loads per column and stage
+    // vo = the column's row offset; so = the super-block's offset in the part's slots; h = half
+    DEV void load(rsrc_t r, uint32_t vo, uint32_t so, int h, int jp, int lq, KqwsRaw &x) {
+        if constexpr (T == HQ_TYPE_Q6_K) {
+            x.q0 = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(r, vo + 32u * jp + 8u * lq, so + 64u * h, 0));
+            x.q1 = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(r, vo + 128u + 8u * lq, so + 32u * h, 0));
+            const u2v sc = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(r, vo + 192u, so + 8u * h, 0));
+            x.sc = u4v{sc.x, sc.y, (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, vo + 208u, so, 0), 0u};
+        } else {
+            x.q0 = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(r, vo + 32u + 8u * lq, so + 32u * h, 0));
+            x.q1 = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(r, vo + 8u * lq, so, 0));
+            x.sc = buf_load16(r, vo + 96u, so);
+        }
+    }
+    // the 8 fp16 B values of j = jp + 2 t
+    DEV h8 decode(const KqwsRaw &x, int h, int jp, int lq, int t) {
+        const int j = jp + 2 * t;
+        uint32_t u[2];
+        float d;
+        int s;
+        _Float16 bias;
+        if constexpr (T == HQ_TYPE_Q6_K) {
+#pragma unroll
+            for (int w = 0; w < 2; w++) u[w] = ((x.q0[w] >> (4 * t)) & 0x0f0f0f0fu) | (((x.q1[w] >> (2 * j)) & 0x03030303u) << 4);
+            const int e = 2 * j + (lq >> 1);  // scale byte of the half's 8
+            s = (int)(int8_t)byte_of(e < 4 ? x.sc.x : x.sc.y, e & 3);
+            d = h2f((uint16_t)x.sc.z);
+            bias = (_Float16)1056.0f;  // 1024 + 32
+        } else {
+#pragma unroll
+            for (int w = 0; w < 2; w++) u[w] = ((x.q0[w] >> (2 * j)) & 0x03030303u) | (((x.q1[w] >> (4 * h + j)) & 0x01010101u) << 2);
+            const int e = 8 * h + 2 * j + (lq >> 1), g = e >> 2, i = e & 3;  // the 6-bit code, as q3k_code
+            s = (int)(((byte_of(g & 1 ? x.sc.y : x.sc.x, i) >> (4 * (g >> 1))) & 15u) | (((byte_of(x.sc.z, i) >> (2 * g)) & 3u) << 4)) - 32;
+            d = h2f((uint16_t)x.sc.w);
+            bias = (_Float16)1028.0f;  // 1024 + 4
+        }
+        const _Float16 ds = (_Float16)(d * (float)s);
+        const h2 kb = {bias, bias}, m2 = {ds, ds};
+        h2 v[4];
+#pragma unroll
+        for (int w = 0; w < 2; w++) {
+            v[2 * w] = (as_h2(perm_lo(u[w])) - kb) * m2;
+            v[2 * w + 1] = (as_h2(perm_hi(u[w])) - kb) * m2;
+        }
+        return h8{v[0].x, v[0].y, v[1].x, v[1].y, v[2].x, v[2].y, v[3].x, v[3].y};
+    }
+};
+
+template <int T, int NB>
+__global__ void __launch_bounds__(WS_NT) k_gemm_kq_ws(KqwsArgs g) {
+    using Src = KqwsSrc<T>;
+    constexpr int BN = 32 * NB, SLOT = Src::SLOT, NLD = Src::NLD;
+    using L = Ws8Lds<NB>;
+    __shared__ __attribute__((aligned(256))) char lds[L::TOTAL];
+    _Float16 *const sA0 = (_Float16 *)(lds + L::A);
+    _Float16 *const sB0 = (_Float16 *)(lds + L::B);
+    auto sA = [&](int h) { return sA0 + h * (L::A_BYTES / 2); };
+    auto sB = [&](int h) { return sB0 + h * (L::B_BYTES / 2); };
+    const int b = blockIdx.x, x = b & 7, j8 = b >> 3, per = g.mt * g.parts;
+    const int nt_i = x + 8 * (j8 / per), part = (j8 % per) / g.mt, mt_i = j8 % g.mt;
+    if (nt_i >= g.nt) return;
+    const int m0 = mt_i * WS_BM, n0 = nt_i * BN;
+    // this part's super-blocks u0 .. u0 + U - 1 (stages 2 u0 .. ); operand bases moved to u0
+    const int M = g.M, N = g.N, K = g.K, UT = K / 256;
+    const int u0 = part * UT / g.parts, U = (part + 1) * UT / g.parts - u0, S2 = 2 * U;
+    const uint16_t *const Ab = g.A + (size_t)u0 * 256;
+    const uint8_t *const Wb = g.W + (size_t)u0 * SLOT;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const rsrc_t ra = make_rsrc(Ab, (uint32_t)((size_t)M * K * 2 - (size_t)u0 * 512));
+    const rsrc_t rw = make_rsrc(Wb, (uint32_t)((size_t)N * g.row_bytes - (size_t)u0 * SLOT));  // rows >= N read as zero
+
+    if (wave >= 4) {
+        // ------------------------------------------------------------------ producers
+        // as in k_gemm_q8_0_ws: stage s's activation tile and decoded B tile are made in stage s - 1,
+        // the weight loads of stage s + 3 issued then too, one column's after each column's decode
+        const int pw = __builtin_amdgcn_readfirstlane(wave - 4);
+        const int pt = tid - 256, xi = pt & 7, jp = xi >> 2, lq = xi & 3;
+        const int arow = 4 * pw + (lane >> 4);
+        const uint32_t a_voff = (uint32_t)(((m0 + arow) * K + 8 * ((lane & 15) ^ (arow & 15))) * 2);
+        auto dma_a = [&](int s, int qq) {
+            dma16(ra, sA(s & 1) + (pw + 4 * qq) * 512, a_voff + (uint32_t)(qq * 16 * K * 2), (uint32_t)(s * WS_KS * 2));
+        };
+        uint32_t w_voff[NB];
+#pragma unroll
+        for (int i = 0; i < NB; i++) w_voff[i] = (uint32_t)(n0 + (pt >> 3) + 32 * i) * g.row_bytes;
+        // NS register sets, loads AHEAD = NS - 1 stages before their decode (three sets for the wide
+        // tiles: four would not fit the registers)
+        constexpr int NS = NB >= 4 ? 3 : 4, AHEAD = NS - 1;
+        KqwsRaw Q[NS][NB];
+        auto load = [&](int set, int s, int i) {
+            Src::load(rw, w_voff[i], (uint32_t)((s >> 1) * SLOT), s & 1, jp, lq, Q[set][i]);
+        };
+        auto decode = [&](auto setc, int s) {
+            constexpr int SET = decltype(setc)::value;
+            _Float16 *dst = sB(s & 1);
+            const int h = s & 1;
+#pragma unroll
+            for (int i = 0; i < NB; i++) {
+                const uint32_t c = (uint32_t)((pt >> 3) + 32 * i), sg = c & 15u;
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const uint32_t slot = (uint32_t)(4 * (jp + 2 * t) + lq);
+                    *(h8 *)(dst + c * WS_KS + 8 * (slot ^ sg)) = Src::decode(Q[SET][i], h, jp, lq, t);
+                }
+                if (s + AHEAD < S2) load((SET + AHEAD) % NS, s + AHEAD, i);
+            }
+        };
+        auto end_stage = [&](bool loads_issued) {
+            if (loads_issued) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(NLD * NB) : "memory");
+            else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+            wg_barrier();
+        };
+        using i0 = std::integral_constant<int, 0>;
+        using i1 = std::integral_constant<int, 1>;
+        using i2 = std::integral_constant<int, 2>;
+        using i3 = std::integral_constant<int, 3>;
+#pragma unroll
+        for (int k = 0; k < AHEAD; k++)
+#pragma unroll
+            for (int i = 0; i < NB; i++) load(k, S2 > k ? k : 0, i);
+#pragma unroll
+        for (int k = 0; k < 8; k++) dma_a(0, k);
+        decode(i0{}, 0);
+        end_stage(AHEAD < S2);
+        // stage t (consumers on stage t): make stage t + 1 from register set (t + 1) % NS
+        auto step = [&](auto setc, int t) {
+            const int s = t + 1;
+            if (s < S2) {
+#pragma unroll
+                for (int k = 0; k < 8; k++) dma_a(s, k);
+                decode(setc, s);
+            }
+            end_stage(s + AHEAD < S2);
+        };
+        int t = 0;
+        if constexpr (NS == 4) {
+            for (; t + 4 <= S2; t += 4) {
+                step(i1{}, t);
+                step(i2{}, t + 1);
+                step(i3{}, t + 2);
+                step(i0{}, t + 3);
+            }
+            if (t < S2) step(i1{}, t++);
+            if (t < S2) step(i2{}, t++);
+            if (t < S2) step(i3{}, t++);
+        } else {
+            for (; t + 3 <= S2; t += 3) {
+                step(i1{}, t);
+                step(i2{}, t + 1);
+                step(i0{}, t + 2);
+            }
+            if (t < S2) step(i1{}, t++);
+            if (t < S2) step(i2{}, t++);
+        }
+        wg_barrier();  // the consumers' output tile is in LDS
+        tile_finish<WS_BM, BN, WS_NT, 4>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::PF));
+        return;
+    }
+
+    // ---------------------------------------------------------------------- consumers
+    // L2 warm-up of super-block s / 2 of the tile's columns (bytes 0, SLOT / 2, SLOT - 1 of each
+    // column's slot; the mt workgroups of an N-tile split the columns)
+    const int pf_cols = (BN - mt_i + g.mt - 1) / g.mt, pf_lanes = 3 * pf_cols;
+    const uint32_t pf_lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds + L::PF) + 256u * (uint32_t)wave);
+    auto prefetch = [&](int s) {
+        for (int e0 = 64 * wave; e0 < pf_lanes; e0 += 256) {
+            const int e = e0 + lane, jc = e / 3, k = e - 3 * jc;
+            const int c = mt_i + g.mt * (e < pf_lanes ? jc : 0);
+            const uint32_t voff = (uint32_t)(n0 + c) * g.row_bytes + (uint32_t)(s >> 1) * SLOT +
+                                  (k == 0 ? 0u : k == 1 ? (uint32_t)SLOT / 2 : (uint32_t)SLOT - 1);
+            l2_touch(rw, voff, pf_lds);
+        }
+    };
+    ws_plain_consumers<NB, L>(lds, wave, lane, S2, prefetch);
+    tile_finish<WS_BM, BN, WS_NT, 4>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::PF));
 }
 }  // namespace
 
@@ -799,4 +1023,41 @@ hipError_t hq_launch_gemm_ws8(const hq_dev_mat *W, const uint16_t *A, int M, voi
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+hipError_t hq_launch_gemm_kqws(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
+                               int nb, int parts, float *partials, int *counters, hipStream_t st) {
+    if ((W->type != HQ_TYPE_Q6_K && W->type != HQ_TYPE_Q3_K) || W->cols % 256 || !hq_kqws_fits(W, M))
+        return hipErrorInvalidValue;
+    KqwsArgs g;
+    g.W = W->qs, g.row_bytes = (uint32_t)W->row_bytes, g.A = A;
+    g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;
+    g.mt = (M + WS_BM - 1) / WS_BM;
+    g.nt = (g.N + 32 * nb - 1) / (32 * nb);
+    g.parts = parts, g.partials = partials, g.counters = counters, g.ntiles = g.mt * g.nt;
+    if (parts < 1 || parts > 4 || parts > g.K / 256 || (parts > 1 && (!partials || !counters))) return hipErrorInvalidValue;
+    if (parts > 1 && (size_t)g.mt * g.nt * parts * WS_BM * 32 * nb * 4 >= ((size_t)1 << 32)) return hipErrorInvalidValue;
+    const unsigned grid = (unsigned)(8 * ((g.nt + 7) / 8) * g.mt * parts);
+#define KQWS(t)                                                                          \
+    switch (nb) {                                                                        \
+    case 2: k_gemm_kq_ws<t, 2><<<grid, WS_NT, 0, st>>>(g); break;                        \
+    case 3: k_gemm_kq_ws<t, 3><<<grid, WS_NT, 0, st>>>(g); break;                        \
+    case 4: k_gemm_kq_ws<t, 4><<<grid, WS_NT, 0, st>>>(g); break;                        \
+    case 5: k_gemm_kq_ws<t, 5><<<grid, WS_NT, 0, st>>>(g); break;                        \
+    default: return hipErrorInvalidValue;                                                \
+    }
+    if (W->type == HQ_TYPE_Q6_K) {
+        KQWS(HQ_TYPE_Q6_K)
+    } else {
+        KQWS(HQ_TYPE_Q3_K)
+    }
+#undef KQWS
+    return hipGetLastError();
+}
+
+// every byte offset of k_gemm_kq_ws fits 32 bits (tile rows and columns past the matrix included)
+int hq_kqws_fits(const hq_dev_mat *W, int M) {
+    const size_t lim = (size_t)1 << 32;
+    return (W->type == HQ_TYPE_Q6_K || W->type == HQ_TYPE_Q3_K) && W->cols % 256 == 0 && M >= 1 &&
+           ((size_t)M + WS_BM) * W->cols * 2 < lim && ((size_t)W->rows + 160) * W->row_bytes < lim;
 }

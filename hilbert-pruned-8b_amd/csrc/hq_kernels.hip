@@ -1333,8 +1333,10 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
     // the narrow kernel), K is whole 128-wide stages and the byte offsets fit 32 bits
     c.ws8_nb = 0;
     c.ws8_parts = 1;
-    if (W->type == HQ_TYPE_Q8_0 && M > 64 && W->cols % 128 == 0 && (size_t)M * W->cols * 2 < ((size_t)1 << 32) &&
-        ((size_t)W->rows + 160) * W->cols < ((size_t)1 << 32)) {
+    // (Q6_K and Q3_K: the same tile kernel with k-quant producers, k_gemm_kq_ws, on the same rule)
+    const bool kqws = (W->type == HQ_TYPE_Q6_K || W->type == HQ_TYPE_Q3_K) && M > 64 && hq_kqws_fits(W, M);
+    if (kqws || (W->type == HQ_TYPE_Q8_0 && M > 64 && W->cols % 128 == 0 && (size_t)M * W->cols * 2 < ((size_t)1 << 32) &&
+                 ((size_t)W->rows + 160) * W->cols < ((size_t)1 << 32))) {
         float eff = 0.f;
         const int nb = hq_ws_choose(M, (int)W->rows, n_cu, &eff);
         const long tiles = (long)((M + 127) / 128) * (((int)W->rows + 32 * nb - 1) / (32 * nb));
@@ -1365,11 +1367,18 @@ SkPlan gemm_plan(const hq_dev_mat *W, int M, const GemmCfg &c, int n_cu) {
 }
 }  // namespace
 
+// device bytes of a row of K values (the upload's layout: Q8_0 quant plane, k-quant slots)
+static size_t shape_row_bytes(int type, int K) {
+    return type == HQ_TYPE_Q4_K ? (size_t)K / 256 * 144 : type == HQ_TYPE_Q8_0 ? (size_t)K
+         : (size_t)K / 256 * (type == HQ_TYPE_Q6_K ? 224 : type == HQ_TYPE_Q5_K ? 176 : type == HQ_TYPE_Q3_K ? 112 : 96);
+}
+
 void hq_gemm_tile_shape(int type, int M, int N, int K, int n_cu, int *rows, int *cols) {
     hq_dev_mat W = {};
     W.type = type;
     W.rows = (uint32_t)N;
     W.cols = (uint32_t)K;
+    W.row_bytes = shape_row_bytes(type, K);
     W.ldd = type == HQ_TYPE_Q8_0 ? (K / 32 + 7) / 8 * 8 : 0;
     const GemmCfg c = gemm_cfg(&W, M, n_cu);
     *rows = c.bt ? 256 : c.wr || c.wr8 ? 128 : c.rbm ? 64 : c.rb8 ? (M <= 16 ? 16 : M <= 32 ? 32 : 64) : c.ws_nb || c.ws8_nb ? 128 : 16 * c.mb;
@@ -1384,11 +1393,16 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
     W.rows = (uint32_t)N;
     W.cols = (uint32_t)K;
     W.ldd = type == HQ_TYPE_Q8_0 ? (K / 32 + 7) / 8 * 8 : 0;
-    W.row_bytes = type == HQ_TYPE_Q4_K ? (size_t)K / 256 * 144 : type == HQ_TYPE_Q6_K ? (size_t)K / 256 * 224 : (size_t)K;
+    W.row_bytes = shape_row_bytes(type, K);
     const char *kq = type == HQ_TYPE_Q2_K ? "10" : type == HQ_TYPE_Q3_K ? "11" : type == HQ_TYPE_Q5_K ? "13" : nullptr;
     if (M == 1 && (kq || type == HQ_TYPE_Q6_K)) {  // template arguments: the ggml type, rows per wave
         const int nsb = K / 256, r = nsb % 8 == 0 ? 1 : nsb % 4 == 0 ? 2 : nsb % 2 == 0 ? 4 : 8;
         snprintf(buf, n, "k_gemv_sb<%d, %d, false>", type, r);
+        return;
+    }
+    const GemmCfg c = gemm_cfg(&W, M, n_cu);
+    if (c.ws8_nb && type != HQ_TYPE_Q8_0) {  // template arguments: the ggml type, the tile width / 32
+        snprintf(buf, n, "k_gemm_kq_ws<%d, %d>", type, c.ws8_nb);
         return;
     }
     if (kq) {  // template argument: the ggml type
@@ -1403,7 +1417,6 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
         else snprintf(buf, n, "%s<%d>", type == HQ_TYPE_Q4_K ? "k_gemv_q4_k" : "k_gemv_q8_0", pl.r);
         return;
     }
-    const GemmCfg c = gemm_cfg(&W, M, n_cu);
     if (c.rbm) snprintf(buf, n, "k_gemm_q4_k_rb<1, 4, 3, 2>");
     else if (c.rb8) snprintf(buf, n, "k_gemm_q8_0_rb<%d, 3, 2>", M <= 16 ? 1 : M <= 32 ? 2 : 4);
     else if (c.bt) snprintf(buf, n, "k_gemm_q4_k_bt");
@@ -1478,6 +1491,8 @@ hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, vo
     }
     if (c.ws_nb)
         return hq_launch_gemm_ws(W, A, wk.sums, M, C, c_f32, accumulate, c.ws_nb, c.ws_parts, wk.partials, wk.counters, st);
+    if (c.ws8_nb && W->type != HQ_TYPE_Q8_0)
+        return hq_launch_gemm_kqws(W, A, M, C, c_f32, accumulate, c.ws8_nb, c.ws8_parts, wk.partials, wk.counters, st);
     if (c.ws8_nb)
         return hq_launch_gemm_ws8(W, A, M, C, c_f32, accumulate, c.ws8_nb, c.ws8_parts, wk.partials, wk.counters, st);
     GemmArgs g;
@@ -1543,6 +1558,10 @@ hipError_t hq_launch_gemm_swiglu(const hq_dev_mat *W, const uint16_t *A, int M, 
     if (W->type == HQ_TYPE_Q8_0 && K % 128 == 0 && ((size_t)N + 160) * K < ((size_t)1 << 32)) {
         *fused = 1;
         return hq_launch_gemm_ws8(W, A, M, out, HQ_OUT_SWIGLU, 0, nb, 1, nullptr, nullptr, st);
+    }
+    if ((W->type == HQ_TYPE_Q6_K || W->type == HQ_TYPE_Q3_K) && hq_kqws_fits(W, M)) {
+        *fused = 1;
+        return hq_launch_gemm_kqws(W, A, M, out, HQ_OUT_SWIGLU, 0, nb, 1, nullptr, nullptr, st);
     }
     return hipSuccess;
 }

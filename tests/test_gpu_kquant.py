@@ -48,7 +48,8 @@ def test_upload_round_trip_and_dequant(hqlib, oracle, gtype):
 
 # GEMV, the Stream-K GEMM at each row-block count, ragged M / N, long K
 CASES = [(9728, 2560, M) for M in (1, 2, 16, 33, 64, 512)] + \
-        [(100, 512, M) for M in (1, 5, 17, 65)] + [(2560, 9728, 1), (2560, 9728, 64), (1000, 256, 3)]
+        [(100, 512, M) for M in (1, 5, 17, 65)] + [(2560, 9728, 1), (2560, 9728, 64), (1000, 256, 3)] + \
+        [(2560, 9728, 512), (9728, 2560, 300)]  # the Q3_K tile kernel: K split in 4, ragged M
 
 
 @pytest.mark.parametrize("gtype", TYPES)
@@ -95,6 +96,39 @@ def test_gemm_special_scales(hqlib, oracle, gtype):
         assert rel_l2(got, ref) <= 1e-3 and max_abs(got, ref) <= 1e-2
         assert np.all(np.abs(got - x @ wf.T) <= 2.0 ** -13 * (np.abs(x) @ np.abs(wf.T)) + 1e-30)
     W.free()
+
+
+@pytest.mark.parametrize("gtype", [synth.Q3_K, synth.Q6_K])
+def test_tile_kernel_special_scales(hqlib, oracle, gtype):
+    """The LDS-decode tile kernel (M > 64; B = fp16(q * fp16(d * s)), two roundings of at most 2^-11
+    each) on the finite special blocks: rel-L2 at the bar, and within 2^-10 |W| @ |a| of the float64
+    product plus 2^-24 sum |a| (fp16 subnormal spacing of d * s and of the weights). (d = 1 with scales
+    of -128 / 127 gives outputs of ~2e5, where fp32 sums alone differ by more than the absolute 1e-2 of
+    the bar; the float64 bound is the element-wise check here.)"""
+    from test_oracle import SPECIAL_BLOCKS
+    sp = SPECIAL_BLOCKS[gtype]().reshape(8, -1)
+    fin = []
+    for i in range(8):
+        w = oracle.dequantize(np.ascontiguousarray(sp[i:i + 1]), gtype, 1, 256)
+        if np.all(np.isfinite(w)) and np.abs(w).max() < 1e4:
+            fin.append(i)
+    N, K, M = 5120, 10 * 256, 512
+    rows = np.stack([np.concatenate([sp[fin[(r + c) % len(fin)]] for c in range(10)]) for r in range(N)])
+    W = hqlib.Mat(np.ascontiguousarray(rows), gtype, N, K)
+    name = hqlib.gemm_kernel(gtype, M, N, K)
+    say(f"{synth.TYPE_NAMES[gtype]} special tile M={M} kernel={name}")
+    assert name.startswith("k_gemm_kq_ws<")
+    a = synth.activations_f16(synth.Rng(79), M, K)
+    got = hqlib.gemm_np(W, a)
+    W.free()
+    wf = oracle.dequantize(np.ascontiguousarray(rows), gtype, N, K).astype(np.float64)
+    x = oracle.f16_to_f32(a).astype(np.float64)
+    ref = oracle.matmul(np.ascontiguousarray(rows), gtype, N, K, oracle.f16_to_f32(a))
+    r, m = rel_l2(got, ref), max_abs(got, ref)
+    say(f"rel_l2 {r:.2e} max_abs {m:.2e} max|ref| {np.abs(ref).max():.2f}")
+    assert r <= 1e-3
+    bound = 2.0 ** -10 * (np.abs(x) @ np.abs(wf.T)) + 2.0 ** -24 * np.abs(x).sum(axis=1, keepdims=True)
+    assert np.all(np.abs(got - x @ wf.T) <= bound)
 
 
 @pytest.mark.parametrize("gtype", TYPES)
