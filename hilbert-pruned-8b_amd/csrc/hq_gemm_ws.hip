@@ -129,8 +129,15 @@ struct WsStep {
     static constexpr bool BAR = BAR_;
 };
 
-template <int NB>
-__global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
+// The tile body of k_gemm_q4_k_ws (T = Q4_K) and k_gemm_q5_k_ws (T = Q5_K: the same header, scale / min
+// packing and sub-blocks, 176-byte super-blocks with the quants at byte 48 and a fifth bit per value in
+// qh[32] at byte 16; its B operand s * q, q <= 31, s <= 63, is still an exact fp16 integer <= 1953).
+template <int T, int NB>
+DEV void ws_q4_tile(const WsArgs &g) {
+    static_assert(T == HQ_TYPE_Q4_K || T == HQ_TYPE_Q5_K, "ws_q4_tile types");
+    constexpr int SLOT = T == HQ_TYPE_Q5_K ? 176 : 144, QS = T == HQ_TYPE_Q5_K ? 48 : 16;
+    constexpr int QL = T == HQ_TYPE_Q5_K ? 2 : 1;  // quant loads per column and stage
+    using QR = std::conditional_t<T == HQ_TYPE_Q5_K, u4v, u2v>;  // Q5_K: qs bytes in .xy, qh bytes in .zw
     constexpr int BN = 32 * NB;
     using L = WsLds<NB>;
     __shared__ __attribute__((aligned(256))) char lds[L::TOTAL];  // fragment addresses XOR bits 6-7
@@ -154,11 +161,11 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
     // strides stay K, UT), so the body below indexes super-blocks from 0
     const int M = g.M, N = g.N, K = g.K, UT = K / 256;
     const int u0 = part * UT / g.parts, U = (part + 1) * UT / g.parts - u0;
-    const uint8_t *const Wb = g.W + (size_t)u0 * 144;
+    const uint8_t *const Wb = g.W + (size_t)u0 * SLOT;
     const uint16_t *const Ab = g.A + (size_t)u0 * 256, *const Sb = g.S + (size_t)u0 * 16;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const rsrc_t ra = make_rsrc(Ab, (uint32_t)((size_t)M * K * 2 - (size_t)u0 * 512));
-    const rsrc_t rw = make_rsrc(Wb, (uint32_t)((size_t)N * g.row_bytes - (size_t)u0 * 144));
+    const rsrc_t rw = make_rsrc(Wb, (uint32_t)((size_t)N * g.row_bytes - (size_t)u0 * SLOT));
 
     if (wave >= 4) {
         // ------------------------------------------------------------------ producers
@@ -182,21 +189,32 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
         const uint32_t s_voff = (uint32_t)(((m0 + 32 * pw + (lane >> 1)) * UT) * 32 + 16 * (lane & 1));
         auto dma_s = [&](int u) { dma16(rs, sS + pw * 512, s_voff, (uint32_t)(u * 32)); };
         // quant bytes: this thread's columns c_i = pt/8 + 32i (i < NB), half-chunk xi of each stage
-        // (bytes 16 + 8(8(s % 2) + xi) of super-block s/2). Four register sets: stage s's go to
-        // Q[s % 4], three stages before its decode.
-        uint32_t w_voff[NB];
+        // (bytes QS + 8(8(s % 2) + xi) of super-block s/2; Q5_K also qh bytes 8(xi % 4) .. + 7, the
+        // fifth bits of the same values). Four register sets: stage s's go to Q[s % 4], three stages
+        // before its decode.
+        uint32_t w_voff[NB], h_voff[NB];
 #pragma unroll
-        for (int i = 0; i < NB; i++) w_voff[i] = (uint32_t)(n0 + (pt >> 3) + 32 * i) * g.row_bytes + 16u + 8u * (uint32_t)xi;
-        u2v Q[4][NB];
-        auto load_q = [&](u2v (&q)[NB], int s, int i) {
-            q[i] = buf_load8(rw, w_voff[i], (uint32_t)((s >> 1) * 144 + 64 * (s & 1)));
+        for (int i = 0; i < NB; i++) {
+            const uint32_t row = (uint32_t)(n0 + (pt >> 3) + 32 * i) * g.row_bytes;
+            w_voff[i] = row + (uint32_t)QS + 8u * (uint32_t)xi;
+            h_voff[i] = row + 16u + 8u * (uint32_t)(xi & 3);
+        }
+        QR Q[4][NB];
+        auto load_q = [&](QR (&q)[NB], int s, int i) {
+            const u2v w = buf_load8(rw, w_voff[i], (uint32_t)((s >> 1) * SLOT + 64 * (s & 1)));
+            if constexpr (QL == 2) {
+                const u2v h = buf_load8(rw, h_voff[i], (uint32_t)((s >> 1) * SLOT));
+                q[i] = u4v{w.x, w.y, h.x, h.y};
+            } else {
+                q[i] = w;
+            }
         };
         // super-block headers, one column per thread (pt < BN; the other threads load column 0's
         // and drop it, so that every wave issues the same loads): H[u % 2] holds unit u's
         const bool colt = pt < BN;
         const uint32_t m_voff = (uint32_t)(n0 + (colt ? pt : 0)) * g.row_bytes;
         u4v H[2];
-        auto load_hdr = [&](u4v &h, int u) { h = buf_load16(rw, m_voff, (uint32_t)(u * 144)); };
+        auto load_hdr = [&](u4v &h, int u) { h = buf_load16(rw, m_voff, (uint32_t)(u * SLOT)); };
         // a unit's scale words for the decode (sub-blocks 0-3 / 4-7; zero where d = 0, so that B = 0
         // there) -> sH[u % 2][pt]
         auto write_scales = [&](const u4v hm, int buf) {
@@ -236,7 +254,7 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
         // NB quant loads (into qd; s_* / u_* < 0: item absent); item k is issued before column
         // k * NB / (10 + NB) of the decode. Whatever is issued after the DMAs may still be in flight
         // at the end of the stage: a load has until the end of the next stage.
-        auto issue = [&](int i, int s_dma, int u_s, int u_h, u4v &hd, int s_q, u2v (&qd)[NB]) {
+        auto issue = [&](int i, int s_dma, int u_s, int u_h, u4v &hd, int s_q, QR (&qd)[NB]) {
 #pragma unroll
             for (int k = 0; k < 10 + NB; k++) {
                 if (k * NB / (10 + NB) != i) continue;
@@ -258,12 +276,14 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
         const int slot_lo = 8 * (xi >> 2) + (xi & 3);
         const uint32_t ssel = (xi >> 2) ? 0x04030402u : 0x04010400u;  // scale bytes 2(p%2), 2(p%2)+1
         uint32_t Sw1[NB];
-        auto decode = [&](auto hc, auto sbc, const u2v (&q)[NB], int s_dma, int u_s, int u_h, u4v &hd, int s_q,
-                          u2v (&qd)[NB]) {
+        auto decode = [&](auto hc, auto sbc, const QR (&q)[NB], int s_dma, int u_s, int u_h, u4v &hd, int s_q,
+                          QR (&qd)[NB]) {
             constexpr int HS = decltype(hc)::value, SB = decltype(sbc)::value;
             _Float16 *dst = sB(HS);
             const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-            const h2 kmul = {(_Float16)1.0f, (_Float16)0.0625f}, kadd = {(_Float16)-1024.0f, (_Float16)-64.0f};
+            // Q4_K: low nibbles as 1024 + q, high as 1024 + 16q; Q5_K: both as 1024 + q (5 bits)
+            const h2 kmul = {(_Float16)1.0f, (_Float16)(QL == 2 ? 1.0f : 0.0625f)};
+            const h2 kadd = {(_Float16)-1024.0f, (_Float16)(QL == 2 ? -1024.0f : -64.0f)};
             uint32_t Sw0[NB];
             if constexpr (HS == 0) {
 #pragma unroll
@@ -280,8 +300,21 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
                 const uint32_t sw = HS ? Sw1[i] : Sw0[i];
                 const h2 sp = as_h2(__builtin_amdgcn_perm(0x64646464u, sw, ssel)) - k1024;
                 const h2 mu = sp * kmul, ad = sp * kadd;
-                const h8 lo = decode8<false>(q[i], h2{mu.x, mu.x}, h2{ad.x, ad.x});
-                const h8 hi = decode8<true>(q[i], h2{mu.y, mu.y}, h2{ad.y, ad.y});
+                h8 lo, hi;
+                if constexpr (QL == 2) {
+                    // sub-blocks 2p (low nibbles, qh bit 2p) and 2p + 1 (high, bit 2p + 1), p = 2H + xi / 4
+                    const int p = 2 * HS + (xi >> 2);
+                    const u4v w = q[i];
+                    const u2v l5 = {(w.x & 0x0f0f0f0fu) | (((w.z >> (2 * p)) & 0x01010101u) << 4),
+                                    (w.y & 0x0f0f0f0fu) | (((w.w >> (2 * p)) & 0x01010101u) << 4)};
+                    const u2v h5 = {((w.x >> 4) & 0x0f0f0f0fu) | (((w.z >> (2 * p + 1)) & 0x01010101u) << 4),
+                                    ((w.y >> 4) & 0x0f0f0f0fu) | (((w.w >> (2 * p + 1)) & 0x01010101u) << 4)};
+                    lo = decode8m(l5, 0xffffffffu, h2{mu.x, mu.x}, h2{ad.x, ad.x});
+                    hi = decode8m(h5, 0xffffffffu, h2{mu.y, mu.y}, h2{ad.y, ad.y});
+                } else {
+                    lo = decode8<false>(q[i], h2{mu.x, mu.x}, h2{ad.x, ad.x});
+                    hi = decode8<true>(q[i], h2{mu.y, mu.y}, h2{ad.y, ad.y});
+                }
                 *(h8 *)(dst + c * WS_KS + 8 * ((uint32_t)slot_lo ^ sg)) = lo;
                 *(h8 *)(dst + c * WS_KS + 8 * ((uint32_t)(slot_lo + 4) ^ sg)) = hi;
             }
@@ -289,9 +322,9 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
         // end of a stage: this wave's LDS writes done, and every load issued before the last
         // n_in_flight ones (the DMAs among them) landed; then the barrier
         auto end_stage = [&](int n_in_flight) {
-            if (n_in_flight == 2 * NB + 1) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(2 * NB + 1) : "memory");
-            else if (n_in_flight == NB + 1) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(NB + 1) : "memory");
-            else if (n_in_flight == NB) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(NB) : "memory");
+            if (n_in_flight == 2 * QL * NB + 1) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(2 * QL * NB + 1) : "memory");
+            else if (n_in_flight == QL * NB + 1) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(QL * NB + 1) : "memory");
+            else if (n_in_flight == QL * NB) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(QL * NB) : "memory");
             else if (n_in_flight == 1) asm volatile("s_waitcnt vmcnt(1) lgkmcnt(0)" ::: "memory");
             else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
             wg_barrier();
@@ -321,7 +354,7 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
         wg_barrier();  // unit 0's scale words are visible
         // phase 2: decode stage 0; the stage-0 barrier
         decode(i0{}, i0{}, Q[0], -1, -1, -1, H[1], -1, Q[3]);
-        end_stage(2 * NB + 1);  // DMAs of phase 1 landed (Q[1], Q[2], H[0] may be in flight)
+        end_stage(2 * QL * NB + 1);  // DMAs of phase 1 landed (Q[1], Q[2], H[0] may be in flight)
         // Super-block u, in stages 2u (P = u % 2 picks the register sets) and 2u + 1.
         auto unit = [&](auto par, int u) {
             constexpr int P = decltype(par)::value;
@@ -332,7 +365,7 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
             decode(i1{}, std::integral_constant<int, P>{}, Q[(2 * P + 1) & 3], t + 1, -1, -1, H[P], q3 ? t + 3 : -1,
                    Q[(2 * P + 3) & 3]);
             if (nx) write_scales(H[P ^ 1], P ^ 1);
-            end_stage(q3 ? NB : 0);
+            end_stage(q3 ? QL * NB : 0);
             if (!nx) return;  // the last stage has nothing to stage
             // stage 2u + 1: the next unit's min-term operands (its header's last use: the register then
             // takes the header of unit u + 3); decode stage 2u + 2 (next unit, even half); activation
@@ -340,7 +373,7 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
             write_min(H[P ^ 1]);
             decode(i0{}, std::integral_constant<int, P ^ 1>{}, Q[(2 * P + 2) & 3], t + 2, u + 1, h3 ? u + 3 : -1,
                    H[P ^ 1], q4 ? t + 4 : -1, Q[(2 * P) & 3]);
-            end_stage((q4 ? NB : 0) + (h3 ? 1 : 0));
+            end_stage((q4 ? QL * NB : 0) + (h3 ? 1 : 0));
         };
         int u = 0;
         for (; u + 1 < U; u += 2) {
@@ -457,7 +490,8 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
         for (int e0 = 64 * wave; e0 < pf_lanes; e0 += 256) {
             const int e = e0 + lane, jc = e / 3, t = e - 3 * jc;
             const int c = mt_i + g.mt * (e < pf_lanes ? jc : 0);
-            const uint32_t voff = (uint32_t)(n0 + c) * g.row_bytes + 144u * (uint32_t)v + (t == 0 ? 0u : t == 1 ? 72u : 143u);
+            const uint32_t voff = (uint32_t)(n0 + c) * g.row_bytes + (uint32_t)SLOT * (uint32_t)v +
+                                  (t == 0 ? 0u : t == 1 ? (uint32_t)SLOT / 2 : (uint32_t)SLOT - 1);
             l2_touch(rw_pf, voff, pf_lds);
         }
     };
@@ -488,6 +522,15 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     wg_barrier();
     tile_finish<WS_BM, 32 * NB, WS_NT, 4>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::PF));
+}
+
+template <int NB>
+__global__ void __launch_bounds__(WS_NT) k_gemm_q4_k_ws(WsArgs g) {
+    ws_q4_tile<HQ_TYPE_Q4_K, NB>(g);
+}
+template <int NB>
+__global__ void __launch_bounds__(WS_NT) k_gemm_q5_k_ws(WsArgs g) {
+    ws_q4_tile<HQ_TYPE_Q5_K, NB>(g);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -748,16 +791,18 @@ __global__ void __launch_bounds__(WS_NT) k_gemm_q8_0_ws(Ws8Args g) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Q6_K and Q3_K tile kernel: the Q8_0 kernel's decomposition, roles and consumers, with producers
+// Q6_K, Q3_K and Q2_K tile kernel: the Q8_0 kernel's decomposition, roles and consumers, with producers
 // that decode the k-quant super-blocks (device slots of hq_kquant.h / hq_q6k.hip). A 128-K stage is
 // half h of a super-block; producer thread (column c = pt / 8 + 32 i, xi = pt % 8) takes the values
 // 32 j + 8 lq .. + 7 of the stage for j = jp and jp + 2 (jp = xi / 4, lq = xi % 4): for both types
-// these share the thread's quant bytes (Q6_K: low and high nibbles of the same ql bytes; Q3_K: bit
-// pairs of the same qs bytes), and each 8 of them share one scale. B = fp16((q) * fp16(d * s)): q
-// exact, d * s exact in fp32 and rounded to fp16, then one rounding of the product (two roundings of
-// the exact weight, each at most 2^-11 relative; the fp16 range bounds |w| < 65504 as for Q8_0).
+// these share the thread's quant bytes (Q6_K: low and high nibbles of the same ql bytes; Q3_K, Q2_K:
+// bit pairs of the same qs bytes), and each 8 of them share one scale. Q6_K, Q3_K: B =
+// fp16(q * fp16(d * s)): q exact, d * s exact in fp32 and rounded to fp16, then one rounding of the
+// product (two roundings of the exact weight, each at most 2^-11 relative). Q2_K: B = fp16 of the
+// fp32 weight (one rounding). The fp16 range bounds |w| < 65504, as for Q8_0.
 //   Q6_K (:151-169)  q = (ql nibble | 2 bits of qh << 4) - 32, s = int8 scales[8h + 2j + l/16]
 //   Q3_K (:112-134)  q = (2 bits of qs | hmask bit 4h + j << 2) - 4, s = 6-bit code 8h + 2j + l/16 - 32
+//   Q2_K (:100-111)  q = 2 bits of qs, w = d (sm & 15) q - dmin (sm >> 4), sm = scales[8h + 2j + l/16]
 struct KqwsArgs {
     const uint8_t *W;  // device slots, row n at n * row_bytes
     uint32_t row_bytes;
@@ -780,8 +825,8 @@ struct KqwsRaw {
 
 template <int T>
 struct KqwsSrc {
-    static_assert(T == HQ_TYPE_Q6_K || T == HQ_TYPE_Q3_K, "k-quant tile kernel types");
-    static constexpr int SLOT = T == HQ_TYPE_Q6_K ? 224 : 112;
+    static_assert(T == HQ_TYPE_Q6_K || T == HQ_TYPE_Q3_K || T == HQ_TYPE_Q2_K, "k-quant tile kernel types");
+    static constexpr int SLOT = T == HQ_TYPE_Q6_K ? 224 : T == HQ_TYPE_Q3_K ? 112 : 96;
     static constexpr int NLD = T == HQ_TYPE_Q6_K ? 4 : 3;  // loads per column and stage
     // vo = the column's row offset; so = the super-block's offset in the part's slots; h = half
     DEV void load(rsrc_t r, uint32_t vo, uint32_t so, int h, int jp, int lq, KqwsRaw &x) {
@@ -790,43 +835,62 @@ struct KqwsSrc {
             x.q1 = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(r, vo + 128u + 8u * lq, so + 32u * h, 0));
             const u2v sc = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(r, vo + 192u, so + 8u * h, 0));
             x.sc = u4v{sc.x, sc.y, (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, vo + 208u, so, 0), 0u};
-        } else {
+        } else if constexpr (T == HQ_TYPE_Q3_K) {
             x.q0 = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(r, vo + 32u + 8u * lq, so + 32u * h, 0));
             x.q1 = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(r, vo + 8u * lq, so, 0));
             x.sc = buf_load16(r, vo + 96u, so);
+        } else {  // Q2_K: qs, scales 8h .. 8h + 7, {d, dmin}
+            x.q0 = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(r, vo + 16u + 8u * lq, so + 32u * h, 0));
+            x.q1 = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(r, vo, so + 8u * h, 0));
+            x.sc = u4v{__builtin_amdgcn_raw_buffer_load_b32(r, vo + 80u, so, 0), 0u, 0u, 0u};
         }
     }
     // the 8 fp16 B values of j = jp + 2 t
     DEV h8 decode(const KqwsRaw &x, int h, int jp, int lq, int t) {
         const int j = jp + 2 * t;
-        uint32_t u[2];
-        float d;
-        int s;
-        _Float16 bias;
-        if constexpr (T == HQ_TYPE_Q6_K) {
+        if constexpr (T == HQ_TYPE_Q2_K) {
+            // w = (d * (sm & 15)) * q - dmin * (sm >> 4) in fp32 (the products exact, as in the
+            // reference decoder), rounded once to fp16: a packed fp16 form would round both terms of a
+            // difference that can cancel. Scale byte 2 j + (lq >> 1) of the half's 8: word j >> 1.
+            const uint32_t sm = byte_of(j < 2 ? x.q1.x : x.q1.y, 2 * (j & 1) + (lq >> 1));
+            const float ds = h2f((uint16_t)x.sc.x) * (float)(sm & 15u), dm = h2f((uint16_t)(x.sc.x >> 16)) * (float)(sm >> 4);
+            h8 out;
 #pragma unroll
-            for (int w = 0; w < 2; w++) u[w] = ((x.q0[w] >> (4 * t)) & 0x0f0f0f0fu) | (((x.q1[w] >> (2 * j)) & 0x03030303u) << 4);
-            const int e = 2 * j + (lq >> 1);  // scale byte of the half's 8
-            s = (int)(int8_t)byte_of(e < 4 ? x.sc.x : x.sc.y, e & 3);
-            d = h2f((uint16_t)x.sc.z);
-            bias = (_Float16)1056.0f;  // 1024 + 32
+            for (int e = 0; e < 8; e++) {
+                const uint32_t q = ((e < 4 ? x.q0.x : x.q0.y) >> (8 * (e & 3) + 2 * j)) & 3u;
+                out[e] = (_Float16)__builtin_fmaf((float)q, ds, -dm);
+            }
+            return out;
         } else {
+            uint32_t u[2];
+            float d;
+            int s;
+            _Float16 bias;
+            if constexpr (T == HQ_TYPE_Q6_K) {
 #pragma unroll
-            for (int w = 0; w < 2; w++) u[w] = ((x.q0[w] >> (2 * j)) & 0x03030303u) | (((x.q1[w] >> (4 * h + j)) & 0x01010101u) << 2);
-            const int e = 8 * h + 2 * j + (lq >> 1), g = e >> 2, i = e & 3;  // the 6-bit code, as q3k_code
-            s = (int)(((byte_of(g & 1 ? x.sc.y : x.sc.x, i) >> (4 * (g >> 1))) & 15u) | (((byte_of(x.sc.z, i) >> (2 * g)) & 3u) << 4)) - 32;
-            d = h2f((uint16_t)x.sc.w);
-            bias = (_Float16)1028.0f;  // 1024 + 4
-        }
-        const _Float16 ds = (_Float16)(d * (float)s);
-        const h2 kb = {bias, bias}, m2 = {ds, ds};
-        h2 v[4];
+                for (int w = 0; w < 2; w++) u[w] = ((x.q0[w] >> (4 * t)) & 0x0f0f0f0fu) | (((x.q1[w] >> (2 * j)) & 0x03030303u) << 4);
+                const int e = 2 * j + (lq >> 1);  // scale byte of the half's 8
+                s = (int)(int8_t)byte_of(e < 4 ? x.sc.x : x.sc.y, e & 3);
+                d = h2f((uint16_t)x.sc.z);
+                bias = (_Float16)1056.0f;  // 1024 + 32
+            } else {
 #pragma unroll
-        for (int w = 0; w < 2; w++) {
-            v[2 * w] = (as_h2(perm_lo(u[w])) - kb) * m2;
-            v[2 * w + 1] = (as_h2(perm_hi(u[w])) - kb) * m2;
+                for (int w = 0; w < 2; w++) u[w] = ((x.q0[w] >> (2 * j)) & 0x03030303u) | (((x.q1[w] >> (4 * h + j)) & 0x01010101u) << 2);
+                const int e = 8 * h + 2 * j + (lq >> 1), g = e >> 2, i = e & 3;  // the 6-bit code, as q3k_code
+                s = (int)(((byte_of(g & 1 ? x.sc.y : x.sc.x, i) >> (4 * (g >> 1))) & 15u) | (((byte_of(x.sc.z, i) >> (2 * g)) & 3u) << 4)) - 32;
+                d = h2f((uint16_t)x.sc.w);
+                bias = (_Float16)1028.0f;  // 1024 + 4
+            }
+            const _Float16 ds = (_Float16)(d * (float)s);
+            const h2 kb = {bias, bias}, m2 = {ds, ds};
+            h2 v[4];
+#pragma unroll
+            for (int w = 0; w < 2; w++) {
+                v[2 * w] = (as_h2(perm_lo(u[w])) - kb) * m2;
+                v[2 * w + 1] = (as_h2(perm_hi(u[w])) - kb) * m2;
+            }
+            return h8{v[0].x, v[0].y, v[1].x, v[1].y, v[2].x, v[2].y, v[3].x, v[3].y};
         }
-        return h8{v[0].x, v[0].y, v[1].x, v[1].y, v[2].x, v[2].y, v[3].x, v[3].y};
     }
 };
 
@@ -993,13 +1057,19 @@ hipError_t hq_launch_gemm_ws(const hq_dev_mat *W, const uint16_t *A, const uint1
     if (parts < 1 || parts > 4 || parts > g.K / 256 || (parts > 1 && (!partials || !counters))) return hipErrorInvalidValue;
     if (parts > 1 && (size_t)g.mt * g.nt * parts * WS_BM * 32 * nb * 4 >= ((size_t)1 << 32)) return hipErrorInvalidValue;
     const unsigned grid = (unsigned)(8 * ((g.nt + 7) / 8) * g.mt * parts);
+    const bool q5 = W->type == HQ_TYPE_Q5_K;
+    if (!q5 && W->type != HQ_TYPE_Q4_K) return hipErrorInvalidValue;
+#define WSQ(nbv)                                                 \
+    if (q5) k_gemm_q5_k_ws<nbv><<<grid, WS_NT, 0, st>>>(g);      \
+    else k_gemm_q4_k_ws<nbv><<<grid, WS_NT, 0, st>>>(g);
     switch (nb) {
-    case 2: k_gemm_q4_k_ws<2><<<grid, WS_NT, 0, st>>>(g); break;
-    case 3: k_gemm_q4_k_ws<3><<<grid, WS_NT, 0, st>>>(g); break;
-    case 4: k_gemm_q4_k_ws<4><<<grid, WS_NT, 0, st>>>(g); break;
-    case 5: k_gemm_q4_k_ws<5><<<grid, WS_NT, 0, st>>>(g); break;
+    case 2: WSQ(2) break;
+    case 3: WSQ(3) break;
+    case 4: WSQ(4) break;
+    case 5: WSQ(5) break;
     default: return hipErrorInvalidValue;
     }
+#undef WSQ
     return hipGetLastError();
 }
 
@@ -1027,7 +1097,7 @@ hipError_t hq_launch_gemm_ws8(const hq_dev_mat *W, const uint16_t *A, int M, voi
 
 hipError_t hq_launch_gemm_kqws(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
                                int nb, int parts, float *partials, int *counters, hipStream_t st) {
-    if ((W->type != HQ_TYPE_Q6_K && W->type != HQ_TYPE_Q3_K) || W->cols % 256 || !hq_kqws_fits(W, M))
+    if ((W->type != HQ_TYPE_Q6_K && W->type != HQ_TYPE_Q3_K && W->type != HQ_TYPE_Q2_K) || W->cols % 256 || !hq_kqws_fits(W, M))
         return hipErrorInvalidValue;
     KqwsArgs g;
     g.W = W->qs, g.row_bytes = (uint32_t)W->row_bytes, g.A = A;
@@ -1048,8 +1118,10 @@ hipError_t hq_launch_gemm_kqws(const hq_dev_mat *W, const uint16_t *A, int M, vo
     }
     if (W->type == HQ_TYPE_Q6_K) {
         KQWS(HQ_TYPE_Q6_K)
-    } else {
+    } else if (W->type == HQ_TYPE_Q3_K) {
         KQWS(HQ_TYPE_Q3_K)
+    } else {
+        KQWS(HQ_TYPE_Q2_K)
     }
 #undef KQWS
     return hipGetLastError();
@@ -1058,6 +1130,6 @@ hipError_t hq_launch_gemm_kqws(const hq_dev_mat *W, const uint16_t *A, int M, vo
 // every byte offset of k_gemm_kq_ws fits 32 bits (tile rows and columns past the matrix included)
 int hq_kqws_fits(const hq_dev_mat *W, int M) {
     const size_t lim = (size_t)1 << 32;
-    return (W->type == HQ_TYPE_Q6_K || W->type == HQ_TYPE_Q3_K) && W->cols % 256 == 0 && M >= 1 &&
+    return (W->type == HQ_TYPE_Q6_K || W->type == HQ_TYPE_Q3_K || W->type == HQ_TYPE_Q2_K) && W->cols % 256 == 0 && M >= 1 &&
            ((size_t)M + WS_BM) * W->cols * 2 < lim && ((size_t)W->rows + 160) * W->row_bytes < lim;
 }

@@ -106,7 +106,7 @@ hipError_t hq_launch_gemm_rb8(const hq_dev_mat *W, const uint16_t *A, int M, voi
                               int parts, float *partials, int *counters, hipStream_t st);
 hipError_t hq_launch_gemm_ws8(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
                               int nb, int parts, float *partials, int *counters, hipStream_t st);
-// Q6_K and Q3_K full-K tile GEMM (hq_gemm_ws.hip: producers decode into an fp16 B tile in LDS;
+// Q6_K, Q3_K and Q2_K full-K tile GEMM (hq_gemm_ws.hip: producers decode into an fp16 B tile in LDS;
 // K split as for the Q8_0 kernel, in whole super-blocks), and whether its byte offsets fit 32 bits.
 hipError_t hq_launch_gemm_kqws(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
                                int nb, int parts, float *partials, int *counters, hipStream_t st);

@@ -1272,7 +1272,8 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
     if ((W->type == HQ_TYPE_Q6_K || hq_is_kq(W->type)) && c.mb > 4) c.mb = 4;  // the narrow kernel, up to 64-row tiles
     c.nb = 2;
     if (W->type == HQ_TYPE_Q4_K && c.mb == 1) c.mb = 2;
-    c.wide = W->type == HQ_TYPE_Q4_K && M > 64;
+    // (Q5_K: the Q4_K LDS-decode tile kernel where it is chosen below, else the Stream-K k-quant kernel)
+    c.wide = (W->type == HQ_TYPE_Q4_K || W->type == HQ_TYPE_Q5_K) && M > 64;
     c.waves = c.wide ? WNW : 4;
     c.ws_nb = 0;
     c.ws_parts = 1;
@@ -1294,6 +1295,17 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
                     c.ws_parts = parts;
                 }
             }
+    }
+    if (W->type == HQ_TYPE_Q5_K && c.wide && !c.ws_nb) {
+        // Q5_K has no large-M kernel of its own: the tile kernel over several rounds when they fill at
+        // least half of the CU time (as the Q8_0 and k-quant tile kernels), else Stream-K
+        float eff = 0.f;
+        const int nb = hq_ws_choose(M, (int)W->rows, n_cu, &eff);
+        if (eff >= 0.5f) c.ws_nb = nb;
+    }
+    if (W->type == HQ_TYPE_Q5_K && !c.ws_nb) {
+        c.wide = false;
+        c.waves = 4;
     }
     // Q4_K full-K tiles without a K split: the 128 x 192 tile kernel, whose waves decode their own
     // columns (M = 512, N = 9728: 204 tiles)
@@ -1333,8 +1345,9 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
     // the narrow kernel), K is whole 128-wide stages and the byte offsets fit 32 bits
     c.ws8_nb = 0;
     c.ws8_parts = 1;
-    // (Q6_K and Q3_K: the same tile kernel with k-quant producers, k_gemm_kq_ws, on the same rule)
-    const bool kqws = (W->type == HQ_TYPE_Q6_K || W->type == HQ_TYPE_Q3_K) && M > 64 && hq_kqws_fits(W, M);
+    // (Q6_K, Q3_K and Q2_K: the same tile kernel with k-quant producers, k_gemm_kq_ws, on the same rule)
+    const bool kqws = (W->type == HQ_TYPE_Q6_K || W->type == HQ_TYPE_Q3_K || W->type == HQ_TYPE_Q2_K) && M > 64 &&
+                      hq_kqws_fits(W, M);
     if (kqws || (W->type == HQ_TYPE_Q8_0 && M > 64 && W->cols % 128 == 0 && (size_t)M * W->cols * 2 < ((size_t)1 << 32) &&
                  ((size_t)W->rows + 160) * W->cols < ((size_t)1 << 32))) {
         float eff = 0.f;
@@ -1401,6 +1414,10 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
         return;
     }
     const GemmCfg c = gemm_cfg(&W, M, n_cu);
+    if (c.ws_nb && type == HQ_TYPE_Q5_K) {
+        snprintf(buf, n, "k_gemm_q5_k_ws<%d>", c.ws_nb);
+        return;
+    }
     if (c.ws8_nb && type != HQ_TYPE_Q8_0) {  // template arguments: the ggml type, the tile width / 32
         snprintf(buf, n, "k_gemm_kq_ws<%d, %d>", type, c.ws8_nb);
         return;
@@ -1548,7 +1565,7 @@ hipError_t hq_launch_gemm_swiglu(const hq_dev_mat *W, const uint16_t *A, int M, 
     }
     float eff = 0.f;
     const int nb = hq_ws_choose(M, N, wk.n_cu, &eff);
-    if (W->type == HQ_TYPE_Q4_K && wk.sums) {
+    if ((W->type == HQ_TYPE_Q4_K || W->type == HQ_TYPE_Q5_K) && wk.sums) {
         const size_t nsub = (size_t)M * (W->cols / 32);
         if (nsub >= ((size_t)1 << 31)) return hipSuccess;
         k_asums<true><<<grid_for(nsub, 256, 16384), 256, 0, st>>>(A, M, K, wk.sums);
@@ -1559,7 +1576,7 @@ hipError_t hq_launch_gemm_swiglu(const hq_dev_mat *W, const uint16_t *A, int M, 
         *fused = 1;
         return hq_launch_gemm_ws8(W, A, M, out, HQ_OUT_SWIGLU, 0, nb, 1, nullptr, nullptr, st);
     }
-    if ((W->type == HQ_TYPE_Q6_K || W->type == HQ_TYPE_Q3_K) && hq_kqws_fits(W, M)) {
+    if ((W->type == HQ_TYPE_Q6_K || W->type == HQ_TYPE_Q3_K || W->type == HQ_TYPE_Q2_K) && hq_kqws_fits(W, M)) {
         *fused = 1;
         return hq_launch_gemm_kqws(W, A, M, out, HQ_OUT_SWIGLU, 0, nb, 1, nullptr, nullptr, st);
     }

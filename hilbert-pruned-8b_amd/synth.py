@@ -139,8 +139,11 @@ def _kquant_blocks(gtype, rng, rows, cols, fp16_at, scale):
     return blk.reshape(rows, row_bytes(gtype, cols))
 
 
-def q2_k_blocks(rng, rows, cols, scale=1e-2):
-    """Q2_K super-blocks: scales and qs uniform bytes, d and dmin = fp16(|N(0,1)| * scale)."""
+def q2_k_blocks(rng, rows, cols, scale=4e-3):
+    """Q2_K super-blocks: scales and qs uniform bytes, d and dmin = fp16(|N(0,1)| * scale). The
+    default scale gives d of a few 1e-3, the size a 2-bit quantiser picks for weights of standard
+    deviation ~0.03 (d ~ 0.1 x the weights' standard deviation: the largest 16-value group range / 3,
+    spread over 15 scale codes); the committed golden fixtures were written with scale 1e-2."""
     return _kquant_blocks(Q2_K, rng, rows, cols, (80, 82), scale)
 
 

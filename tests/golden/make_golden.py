@@ -66,7 +66,7 @@ def main():
 
     # matmul (reference selftest quant shape N=40, K=512, M=5; accumulate into y0)
     for name, gtype in (("matmul_q8_0.npz", synth.Q8_0), ("matmul_q4_k.npz", synth.Q4_K)):
-        blocks = synth.random_blocks(gtype, rng, 40, 512)
+        blocks = gen(rng, 40, 512)
         x = synth.activations_f16(rng, 5, 512).view(np.float16).astype(np.float32)
         y0 = rng.normal(5 * 40).astype(np.float32).reshape(5, 40)
         y = ref.matmul(blocks, gtype, 40, 512, x, y0.copy(), True)
@@ -107,11 +107,13 @@ def kquants():
         name = synth.TYPE_NAMES[gtype].lower()
         rng = synth.Rng(7000 + gtype)
         sp = special_kquant_blocks(gtype)  # 2 rows x 1024 values
-        blocks = np.ascontiguousarray(np.concatenate([sp, synth.random_blocks(gtype, rng, 6, 1024)]))
+        gen = (lambda r, n, k: synth.q2_k_blocks(r, n, k, scale=1e-2)) if gtype == synth.Q2_K else \
+            (lambda r, n, k: synth.random_blocks(gtype, r, n, k))  # (the scale these fixtures were written with)
+        blocks = np.ascontiguousarray(np.concatenate([sp, gen(rng, 6, 1024)]))
         vals = ref.dequantize(blocks, gtype, 8, 1024, perm_heads=2)
         np.savez_compressed(os.path.join(HERE, f"dequant_{name}.npz"), blocks=blocks, values=vals, gtype=gtype, rows=8,
                             cols=1024, perm_heads=2)
-        blocks = synth.random_blocks(gtype, rng, 40, 512)
+        blocks = gen(rng, 40, 512)
         x = synth.activations_f16(rng, 5, 512).view(np.float16).astype(np.float32)
         y0 = rng.normal(5 * 40).astype(np.float32).reshape(5, 40)
         y = ref.matmul(blocks, gtype, 40, 512, x, y0.copy(), True)

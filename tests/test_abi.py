@@ -121,9 +121,12 @@ def test_gemm_kernel_names():
              # k-quant GEMVs: rows per wave = 8 / gcd(K / 256, 8)
              (synth.Q6_K, 1, 9728, 2560): "k_gemv_sb<14, 4, false>", (synth.Q3_K, 1, 2560, 9728): "k_gemv_sb<11, 4, false>",
              (synth.Q5_K, 1, 100, 2048): "k_gemv_sb<13, 1, false>", (synth.Q2_K, 1, 100, 768): "k_gemv_sb<10, 8, false>",
-             # Q6_K / Q3_K above M = 64: the LDS-decode tile kernel (template: the ggml type, tile width / 32)
+             # Q6_K / Q3_K / Q2_K above M = 64: the LDS-decode tile kernel (template: the ggml type, tile width / 32)
              (synth.Q6_K, 512, 9728, 2560): "k_gemm_kq_ws<14, 5>", (synth.Q3_K, 128, 9728, 2560): "k_gemm_kq_ws<11, 2>",
-             (synth.Q6_K, 64, 9728, 2560): "k_gemm_q6_k<4, 2>", (synth.Q5_K, 512, 9728, 2560): "k_gemm_kq<13, 4, 2>",
+             (synth.Q2_K, 512, 9728, 2560): "k_gemm_kq_ws<10, 5>",
+             (synth.Q6_K, 64, 9728, 2560): "k_gemm_q6_k<4, 2>", (synth.Q5_K, 64, 9728, 2560): "k_gemm_kq<13, 4, 2>",
+             # Q5_K above M = 64: the Q4_K LDS-decode tile kernel's Q5_K instance
+             (synth.Q5_K, 512, 9728, 2560): "k_gemm_q5_k_ws<5>", (synth.Q5_K, 300, 9728, 2560): "k_gemm_q5_k_ws<4>",
              # special-scale cases: the narrow kernel at M = 16, the mid-M kernel with a 6-way K split
              (synth.Q4_K, 16, 9728, 2560): "k_gemm_q4_k<2, 2>", (synth.Q4_K, 48, 9728, 2560): "k_gemm_q4_k_rb<1, 4, 3, 2>",
              (synth.Q4_K, 350, 9728, 512): "k_gemm_q4_k_wr160"}

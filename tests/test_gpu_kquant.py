@@ -98,13 +98,16 @@ def test_gemm_special_scales(hqlib, oracle, gtype):
     W.free()
 
 
-@pytest.mark.parametrize("gtype", [synth.Q3_K, synth.Q6_K])
-def test_tile_kernel_special_scales(hqlib, oracle, gtype):
-    """The LDS-decode tile kernel (M > 64; B = fp16(q * fp16(d * s)), two roundings of at most 2^-11
-    each) on the finite special blocks: rel-L2 at the bar, and within 2^-10 |W| @ |a| of the float64
-    product plus 2^-24 sum |a| (fp16 subnormal spacing of d * s and of the weights). (d = 1 with scales
-    of -128 / 127 gives outputs of ~2e5, where fp32 sums alone differ by more than the absolute 1e-2 of
-    the bar; the float64 bound is the element-wise check here.)"""
+@pytest.mark.parametrize("gtype,rel", [(synth.Q3_K, 2.0 ** -10), (synth.Q6_K, 2.0 ** -10), (synth.Q2_K, 2.0 ** -10),
+                                       (synth.Q5_K, 2.0 ** -13)])
+def test_tile_kernel_special_scales(hqlib, oracle, gtype, rel):
+    """The LDS-decode tile kernels (M > 64) on the finite special blocks: rel-L2 at the bar, and within
+    rel |W| @ |a| of the float64 product plus 2^-24 sum |a|. Q3_K / Q6_K (k_gemm_kq_ws: B =
+    fp16(q * fp16(d * s)), two roundings of at most 2^-11 each, and the fp16 subnormal spacing of d * s
+    and of the weights) and Q2_K (k_gemm_kq_ws: B = fp16 of the fp32 weight): rel = 2^-10. Q5_K (k_gemm_q5_k_ws: B the exact integer s * q in units of d, the
+    min term through bf16 hi / lo parts): rel = 2^-13, as for the exact kernels. (d = 1 with extreme
+    scales gives outputs of ~2e5, where fp32 sums alone differ by more than the absolute 1e-2 of the
+    bar; the float64 bound is the element-wise check here.)"""
     from test_oracle import SPECIAL_BLOCKS
     sp = SPECIAL_BLOCKS[gtype]().reshape(8, -1)
     fin = []
@@ -117,7 +120,7 @@ def test_tile_kernel_special_scales(hqlib, oracle, gtype):
     W = hqlib.Mat(np.ascontiguousarray(rows), gtype, N, K)
     name = hqlib.gemm_kernel(gtype, M, N, K)
     say(f"{synth.TYPE_NAMES[gtype]} special tile M={M} kernel={name}")
-    assert name.startswith("k_gemm_kq_ws<")
+    assert name.startswith("k_gemm_q5_k_ws<" if gtype == synth.Q5_K else "k_gemm_kq_ws<")
     a = synth.activations_f16(synth.Rng(79), M, K)
     got = hqlib.gemm_np(W, a)
     W.free()
@@ -127,7 +130,7 @@ def test_tile_kernel_special_scales(hqlib, oracle, gtype):
     r, m = rel_l2(got, ref), max_abs(got, ref)
     say(f"rel_l2 {r:.2e} max_abs {m:.2e} max|ref| {np.abs(ref).max():.2f}")
     assert r <= 1e-3
-    bound = 2.0 ** -10 * (np.abs(x) @ np.abs(wf.T)) + 2.0 ** -24 * np.abs(x).sum(axis=1, keepdims=True)
+    bound = rel * (np.abs(x) @ np.abs(wf.T)) + 2.0 ** -24 * np.abs(x).sum(axis=1, keepdims=True)
     assert np.all(np.abs(got - x @ wf.T) <= bound)
 
 
