@@ -106,6 +106,11 @@ hipError_t hq_launch_gemm_rb8(const hq_dev_mat *W, const uint16_t *A, int M, voi
                               int parts, float *partials, int *counters, hipStream_t st);
 hipError_t hq_launch_gemm_ws8(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
                               int nb, int parts, float *partials, int *counters, hipStream_t st);
+// Q4_K GEMM with at most 32 output columns (hq_gemm_nn.hip: 64-row workgroups streaming A once, the
+// weights decoded per workgroup into LDS as exact fp16 hi / lo pairs); whether a shape suits it.
+int hq_nn_fits(const hq_dev_mat *W, int M);
+hipError_t hq_launch_gemm_nn(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
+                             hipStream_t st);
 // Q6_K, Q3_K and Q2_K full-K tile GEMM (hq_gemm_ws.hip: producers decode into an fp16 B tile in LDS;
 // K split as for the Q8_0 kernel, in whole super-blocks), and whether its byte offsets fit 32 bits.
 hipError_t hq_launch_gemm_kqws(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,

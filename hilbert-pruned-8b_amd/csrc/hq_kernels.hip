@@ -1259,6 +1259,7 @@ struct GemmCfg {
     int wr_parts;   // with wr: workgroups per tile (K split), 1: whole K
     int wr_tw;      // with wr: tile width, 192 or 160 columns (k_gemm_q4_k_wr160)
     bool wr8;       // Q8_0, the same: k_gemm_q8_0_wr (hq_gemm_wr8.hip)
+    bool nn;        // Q4_K with N <= 32 and many rows: k_gemm_q4_k_nn (hq_gemm_nn.hip)
 };
 
 // Q4_K with M > 64 runs the full-K tile kernel when its tiles fit in one round on the CUs and fill
@@ -1372,6 +1373,15 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
     // at most one round each fill at least 70 % of the CU time (M = 512, N = 9728: one launch of 204
     // tiles; M = 2048: four launches of 16 x 13 tiles)
     c.wr8 = W->type == HQ_TYPE_Q8_0 && M > 64 && hq_wr8_fits(W, M) && wr_plan(M, (int)W->rows, n_cu).fill;
+    // N <= 32 with at least 64 workgroups of 64 rows (config 4's b / a projections at M = 16384: 256):
+    // the skinny kernel, which reads A once with every CU streaming
+    c.nn = W->type == HQ_TYPE_Q4_K && W->rows <= 32 && M >= 64 * 64 && hq_nn_fits(W, M);
+    if (c.nn) {
+        c.wide = c.wr = c.bt = false;
+        c.ws_nb = c.rbm = 0;
+        c.ws_parts = 1;
+        c.waves = 4;
+    }
     return c;
 }
 
@@ -1394,6 +1404,10 @@ void hq_gemm_tile_shape(int type, int M, int N, int K, int n_cu, int *rows, int 
     W.row_bytes = shape_row_bytes(type, K);
     W.ldd = type == HQ_TYPE_Q8_0 ? (K / 32 + 7) / 8 * 8 : 0;
     const GemmCfg c = gemm_cfg(&W, M, n_cu);
+    if (c.nn) {
+        *rows = 64, *cols = 32;
+        return;
+    }
     *rows = c.bt ? 256 : c.wr || c.wr8 ? 128 : c.rbm ? 64 : c.rb8 ? (M <= 16 ? 16 : M <= 32 ? 32 : 64) : c.ws_nb || c.ws8_nb ? 128 : 16 * c.mb;
     *cols = c.bt ? 256 : c.wr ? c.wr_tw : c.wr8 ? 192 : c.rbm || c.rb8 ? 64 : c.ws_nb ? 32 * c.ws_nb : c.ws8_nb ? 32 * c.ws8_nb : 16 * c.nb * c.waves;
 }
@@ -1434,7 +1448,8 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
         else snprintf(buf, n, "%s<%d>", type == HQ_TYPE_Q4_K ? "k_gemv_q4_k" : "k_gemv_q8_0", pl.r);
         return;
     }
-    if (c.rbm) snprintf(buf, n, "k_gemm_q4_k_rb<1, 4, 3, 2>");
+    if (c.nn) snprintf(buf, n, "k_gemm_q4_k_nn<%d>", N <= 16 ? 1 : 2);
+    else if (c.rbm) snprintf(buf, n, "k_gemm_q4_k_rb<1, 4, 3, 2>");
     else if (c.rb8) snprintf(buf, n, "k_gemm_q8_0_rb<%d, 3, 2>", M <= 16 ? 1 : M <= 32 ? 2 : 4);
     else if (c.bt) snprintf(buf, n, "k_gemm_q4_k_bt");
     else if (c.wr) snprintf(buf, n, c.wr_parts > 1 ? "k_gemm_q4_k_wr_ks<3>" : c.wr_tw == 160 ? "k_gemm_q4_k_wr160" : "k_gemm_q4_k_wr<3>");
@@ -1449,6 +1464,10 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
 void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_bytes, size_t *counter_bytes,
                         size_t *sums_bytes) {
     const GemmCfg c = gemm_cfg(W, M, n_cu);
+    if (c.nn) {  // no workspace
+        *partial_bytes = *counter_bytes = *sums_bytes = 0;
+        return;
+    }
     const SkPlan p = gemm_plan(W, M, c, n_cu);
     const bool tile = c.ws_nb || c.ws8_nb || c.bt;  // tile kernels: partial tiles only when K is split (below)
     *partial_bytes = tile ? 0 : (size_t)2 * p.G * 64 * c.waves * c.mb * c.nb * 4 * sizeof(float);
@@ -1496,6 +1515,7 @@ hipError_t hq_launch_gemm_pre(const hq_dev_mat *W, const uint16_t *A, int M, con
 hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
                                const HqGemmWork &wk, hipStream_t st) {
     const GemmCfg c = gemm_cfg(W, M, wk.n_cu);
+    if (c.nn) return hq_launch_gemm_nn(W, A, M, C, c_f32, accumulate, st);
     if (c.rbm) return hq_launch_gemm_rb(W, A, wk.sums, M, C, c_f32, accumulate, c.rbm, wk.partials, wk.counters, st);
     if (c.rb8) return hq_launch_gemm_rb8(W, A, M, C, c_f32, accumulate, c.rb8, wk.partials, wk.counters, st);
     if (c.bt) return hq_launch_gemm_bt(W, A, wk.sums, M, C, c_f32, accumulate, st);

@@ -127,6 +127,9 @@ def test_gemm_kernel_names():
              (synth.Q6_K, 64, 9728, 2560): "k_gemm_q6_k<4, 2>", (synth.Q5_K, 64, 9728, 2560): "k_gemm_kq<13, 4, 2>",
              # Q5_K above M = 64: the Q4_K LDS-decode tile kernel's Q5_K instance
              (synth.Q5_K, 512, 9728, 2560): "k_gemm_q5_k_ws<5>", (synth.Q5_K, 300, 9728, 2560): "k_gemm_q5_k_ws<4>",
+             # Q4_K with N <= 32 at M >= 4096: the skinny kernel (template: 16-column blocks)
+             (synth.Q4_K, 16384, 32, 2560): "k_gemm_q4_k_nn<2>", (synth.Q4_K, 4096, 9, 256): "k_gemm_q4_k_nn<1>",
+             (synth.Q4_K, 4095, 32, 2560): "k_gemm_q4_k_w<8>",
              # special-scale cases: the narrow kernel at M = 16, the mid-M kernel with a 6-way K split
              (synth.Q4_K, 16, 9728, 2560): "k_gemm_q4_k<2, 2>", (synth.Q4_K, 48, 9728, 2560): "k_gemm_q4_k_rb<1, 4, 3, 2>",
              (synth.Q4_K, 350, 9728, 512): "k_gemm_q4_k_wr160"}
