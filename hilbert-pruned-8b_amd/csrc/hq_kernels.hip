@@ -1423,8 +1423,7 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
     W.row_bytes = shape_row_bytes(type, K);
     const char *kq = type == HQ_TYPE_Q2_K ? "10" : type == HQ_TYPE_Q3_K ? "11" : type == HQ_TYPE_Q5_K ? "13" : nullptr;
     if (M == 1 && (kq || type == HQ_TYPE_Q6_K)) {  // template arguments: the ggml type, rows per wave
-        const int nsb = K / 256, r = nsb % 8 == 0 ? 1 : nsb % 4 == 0 ? 2 : nsb % 2 == 0 ? 4 : 8;
-        snprintf(buf, n, "k_gemv_sb<%d, %d, false>", type, r);
+        snprintf(buf, n, "k_gemv_sb<%d, %d, false>", type, hq_sb_rows(N));
         return;
     }
     const GemmCfg c = gemm_cfg(&W, M, n_cu);

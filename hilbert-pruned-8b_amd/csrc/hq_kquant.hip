@@ -211,17 +211,11 @@ __global__ void __launch_bounds__(256) k_gemv_sb(const uint8_t *__restrict__ W, 
     }
 }
 
-// rows per wave of k_gemv_sb: enough waves to keep the weight stream's loads in flight, few enough
-// super-blocks per lane to stay short
-int sb_rows(int n_out, int nsb) {
-    (void)nsb;
-    return n_out >= 8192 ? 2 : 1;
-}
 
 template <int T, bool GATHER>
 hipError_t launch_sb(const hq_dev_mat *W, const uint16_t *a, const uint32_t *ids, int n_out, int k_opts, void *C, int c_f32,
                      int accumulate, hipStream_t st) {
-    const int R = sb_rows(n_out, (int)W->cols / 256);
+    const int R = hq_sb_rows(n_out);
     const unsigned grid = (unsigned)(((n_out + R - 1) / R + 3) / 4);
 #define SB(r) k_gemv_sb<T, r, GATHER><<<grid, 256, 0, st>>>(W->qs, W->row_bytes, a, ids, n_out, k_opts, (int)W->cols, W->rows, C, c_f32, accumulate)
     switch (R) {
@@ -454,6 +448,10 @@ hipError_t hq_launch_dequant_kq(const hq_dev_mat *W, uint32_t row0, const uint32
 #undef DQ
     return hipGetLastError();
 }
+
+// rows per wave of k_gemv_sb (GEMV and gather): two at n_out >= 8192 (K = 2560: 2432 waves), else one
+// (K = 9728, N = 2560: eight super-blocks side by side); measured over 1 .. 8 rows on both headline shapes
+int hq_sb_rows(int n_out) { return n_out >= 8192 ? 2 : 1; }
 
 hipError_t hq_launch_gemv_kq(const hq_dev_mat *W, const uint16_t *a, void *C, int c_f32, int accumulate, hipStream_t st) {
     const int n = (int)W->rows;

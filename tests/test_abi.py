@@ -118,9 +118,9 @@ def test_gemm_kernel_names():
              (synth.Q4_K, 1, 2560, 9728): "k_gemv_q4_k_s<4>", (synth.Q4_K, 1, 100, 512): "k_gemv_q4_k_s<1>",
              (synth.Q4_K, 1, 9728, 256): "k_gemv_q4_k_s<16>", (synth.Q8_0, 1, 9728, 2560): "k_gemv_q8_0<2>",
              (synth.Q8_0, 1, 100, 512): "k_gemv_q8_0<1>",
-             # k-quant GEMVs: rows per wave = 8 / gcd(K / 256, 8)
-             (synth.Q6_K, 1, 9728, 2560): "k_gemv_sb<14, 4, false>", (synth.Q3_K, 1, 2560, 9728): "k_gemv_sb<11, 4, false>",
-             (synth.Q5_K, 1, 100, 2048): "k_gemv_sb<13, 1, false>", (synth.Q2_K, 1, 100, 768): "k_gemv_sb<10, 8, false>",
+             # k-quant GEMVs: rows per wave, 2 at N >= 8192
+             (synth.Q6_K, 1, 9728, 2560): "k_gemv_sb<14, 2, false>", (synth.Q3_K, 1, 2560, 9728): "k_gemv_sb<11, 1, false>",
+             (synth.Q5_K, 1, 100, 2048): "k_gemv_sb<13, 1, false>", (synth.Q2_K, 1, 100, 20480): "k_gemv_sb<10, 1, false>",
              # Q6_K / Q3_K / Q2_K above M = 64: the LDS-decode tile kernel (template: the ggml type, tile width / 32)
              (synth.Q6_K, 512, 9728, 2560): "k_gemm_kq_ws<14, 5>", (synth.Q3_K, 128, 9728, 2560): "k_gemm_kq_ws<11, 2>",
              (synth.Q2_K, 512, 9728, 2560): "k_gemm_kq_ws<10, 5>",
