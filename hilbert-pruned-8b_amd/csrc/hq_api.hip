@@ -601,7 +601,7 @@ NoallocLayout noalloc_layout(size_t pb, size_t cb, size_t sb) {
 
 extern "C" int hq_gemm_workspace_bytes(int ggml_type, int M, uint32_t N, uint32_t K, int n_cu, size_t *partial_bytes,
                                        size_t *counter_bytes, size_t *sums_bytes, int *fits_noalloc) {
-    if (ggml_type != HQ_GGML_Q8_0 && ggml_type != HQ_GGML_Q4_K) return fail("hq_gemm_workspace_bytes: type %d", ggml_type);
+    if (!block_values(ggml_type)) return fail("hq_gemm_workspace_bytes: type %d (supported: %s)", ggml_type, SUPPORTED);
     if (M < 2 || N == 0 || K == 0 || K % block_values(ggml_type) || n_cu < 1)
         return fail("hq_gemm_workspace_bytes: M = %d, N = %u, K = %u, n_cu = %d", M, N, K, n_cu);
     if ((size_t)M > gemm_rows_per_launch(K))
@@ -611,7 +611,10 @@ extern "C" int hq_gemm_workspace_bytes(int ggml_type, int M, uint32_t N, uint32_
     W.type = ggml_type;
     W.rows = N;
     W.cols = K;
-    W.row_bytes = (size_t)(K / block_values(ggml_type)) * block_bytes(ggml_type);
+    // the upload's device layout: k-quant super-blocks in their aligned slots, the Q8_0 scale plane
+    const size_t nb = K / block_values(ggml_type);
+    W.row_bytes = nb * (slot_bytes(ggml_type) ? slot_bytes(ggml_type) : block_bytes(ggml_type));
+    W.ldd = ggml_type == HQ_GGML_Q8_0 ? (int)round_up(K / 32, 8) : 0;
     size_t pb, cb, sb;
     hq_gemm_work_bytes(&W, M, n_cu, &pb, &cb, &sb);
     if (partial_bytes) *partial_bytes = pb;

@@ -1356,13 +1356,18 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
         const long tiles = (long)((M + 127) / 128) * (((int)W->rows + 32 * nb - 1) / (32 * nb));
         if (eff >= 0.5f) c.ws8_nb = nb;
         // fewer tiles than 3/4 of the CUs over a long K (M = 512, N = 2560, K = 9728: 160 tiles of
-        // 128 x 64 through 76 stages, 66 us): each tile's K split over 2 or 4 workgroups of >= 16
-        // stages, the widest tiles that fill >= 3/4 of the CUs in one round
+        // 128 x 64 through 76 stages, 66 us): each tile's K split over 2 or 4 workgroups, the widest
+        // tiles that fill >= 3/4 of the CUs in one round. Parts of >= 8 stages where no unsplit tiling
+        // fills half the CU time (M = 96, N = 9728, K = 2560: Q8_0 24.6 -> 21.4 us, Q6_K 31.9 -> 21.5;
+        // M = 128, N = K = 4096: 25.2 -> 17.6, 26.3 -> 17.4) and for Q8_0 (M = 128, N = 9728, K = 2560:
+        // 22.7 -> 21.8); >= 16 stages for the k-quants otherwise (the same shape: Q6_K 21.0 unsplit
+        // against 21.9 split, Q3_K 19.3 against 20.5)
+        const int min_stages = c.ws8_nb && kqws ? 16 : 8;
         if (4 * tiles < 3L * n_cu || !c.ws8_nb)
             for (int parts = 4, done = 0; !done && parts >= 2; parts /= 2)
                 for (int w = 5; !done && w >= 2; w--) {
                     const long t = (long)((M + 127) / 128) * (((int)W->rows + 32 * w - 1) / (32 * w));
-                    if (t * parts <= n_cu && 4 * t * parts >= 3L * n_cu && (int)(W->cols / 128) >= 16 * parts) {
+                    if (t * parts <= n_cu && 4 * t * parts >= 3L * n_cu && (int)(W->cols / 128) >= min_stages * parts) {
                         c.ws8_nb = w;
                         c.ws8_parts = parts;
                         done = 1;

@@ -95,6 +95,14 @@ def test_gemm_workspace_bytes():
     assert hq.gemm_workspace_bytes(synth.Q8_0, 512, 9728, 2560) == (0, 0, 0, True)
     assert hq.gemm_workspace_bytes(synth.Q4_K, 16384, 2560, 9216)[3]
     assert not hq.gemm_workspace_bytes(synth.Q4_K, 131072, 256, 9216)[3]  # 151 MB of sub-block sums
+    # the k-quant tile kernel (Q6_K, M = 512, N = 2560, K = 9728): 4 x 16 tiles of 128 x 160 with K
+    # split over 4 workgroups; the Q5_K tile kernel (M = 512, N = 9728): sub-block sums only; the Q8_0
+    # tile kernel at M = 96 (one row tile): 102 tiles of 128 x 96 with K split over 2 workgroups
+    assert hq.gemm_workspace_bytes(synth.Q6_K, 512, 2560, 9728) == (64 * 4 * 128 * 160 * 4, 64 * 4, 0, True)
+    assert hq.gemm_workspace_bytes(synth.Q5_K, 512, 9728, 2560) == (0, 0, 512 * 10 * 32, True)
+    assert hq.gemm_workspace_bytes(synth.Q8_0, 96, 9728, 2560) == (102 * 2 * 128 * 96 * 4, 102 * 4, 0, True)
+    with pytest.raises(hq.HQError, match="type 9"):
+        hq.gemm_workspace_bytes(9, 512, 256, 256)
     with pytest.raises(hq.HQError, match="M = 1"):
         hq.gemm_workspace_bytes(synth.Q4_K, 1, 256, 256)
 
@@ -103,8 +111,9 @@ def test_gemm_kernel_names():
     """hq_gemm_kernel names the kernel the launch plan picks (the names rocprofv3 lists)."""
     cases = {(synth.Q4_K, 512, 9728, 2560): "k_gemm_q4_k_wr160", (synth.Q4_K, 256, 9728, 2560): "k_gemm_q4_k_wr160",
              (synth.Q4_K, 384, 13000, 2560): "k_gemm_q4_k_wr<3>", (synth.Q8_0, 512, 9728, 2560): "k_gemm_q8_0_wr",
-             (synth.Q8_0, 2048, 9728, 2560): "k_gemm_q8_0_wr", (synth.Q8_0, 128, 9728, 2560): "k_gemm_q8_0_ws<2>",
-             (synth.Q8_0, 65, 9728, 2560): "k_gemm_q8_0<8, 2>",
+             (synth.Q8_0, 2048, 9728, 2560): "k_gemm_q8_0_wr", (synth.Q8_0, 128, 9728, 2560): "k_gemm_q8_0_ws<3>",
+             (synth.Q8_0, 65, 9728, 2560): "k_gemm_q8_0_ws<3>", (synth.Q8_0, 128, 4096, 4096): "k_gemm_q8_0_ws<2>",
+             (synth.Q6_K, 96, 9728, 2560): "k_gemm_kq_ws<14, 3>",
              (synth.Q4_K, 4096, 9728, 2560): "k_gemm_q4_k_bt", (synth.Q4_K, 16384, 2560, 9216): "k_gemm_q4_k_bt",
              (synth.Q4_K, 16384, 1024, 2560): "k_gemm_q4_k_bt", (synth.Q4_K, 2048, 9728, 2560): "k_gemm_q4_k_w<8>",
              (synth.Q4_K, 64, 9728, 2560): "k_gemm_q4_k_rb<1, 4, 3, 2>",

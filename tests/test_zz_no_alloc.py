@@ -15,9 +15,12 @@ def say(*a):
 
 # each case uses the scratch differently: a K-split tile GEMM (partial tiles, counters, sums), then a
 # smaller mid-M K split (partials, counters), a Stream-K GEMM (64 MiB of partial tiles, counters,
-# sums), then a smaller mid-M GEMM (sums only) and a tile GEMM with no workspace at all
+# sums), then a smaller mid-M GEMM (sums only) and a tile GEMM with no workspace at all; then the
+# k-quant tile kernel with K split over 4 (Q6_K), the Q5_K tile kernel (sums only) and the Q8_0 tile
+# kernel with K split over 2 workgroups (partials, counters)
 CASES = [(synth.Q4_K, 512, 2560, 9728), (synth.Q8_0, 16, 2560, 9728), (synth.Q4_K, 4096, 9728, 2560),
-         (synth.Q4_K, 64, 9728, 2560), (synth.Q8_0, 512, 9728, 2560)]
+         (synth.Q4_K, 64, 9728, 2560), (synth.Q8_0, 512, 9728, 2560), (synth.Q6_K, 512, 2560, 9728),
+         (synth.Q5_K, 512, 9728, 2560), (synth.Q8_0, 96, 9728, 2560)]
 
 
 def test_noalloc_matches_hq_gemm_call_after_call(hqlib):
