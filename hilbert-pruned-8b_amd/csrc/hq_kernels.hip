@@ -1287,22 +1287,25 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
         if (eff >= 0.7f && tiles <= n_cu) c.ws_nb = nb;
         // few tiles over a long K (M = 512, N = 2560, K = 9728: 64 tiles of 128 x 160): split each
         // tile's K over 2 or 4 workgroups, the widest tiles for which that fills at least 3/4 of the
-        // CUs in one round, with >= 8 super-blocks per part
-        for (int parts = 4; !c.ws_nb && parts >= 2; parts /= 2)
-            for (int w = 5; !c.ws_nb && w >= 2; w--) {
-                const long t = (long)((M + 127) / 128) * (((int)W->rows + 32 * w - 1) / (32 * w));
-                if (t * parts <= n_cu && 4 * t * parts >= 3L * n_cu && (int)(W->cols / 256) >= 8 * parts) {
-                    c.ws_nb = w;
-                    c.ws_parts = parts;
+        // CUs in one round, with >= min_sb super-blocks per part
+        auto split = [&](int min_sb) {
+            for (int parts = 4; !c.ws_nb && parts >= 2; parts /= 2)
+                for (int w = 5; !c.ws_nb && w >= 2; w--) {
+                    const long t = (long)((M + 127) / 128) * (((int)W->rows + 32 * w - 1) / (32 * w));
+                    if (t * parts <= n_cu && 4 * t * parts >= 3L * n_cu && (int)(W->cols / 256) >= min_sb * parts) {
+                        c.ws_nb = w;
+                        c.ws_parts = parts;
+                    }
                 }
-            }
-    }
-    if (W->type == HQ_TYPE_Q5_K && c.wide && !c.ws_nb) {
+        };
+        split(8);
         // Q5_K has no large-M kernel of its own: the tile kernel over several rounds when they fill at
-        // least half of the CU time (as the Q8_0 and k-quant tile kernels), else Stream-K
-        float eff = 0.f;
-        const int nb = hq_ws_choose(M, (int)W->rows, n_cu, &eff);
-        if (eff >= 0.5f) c.ws_nb = nb;
+        // least half of the CU time (as the Q8_0 and k-quant tile kernels)
+        if (W->type == HQ_TYPE_Q5_K && !c.ws_nb && eff >= 0.5f) c.ws_nb = nb;
+        // then parts of >= 4 super-blocks (M = 128, N = 9728, K = 2560: 102 tiles of 128 x 96 in 2
+        // parts, 22.2 us against 29.8 for Stream-K; M = 512, N = 1024, K = 4096: 18.9 against 37.1;
+        // M = 1024, N = 1024, K = 2560: 19.2 against 29.1), where the Stream-K kernel is left
+        if (!c.ws_nb) split(4);
     }
     if (W->type == HQ_TYPE_Q5_K && !c.ws_nb) {
         c.wide = false;
@@ -1322,13 +1325,16 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
         if (mt * ((n160 + 7) / 8) <= per_xcd && n160 > n192) c.wr_tw = 160;
     }
     // few tiles over a long K, where the LDS-decode kernel splits K (M = 512, N = 2560, K = 9728): the
-    // register-decode kernel with each tile's K split over 4 or 2 workgroups of >= 8 super-blocks,
-    // when its tiles x parts fit one round on every XCD and fill >= 70 % of the CUs (4 x 14 x 4 = 224)
+    // register-decode kernel with each tile's K split over 4 or 2 workgroups of >= 5 super-blocks,
+    // when its tiles x parts fit one round on every XCD and fill >= 70 % of the CUs (4 x 14 x 4 = 224;
+    // M = 200, N = 9728, K = 2560: 2 x 51 x 2, 31.9 us against 36.3 for the LDS-decode kernel's split;
+    // parts of 4 super-blocks measured slower than the LDS-decode kernel's, e.g. 34.4 against 29.0 us
+    // at M = 512, N = 2560, K = 4096)
     if (!c.wr && c.ws_nb && c.ws_parts > 1 && hq_wr_fits(W, M)) {
         const int mt = (M + 127) / 128, nt = ((int)W->rows + 191) / 192, per_xcd = std::max(1, n_cu / 8);
         for (int parts = 4; !c.wr && parts >= 2; parts /= 2) {
             const int units = nt * parts;
-            if (mt * ((units + 7) / 8) <= per_xcd && 10L * mt * units >= 7L * n_cu && (int)(W->cols / 256) >= 8 * parts) {
+            if (mt * ((units + 7) / 8) <= per_xcd && 10L * mt * units >= 7L * n_cu && (int)(W->cols / 256) >= 5 * parts) {
                 c.wr = true;
                 c.wr_parts = parts;
             }

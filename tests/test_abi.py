@@ -113,7 +113,8 @@ def test_gemm_kernel_names():
              (synth.Q4_K, 384, 13000, 2560): "k_gemm_q4_k_wr<3>", (synth.Q8_0, 512, 9728, 2560): "k_gemm_q8_0_wr",
              (synth.Q8_0, 2048, 9728, 2560): "k_gemm_q8_0_wr", (synth.Q8_0, 128, 9728, 2560): "k_gemm_q8_0_ws<3>",
              (synth.Q8_0, 65, 9728, 2560): "k_gemm_q8_0_ws<3>", (synth.Q8_0, 128, 4096, 4096): "k_gemm_q8_0_ws<2>",
-             (synth.Q6_K, 96, 9728, 2560): "k_gemm_kq_ws<14, 3>",
+             (synth.Q6_K, 96, 9728, 2560): "k_gemm_kq_ws<14, 3>", (synth.Q4_K, 128, 9728, 2560): "k_gemm_q4_k_ws<3>",
+             (synth.Q4_K, 200, 9728, 2560): "k_gemm_q4_k_wr_ks<3>", (synth.Q5_K, 96, 9728, 2560): "k_gemm_q5_k_ws<3>",
              (synth.Q4_K, 4096, 9728, 2560): "k_gemm_q4_k_bt", (synth.Q4_K, 16384, 2560, 9216): "k_gemm_q4_k_bt",
              (synth.Q4_K, 16384, 1024, 2560): "k_gemm_q4_k_bt", (synth.Q4_K, 2048, 9728, 2560): "k_gemm_q4_k_w<8>",
              (synth.Q4_K, 64, 9728, 2560): "k_gemm_q4_k_rb<1, 4, 3, 2>",

@@ -124,7 +124,8 @@ RAGGED = [(synth.Q8_0, 100, 512, M) for M in (1, 2, 5, 17, 33, 65, 200)] + \
          [(synth.Q8_0, 8200, 1024, 5), (synth.Q8_0, 9728, 512, 40), (synth.Q8_0, 8192, 256, 30)] + \
          [(synth.Q4_K, 2500, 4096, 40), (synth.Q4_K, 4096, 2560, 48)] + \
          [(synth.Q8_0, 2560, 9728, 16), (synth.Q8_0, 2500, 4096, 40)] + \
-         [(synth.Q8_0, 9728, 2560, 96), (synth.Q8_0, 4000, 4096, 100)]
+         [(synth.Q8_0, 9728, 2560, 96), (synth.Q8_0, 4000, 4096, 100)] + \
+         [(synth.Q4_K, 9728, 2560, 100), (synth.Q4_K, 4000, 4096, 96), (synth.Q4_K, 9728, 2560, 200)]
 # (the last: full-K tiles; Stream-K with more tiles than CUs; the streamed GEMV with a ragged last
 # row group and an odd K split, with one wave per row group, and with an even split; the Q8_0 tile
 # kernel with ragged M and N, and with an odd number of 128-wide stages; the Q4_K tile kernel with
@@ -134,7 +135,9 @@ RAGGED = [(synth.Q8_0, 100, 512, M) for M in (1, 2, 5, 17, 33, 65, 200)] + \
 # mid-M Q8_0 kernel with ragged N and M at each of its row-block counts, and with one stage per
 # pipeline; the mid-M Q4_K kernel with each tile's K split over 4 (ragged N, M) and 2 workgroups; the
 # mid-M Q8_0 kernel with K splits over 6 and (ragged N, M) 4 workgroups; the Q8_0 tile kernel with K
-# split over 2 workgroups of 10 stages (ragged M) and over 4 of 8 stages (ragged N, M))
+# split over 2 workgroups of 10 stages (ragged M) and over 4 of 8 stages (ragged N, M); the Q4_K tile
+# kernel with K split over 2 workgroups of 5 super-blocks (ragged M) and over 4 of 4 (ragged N, M); the
+# 128 x 192 register-decode kernel with K split over 2 workgroups of 5 super-blocks (ragged M))
 
 
 @pytest.mark.parametrize("gtype,N,K,M", FULL + RAGGED)
