@@ -103,8 +103,12 @@ DEV void wait_vmcnt(int n) {
 // are not serialized, so a 16-byte access per (row block, column block) is in flight at once.
 constexpr int CPOL_SC1 = 16;
 
-DEV void buf_store16(rsrc_t r, f4 v, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, v), r, voff, soff, CPOL_SC1);
+// The whole offset is in the VGPR operand (range-checked) and the scalar offset is the constant 0:
+// with a scalar-register offset the compiler inserts no wait states between a 16-byte buffer store
+// and a VALU write of its data registers, and on gfx950 such a write right behind the store was
+// seen to reach memory in place of the store's first data word.
+DEV void buf_store16(rsrc_t r, f4 v, uint32_t voff) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, v), r, voff, 0u, CPOL_SC1);
 }
 
 DEV f4 buf_load16_sc1(rsrc_t r, uint32_t voff, uint32_t soff) {
@@ -234,6 +238,9 @@ DEV uint32_t swiglu_pair2(const f4 &v, int lg) {
 // on counters[tile]; the last of the tile's parts loads the others' in one round trip and adds all
 // of them in part order (its own from LDS in its place), so the sum is the same whichever part
 // arrives last, then writes C; the counter is left at zero. flag: an LDS word outside the tile.
+// A partial tile is laid out by store instruction, not by row: 16-byte piece h (0, 1) of thread
+// chunk c at (h NCH + c) 16 bytes, so the 64 lanes of each store and load cover 1 KB contiguously
+// (row order would leave every 32-byte sector half written by each of two instructions).
 template <int BM, int BN, int NT, int MAXP, class Args>
 DEV void tile_finish(const char *lds, const Args &g, int m0, int n0, int tile, int part, int *flag) {
     constexpr int LD = BN + 4, CH = BN / 8, NCH = BM * CH, CPT = (NCH + NT - 1) / NT;  // 8-value chunks
@@ -249,9 +256,9 @@ DEV void tile_finish(const char *lds, const Args &g, int m0, int n0, int tile, i
         for (int i = 0; i < CPT; i++) {
             const int c = (int)threadIdx.x + NT * i, row = c / CH, ch = c - row * CH;
             if (c >= NCH) break;
-            const uint32_t off = (uint32_t)(row * BN + 8 * ch) * 4u;
-            buf_store16(rp, *(const f4 *)(lds + (row * LD + 8 * ch) * 4), off, own);
-            buf_store16(rp, *(const f4 *)(lds + (row * LD + 8 * ch + 4) * 4), off + 16u, own);
+            const uint32_t off = (uint32_t)c * 16u;
+            buf_store16(rp, *(const f4 *)(lds + (row * LD + 8 * ch) * 4), own + off);
+            buf_store16(rp, *(const f4 *)(lds + (row * LD + 8 * ch + 4) * 4), own + off + NCH * 16u);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
@@ -267,13 +274,13 @@ DEV void tile_finish(const char *lds, const Args &g, int m0, int n0, int tile, i
 #pragma unroll
             for (int i = 0; i < CPT; i++) {
                 const int c = (int)threadIdx.x + NT * i, row = c / CH, ch = c - row * CH;
-                const uint32_t off = (uint32_t)(row * BN + 8 * ch) * 4u;
+                const uint32_t off = (uint32_t)c * 16u;
                 const uint32_t pb = ((uint32_t)tile * (uint32_t)g.parts + (uint32_t)p) * TILE;
                 if (c >= NCH) {
                     pv[p][i][0] = pv[p][i][1] = f4{0.f, 0.f, 0.f, 0.f};
                 } else if (p < g.parts && p != part) {
                     pv[p][i][0] = buf_load16_sc1(rp, off, pb);
-                    pv[p][i][1] = buf_load16_sc1(rp, off + 16u, pb);
+                    pv[p][i][1] = buf_load16_sc1(rp, off + NCH * 16u, pb);
                 } else {
                     pv[p][i][0] = *(const f4 *)(lds + (row * LD + 8 * ch) * 4);
                     pv[p][i][1] = *(const f4 *)(lds + (row * LD + 8 * ch + 4) * 4);

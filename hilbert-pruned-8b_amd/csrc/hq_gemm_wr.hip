@@ -563,7 +563,7 @@ DEV void wr_tile(const WrArgs &g) {
             if (vec) {
                 if (g.c_f32) {
                     if (g.accumulate) v += *(const f4 *)((const float *)g.C + idx);
-                    buf_store16(rc, v, (uint32_t)(idx * 4), 0u);
+                    buf_store16(rc, v, (uint32_t)(idx * 4));
                 } else {
                     if (g.accumulate) {
                         const h4 o = *(const h4 *)((const _Float16 *)g.C + idx);

@@ -344,7 +344,7 @@ __global__ void __launch_bounds__(W8_NT) k_gemm_q8_0_wr(Wr8Args g) {
             if (vec) {
                 if (g.c_f32) {
                     if (g.accumulate) v += *(const f4 *)((const float *)g.C + idx);
-                    buf_store16(rc, v, (uint32_t)(idx * 4), 0u);
+                    buf_store16(rc, v, (uint32_t)(idx * 4));
                 } else {
                     if (g.accumulate) {
                         const h4 o = *(const h4 *)((const _Float16 *)g.C + idx);

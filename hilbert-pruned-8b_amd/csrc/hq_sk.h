@@ -150,7 +150,7 @@ DEV void finish_tile(f4 (&acc)[MB][NB], const SkPlan &p, int w, int u0, int u1, 
 #pragma unroll
     for (int i = 0; i < MB; i++)
 #pragma unroll
-        for (int j = 0; j < NB; j++) buf_store16(rpart, acc[i][j], (uint32_t)tid * 16u, slot * PER + (i * NB + j) * NT * 16);
+        for (int j = 0; j < NB; j++) buf_store16(rpart, acc[i][j], (uint32_t)tid * 16u + slot * PER + (i * NB + j) * NT * 16);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     const int wf = sk_owner(p, t0), wl = sk_owner(p, t1 - 1);
