@@ -484,15 +484,13 @@ int device_cus(int device, int *n_cu) {
     return 0;
 }
 
-// GEMM workspace of an M-row hq_gemm on W's device and `stream` (swiglu: also the activation
-// sub-block sums of hq_launch_gemm_swiglu's fused Q4_K path). A counter array that grows is zeroed
-// once here, synchronously; the kernels leave every counter back at zero.
-int gemm_work(const hq_mat *W, int M, void *stream, HqGemmWork *wk, bool swiglu = false) {
+// GEMM workspace of an M-row hq_gemm on W's device and `stream`. A counter array that grows is
+// zeroed once here, synchronously; the kernels leave every counter back at zero.
+int gemm_work(const hq_mat *W, int M, void *stream, HqGemmWork *wk) {
     int n_cu;
     if (device_cus(W->device, &n_cu)) return -1;
     size_t pb, cb, sb;
     hq_gemm_work_bytes(&W->m, M, n_cu, &pb, &cb, &sb);
-    if (swiglu && W->m.type == HQ_TYPE_Q4_K) sb = std::max(sb, (size_t)M * (W->m.cols / 256) * 32);
     void *part, *cnt, *sums = nullptr;
     int grew = 0;
     if (staging(W->device, stream, 5, pb, &part) || staging(W->device, stream, 6, cb, &cnt, &grew)) return -1;
@@ -687,7 +685,7 @@ extern "C" int hq_gemm_swiglu(const hq_mat *pair, const uint16_t *A, int M, uint
         HqGemmWork wk = {};
         int fused = 0;
         if (mc > 1) {
-            if (gemm_work(pair, mc, stream, &wk, true)) return -1;
+            if (gemm_work(pair, mc, stream, &wk)) return -1;
             HIPCK(hq_launch_gemm_swiglu(&pair->m, Ap, mc, Op, wk, S(stream), &fused));
         }
         if (fused) continue;

@@ -22,12 +22,16 @@
 // Arithmetic (no weight is ever rounded to 16 bits). Column n's accumulators hold its dot products
 // in units of c_u = d_u (the super-block scale; 1 where d_u = 0) during super-block u: the main B
 // operand is then the integer s*q (<= 945, exact in fp16; 0 where d_u = 0), where a super-block
-// begins the accumulators are multiplied by c_{u-1} / c_u (fp32), and at the end by c_{U-1}. The min
-// term -dmin * sum_sub m_sub * S_sub (S_sub = fp32 sum of the sub-block's 32 activations, from
-// k_asums as bf16 hi + lo) is one bf16 MFMA per (row block, column block, super-block): A slots hold
-// S_hi, S_lo, S_hi, S_lo of the 8 sub-blocks, B slots Bh, Bh, Bl, Bl with x = -dmin * m / c_u
+// ends the accumulators are multiplied by c_u / c_{u+1} (fp32), and at the end by c_{U-1}. The min
+// term -dmin * sum_sub m_sub * S_sub (S_sub = fp32 sum of the sub-block's 32 activations, as bf16
+// hi + lo) is one bf16 MFMA per (row block, column block, super-block), after the rescale: A slots
+// hold S_hi, S_lo, S_hi, S_lo of the 8 sub-blocks, B slots Bh, Bh, Bl, Bl with x = -dmin * m / c
 // (fp32), Bh = bf16(x), Bl = bf16(x - Bh); the four products sum to S * x to about 2^-16 relative
-// (bf16 keeps fp32's exponent range, so no S or x overflows).
+// (bf16 keeps fp32's exponent range, so no S or x overflows). Q4_K: the producers form S from the
+// staged activation tiles, so a super-block's min step runs at its end, once both of its stages are
+// in LDS, in the next one's units (c = c_{u+1}; c_U = c_{U-1}). Q5_K (whose producers have no
+// VALU time to spare for the sums): S comes from k_asums in HBM and the min step runs at the
+// super-block's start, in its own units (c = c_u; the rescale by c_{u-1} / c_u comes first).
 //
 // LDS layouts (16-byte slots; a stage row is 128 k = 16 slots):
 //   A tile [128 rows][16 slots], slot p of row r at p ^ (r & 15);
@@ -51,10 +55,10 @@ struct WsArgs {
     const uint8_t *W;  // Q4_K super-blocks, row n at n * row_bytes
     uint32_t row_bytes;
     const uint16_t *A;  // fp16 [M][K]
-    const uint16_t *S;  // activation sub-block sums [M][K/256][16] (k_asums)
     int M, N, K;
     void *C;
     int c_f32, accumulate;
+    const uint16_t *S;  // Q5_K: activation sub-block sums [M][K/256][16] (k_asums); Q4_K: unused
     int mt, nt;  // M-tiles, N-tiles
     // K split: each tile's super-blocks are cut into `parts` contiguous ranges, one workgroup each;
     // with parts > 1 every part stores its fp32 tile in partials[tile][part] and the last to arrive
@@ -138,6 +142,7 @@ DEV void ws_q4_tile(const WsArgs &g) {
     constexpr int SLOT = T == HQ_TYPE_Q5_K ? 176 : 144, QS = T == HQ_TYPE_Q5_K ? 48 : 16;
     constexpr int QL = T == HQ_TYPE_Q5_K ? 2 : 1;  // quant loads per column and stage
     using QR = std::conditional_t<T == HQ_TYPE_Q5_K, u4v, u2v>;  // Q5_K: qs bytes in .xy, qh bytes in .zw
+    constexpr bool SUMS = T == HQ_TYPE_Q4_K;  // the producers form the activation sums
     constexpr int BN = 32 * NB;
     using L = WsLds<NB>;
     __shared__ __attribute__((aligned(256))) char lds[L::TOTAL];  // fragment addresses XOR bits 6-7
@@ -162,21 +167,21 @@ DEV void ws_q4_tile(const WsArgs &g) {
     const int M = g.M, N = g.N, K = g.K, UT = K / 256;
     const int u0 = part * UT / g.parts, U = (part + 1) * UT / g.parts - u0;
     const uint8_t *const Wb = g.W + (size_t)u0 * SLOT;
-    const uint16_t *const Ab = g.A + (size_t)u0 * 256, *const Sb = g.S + (size_t)u0 * 16;
+    const uint16_t *const Ab = g.A + (size_t)u0 * 256, *const Sb = SUMS ? g.A : g.S + (size_t)u0 * 16;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const rsrc_t ra = make_rsrc(Ab, (uint32_t)((size_t)M * K * 2 - (size_t)u0 * 512));
     const rsrc_t rw = make_rsrc(Wb, (uint32_t)((size_t)N * g.row_bytes - (size_t)u0 * SLOT));
 
     if (wave >= 4) {
         // ------------------------------------------------------------------ producers
-        // Stage s's work, done in stage s - 1: its activation tile (LDS DMA), its decoded B tile, and
-        // in an odd stage the next super-block's S tile and min-term operands. Vector-memory
+        // Stage s's work, done in stage s - 1: its activation tile (LDS DMA) and its decoded B tile; in
+        // an odd stage the min-term operands of the super-block it ends (Q4_K, with its activation
+        // sums) or of the next one (Q5_K, with its S tile from HBM). Vector-memory
         // instructions are spread over the decode of the thread's columns (the texture path takes
         // ~20 clocks per instruction per CU, so a burst of them would stall the wave for the whole
         // burst); the end-of-stage wait covers the DMAs only (loads issued after them retire later).
         const int pw = __builtin_amdgcn_readfirstlane(wave - 4);  // wave-uniform LDS targets
         const int pt = tid - 256, xi = pt & 7;
-        const rsrc_t rs = make_rsrc(Sb, (uint32_t)((size_t)M * UT * 32 - (size_t)u0 * 32));
         // activation DMA: instruction qq of wave pw fills rows 4(pw + 4qq) .. +4 (1 KB); lane l takes
         // row 4(pw + 4qq) + l/16, LDS slot l % 16, global chunk (l % 16) ^ (row & 15) (the row in the
         // VGPR offset, the one a buffer load range-checks: rows past M read zeros, none past A's end)
@@ -185,9 +190,45 @@ DEV void ws_q4_tile(const WsArgs &g) {
         auto dma_a = [&](int s, int qq) {
             dma16(ra, sA(s & 1) + (pw + 4 * qq) * 512, a_voff + (uint32_t)(qq * 16 * K * 2), (uint32_t)(s * WS_KS * 2));
         };
-        // S tile of unit u: 32 rows (1 KB) per wave; lane l: row 32pw + l/2, half l % 2
+        // Q5_K: S tile of unit u from HBM, 32 rows (1 KB) per wave; lane l: row 32pw + l/2, half l % 2
+        const rsrc_t rs = make_rsrc(Sb, SUMS ? 0u : (uint32_t)((size_t)M * UT * 32 - (size_t)u0 * 32));
         const uint32_t s_voff = (uint32_t)(((m0 + 32 * pw + (lane >> 1)) * UT) * 32 + 16 * (lane & 1));
         auto dma_s = [&](int u) { dma16(rs, sS + pw * 512, s_voff, (uint32_t)(u * 32)); };
+        // Q4_K: activation sub-block sums, from the stage buffers (the consumers read the same tiles): thread
+        // pt takes row s_row = pt / 2 and, of a stage's four 32-value sub-blocks, 2 s_h and 2 s_h + 1
+        // (chunks 8 s_h .. + 7, at slots chunk ^ (row & 15)); fp32 sums in the order of the stored
+        // fp16 values, eight at a time (the reference's fp32 sum of fp16 activations); the even
+        // stage's two wait in registers for the odd stage's, then the unit's S row goes out as bf16
+        // hi, lo
+        const int s_row = pt >> 1, s_h = pt & 1;
+        auto stage_sums = [&](int buf, float &t0, float &t1) {
+            using lds_u4 = const __attribute__((address_space(3))) u4v;
+            const uint32_t base = (uint32_t)(uintptr_t)sA(buf) + (uint32_t)s_row * (WS_KS * 2);
+            u4v v[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                v[q] = *(lds_u4 *)(uintptr_t)(base + 16u * ((uint32_t)(8 * s_h + q) ^ (uint32_t)(s_row & 15)));
+            t0 = sum8(v[3], sum8(v[2], sum8(v[1], sum8(v[0], 0.f))));
+            t1 = sum8(v[7], sum8(v[6], sum8(v[5], sum8(v[4], 0.f))));
+        };
+        auto bf_pair = [](float a, float b, uint32_t &hi, uint32_t &lo) {
+            const __bf16 ha = (__bf16)a, hb = (__bf16)b;
+            const __bf16 la = (__bf16)(a - (float)ha), lb = (__bf16)(b - (float)hb);
+            hi = (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+            lo = (uint32_t)__builtin_bit_cast(uint16_t, la) | ((uint32_t)__builtin_bit_cast(uint16_t, lb) << 16);
+        };
+        float se0 = 0.f, se1 = 0.f;  // this unit's even-stage sums
+        auto write_sums = [&](float so0, float so1) {
+            using lds_u32 = __attribute__((address_space(3))) uint32_t;
+            uint32_t he, le, ho, lo;
+            bf_pair(se0, se1, he, le);
+            bf_pair(so0, so1, ho, lo);
+            const uint32_t row = (uint32_t)(uintptr_t)(sS + s_row * 16);
+            *(lds_u32 *)(uintptr_t)(row + 4u * (uint32_t)s_h) = he;          // hi of sub-blocks 2 s_h, + 1
+            *(lds_u32 *)(uintptr_t)(row + 4u * (uint32_t)(2 + s_h)) = ho;    // hi of 4 + 2 s_h, + 1
+            *(lds_u32 *)(uintptr_t)(row + 16u + 4u * (uint32_t)s_h) = le;    // lo
+            *(lds_u32 *)(uintptr_t)(row + 16u + 4u * (uint32_t)(2 + s_h)) = lo;
+        };
         // quant bytes: this thread's columns c_i = pt/8 + 32i (i < NB), half-chunk xi of each stage
         // (bytes QS + 8(8(s % 2) + xi) of super-block s/2; Q5_K also qh bytes 8(xi % 4) .. + 7, the
         // fifth bits of the same values). Four register sets: stage s's go to Q[s % 4], three stages
@@ -224,10 +265,35 @@ DEV void ws_q4_tile(const WsArgs &g) {
             const uint32_t nz = (hm.x & 0x7fffu) ? 0xffffffffu : 0u;
             *(u2v *)(sH + (buf * BN + pt) * 2) = u2v{sw0 & nz, sw1 & nz};
         };
-        // min-term operands, rescale ratio and unit of a super-block (header hm of column pt;
+        // Q4_K: min-term operands of a super-block (header hm of column pt) in the units of the next
+        // one (header hn; the last super-block: hn = hm), the rescale ratio c_u / c_{u+1} (1 for the
+        // last) and c_{u+1}
+        auto write_min = [&](const u4v hm, const u4v hn, bool last) {
+            if (!colt) return;
+            uint32_t sw0, sw1, mw0, mw1;
+            q4k_scale_words(hm.y, hm.z, hm.w, sw0, sw1, mw0, mw1);
+            const float d = h2f((uint16_t)hm.x), dmin = h2f((uint16_t)(hm.x >> 16)), dn = h2f((uint16_t)hn.x);
+            const float c_u = d != 0.0f ? d : 1.0f, c = dn != 0.0f ? dn : 1.0f, inv = 1.0f / c;
+            u4v bh, bl;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint32_t w = q < 2 ? mw0 : mw1;
+                const float x0 = (-dmin * (float)byte_of(w, 2 * (q & 1))) * inv;  // -dmin * m is exact
+                const float x1 = (-dmin * (float)byte_of(w, 2 * (q & 1) + 1)) * inv;
+                const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
+                const __bf16 l0 = (__bf16)(x0 - (float)h0), l1 = (__bf16)(x1 - (float)h1);
+                bh[q] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+                bl[q] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+            }
+            *(u4v *)(sBm + pt * 16) = bh;
+            *(u4v *)(sBm + pt * 16 + 8) = bl;
+            sR[pt] = last ? 1.0f : c_u * inv;
+            sCL[pt] = c;
+        };
+        // Q5_K: min-term operands, rescale ratio and unit of a super-block (header hm of column pt;
         // c_prev = the column's previous unit, 1 before the first)
         float c_prev = 1.0f;
-        auto write_min = [&](const u4v hm) {
+        auto write_min_start = [&](const u4v hm) {
             if (!colt) return;
             uint32_t sw0, sw1, mw0, mw1;
             q4k_scale_words(hm.y, hm.z, hm.w, sw0, sw1, mw0, mw1);
@@ -250,22 +316,23 @@ DEV void ws_q4_tile(const WsArgs &g) {
             sCL[pt] = c;
             c_prev = c;
         };
-        // The vector-memory items of a stage: 8 activation DMAs, the S DMA, a header load (into hd),
-        // NB quant loads (into qd; s_* / u_* < 0: item absent); item k is issued before column
-        // k * NB / (10 + NB) of the decode. Whatever is issued after the DMAs may still be in flight
-        // at the end of the stage: a load has until the end of the next stage.
+        // The vector-memory items of a stage: 8 activation DMAs, (Q5_K) the S DMA, a header load
+        // (into hd), NB quant loads (into qd; s_* / u_* < 0: item absent); item k is issued before
+        // column k * NB / NI of the decode. Whatever is issued after the DMAs may still be in flight at
+        // the end of the stage: a load has until the end of the next stage.
+        constexpr int KH = SUMS ? 8 : 9, NI = KH + 1 + NB;  // the header's item, items
         auto issue = [&](int i, int s_dma, int u_s, int u_h, u4v &hd, int s_q, QR (&qd)[NB]) {
 #pragma unroll
-            for (int k = 0; k < 10 + NB; k++) {
-                if (k * NB / (10 + NB) != i) continue;
+            for (int k = 0; k < NI; k++) {
+                if (k * NB / NI != i) continue;
                 if (k < 8) {
                     if (s_dma >= 0) dma_a(s_dma, k);
-                } else if (k == 8) {
+                } else if (k < KH) {
                     if (u_s >= 0) dma_s(u_s);
-                } else if (k == 9) {
+                } else if (k == KH) {
                     if (u_h >= 0) load_hdr(hd, u_h);
                 } else if (s_q >= 0) {
-                    load_q(qd, s_q, k - 10);
+                    load_q(qd, s_q, k - KH - 1);
                 }
             }
         };
@@ -332,19 +399,30 @@ DEV void ws_q4_tile(const WsArgs &g) {
         using i0 = std::integral_constant<int, 0>;
         using i1 = std::integral_constant<int, 1>;
         const int S2 = 2 * U;  // stages
-        // prologue, phase 1: headers of units 0 and 1, stage 0's quants, stage 0's activation tile and
-        // unit 0's S tile, all in flight together (the compiler waits for the outstanding DMAs before
-        // the LDS writes that follow, so they cost one memory latency, not two); unit 0's scale words
-        // and min-term operands; the quants of stages 1 and 2, the header of unit 2
+        // prologue, phase 1: headers of units 0 and 1, stage 0's quants and activation tile (Q5_K:
+        // and unit 0's S tile), all in flight together (the compiler waits for the outstanding DMAs
+        // before the LDS writes that follow, so they cost one memory latency, not two); unit 0's scale
+        // words; the min-term tiles of the consumers' first min step: Q4_K, "unit -1" (zero S and
+        // Bmin, ratio 1), Q5_K, unit 0's; the quants of stages 1 and 2, the header of unit 2
         load_hdr(H[0], 0);
         load_hdr(H[1], U > 1 ? 1 : 0);
 #pragma unroll
         for (int i = 0; i < NB; i++) load_q(Q[0], 0, i);
 #pragma unroll
         for (int k = 0; k < 8; k++) dma_a(0, k);
-        dma_s(0);
+        if constexpr (!SUMS) dma_s(0);
         write_scales(H[0], 0);
-        write_min(H[0]);
+        if constexpr (SUMS) {
+            *(u4v *)(sS + pt * 8) = u4v{0u, 0u, 0u, 0u};
+            if (colt) {
+                *(u4v *)(sBm + pt * 16) = u4v{0u, 0u, 0u, 0u};
+                *(u4v *)(sBm + pt * 16 + 8) = u4v{0u, 0u, 0u, 0u};
+                sR[pt] = 1.0f;
+            }
+        } else {
+            write_min_start(H[0]);
+        }
+        u4v hcur = H[0];  // Q4_K: header of the super-block whose min-term operands go out next
 #pragma unroll
         for (int i = 0; i < NB; i++) load_q(Q[1], 1, i);
 #pragma unroll
@@ -361,18 +439,35 @@ DEV void ws_q4_tile(const WsArgs &g) {
             const int t = 2 * u;
             const bool q3 = t + 3 < S2, q4 = t + 4 < S2, nx = u + 1 < U, h3 = u + 3 < U;
             // stage 2u: decode stage 2u + 1 (this unit, odd half); activation tile 2u + 1; quants
-            // of stage 2u + 3; the next unit's scale words
+            // of stage 2u + 3; the next unit's scale words; Q4_K: the sums of stage 2u (buffer 0)
             decode(i1{}, std::integral_constant<int, P>{}, Q[(2 * P + 1) & 3], t + 1, -1, -1, H[P], q3 ? t + 3 : -1,
                    Q[(2 * P + 3) & 3]);
             if (nx) write_scales(H[P ^ 1], P ^ 1);
+            if constexpr (SUMS) stage_sums(0, se0, se1);
             end_stage(q3 ? QL * NB : 0);
-            if (!nx) return;  // the last stage has nothing to stage
-            // stage 2u + 1: the next unit's min-term operands (its header's last use: the register then
-            // takes the header of unit u + 3); decode stage 2u + 2 (next unit, even half); activation
-            // tile 2u + 2, the next unit's S tile, header u + 3, quants of stage 2u + 4
-            write_min(H[P ^ 1]);
-            decode(i0{}, std::integral_constant<int, P ^ 1>{}, Q[(2 * P + 2) & 3], t + 2, u + 1, h3 ? u + 3 : -1,
-                   H[P ^ 1], q4 ? t + 4 : -1, Q[(2 * P) & 3]);
+            // stage 2u + 1, Q4_K: this unit's S tile (with the sums of stage 2u + 1, buffer 1) and
+            // min-term operands in the next unit's units (read by the consumers' min step at this
+            // stage's end); Q5_K: the next unit's min-term operands (its S tile comes by DMA below)
+            if constexpr (SUMS) {
+                float so0, so1;
+                stage_sums(1, so0, so1);
+                write_sums(so0, so1);
+                if (!nx) {  // the last stage: nothing else to stage; the LDS writes land before its barrier
+                    write_min(hcur, hcur, true);
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    return;
+                }
+                write_min(hcur, H[P ^ 1], false);
+                hcur = H[P ^ 1];
+            } else {
+                if (!nx) return;  // the last stage has nothing to stage
+                write_min_start(H[P ^ 1]);
+            }
+            // (the next unit's header's last use here: the register then takes the header of unit
+            // u + 3); decode stage 2u + 2 (next unit, even half); activation tile 2u + 2, (Q5_K) the
+            // next unit's S tile, header u + 3, quants of stage 2u + 4
+            decode(i0{}, std::integral_constant<int, P ^ 1>{}, Q[(2 * P + 2) & 3], t + 2, SUMS ? -1 : u + 1,
+                   h3 ? u + 3 : -1, H[P ^ 1], q4 ? t + 4 : -1, Q[(2 * P) & 3]);
             end_stage((q4 ? QL * NB : 0) + (h3 ? 1 : 0));
         };
         int u = 0;
@@ -495,9 +590,11 @@ DEV void ws_q4_tile(const WsArgs &g) {
             l2_touch(rw_pf, voff, pf_lds);
         }
     };
-    // per super-block: its min k-step, 4 k-steps of the even stage (buffer 0), 4 of the odd stage
-    // (buffer 1). The last k-step also reads the next super-block's min operands; after the last
-    // super-block those reads return stale LDS contents that are never used.
+    // per super-block: a min k-step (Q4_K: the previous super-block's, before the first with zero
+    // operands and ratio 1; Q5_K: its own), 4 k-steps of the even stage (buffer 0), 4 of the odd stage
+    // (buffer 1); the last k-step reads the next min k-step's operands. Q4_K: the last super-block's
+    // min k-step follows the loop; Q5_K: after the last super-block those reads return stale LDS
+    // contents that are never used.
     for (int u = 0; u < U; u++) {
         if (u + 3 < U) prefetch(u + 3);
         kstep(WsStep<1, 2, 0, false, 0, 0>{});  // P = 1: E0's A fragments go to fa[0]
@@ -510,6 +607,7 @@ DEV void ws_q4_tile(const WsArgs &g) {
         kstep(WsStep<0, 1, 2, false, 1, 3>{});
         kstep(WsStep<1, 1, 3, true, 2, 0>{});
     }
+    if constexpr (SUMS) kstep(WsStep<1, 2, 0, false, 0, 0>{});  // the last super-block's min k-step (ratio 1)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the prefetches
     // back to true units: multiply by the last super-block's c (written with its min-term tiles)
 #pragma unroll
@@ -1048,6 +1146,7 @@ int hq_ws_choose(int M, int N, int n_cu, float *eff) {
 
 hipError_t hq_launch_gemm_ws(const hq_dev_mat *W, const uint16_t *A, const uint16_t *S, int M, void *C, int c_f32,
                              int accumulate, int nb, int parts, float *partials, int *counters, hipStream_t st) {
+    if (W->type == HQ_TYPE_Q5_K && !S) return hipErrorInvalidValue;
     WsArgs g;
     g.W = W->qs, g.row_bytes = (uint32_t)W->row_bytes, g.A = A, g.S = S;
     g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;

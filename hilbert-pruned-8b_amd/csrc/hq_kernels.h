@@ -67,10 +67,10 @@ hipError_t hq_launch_swiglu_pairs(const float *C, uint16_t *out, size_t n_out, h
 // rows x columns of one GEMM output tile (M >= 2) on a device with n_cu CUs
 void hq_gemm_tile_shape(int type, int M, int N, int K, int n_cu, int *rows, int *cols);
 void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, size_t n);
-// Full-K tile Q4_K GEMM (hq_gemm_ws.hip): the tile width (32 * nb columns) for an M x N problem on
-// n_cu CUs and the fraction of CU time its tiles fill; the launch (S = k_asums output for A; each
-// tile's K split into `parts` workgroups when parts > 1, with fp32 partial tiles and per-tile
-// counters as for Stream-K).
+// Full-K tile Q4_K / Q5_K GEMM (hq_gemm_ws.hip): the tile width (32 * nb columns) for an M x N problem
+// on n_cu CUs and the fraction of CU time its tiles fill; the launch (S: Q5_K, the k_asums output for
+// A; Q4_K forms its activation sums in the kernel and takes none; each tile's K split into `parts`
+// workgroups when parts > 1, with fp32 partial tiles and per-tile counters as for Stream-K).
 int hq_ws_choose(int M, int N, int n_cu, float *eff);
 hipError_t hq_launch_gemm_ws(const hq_dev_mat *W, const uint16_t *A, const uint16_t *S, int M, void *C, int c_f32,
                              int accumulate, int nb, int parts, float *partials, int *counters, hipStream_t st);

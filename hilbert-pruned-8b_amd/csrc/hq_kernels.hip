@@ -1495,7 +1495,8 @@ void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_by
         *partial_bytes = tiles * rparts * 64 * 64 * sizeof(float);
         *counter_bytes = tiles * sizeof(int);
     }
-    *sums_bytes = (c.wide && !c.wr) || c.rbm ? (size_t)M * (W->cols / KC) * 32 : 0;  // (wr forms its own)
+    // (the Q4_K tile kernels wr, ws form their own)
+    *sums_bytes = (c.wide && !c.wr && !(c.ws_nb && W->type == HQ_TYPE_Q4_K)) || c.rbm ? (size_t)M * (W->cols / KC) * 32 : 0;
     if (c.wr8) *partial_bytes = *counter_bytes = 0;  // (no K split)
     if (c.wr) {  // K split: one fp32 128 x 192 tile per (tile, part)
         const size_t tiles = (size_t)((M + 127) / 128) * ((W->rows + 191) / 192);
@@ -1505,14 +1506,14 @@ void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_by
 }
 
 // Pre-pass of a GEMM (the activation sub-block sums of the Q4_K kernels that read them from HBM;
-// nothing otherwise: the one-round tile kernel k_gemm_q4_k_wr forms its own).
+// nothing otherwise: the Q4_K tile kernels k_gemm_q4_k_wr and k_gemm_q4_k_ws form their own).
 hipError_t hq_launch_gemm_pre(const hq_dev_mat *W, const uint16_t *A, int M, const HqGemmWork &wk, hipStream_t st) {
     const GemmCfg c = gemm_cfg(W, M, wk.n_cu);
     if (c.rbm) {
         const size_t nsub = (size_t)M * (W->cols / 32);
         k_asums<true, true><<<grid_for(nsub, 256, 16384), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
     }
-    if (c.wide && !c.wr) {
+    if (c.wide && !c.wr && !(c.ws_nb && W->type == HQ_TYPE_Q4_K)) {
         const size_t nsub = (size_t)M * (W->cols / 32);
         if (nsub >= ((size_t)1 << 31)) return hipErrorInvalidValue;
         if (c.ws_nb || c.bt) k_asums<true><<<grid_for(nsub, 256, 16384), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
@@ -1595,7 +1596,11 @@ hipError_t hq_launch_gemm_swiglu(const hq_dev_mat *W, const uint16_t *A, int M, 
     }
     float eff = 0.f;
     const int nb = hq_ws_choose(M, N, wk.n_cu, &eff);
-    if ((W->type == HQ_TYPE_Q4_K || W->type == HQ_TYPE_Q5_K) && wk.sums) {
+    if (W->type == HQ_TYPE_Q4_K && (size_t)M * K * 2 < ((size_t)1 << 32)) {
+        *fused = 1;
+        return hq_launch_gemm_ws(W, A, nullptr, M, out, HQ_OUT_SWIGLU, 0, nb, 1, nullptr, nullptr, st);
+    }
+    if (W->type == HQ_TYPE_Q5_K && wk.sums) {  // (the sums buffer of its own plan's tile kernel)
         const size_t nsub = (size_t)M * (W->cols / 32);
         if (nsub >= ((size_t)1 << 31)) return hipSuccess;
         k_asums<true><<<grid_for(nsub, 256, 16384), 256, 0, st>>>(A, M, K, wk.sums);

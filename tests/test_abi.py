@@ -96,10 +96,12 @@ def test_gemm_workspace_bytes():
     assert hq.gemm_workspace_bytes(synth.Q4_K, 16384, 2560, 9216)[3]
     assert not hq.gemm_workspace_bytes(synth.Q4_K, 131072, 256, 9216)[3]  # 151 MB of sub-block sums
     # the k-quant tile kernel (Q6_K, M = 512, N = 2560, K = 9728): 4 x 16 tiles of 128 x 160 with K
-    # split over 4 workgroups; the Q5_K tile kernel (M = 512, N = 9728): sub-block sums only; the Q8_0
-    # tile kernel at M = 96 (one row tile): 102 tiles of 128 x 96 with K split over 2 workgroups
+    # split over 4 workgroups; the Q5_K tile kernel (M = 512, N = 9728): sub-block sums only; the Q4_K
+    # tile kernel at M = 128 (one row tile): 102 tiles of 128 x 96 with K split over 2 workgroups, no
+    # sums (it forms them itself); the Q8_0 tile kernel at M = 96: the same split
     assert hq.gemm_workspace_bytes(synth.Q6_K, 512, 2560, 9728) == (64 * 4 * 128 * 160 * 4, 64 * 4, 0, True)
     assert hq.gemm_workspace_bytes(synth.Q5_K, 512, 9728, 2560) == (0, 0, 512 * 10 * 32, True)
+    assert hq.gemm_workspace_bytes(synth.Q4_K, 128, 9728, 2560) == (102 * 2 * 128 * 96 * 4, 102 * 4, 0, True)
     assert hq.gemm_workspace_bytes(synth.Q8_0, 96, 9728, 2560) == (102 * 2 * 128 * 96 * 4, 102 * 4, 0, True)
     with pytest.raises(hq.HQError, match="type 9"):
         hq.gemm_workspace_bytes(9, 512, 256, 256)
