@@ -127,15 +127,17 @@ def bench_gemm(hq, synth, gtype, N, K, M, c_f32, steps, warmup, stream, eager_wa
 
 def bench_config4(hq, synth, stream, M=16384, reading="baseline"):
     """Config 4: the hybrid 4B projection sequence (32 layers) at M = 16384; each distinct shape timed
-    once (3 launches), total = sum over the sequence. reading: BASELINE's literal widths or the
-    reference's layer_weights() list (synth.hybrid_4b_projections)."""
+    as the median of MEDIAN_REPS graph replays of 3 launches after SETTLE_S of untimed calls, total =
+    sum over the sequence. reading: BASELINE's literal widths or the reference's layer_weights() list
+    (synth.hybrid_4b_projections)."""
     counts = {}
     for layer in synth.hybrid_4b_projections(reading):
         for _, n, k in layer:
             counts[(n, k)] = counts.get((n, k), 0) + 1
     total_us, flop, shapes = 0.0, 0.0, []
     for (n, k), cnt in sorted(counts.items()):
-        r = bench_gemm(hq, synth, synth.Q4_K, n, k, M, False, 3, 1, stream, rotate=False)
+        r = bench_gemm(hq, synth, synth.Q4_K, n, k, M, False, 3, 1, stream, rotate=False, settle_s=SETTLE_S,
+                       reps=MEDIAN_REPS)
         total_us += cnt * r["us"]
         flop += cnt * 2.0 * M * n * k
         shapes.append({"N": n, "K": k, "count": cnt, "us": round(r["us"], 2), "tflops": round(r["tflops"], 1),
