@@ -8,17 +8,18 @@ replays of exactly `steps` launches, timed with HIP events on the launch stream,
 eager launches, 0.3 s of untimed launches and one untimed replay: five such replays, each graph
 continuing the weight rotation, a HIP event between replays; `ms_per_step` and `value` come from the
 median of the five per-launch times (`us_first_replay` is the first replay alone). `us_median` and
-the roofline's `kernel_us` are the same median over five replays of 20-launch graphs. The headline
-is also timed with fp32 C (`headline_fp32_c`), the output mode the parity bar covers and the
-reference's output type.
+the roofline's `kernel_us` are medians over five replays of 20-launch graphs of whole calls and of
+the main kernel alone; the three kinds of replay are interleaved (one of each per round), so clock
+drift during the measurement moves them alike. The headline is also timed with fp32 C
+(`headline_fp32_c`), the output mode the parity bar covers and the reference's output type.
 
 Also reported (key "sweep"): the config 2 / 3 M sweeps and the config 5 option readout, each as
 achieved TFLOP/s and GB/s of algorithmic bytes (W blocks once + A + C) and their roofline fractions,
 and config 4 (the 4B-class hybrid's 32-layer projection sequence at M = 16384, BASELINE's literal
 widths: each distinct projection shape timed, weighted by its count in the sequence).
 
-roofline: the headline GEMM's main kernel (k_gemm_q4_k_wr<3>: full-K 128 x 192 tiles), timed alone
-(hq_time_gemm_kernel; the Q4_K activation pre-pass runs once outside the timed graphs) with HIP
+roofline: the headline GEMM's main kernel (k_gemm_q4_k_wr160: full-K 128 x 160 tiles), timed alone
+(hq_time_gemm_kernel; a pre-pass, where the plan has one, runs once outside the timed graphs) with HIP
 events on its stream, median of five replays of 20 launches; `traffic` is its HBM bytes per launch from the committed rocprofv3
 FETCH_SIZE / WRITE_SIZE summary (calibrated against a device copy of known size), null when that
 summary was taken for a different kernel.
@@ -102,12 +103,21 @@ def bench_gemm(hq, synth, gtype, N, K, M, c_f32, steps, warmup, stream, eager_wa
                 i += 1
             stream.sync()
     t0 = time.perf_counter()
-    ms = hq.time_gemm(mats, A, M, C, c_f32, steps, reps, stream)
+    ms_first = ms_med = ms_kernel = None
+    if kernel_time and M > 1:
+        # whole calls and the main kernel alone, replays interleaved (each rep: one graph of `steps`
+        # calls, one of MEDIAN_ITERS calls, one of MEDIAN_ITERS main-kernel launches), so that clock
+        # drift during the measurement moves all three alike; medians over the reps
+        calls, meds, kerns = [], [], []
+        for _ in range(max(reps, 1)):
+            calls.append(hq.time_gemm(mats, A, M, C, c_f32, steps, 1, stream))
+            meds.append(hq.time_gemm(mats, A, M, C, c_f32, MEDIAN_ITERS, 1, stream))
+            kerns.append(hq.time_gemm_kernel(mats, A, M, C, c_f32, MEDIAN_ITERS, 1, stream))
+        ms, ms_first = statistics.median(calls), calls[0]
+        ms_med, ms_kernel = statistics.median(meds), statistics.median(kerns)
+    else:
+        ms = hq.time_gemm(mats, A, M, C, c_f32, steps, reps, stream)
     wall = time.perf_counter() - t0
-    ms_first = hq.time_gemm(mats, A, M, C, c_f32, steps, 1, stream) if reps > 1 and kernel_time else None
-    ms_med = hq.time_gemm(mats, A, M, C, c_f32, MEDIAN_ITERS, MEDIAN_REPS, stream) if kernel_time else None
-    ms_kernel = (hq.time_gemm_kernel(mats, A, M, C, c_f32, MEDIAN_ITERS, MEDIAN_REPS, stream)
-                 if (kernel_time and M > 1) else None)
     for m in mats:
         m.free()
     A.free(), C.free()
