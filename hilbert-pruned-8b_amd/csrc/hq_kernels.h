@@ -127,7 +127,8 @@ hipError_t hq_launch_gemm_q6k(const GemmArgs &g, int mb, hipStream_t st);
 hipError_t hq_launch_dequant_kq(const hq_dev_mat *W, uint32_t row0, const uint32_t *ids, uint32_t nrows, float *out,
                                 hipStream_t st);
 hipError_t hq_launch_gemv_kq(const hq_dev_mat *W, const uint16_t *a, void *C, int c_f32, int accumulate, hipStream_t st);
-int hq_sb_rows(int n_out);  // rows per wave of that GEMV and gather for n_out rows
+int hq_sb_rows(int n_out);       // rows per wave of that GEMV and gather for n_out rows
+int hq_sb_lds(int type, int K);  // whether that GEMV copies its activation vector into LDS
 hipError_t hq_launch_gather_kq(const hq_dev_mat *W, const uint16_t *H, const uint32_t *ids, int B, int k, float *out,
                                hipStream_t st);
 hipError_t hq_launch_gemm_kq(int type, const GemmArgs &g, int mb, hipStream_t st);

@@ -1433,8 +1433,8 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
     W.ldd = type == HQ_TYPE_Q8_0 ? (K / 32 + 7) / 8 * 8 : 0;
     W.row_bytes = shape_row_bytes(type, K);
     const char *kq = type == HQ_TYPE_Q2_K ? "10" : type == HQ_TYPE_Q3_K ? "11" : type == HQ_TYPE_Q5_K ? "13" : nullptr;
-    if (M == 1 && (kq || type == HQ_TYPE_Q6_K)) {  // template arguments: the ggml type, rows per wave
-        snprintf(buf, n, "k_gemv_sb<%d, %d, false>", type, hq_sb_rows(N));
+    if (M == 1 && (kq || type == HQ_TYPE_Q6_K)) {  // template arguments: the ggml type, rows per wave, gather, LDS copy of a
+        snprintf(buf, n, "k_gemv_sb<%d, %d, false, %s>", type, hq_sb_rows(N), hq_sb_lds(type, K) ? "true" : "false");
         return;
     }
     const GemmCfg c = gemm_cfg(&W, M, n_cu);

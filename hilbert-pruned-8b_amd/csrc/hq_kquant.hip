@@ -66,22 +66,35 @@ struct SbRaw {
     u4v a[4];
 };
 
-// Loads of eighth p of the super-block at blk (device slot) and of its 256 activations a.
+// Loads of eighth p of the super-block at blk (device slot) and of its 256 activations a (global
+// memory, or the workgroup's LDS copy of the vector).
 //   Q2_K, Q3_K, Q6_K: values 128 h + 32 j + l0 .. + 7 for j = 0 .. 3 (h = p / 4, l0 = 8 (p % 4)).
 //   Q5_K: values 16 (p % 2) .. + 15 of sub-blocks 2 (p / 2) and 2 (p / 2) + 1.
+typedef const __attribute__((address_space(3))) uint16_t lds_u16c;
+DEV u4v ld_a16(const uint16_t *p) { return *(const u4v *)p; }
+DEV u4v ld_a16(lds_u16c *p) { return *(const __attribute__((address_space(3))) u4v *)p; }
+template <int T, class AP>
+DEV void sb_load_a(SbRaw &x, AP a, int p) {
+    if constexpr (T == HQ_TYPE_Q5_K) {
+        const int sp = p >> 1, l0 = 16 * (p & 1);
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            x.a[2 * t] = ld_a16(a + 32 * (2 * sp + t) + l0);
+            x.a[2 * t + 1] = ld_a16(a + 32 * (2 * sp + t) + l0 + 8);
+        }
+    } else {
+        const int h = p >> 2, l0 = 8 * (p & 3);
+#pragma unroll
+        for (int j = 0; j < 4; j++) x.a[j] = ld_a16(a + 128 * h + 32 * j + l0);
+    }
+}
 template <int T>
-DEV SbRaw sb_load(const uint8_t *__restrict__ blk, const uint16_t *__restrict__ a, int p) {
-    SbRaw x;
+DEV void sb_load_w(SbRaw &x, const uint8_t *__restrict__ blk, int p) {
     if constexpr (T == HQ_TYPE_Q5_K) {
         const int sp = p >> 1, l0 = 16 * (p & 1);
         x.w0 = *(const u4v *)blk;                          // d, dmin, scales[12]
         x.w1 = *(const u4v *)(blk + 48 + 32 * sp + l0);    // qs
         x.w2 = *(const u4v *)(blk + 16 + l0);              // qh
-#pragma unroll
-        for (int t = 0; t < 2; t++) {
-            x.a[2 * t] = *(const u4v *)(a + 32 * (2 * sp + t) + l0);
-            x.a[2 * t + 1] = *(const u4v *)(a + 32 * (2 * sp + t) + l0 + 8);
-        }
     } else {
         const int h = p >> 2, l0 = 8 * (p & 3);
         if constexpr (T == HQ_TYPE_Q2_K) {
@@ -100,10 +113,7 @@ DEV SbRaw sb_load(const uint8_t *__restrict__ blk, const uint16_t *__restrict__ 
             x.w1 = u4v{q0.x, q0.y, q1.x, q1.y};
             x.w2 = u4v{qh.x, qh.y, (uint32_t)*(const uint16_t *)(blk + 208), 0u};  // qh, d
         }
-#pragma unroll
-        for (int j = 0; j < 4; j++) x.a[j] = *(const u4v *)(a + 128 * h + 32 * j + l0);
     }
-    return x;
 }
 
 // The lane task's dot product from its loaded bytes. For Q2_K, Q3_K, Q6_K the scale of group j is
@@ -176,14 +186,20 @@ DEV float sb_dot(const SbRaw &x, int p) {
 // GATHER = false: C[o] = dot(W[o], a) for o < n_out = N (store_out modes). GATHER = true:
 // out[o] = dot(W[ids[o]], a + (o / k_opts) K) for o < n_out = B k; an id >= rows stores NaN (its lanes
 // read row 0). Rows of a wave past n_out compute row n_out - 1 and store nothing.
-template <int T, int RW, bool GATHER>
+// LDSA (GEMV): the workgroup copies the activation vector into LDS once (dynamic shared memory of
+// 2 K bytes) and every lane reads its activations from there: the lanes of a row together read 2 K
+// bytes of activations per row against K / 4 .. 7 K / 8 bytes of weights, so from L2 / L1 they
+// would set the pace. The first weight loads are issued before the copy.
+template <int T, int RW, bool GATHER, bool LDSA>
 __global__ void __launch_bounds__(256) k_gemv_sb(const uint8_t *__restrict__ W, size_t row_bytes,
                                                  const uint16_t *__restrict__ a, const uint32_t *__restrict__ ids,
                                                  int n_out, int k_opts, int K, uint32_t rows, void *C, int c_f32,
                                                  int accumulate) {
+    static_assert(!(GATHER && LDSA), "the gather reads one activation vector per state");
+    extern __shared__ __attribute__((aligned(16))) uint16_t sb_act[];
     constexpr int S = 8 / RW, G = 8 * S;  // super-blocks side by side, lanes per row
     const int lane = threadIdx.x & 63, o0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RW;
-    if (o0 >= n_out) return;
+    if (!LDSA && o0 >= n_out) return;
     const int p = lane & 7, s = (lane >> 3) & (S - 1), o = o0 + lane / G, oc = min(o, n_out - 1);
     uint32_t row = (uint32_t)oc;
     const uint16_t *av = a;
@@ -196,10 +212,26 @@ __global__ void __launch_bounds__(256) k_gemv_sb(const uint8_t *__restrict__ W, 
     const uint8_t *base = W + (size_t)row * row_bytes;
     float acc = 0.f;
     int u = min(s, nsb - 1);
-    SbRaw x = sb_load<T>(base + (size_t)u * kq_slot(T), av + 256 * u, p);
+    SbRaw x;
+    sb_load_w<T>(x, base + (size_t)u * kq_slot(T), p);
+    auto act = [&]() {
+        if constexpr (LDSA) return (lds_u16c *)(uintptr_t)(uint32_t)(uintptr_t)sb_act;
+        else return av;
+    }();
+    if constexpr (LDSA) {
+        // every wave takes part (waves past n_out leave after the barrier)
+        using lds_u4 = __attribute__((address_space(3))) u4v;
+        for (int i = threadIdx.x; i < K / 8; i += 256)
+            *(lds_u4 *)(uintptr_t)((uint32_t)(uintptr_t)sb_act + 16u * (uint32_t)i) = *(const u4v *)(a + 8 * i);
+        __syncthreads();
+        if (o0 >= n_out) return;
+    }
+    sb_load_a<T>(x, act + 256 * u, p);
     for (u = s; u < nsb; u += S) {
         const int un = min(u + S, nsb - 1);  // the next super-block (the last one again at the end)
-        const SbRaw y = sb_load<T>(base + (size_t)un * kq_slot(T), av + 256 * un, p);
+        SbRaw y;
+        sb_load_w<T>(y, base + (size_t)un * kq_slot(T), p);
+        sb_load_a<T>(y, act + 256 * un, p);
         acc += sb_dot<T>(x, p);
         x = y;
     }
@@ -217,7 +249,15 @@ hipError_t launch_sb(const hq_dev_mat *W, const uint16_t *a, const uint32_t *ids
                      int accumulate, hipStream_t st) {
     const int R = hq_sb_rows(n_out);
     const unsigned grid = (unsigned)(((n_out + R - 1) / R + 3) / 4);
-#define SB(r) k_gemv_sb<T, r, GATHER><<<grid, 256, 0, st>>>(W->qs, W->row_bytes, a, ids, n_out, k_opts, (int)W->cols, W->rows, C, c_f32, accumulate)
+    // the GEMV's activation vector in LDS (up to 64 KB: K <= 32768; not Q5_K, whose lanes read 16
+    // contiguous values per sub-block and measured no faster from LDS)
+    const bool lds = hq_sb_lds(T, (int)W->cols) && !GATHER;
+    const size_t shm = lds ? (size_t)W->cols * 2 : 0;
+#define SB(r)                                                                                                          \
+    if (lds) k_gemv_sb<T, r, GATHER, !GATHER><<<grid, 256, shm, st>>>(W->qs, W->row_bytes, a, ids, n_out, k_opts,        \
+                                                                     (int)W->cols, W->rows, C, c_f32, accumulate);    \
+    else k_gemv_sb<T, r, GATHER, false><<<grid, 256, 0, st>>>(W->qs, W->row_bytes, a, ids, n_out, k_opts, (int)W->cols, \
+                                                             W->rows, C, c_f32, accumulate)
     switch (R) {
     case 1: SB(1); break;
     case 2: SB(2); break;
@@ -452,6 +492,9 @@ hipError_t hq_launch_dequant_kq(const hq_dev_mat *W, uint32_t row0, const uint32
 // rows per wave of k_gemv_sb (GEMV and gather): two at n_out >= 8192 (K = 2560: 2432 waves), else one
 // (K = 9728, N = 2560: eight super-blocks side by side); measured over 1 .. 8 rows on both headline shapes
 int hq_sb_rows(int n_out) { return n_out >= 8192 ? 2 : 1; }
+
+// whether the k-quant GEMV stages its activation vector in LDS (k_gemv_sb<T, RW, false, true>)
+int hq_sb_lds(int type, int K) { return type != HQ_TYPE_Q5_K && K <= 32768; }
 
 hipError_t hq_launch_gemv_kq(const hq_dev_mat *W, const uint16_t *a, void *C, int c_f32, int accumulate, hipStream_t st) {
     const int n = (int)W->rows;

@@ -130,9 +130,10 @@ def test_gemm_kernel_names():
              (synth.Q4_K, 1, 2560, 9728): "k_gemv_q4_k_s<4>", (synth.Q4_K, 1, 100, 512): "k_gemv_q4_k_s<1>",
              (synth.Q4_K, 1, 9728, 256): "k_gemv_q4_k_s<16>", (synth.Q8_0, 1, 9728, 2560): "k_gemv_q8_0<2>",
              (synth.Q8_0, 1, 100, 512): "k_gemv_q8_0<1>",
-             # k-quant GEMVs: rows per wave, 2 at N >= 8192
-             (synth.Q6_K, 1, 9728, 2560): "k_gemv_sb<14, 2, false>", (synth.Q3_K, 1, 2560, 9728): "k_gemv_sb<11, 1, false>",
-             (synth.Q5_K, 1, 100, 2048): "k_gemv_sb<13, 1, false>", (synth.Q2_K, 1, 100, 20480): "k_gemv_sb<10, 1, false>",
+             # k-quant GEMVs: rows per wave, 2 at N >= 8192; the activation vector in LDS but for Q5_K
+             (synth.Q6_K, 1, 9728, 2560): "k_gemv_sb<14, 2, false, true>", (synth.Q3_K, 1, 2560, 9728): "k_gemv_sb<11, 1, false, true>",
+             (synth.Q5_K, 1, 100, 2048): "k_gemv_sb<13, 1, false, false>", (synth.Q2_K, 1, 100, 20480): "k_gemv_sb<10, 1, false, true>",
+             (synth.Q2_K, 1, 100, 33024): "k_gemv_sb<10, 1, false, false>",
              # Q6_K / Q3_K / Q2_K above M = 64: the LDS-decode tile kernel (template: the ggml type, tile width / 32)
              (synth.Q6_K, 512, 9728, 2560): "k_gemm_kq_ws<14, 5>", (synth.Q3_K, 128, 9728, 2560): "k_gemm_kq_ws<11, 2>",
              (synth.Q2_K, 512, 9728, 2560): "k_gemm_kq_ws<10, 5>",

@@ -50,9 +50,10 @@ def test_upload_round_trip_and_dequant(hqlib, oracle, gtype):
 CASES = [(9728, 2560, M) for M in (1, 2, 16, 33, 64, 512)] + \
         [(100, 512, M) for M in (1, 5, 17, 65)] + [(2560, 9728, 1), (2560, 9728, 64), (1000, 256, 3)] + \
         [(2560, 9728, 512), (9728, 2560, 300), (200, 20480, 1)] + \
-        [(9728, 2560, 96), (4000, 4096, 100)]
-# (the last five: the tile kernel with K split in 4, ragged M; a GEMV over a long K; the tile kernel
-# with K split in 2 parts of 10 stages, ragged M, and in 4 parts of 8 stages, ragged M and N)
+        [(9728, 2560, 96), (4000, 4096, 100), (100, 33024, 1)]
+# (the last six: the tile kernel with K split in 4, ragged M; a GEMV over a long K; the tile kernel
+# with K split in 2 parts of 10 stages, ragged M, and in 4 parts of 8 stages, ragged M and N; a GEMV
+# whose activation vector (K > 32768) stays in global memory)
 
 
 @pytest.mark.parametrize("gtype", TYPES)
