@@ -111,6 +111,20 @@ DEV void buf_store16(rsrc_t r, f4 v, uint32_t voff) {
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, v), r, voff, 0u, CPOL_SC1);
 }
 
+// 16 bytes of an fp16 activation vector, from global memory or from a workgroup's LDS copy
+typedef const __attribute__((address_space(3))) uint16_t lds_u16c;
+DEV u4v ld_a16(const uint16_t *p) { return *(const u4v *)p; }
+DEV u4v ld_a16(lds_u16c *p) { return *(const __attribute__((address_space(3))) u4v *)p; }
+// Copy of the K fp16 values at a into LDS at lds (K % 8 == 0) by the workgroup's NT threads; the caller
+// waits at a barrier before reading it. Returns the copy's LDS pointer.
+template <int NT>
+DEV lds_u16c *stage_act(const uint16_t *__restrict__ a, int K, uint16_t *lds) {
+    using lds_u4 = __attribute__((address_space(3))) u4v;
+    const uint32_t base = (uint32_t)(uintptr_t)lds;
+    for (int i = threadIdx.x; i < K / 8; i += NT) *(lds_u4 *)(uintptr_t)(base + 16u * (uint32_t)i) = *(const u4v *)(a + 8 * i);
+    return (lds_u16c *)(uintptr_t)base;
+}
+
 DEV f4 buf_load16_sc1(rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, CPOL_SC1));
 }

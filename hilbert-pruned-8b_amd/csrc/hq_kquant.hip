@@ -70,9 +70,6 @@ struct SbRaw {
 // memory, or the workgroup's LDS copy of the vector).
 //   Q2_K, Q3_K, Q6_K: values 128 h + 32 j + l0 .. + 7 for j = 0 .. 3 (h = p / 4, l0 = 8 (p % 4)).
 //   Q5_K: values 16 (p % 2) .. + 15 of sub-blocks 2 (p / 2) and 2 (p / 2) + 1.
-typedef const __attribute__((address_space(3))) uint16_t lds_u16c;
-DEV u4v ld_a16(const uint16_t *p) { return *(const u4v *)p; }
-DEV u4v ld_a16(lds_u16c *p) { return *(const __attribute__((address_space(3))) u4v *)p; }
 template <int T, class AP>
 DEV void sb_load_a(SbRaw &x, AP a, int p) {
     if constexpr (T == HQ_TYPE_Q5_K) {
@@ -215,16 +212,12 @@ __global__ void __launch_bounds__(256) k_gemv_sb(const uint8_t *__restrict__ W, 
     SbRaw x;
     sb_load_w<T>(x, base + (size_t)u * kq_slot(T), p);
     auto act = [&]() {
-        if constexpr (LDSA) return (lds_u16c *)(uintptr_t)(uint32_t)(uintptr_t)sb_act;
+        if constexpr (LDSA) return stage_act<256>(a, K, sb_act);  // every wave takes part
         else return av;
     }();
     if constexpr (LDSA) {
-        // every wave takes part (waves past n_out leave after the barrier)
-        using lds_u4 = __attribute__((address_space(3))) u4v;
-        for (int i = threadIdx.x; i < K / 8; i += 256)
-            *(lds_u4 *)(uintptr_t)((uint32_t)(uintptr_t)sb_act + 16u * (uint32_t)i) = *(const u4v *)(a + 8 * i);
         __syncthreads();
-        if (o0 >= n_out) return;
+        if (o0 >= n_out) return;  // (waves past n_out leave after the barrier)
     }
     sb_load_a<T>(x, act + 256 * u, p);
     for (u = s; u < nsb; u += S) {
