@@ -197,9 +197,9 @@ DEV void ws_q4_tile(const WsArgs &g) {
         // Q4_K: activation sub-block sums, from the stage buffers (the consumers read the same tiles): thread
         // pt takes row s_row = pt / 2 and, of a stage's four 32-value sub-blocks, 2 s_h and 2 s_h + 1
         // (chunks 8 s_h .. + 7, at slots chunk ^ (row & 15)); fp32 sums in the order of the stored
-        // fp16 values, eight at a time (the reference's fp32 sum of fp16 activations); the even
-        // stage's two wait in registers for the odd stage's, then the unit's S row goes out as bf16
-        // hi, lo
+        // fp16 values, eight at a time (the order of the k_asums pre-pass, so S is the same bits);
+        // the even stage's two wait in registers for the odd stage's, then the unit's S row goes out
+        // as bf16 hi, lo
         const int s_row = pt >> 1, s_h = pt & 1;
         auto stage_sums = [&](int buf, float &t0, float &t1) {
             using lds_u4 = const __attribute__((address_space(3))) u4v;
