@@ -46,10 +46,16 @@
 
 namespace {
 constexpr int WR_BM = 128, WR_KS = 64, WR_NT = 512, WR_RING = 4;
+// activation operand read-ahead in groups (< WR_AF; reads of the next stage start after its barrier)
+// and the ring they land in: 7 of 8 takes the 128-row tile kernel to 220 VGPRs (two waves per SIMD
+// still) and saved 2 % at M = 512, N = 9728, K = 2560 against 3 of 4 in a same-box A/B
 #ifndef WR_AD
-#define WR_AD 3  // activation operand read-ahead in groups (< WR_AF; reads of the next stage start after its barrier)
+#define WR_AD 7
 #endif
-constexpr int WR_AF = 4;
+#ifndef WR_AFN
+#define WR_AFN 8
+#endif
+constexpr int WR_AF = WR_AFN;
 static_assert(WR_AD < WR_AF && 16 - WR_AD > 6 && 16 % WR_AF == 0, "activation read-ahead");
 
 struct WrArgs {
