@@ -1209,12 +1209,13 @@ namespace {
 // in the last-level cache, and a slice of A), then chunks of columns. `fill` when the launches'
 // tiles fill at least 70 % of the CU time.
 struct WrPlan {
-    int row_tiles, col_tiles, launches;
+    int row_tiles, col_tiles, launches, tw;  // tw: tile width in columns (192, or 160 for k_gemm_q4_k_wr160)
     bool fill;
 };
-WrPlan wr_plan(int M, int N, int n_cu) {
+WrPlan wr_plan(int M, int N, int n_cu, int tw = 192) {
     WrPlan w;
-    const int mt = (M + 127) / 128, nt = (N + 191) / 192, per_xcd = std::max(1, n_cu / 8), ncx = (nt + 7) / 8;
+    w.tw = tw;
+    const int mt = (M + 127) / 128, nt = (N + tw - 1) / tw, per_xcd = std::max(1, n_cu / 8), ncx = (nt + 7) / 8;
     if (mt * ncx <= per_xcd) {
         w.row_tiles = mt, w.col_tiles = nt;
     } else if (ncx <= per_xcd) {
@@ -1230,7 +1231,7 @@ WrPlan wr_plan(int M, int N, int n_cu) {
 // t0 .. t1 - 1
 template <class F>
 hipError_t wr_launches(const WrPlan &pl, int M, int N, F &&launch) {
-    const int mt = (M + 127) / 128, nt = (N + 191) / 192;
+    const int mt = (M + 127) / 128, nt = (N + pl.tw - 1) / pl.tw;
     for (int r = 0; r < mt; r += pl.row_tiles)
         for (int t = 0; t < nt; t += pl.col_tiles) {
             const int m0 = 128 * r;
@@ -1583,15 +1584,21 @@ hipError_t hq_launch_gemm_swiglu(const hq_dev_mat *W, const uint16_t *A, int M, 
     // fill at least 70 % of the CU time (M = 512, pair matrix of I = 9728: 4 x 102 tiles as two
     // launches; measured faster than one launch of two rounds); the Q4_K one needs its upload-time
     // column tables
+    // The Q4_K kernel takes 160-column tiles where they need no more launches than 192-column ones
+    // (M = 512, I = 9728: two launches of 4 x 122 / 2 tiles, 244 of 256 CUs, instead of 204)
     const bool wr8 = W->type == HQ_TYPE_Q8_0 && hq_wr8_fits(W, M), wr4 = W->type == HQ_TYPE_Q4_K && W->tab && hq_wr_fits(W, M);
-    const WrPlan pl = wr_plan(M, N, wk.n_cu);
+    WrPlan pl = wr_plan(M, N, wk.n_cu);
+    if (wr4) {
+        const WrPlan p160 = wr_plan(M, N, wk.n_cu, 160);
+        if (p160.fill && p160.launches <= pl.launches) pl = p160;
+    }
     if (pl.fill && (wr8 || wr4)) {
         *fused = 1;
         return wr_launches(pl, M, N, [&](int m0, int rows, int t0, int t1) {
             const uint16_t *Am = A + (size_t)m0 * K;
             uint16_t *om = out + (size_t)m0 * (N / 2);
             return wr8 ? hq_launch_gemm_wr8(W, Am, rows, om, HQ_OUT_SWIGLU, 0, t0, t1, st)
-                       : hq_launch_gemm_wr(W, Am, rows, om, HQ_OUT_SWIGLU, 0, t0, t1, 1, nullptr, nullptr, st);
+                       : hq_launch_gemm_wr(W, Am, rows, om, HQ_OUT_SWIGLU, 0, t0, t1, 1, nullptr, nullptr, st, pl.tw);
         });
     }
     float eff = 0.f;

@@ -2,9 +2,9 @@
 gate/up pair matrix (hq_mat_upload_pair + hq_gemm_swiglu), through the C ABI, against the oracle's
 gate and up matmuls: silu(g) * u in float64, the GPU's fp16 output within half an ulp of |y| on top
 of the 1e-2 bar. M > 64 runs the fused epilogue of the full-K tile kernels (the product never
-leaves the tile: the register-decode kernels k_gemm_q4_k_wr / k_gemm_q8_0_wr where their 128 x 192
-tiles fill the CUs, e.g. M = 512 at I = 9728, else the LDS-decode kernels); other M run one GEMM for
-both halves and a separate epilogue pass."""
+leaves the tile: the register-decode kernels k_gemm_q4_k_wr / k_gemm_q4_k_wr160 / k_gemm_q8_0_wr where
+their 128 x 192 or 128 x 160 tiles fill the CUs, e.g. M = 512 at I = 9728, else the LDS-decode
+kernels); other M run one GEMM for both halves and a separate epilogue pass."""
 import numpy as np
 import pytest
 
@@ -23,8 +23,8 @@ CASES = [(synth.Q4_K, 9728, 2560, M) for M in (1, 16, 64, 65, 512)] + \
          (synth.Q4_K, 2560, 9728, 300)] + \
         [(synth.Q4_K, 9728, 1024, 448), (synth.Q8_0, 9728, 1024, 500), (synth.Q4_K, 9720, 512, 512),
          (synth.Q8_0, 9720, 512, 512)]
-# (the last four: the register-decode tile kernels' epilogue over two rounds of 128 x 192 tiles, with
-# a ragged last row tile, and with a ragged last column tile: 2 x 9720 = 101 x 192 + 48)
+# (the last four: the register-decode tile kernels' epilogue over two launches, with a ragged last row
+# tile, and with a ragged last column tile: 2 x 9720 = 101 x 192 + 48 = 121 x 160 + 80)
 
 
 @pytest.mark.parametrize("gtype,I,K,M", CASES)
