@@ -263,11 +263,11 @@ DEV void wr_tile(const WrArgs &g) {
     auto rdq = [&](int buf, int j) {
         return *(const __attribute__((address_space(3))) u2v *)(uintptr_t)(q_lane[j] + (uint32_t)(buf * L::Q_BYTES));
     };
-    // scale word p / 2 of operand j in record slot v, shifted to sub-blocks 2p, 2p + 1 in its low bytes
+    // the scales of sub-blocks 2p, 2p + 1 of operand j in record slot v (16 bits of scale word p / 2,
+    // read as such: no shift, which the compiler would place right behind the read and wait for)
     auto rdsw = [&](int p, int v, int j) {
-        return *(const __attribute__((address_space(3))) uint32_t *)(uintptr_t)(lds0 + (uint32_t)(L::T_REC + (v * G::RC + c0[j] + ln) * 16 +
-                                                                                                   (p >> 1) * 4)) >>
-               ((p & 1) * 16);
+        return (uint32_t) * (const __attribute__((address_space(3))) uint16_t *)(uintptr_t)(lds0 + (uint32_t)(L::T_REC + (v * G::RC + c0[j] + ln) * 16 +
+                                                                                                             (p >> 1) * 4 + (p & 1) * 2));
     };
     const uint32_t s_lane = lds0 + (uint32_t)(L::S + ln * 32 + 16 * (lg & 1));
     const uint32_t s_lo = s_lane + (uint32_t)(4 * hr * 16 * 32), s_hi = s_lane - (uint32_t)(4 * hr * 16 * 32);
@@ -398,14 +398,20 @@ DEV void wr_tile(const WrArgs &g) {
     u2v qc[NB];
     h2 muh[NB], adh[NB];
 #pragma unroll
-    for (int k = 0; k < WR_AD; k++) af[k] = rd(0, k);
-#pragma unroll
     for (int j = 0; j < NB; j++) {
         qc[j] = rdq(0, j);
         h2 mu, ad;
         scales(rdsw(0, 0, j), mu, ad);  // (super-block 0's records: slot 0)
         muh[j] = h2{mu.y, mu.y}, adh[j] = h2{ad.y, ad.y};
         b0[j] = decode8<false>(qc[j], h2{mu.x, mu.x}, h2{ad.x, ad.x});
+    }
+    // the activation reads last and in group order, as the loop leaves them pending at its back edge
+    // (the wait before the loop's first MFMA then counts the same on both ways in)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < WR_AD; k++) {
+        af[k] = rd(0, k);
+        __builtin_amdgcn_sched_barrier(0);
     }
     h8 bm[NB], sa[3];
     f4 r[NB];
@@ -469,15 +475,17 @@ DEV void wr_tile(const WrArgs &g) {
                     const int pn = (p + 1) & 3, un = p == 3 ? rsn : rs;
 #pragma unroll
                     for (int j = 0; j < NB; j++) qc[j] = rdq(nxt, j), swn[j] = rdsw(pn, un, j);
-                    // at p = 3 this super-block's Bmin (landed by this barrier; the loaders rewrite it
-                    // from p = 1 of the next one) and its rescale factor F = c_u / c_{u+1}
-                    if (p == 3)
-#pragma unroll
-                        for (int j = 0; j < NB; j++) {
-                            bm[j] = rdbm(j);
-                            r[j] = rdr(j, rs, 2);
-                        }
                 }
+                // at p = 3 this super-block's rescale factor F = c_u / c_{u+1} and its Bmin (landed by the
+                // barrier; the loaders rewrite Bmin from p = 1 of the next one), one group each after
+                // the barrier's reads (one burst would exceed what an LDS wait count can leave
+                // outstanding, and the next MFMA would wait for part of it)
+                if (p == 3 && gg == 7)
+#pragma unroll
+                    for (int j = 0; j < NB; j++) r[j] = rdr(j, rs, 2);
+                if (p == 3 && gg == 8)
+#pragma unroll
+                    for (int j = 0; j < NB; j++) bm[j] = rdbm(j);
                 // the next stage's scales and k-step 0 weights (b0 is free after group 7), half a
                 // column block per group
                 if (gg >= 9 && gg < 9 + 2 * NB) {
