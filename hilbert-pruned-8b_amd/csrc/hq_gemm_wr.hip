@@ -120,47 +120,12 @@ DEV void wr_dec_half(h8 &b, u2v q, int hf, uint32_t mask, h2 mul, h2 add) {
 }
 
 
-// Output through LDS (tiles of a whole K, fp32 C, or fp16 C without accumulate, rows of 16-byte
-// multiples): the MFMA waves put their accumulators into LDS as C's element type (rows of BN
-// elements, a row stride 16 bytes longer so that the 16 rows of a block start 4 banks apart), then all
-// 8 waves store whole 16-byte pieces, consecutive lanes on consecutive bytes of a row, so that an
-// instruction writes whole 128-byte lines (a store from the accumulators covers 16 rows x 32 or 64
-// bytes). Rows past M are skipped; the piece that crosses column N is stored element by element.
-template <int BN, int ES>
-struct WrOut {
-    static constexpr int ROW = BN * ES, LDR = ROW + 16, CPR = ROW / 16;  // bytes per row, LDS row stride, pieces per row
-    static_assert((WR_BM * CPR) % WR_NT == 0, "store pieces per thread");
-};
-DEV bool wr_staged(const WrArgs &g) {
-    return (g.c_f32 == 1 || (g.c_f32 == 0 && !g.accumulate)) && ((size_t)g.N * (g.c_f32 ? 4 : 2)) % 16 == 0 &&
-           ((uintptr_t)g.C & 15u) == 0;
-}
-template <int BN, int ES>
-DEV void wr_store_tile(const char *lds, const WrArgs &g, int m0, int n0, int tid) {
-    using O = WrOut<BN, ES>;
-    const int M = g.M, N = g.N;
-    const rsrc_t rc = make_rsrc(g.C, (uint32_t)((size_t)M * N * ES));
-#pragma unroll
-    for (int k = 0; k < WR_BM * O::CPR / WR_NT; k++) {
-        const int c = tid + k * WR_NT, row = c / O::CPR, pc = c - row * O::CPR;
-        const int n = n0 + pc * (16 / ES);
-        if (m0 + row >= M) continue;
-        f4 v = *(const f4 *)(lds + row * O::LDR + pc * 16);
-        const uint32_t off = (uint32_t)(((size_t)(m0 + row) * N + n) * ES);
-        if (n + 16 / ES <= N) {
-            if (ES == 4 && g.accumulate) v += *(const f4 *)((const float *)g.C + off / 4);
-            buf_store16(rc, v, off);
-        } else if (n < N) {
-            for (int e = 0; e < N - n; e++) {
-                if (ES == 4) {
-                    float *q = (float *)g.C + off / 4 + e;
-                    *q = g.accumulate ? *q + v[e] : v[e];
-                } else {
-                    ((uint16_t *)g.C)[off / 2 + e] = __builtin_bit_cast(u4v, v)[e / 2] >> (16 * (e & 1));
-                }
-            }
-        }
-    }
+// the store phase of an fp16 output tile staged in LDS (tile_store_rows)
+template <int BN>
+DEV void wr_store(const char *lds, const WrArgs &g, int m0, int n0, int tid) {
+    const uint32_t pitch = (uint32_t)g.N * 2u;
+    tile_store_rows<WR_BM, WR_NT, BN * 2>(lds, (char *)g.C + (size_t)m0 * pitch, min(WR_BM, g.M - m0), pitch, (uint32_t)n0 * 2u,
+                                          (uint32_t)min(BN, g.N - n0) * 2u, tid);
 }
 
 // The tile body; KS: with the K split (parts > 1; the split-only work is compiled out of the whole-K
@@ -171,7 +136,7 @@ DEV void wr_tile(const WrArgs &g) {
     using G = WrGeo<TW>;
     constexpr int NB = 3, BN = L::BN;
     static_assert(!(KS && G::SPLIT), "the K split runs 192-column tiles");
-    static_assert(WR_BM * WrOut<BN, 4>::LDR <= L::TOTAL, "output tile in LDS");
+    static_assert(WR_BM * tile_ldr<BN * 2>() <= L::TOTAL, "output tile in LDS");
     __shared__ __attribute__((aligned(256))) char lds[L::TOTAL];
     // tile and K part: XCD x = b % 8 takes column units x, x + 8, ... (unit = N-tile x parts + part);
     // its slots run over the M-tiles of one unit first (the unit's weight slab is then fetched once
@@ -430,12 +395,11 @@ DEV void wr_tile(const WrArgs &g) {
             wr_barrier();
             wr_barrier();
             tile_finish<WR_BM, BN, WR_NT, 4>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::T_REC));
-        } else if (wr_staged(g)) {
+        } else if (tile_store_ok(g.c_f32, g.accumulate, g.N, g.C)) {
             // the same two meetings, then store the tile with them
             wr_barrier();
             wr_barrier();
-            if (g.c_f32) wr_store_tile<BN, 4>(lds, g, m0, n0, tid);
-            else wr_store_tile<BN, 2>(lds, g, m0, n0, tid);
+            wr_store<BN>(lds, g, m0, n0, tid);
         }
         return;
     }
@@ -591,33 +555,22 @@ DEV void wr_tile(const WrArgs &g) {
         tile_finish<WR_BM, BN, WR_NT, 4>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::T_REC));
         return;
     }
-    if (wr_staged(g)) {
+    // fp16 C through LDS (tile_store_rows) where C allows it: the accumulators as fp16 at their rows
+    // and columns, then all 8 waves store
+    if (tile_store_ok(g.c_f32, g.accumulate, g.N, g.C)) {
         wr_barrier();  // every wave is done with the rings, sums and tables
-        const int row_l = ln;
-        if (g.c_f32) {
-            using O = WrOut<BN, 4>;
 #pragma unroll
-            for (int i = 0; i < 8; i++)
+        for (int i = 0; i < 8; i++)
 #pragma unroll
-                for (int j = 0; j < NB; j++)
-                    if (G::has(i, j))
-                        *(f4 *)(lds + (16 * rb_of(i) + row_l) * O::LDR + (c0[j] + 4 * lg) * 4) = acc[i][j];
-        } else {
-            using O = WrOut<BN, 2>;
-#pragma unroll
-            for (int i = 0; i < 8; i++)
-#pragma unroll
-                for (int j = 0; j < NB; j++)
-                    if (G::has(i, j)) {
-                        const f4 v = acc[i][j];
-                        *(h4 *)(lds + (16 * rb_of(i) + row_l) * O::LDR + (c0[j] + 4 * lg) * 2) =
-                            h4{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
-                    }
-        }
+            for (int j = 0; j < NB; j++) {
+                if (!G::has(i, j)) continue;
+                const int row = 16 * rb_of(i) + ln;
+                const f4 v = acc[i][j];
+                *(h4 *)(lds + row * tile_ldr<BN * 2>() + (c0[j] + 4 * lg) * 2) = h4{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+            }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         wr_barrier();
-        if (g.c_f32) wr_store_tile<BN, 4>(lds, g, m0, n0, tid);
-        else wr_store_tile<BN, 2>(lds, g, m0, n0, tid);
+        wr_store<BN>(lds, g, m0, n0, tid);
         return;
     }
     // (vector stores write through to memory: SC1, measured faster than write-back here, where every

@@ -64,6 +64,14 @@ struct Wr8Lds {
 };
 
 DEV void w8_barrier() { asm volatile("s_barrier" ::: "memory"); }
+// the store phase of an fp16 output tile staged in LDS (tile_store_rows)
+DEV void w8_store(const char *lds, const Wr8Args &g, int m0, int n0, int tid) {
+    constexpr int BN = Wr8Lds::BN;
+    static_assert(W8_BM * tile_ldr<BN * 2>() <= Wr8Lds::TOTAL, "output tile in LDS");
+    const uint32_t pitch = (uint32_t)g.N * 2u;
+    tile_store_rows<W8_BM, W8_NT, BN * 2>(lds, (char *)g.C + (size_t)m0 * pitch, min(W8_BM, g.M - m0), pitch, (uint32_t)n0 * 2u,
+                                          (uint32_t)min(BN, g.N - n0) * 2u, tid);
+}
 // a loader wave's wait before a barrier: every LDS DMA but the last n issued
 template <int n>
 DEV void w8_wait() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory"); }
@@ -214,6 +222,13 @@ __global__ void __launch_bounds__(W8_NT) k_gemm_q8_0_wr(Wr8Args g) {
             }
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last (clamped, unused) loads
+        if (tile_store_ok(g.c_f32, g.accumulate, g.N, g.C)) {
+            // meet the MFMA waves once they are done with the rings and once their tile is in LDS,
+            // then store it with them
+            w8_barrier();
+            w8_barrier();
+            w8_store(lds, g, m0, n0, tid);
+        }
         return;
     }
 
@@ -307,6 +322,23 @@ __global__ void __launch_bounds__(W8_NT) k_gemm_q8_0_wr(Wr8Args g) {
         }
     }
     w8_mfma_drain();
+    // fp16 C through LDS (tile_store_rows) where C allows it: the accumulators as fp16 at their rows
+    // and columns, then all 8 waves store
+    if (tile_store_ok(g.c_f32, g.accumulate, g.N, g.C)) {
+        w8_barrier();  // every wave is done with the rings and scales
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+#pragma unroll
+            for (int j = 0; j < NB; j++) {
+                const int row = 16 * i + ln, col = wc0 + 16 * j;
+                const f4 v = acc[i][j];
+                *(h4 *)(lds + row * tile_ldr<BN * 2>() + (col + 4 * lg) * 2) = h4{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+            }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        w8_barrier();
+        w8_store(lds, g, m0, n0, tid);
+        return;
+    }
     // lane (ln, lg) of block (i, j) holds row 16i + ln, columns 16j + 4lg .. + 3 of the wave's columns
     // (one 16-byte fp32 or 8-byte fp16 store; element by element at the matrix edge or where N % 4 or
     // C's alignment does not allow it). Vector stores write through to memory (SC1), measured faster
