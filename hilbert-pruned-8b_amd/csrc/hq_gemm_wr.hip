@@ -91,16 +91,19 @@ struct WrGeo {
     static constexpr bool has(int i, int j) { return !SPLIT || j < 2 || i < 4; }
 };
 
+// (the tables first: their reads then take their constant offsets in the instruction's 16-bit offset
+// field; the activation ring's reads do from their own base)
 template <int TW>
 struct WrLds {
     static constexpr int BN = TW;
-    static constexpr int A = 0, A_BYTES = WR_BM * WR_KS * 2;            // per ring slot
-    static constexpr int Q = WR_RING * A_BYTES, Q_BYTES = BN * 32;       // quant groups per ring slot
-    static constexpr int S = Q + WR_RING * Q_BYTES, S_BYTES = WR_BM * 32;  // per parity
-    static constexpr int T_BM = S + 2 * S_BYTES;                         // column tables: Bmin [BN][32 B],
-    static constexpr int T_REC = T_BM + BN * 32;                         // records [3][192][16 B]
-    static constexpr int TOTAL = T_REC + 3 * WrGeo<TW>::RC * 16;
+    static constexpr int T_REC = 0;                                       // column tables: records [3][192][16 B],
+    static constexpr int T_BM = T_REC + 3 * WrGeo<TW>::RC * 16;           // Bmin [BN][32 B]
+    static constexpr int S = T_BM + BN * 32, S_BYTES = WR_BM * 32;        // sub-block sums, per parity
+    static constexpr int Q = S + 2 * S_BYTES, Q_BYTES = BN * 32;          // quant groups per ring slot
+    static constexpr int A = Q + WR_RING * Q_BYTES, A_BYTES = WR_BM * WR_KS * 2;  // activations per ring slot
+    static constexpr int TOTAL = A + WR_RING * A_BYTES;
     static_assert(TOTAL <= 160 * 1024, "LDS budget");
+    static_assert(T_BM + BN * 32 <= 65536, "table offsets in the offset field");
 };
 
 DEV void wr_barrier() { asm volatile("s_barrier" ::: "memory"); }
@@ -300,13 +303,14 @@ DEV void wr_tile(const WrArgs &g) {
     for (int i = 0; i < 8; i++)
 #pragma unroll
         for (int j = 0; j < NB; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
-    // decode scales of stage p: (s_lo, s_hi) of sub-blocks 2p, 2p + 1 -> multipliers and addends for
-    // the low (x) and high (y) nibbles
+    // decode scales of stage p: (s_lo, s_hi) of sub-blocks 2p, 2p + 1 -> multipliers (s_lo, s_hi / 16)
+    // and addends (-1024 s_lo, -64 s_hi) for the low (x) and high (y) nibbles: the scales as the fp16
+    // (1024 + s), then one fma for both multipliers ((1024 + s) / 16 - 64 = s / 16, exact) and one
+    // product for both addends
     auto scales = [&](uint32_t w, h2 &mu, h2 &ad) {
-        const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-        const h2 sp = as_h2(__builtin_amdgcn_perm(0x64646464u, w, 0x04010400u)) - k1024;
-        mu = sp * h2{(_Float16)1.0f, (_Float16)0.0625f};
-        ad = sp * h2{(_Float16)-1024.0f, (_Float16)-64.0f};
+        const h2 x = as_h2(__builtin_amdgcn_perm(0x64646464u, w, 0x04010400u));
+        mu = __builtin_elementwise_fma(x, h2{(_Float16)1.0f, (_Float16)0.0625f}, h2{(_Float16)-1024.0f, (_Float16)-64.0f});
+        ad = mu * h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
     };
 
     const int u_last = U - 1;
@@ -394,7 +398,7 @@ DEV void wr_tile(const WrArgs &g) {
             // in LDS, then store or reduce it with them
             wr_barrier();
             wr_barrier();
-            tile_finish<WR_BM, BN, WR_NT, 4>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::T_REC));
+            tile_finish<WR_BM, BN, WR_NT, 4>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::TOTAL - 16));
         } else if (tile_store_ok(g.c_f32, g.accumulate, g.N, g.C)) {
             // the same two meetings, then store the tile with them
             wr_barrier();
@@ -552,7 +556,7 @@ DEV void wr_tile(const WrArgs &g) {
                 *(f4 *)(lds + ((16 * i + ln) * LD + c0[j] + 4 * lg) * 4) = acc[i][j];  // (KS: TW = 192, no rotation)
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         wr_barrier();
-        tile_finish<WR_BM, BN, WR_NT, 4>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::T_REC));
+        tile_finish<WR_BM, BN, WR_NT, 4>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::TOTAL - 16));
         return;
     }
     // fp16 C through LDS (tile_store_rows) where C allows it: the accumulators as fp16 at their rows
