@@ -138,8 +138,7 @@ DEV void wr_tile(const WrArgs &g) {
     using L = WrLds<TW>;
     using G = WrGeo<TW>;
     constexpr int NB = 3, BN = L::BN;
-    static_assert(!(KS && G::SPLIT), "the K split runs 192-column tiles");
-    static_assert(WR_BM * tile_ldr<BN * 2>() <= L::TOTAL, "output tile in LDS");
+    static_assert(WR_BM * tile_ldr<BN * 2>() <= L::TOTAL && WR_BM * (BN + 4) * 4 <= L::TOTAL - 16, "output tile in LDS");
     __shared__ __attribute__((aligned(256))) char lds[L::TOTAL];
     // tile and K part: XCD x = b % 8 takes column units x, x + 8, ... (unit = N-tile x parts + part);
     // its slots run over the M-tiles of one unit first (the unit's weight slab is then fetched once
@@ -531,7 +530,10 @@ DEV void wr_tile(const WrArgs &g) {
     // N % 4 or C's alignment does not allow it)
     if constexpr (KS)
 #pragma unroll
-        for (int j = 0; j < NB; j++) acc[6][j] *= r[j], acc[7][j] *= r[j];
+        for (int j = 0; j < NB; j++) {
+            if (G::has(6, j)) acc[6][j] *= r[j];
+            if (G::has(7, j)) acc[7][j] *= r[j];
+        }
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const h8 si = rds(u_last & 1, i);
@@ -553,7 +555,7 @@ DEV void wr_tile(const WrArgs &g) {
         for (int i = 0; i < 8; i++)
 #pragma unroll
             for (int j = 0; j < NB; j++)
-                *(f4 *)(lds + ((16 * i + ln) * LD + c0[j] + 4 * lg) * 4) = acc[i][j];  // (KS: TW = 192, no rotation)
+                if (G::has(i, j)) *(f4 *)(lds + ((16 * rb_of(i) + ln) * LD + c0[j] + 4 * lg) * 4) = acc[i][j];
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         wr_barrier();
         tile_finish<WR_BM, BN, WR_NT, 4>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::TOTAL - 16));
@@ -649,6 +651,9 @@ template <int NB>
 __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr_ks(WrArgs g) {
     wr_tile<true, 64 * NB>(g);
 }
+// the K split with 160-column tiles (M = 512, N = 2560: 4 x 16 tiles x 4 parts = 256 workgroups
+// instead of 4 x 14 x 4 = 224)
+__global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr_ks160(WrArgs g) { wr_tile<true, 160>(g); }
 }  // namespace
 
 // Per-column tables of every super-block of a Q4_K matrix (one thread per row, super-blocks in order):
@@ -711,7 +716,7 @@ int hq_wr_fits(const hq_dev_mat *W, int M) {
 hipError_t hq_launch_gemm_wr(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
                              int nt0, int nt1, int parts, float *partials, int *counters, hipStream_t st, int tw) {
     if (!hq_wr_fits(W, M) || !W->tab) return hipErrorInvalidValue;  // (every uploaded Q4_K matrix has its tables)
-    if (tw != 192 && !(tw == 160 && parts == 1)) return hipErrorInvalidValue;
+    if (tw != 192 && tw != 160) return hipErrorInvalidValue;
     constexpr int NB = 3;
     WrArgs g;
     g.W = W->qs, g.row_bytes = (uint32_t)W->row_bytes, g.A = A, g.tab = W->tab;
@@ -725,12 +730,13 @@ hipError_t hq_launch_gemm_wr(const hq_dev_mat *W, const uint16_t *A, int M, void
     g.parts = parts, g.partials = partials, g.counters = counters, g.ntiles = g.mt * g.nt;
     if (parts < 1 || parts > 4 || parts > g.K / 256) return hipErrorInvalidValue;
     if (parts > 1 && (!partials || !counters || nt0 != 0 || c_f32 == HQ_OUT_SWIGLU ||
-                      (size_t)g.ntiles * parts * WR_BM * 64 * NB * 4 >= ((size_t)1 << 32)))
+                      (size_t)g.ntiles * parts * WR_BM * tw * 4 >= ((size_t)1 << 32)))
         return hipErrorInvalidValue;
     // fp32 or fp16 C, or the SwiGLU output of a gate/up pair matrix (N a multiple of 16, no accumulate)
     if (c_f32 != 0 && c_f32 != 1 && !(c_f32 == HQ_OUT_SWIGLU && W->rows % 16 == 0 && !accumulate)) return hipErrorInvalidValue;
     const unsigned grid = (unsigned)(8 * (((g.nt - g.nt0) * parts + 7) / 8) * g.mt);
-    if (parts > 1) k_gemm_q4_k_wr_ks<NB><<<grid, WR_NT, 0, st>>>(g);
+    if (parts > 1 && tw == 160) k_gemm_q4_k_wr_ks160<<<grid, WR_NT, 0, st>>>(g);
+    else if (parts > 1) k_gemm_q4_k_wr_ks<NB><<<grid, WR_NT, 0, st>>>(g);
     else if (tw == 160) k_gemm_q4_k_wr160<<<grid, WR_NT, 0, st>>>(g);
     else k_gemm_q4_k_wr<NB><<<grid, WR_NT, 0, st>>>(g);
     return hipGetLastError();

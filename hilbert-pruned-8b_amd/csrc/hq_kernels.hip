@@ -1331,15 +1331,18 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
     // M = 200, N = 9728, K = 2560: 2 x 51 x 2, 31.9 us against 36.3 for the LDS-decode kernel's split;
     // parts of 4 super-blocks measured slower than the LDS-decode kernel's, e.g. 34.4 against 29.0 us
     // at M = 512, N = 2560, K = 4096)
+    // 160-column tiles first (more workgroups in the round: M = 512, N = 2560, 4 x 16 x 4 = 256)
     if (!c.wr && c.ws_nb && c.ws_parts > 1 && hq_wr_fits(W, M)) {
-        const int mt = (M + 127) / 128, nt = ((int)W->rows + 191) / 192, per_xcd = std::max(1, n_cu / 8);
-        for (int parts = 4; !c.wr && parts >= 2; parts /= 2) {
-            const int units = nt * parts;
-            if (mt * ((units + 7) / 8) <= per_xcd && 10L * mt * units >= 7L * n_cu && (int)(W->cols / 256) >= 5 * parts) {
-                c.wr = true;
-                c.wr_parts = parts;
+        const int mt = (M + 127) / 128, per_xcd = std::max(1, n_cu / 8);
+        for (int parts = 4; !c.wr && parts >= 2; parts /= 2)
+            for (int tw = 160; !c.wr && tw <= 192; tw += 32) {
+                const int units = ((int)W->rows + tw - 1) / tw * parts;
+                if (mt * ((units + 7) / 8) <= per_xcd && 10L * mt * units >= 7L * n_cu && (int)(W->cols / 256) >= 5 * parts) {
+                    c.wr = true;
+                    c.wr_parts = parts;
+                    c.wr_tw = tw;
+                }
             }
-        }
     }
     // Q4_K where the Stream-K wide kernel would run: the 256 x 256 tile kernel when its rounds of
     // tiles fill at least 3/4 of the CU time (M = 16384, N = 9728: 2432 tiles in 9.5 rounds)
@@ -1463,7 +1466,9 @@ void hq_gemm_kernel_name(int type, int M, int N, int K, int n_cu, char *buf, siz
     else if (c.rbm) snprintf(buf, n, "k_gemm_q4_k_rb<1, 4, 3, 2>");
     else if (c.rb8) snprintf(buf, n, "k_gemm_q8_0_rb<%d, 3, 2>", M <= 16 ? 1 : M <= 32 ? 2 : 4);
     else if (c.bt) snprintf(buf, n, "k_gemm_q4_k_bt");
-    else if (c.wr) snprintf(buf, n, c.wr_parts > 1 ? "k_gemm_q4_k_wr_ks<3>" : c.wr_tw == 160 ? "k_gemm_q4_k_wr160" : "k_gemm_q4_k_wr<3>");
+    else if (c.wr)
+        snprintf(buf, n, c.wr_parts > 1 ? (c.wr_tw == 160 ? "k_gemm_q4_k_wr_ks160" : "k_gemm_q4_k_wr_ks<3>")
+                                        : c.wr_tw == 160 ? "k_gemm_q4_k_wr160" : "k_gemm_q4_k_wr<3>");
     else if (c.wr8) snprintf(buf, n, "k_gemm_q8_0_wr");
     else if (c.ws_nb) snprintf(buf, n, "k_gemm_q4_k_ws<%d>", c.ws_nb);
     else if (c.ws8_nb) snprintf(buf, n, "k_gemm_q8_0_ws<%d>", c.ws8_nb);
@@ -1499,9 +1504,9 @@ void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_by
     // (the Q4_K tile kernels wr, ws form their own)
     *sums_bytes = (c.wide && !c.wr && !(c.ws_nb && W->type == HQ_TYPE_Q4_K)) || c.rbm ? (size_t)M * (W->cols / KC) * 32 : 0;
     if (c.wr8) *partial_bytes = *counter_bytes = 0;  // (no K split)
-    if (c.wr) {  // K split: one fp32 128 x 192 tile per (tile, part)
-        const size_t tiles = (size_t)((M + 127) / 128) * ((W->rows + 191) / 192);
-        *partial_bytes = c.wr_parts > 1 ? tiles * c.wr_parts * 128 * 192 * sizeof(float) : 0;
+    if (c.wr) {  // K split: one fp32 128 x wr_tw tile per (tile, part)
+        const size_t tiles = (size_t)((M + 127) / 128) * ((W->rows + c.wr_tw - 1) / c.wr_tw);
+        *partial_bytes = c.wr_parts > 1 ? tiles * c.wr_parts * 128 * c.wr_tw * sizeof(float) : 0;
         *counter_bytes = c.wr_parts > 1 ? tiles * sizeof(int) : 0;
     }
 }

@@ -82,10 +82,10 @@ def test_gemm_workspace_bytes():
     one fp32 tile per (tile, part) plus a counter per tile; the Stream-K kernel two 128 x 256 fp32
     tiles per CU; the large-M tile kernel only the activation sub-block sums; hq_gemm_noalloc's
     96 MiB scratch holds the BASELINE shapes and refuses larger."""
-    # (M = 512, N = 2560, K = 9728: the 128 x 192 register-decode kernel, 4 x 14 tiles with K split
+    # (M = 512, N = 2560, K = 9728: the 128 x 160 register-decode kernel, 4 x 16 tiles with K split
     # over 4 workgroups, no sub-block sums)
     pb, cb, sb, fits = hq.gemm_workspace_bytes(synth.Q4_K, 512, 2560, 9728)
-    assert (pb, cb, sb, fits) == (56 * 4 * 128 * 192 * 4, 56 * 4, 0, True)
+    assert (pb, cb, sb, fits) == (64 * 4 * 128 * 160 * 4, 64 * 4, 0, True)
     pb, cb, sb, fits = hq.gemm_workspace_bytes(synth.Q4_K, 4096, 2560, 9728)
     assert (pb, cb, fits) == (2 * 256 * 128 * 256 * 4, 32 * 10 * 4, True)
     assert hq.gemm_workspace_bytes(synth.Q4_K, 4096, 9728, 2560) == (0, 0, 4096 * 10 * 32, True)
@@ -116,13 +116,14 @@ def test_gemm_kernel_names():
              (synth.Q8_0, 2048, 9728, 2560): "k_gemm_q8_0_wr", (synth.Q8_0, 128, 9728, 2560): "k_gemm_q8_0_ws<3>",
              (synth.Q8_0, 65, 9728, 2560): "k_gemm_q8_0_ws<3>", (synth.Q8_0, 128, 4096, 4096): "k_gemm_q8_0_ws<2>",
              (synth.Q6_K, 96, 9728, 2560): "k_gemm_kq_ws<14, 3>", (synth.Q4_K, 128, 9728, 2560): "k_gemm_q4_k_ws<3>",
-             (synth.Q4_K, 200, 9728, 2560): "k_gemm_q4_k_wr_ks<3>", (synth.Q5_K, 96, 9728, 2560): "k_gemm_q5_k_ws<3>",
+             (synth.Q4_K, 200, 9728, 2560): "k_gemm_q4_k_wr_ks160", (synth.Q5_K, 96, 9728, 2560): "k_gemm_q5_k_ws<3>",
              (synth.Q4_K, 4096, 9728, 2560): "k_gemm_q4_k_bt", (synth.Q4_K, 16384, 2560, 9216): "k_gemm_q4_k_bt",
              (synth.Q4_K, 16384, 1024, 2560): "k_gemm_q4_k_bt", (synth.Q4_K, 2048, 9728, 2560): "k_gemm_q4_k_w<8>",
              (synth.Q4_K, 64, 9728, 2560): "k_gemm_q4_k_rb<1, 4, 3, 2>",
              (synth.Q4_K, 64, 2560, 9728): "k_gemm_q4_k_rb<1, 4, 3, 2>", (synth.Q4_K, 64, 1024, 2560): "k_gemm_q4_k<4, 2>", (synth.Q4_K, 32, 9728, 2560): "k_gemm_q4_k<2, 2>",
              (synth.Q4_K, 64, 9728, 2304): "k_gemm_q4_k<4, 2>",
-             (synth.Q4_K, 512, 2560, 9728): "k_gemm_q4_k_wr_ks<3>", (synth.Q4_K, 256, 2560, 9728): "k_gemm_q4_k_ws<3>",
+             (synth.Q4_K, 512, 2560, 9728): "k_gemm_q4_k_wr_ks160",
+             (synth.Q4_K, 100, 10996, 5120): "k_gemm_q4_k_wr_ks<3>", (synth.Q4_K, 256, 2560, 9728): "k_gemm_q4_k_ws<3>",
              (synth.Q4_K, 512, 1024, 2560): "k_gemm_q4_k_w<8>", (synth.Q4_K, 4096, 2560, 9728): "k_gemm_q4_k_w<8>",
              (synth.Q8_0, 512, 2560, 9728): "k_gemm_q8_0_ws<5>", (synth.Q8_0, 256, 2560, 9728): "k_gemm_q8_0_ws<3>",
              (synth.Q8_0, 16, 9728, 2560): "k_gemm_q8_0_rb<1, 3, 2>", (synth.Q8_0, 64, 9728, 2560): "k_gemm_q8_0_rb<4, 3, 2>",

@@ -125,7 +125,8 @@ RAGGED = [(synth.Q8_0, 100, 512, M) for M in (1, 2, 5, 17, 33, 65, 200)] + \
          [(synth.Q4_K, 2500, 4096, 40), (synth.Q4_K, 4096, 2560, 48)] + \
          [(synth.Q8_0, 2560, 9728, 16), (synth.Q8_0, 2500, 4096, 40)] + \
          [(synth.Q8_0, 9728, 2560, 96), (synth.Q8_0, 4000, 4096, 100)] + \
-         [(synth.Q4_K, 9728, 2560, 100), (synth.Q4_K, 4000, 4096, 96), (synth.Q4_K, 9728, 2560, 200)]
+         [(synth.Q4_K, 9728, 2560, 100), (synth.Q4_K, 4000, 4096, 96), (synth.Q4_K, 9728, 2560, 200),
+          (synth.Q4_K, 10996, 5120, 100)]
 # (the last: full-K tiles; Stream-K with more tiles than CUs; the streamed GEMV with a ragged last
 # row group and an odd K split, with one wave per row group, and with an even split; the Q8_0 tile
 # kernel with ragged M and N, and with an odd number of 128-wide stages; the Q4_K tile kernel with
@@ -137,7 +138,9 @@ RAGGED = [(synth.Q8_0, 100, 512, M) for M in (1, 2, 5, 17, 33, 65, 200)] + \
 # mid-M Q8_0 kernel with K splits over 6 and (ragged N, M) 4 workgroups; the Q8_0 tile kernel with K
 # split over 2 workgroups of 10 stages (ragged M) and over 4 of 8 stages (ragged N, M); the Q4_K tile
 # kernel with K split over 2 workgroups of 5 super-blocks (ragged M) and over 4 of 4 (ragged N, M); the
-# 128 x 192 register-decode kernel with K split over 2 workgroups of 5 super-blocks (ragged M))
+# register-decode kernel with K split over 2 workgroups of 5 super-blocks, ragged M, with 128 x 160
+# tiles and, where those would not fit one round, 128 x 192 ones (4 workgroups of 5 super-blocks,
+# ragged M and a ragged last column tile))
 
 
 @pytest.mark.parametrize("gtype,N,K,M", FULL + RAGGED)
