@@ -250,8 +250,9 @@ DEV uint32_t swiglu_pair2(const f4 &v, int lg) {
 // its tile into LDS as fp16 (row r at r * tile_ldr<ROWB>() bytes, so that consecutive rows start 4
 // banks apart), then all NT threads store whole 16-byte pieces, consecutive lanes on consecutive bytes
 // of a row: a store instruction writes whole 128-byte lines, where an 8-byte store from the
-// accumulators covers 16 rows x 32 bytes. (Measured on the register-decode kernels: faster for fp16 C,
-// slower for fp32 C and the SwiGLU output, whose LDS pass costs more than the stores gain.)
+// accumulators covers 16 rows x 32 bytes. (Measured on the register-decode kernels: faster for fp16 C
+// and for the Q4_K kernel's SwiGLU output, slower for fp32 C, whose LDS pass costs more than the
+// stores gain.)
 // tile_store_ok: fp16 C without accumulate, rows of whole 16-byte pieces, C 16-byte aligned.
 DEV bool tile_store_ok(int c_f32, int accumulate, int N, const void *C) {
     return c_f32 == 0 && !accumulate && N % 8 == 0 && ((uintptr_t)C & 15u) == 0;

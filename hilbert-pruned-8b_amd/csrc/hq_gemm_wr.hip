@@ -123,12 +123,24 @@ DEV void wr_dec_half(h8 &b, u2v q, int hf, uint32_t mask, h2 mul, h2 add) {
 }
 
 
-// the store phase of an fp16 output tile staged in LDS (tile_store_rows)
+// whether the tile kernels store their output staged in LDS: fp16 C (tile_store_ok) or the SwiGLU
+// output of a pair matrix (C 16-byte aligned; N is a multiple of 16); the SwiGLU pair GEMM at
+// M = 512, I = 9728, K = 2560 measured 2-3 us faster so in same-box A/Bs
+DEV bool wr_staged(const WrArgs &g) {
+    return tile_store_ok(g.c_f32, g.accumulate, g.N, g.C) || (g.c_f32 == HQ_OUT_SWIGLU && ((uintptr_t)g.C & 15u) == 0);
+}
+// the store phase of an output tile staged in LDS (tile_store_rows): fp16 C [M][N], or the SwiGLU
+// output fp16 [M][N / 2] (the tile's BN / 2 output columns from n0 / 2)
 template <int BN>
 DEV void wr_store(const char *lds, const WrArgs &g, int m0, int n0, int tid) {
-    const uint32_t pitch = (uint32_t)g.N * 2u;
-    tile_store_rows<WR_BM, WR_NT, BN * 2>(lds, (char *)g.C + (size_t)m0 * pitch, min(WR_BM, g.M - m0), pitch, (uint32_t)n0 * 2u,
-                                          (uint32_t)min(BN, g.N - n0) * 2u, tid);
+    const int rows = min(WR_BM, g.M - m0), cols = min(BN, g.N - n0);
+    if (g.c_f32 == HQ_OUT_SWIGLU) {
+        const uint32_t pitch = (uint32_t)g.N;
+        tile_store_rows<WR_BM, WR_NT, BN>(lds, (char *)g.C + (size_t)m0 * pitch, rows, pitch, (uint32_t)n0, (uint32_t)cols, tid);
+    } else {
+        const uint32_t pitch = (uint32_t)g.N * 2u;
+        tile_store_rows<WR_BM, WR_NT, BN * 2>(lds, (char *)g.C + (size_t)m0 * pitch, rows, pitch, (uint32_t)n0 * 2u, (uint32_t)cols * 2u, tid);
+    }
 }
 
 // The tile body; KS: with the K split (parts > 1; the split-only work is compiled out of the whole-K
@@ -398,7 +410,7 @@ DEV void wr_tile(const WrArgs &g) {
             wr_barrier();
             wr_barrier();
             tile_finish<WR_BM, BN, WR_NT, 4>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::TOTAL - 16));
-        } else if (tile_store_ok(g.c_f32, g.accumulate, g.N, g.C)) {
+        } else if (wr_staged(g)) {
             // the same two meetings, then store the tile with them
             wr_barrier();
             wr_barrier();
@@ -561,9 +573,10 @@ DEV void wr_tile(const WrArgs &g) {
         tile_finish<WR_BM, BN, WR_NT, 4>(lds, g, m0, n0, nt_i * g.mt + mt_i, part, (int *)(lds + L::TOTAL - 16));
         return;
     }
-    // fp16 C through LDS (tile_store_rows) where C allows it: the accumulators as fp16 at their rows
-    // and columns, then all 8 waves store
-    if (tile_store_ok(g.c_f32, g.accumulate, g.N, g.C)) {
+    // fp16 C, or the SwiGLU output, through LDS (tile_store_rows) where C allows it: the accumulators
+    // as fp16 (or the pairs' fp16 products silu(gate) * up) at their rows and columns, then all 8
+    // waves store
+    if (wr_staged(g)) {
         wr_barrier();  // every wave is done with the rings, sums and tables
 #pragma unroll
         for (int i = 0; i < 8; i++)
@@ -572,7 +585,10 @@ DEV void wr_tile(const WrArgs &g) {
                 if (!G::has(i, j)) continue;
                 const int row = 16 * rb_of(i) + ln;
                 const f4 v = acc[i][j];
-                *(h4 *)(lds + row * tile_ldr<BN * 2>() + (c0[j] + 4 * lg) * 2) = h4{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+                if (g.c_f32 == HQ_OUT_SWIGLU)
+                    *(uint32_t *)(lds + row * tile_ldr<BN>() + (c0[j] / 2 + 4 * (lg & 1) + 2 * (lg >> 1)) * 2) = swiglu_pair2(v, lg);
+                else
+                    *(h4 *)(lds + row * tile_ldr<BN * 2>() + (c0[j] + 4 * lg) * 2) = h4{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
             }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         wr_barrier();
