@@ -14,16 +14,18 @@
 // accumulators belong to one output column); no decoded B tile is stored. Per pipeline, an LDS ring
 // of NSTG 128-K stages (activation tile + the quant bytes of its columns, both LDS-DMA'd, written as
 // assembly and waited with explicit s_waitcnt vmcnt) and a ring of super-block slots (the
-// activations' sub-block sums from the k_asums pre-pass in (hi, lo) pair layout, and the column
-// headers).
+// activations' sub-block sums in (hi, lo) pair layout, which the waves form from the staged tiles,
+// one (row, sub-block) per lane and stage, and the column headers).
 //
 // Arithmetic as in the full-K tile kernel of hq_gemm_ws.hip: the B operand is the exact integer
 // s*q (fp16 1024 + q via v_perm_b32, one v_pk_fma_f16 with (s, -1024 s) or (s/16, -64 s)); a
 // column's accumulators are in units of c_u = d_u (1 where d_u = 0) during super-block u and are
 // rescaled by c_{u'} / c_u when the pipeline moves on (u' its previous super-block), then by its
 // last c; the min term -dmin * sum_sub m_sub * S_sub is one bf16 MFMA per row block and super-block
-// whose k slots pair (S hi, S lo, S hi, S lo) with (x hi, x hi, x lo, x lo), x = -dmin m / c_u, so a
-// lane needs only the two sub-blocks of its own lane group. Each lane reads its column's 16-byte
+// whose k slots pair (S hi, S lo, S hi, S lo) with (x hi, x hi, x lo, x lo), so a lane needs only the
+// two sub-blocks of its own lane group. It runs one super-block late (S of u is whole once u's last
+// stage is summed): at the start of u's successor u', after the rescale, with x = -dmin_u m_u / c_{u'};
+// the last super-block's after the loop, in its own units. Each lane reads its column's 16-byte
 // header and forms every per-column value itself (no cross-lane exchange). The two pipelines' tiles
 // are added in pipeline order through LDS before the store.
 #include <type_traits>
@@ -36,7 +38,6 @@ struct RbArgs {
     const uint8_t *W;  // Q4_K super-blocks, row n at n * row_bytes
     uint32_t row_bytes;
     const uint16_t *A;  // fp16 [M][K]
-    const uint16_t *S;  // activation sub-block sums [M][K/256][8][hi, lo] (k_asums, pair layout)
     int M, N, K;
     void *C;
     int c_f32, accumulate;
@@ -111,7 +112,6 @@ __global__ void __launch_bounds__(RB_NT * PIPE) k_gemm_q4_k_rb(RbArgs g) {
     const int ln = lane & 15, lg = lane >> 4;
     const rsrc_t ra = make_rsrc(g.A + (size_t)u0 * 256, (uint32_t)((size_t)M * K * 2 - (size_t)u0 * 512));
     const rsrc_t rw = make_rsrc(g.W + (size_t)u0 * 144, (uint32_t)((size_t)N * g.row_bytes - (size_t)u0 * 144));
-    const rsrc_t rs = make_rsrc(g.S + (size_t)u0 * 16, (uint32_t)((size_t)M * UT * 32 - (size_t)u0 * 32));
     const uint32_t lds0 = (uint32_t)(uintptr_t)lds + (uint32_t)(kh * L::TOTAL);
     const int nw = n0 + 16 * NB * wave;  // the wave's first column
     const uint32_t rb = g.row_bytes;
@@ -131,10 +131,6 @@ __global__ void __launch_bounds__(RB_NT * PIPE) k_gemm_q4_k_rb(RbArgs g) {
     auto dma_b = [&](int s, int j) __attribute__((always_inline)) {
         dma16_so(rw, lds0 + (uint32_t)((s % NSTG) * L::STG + L::A_BYTES + (wave * NB + j) * 1024), b_voff[j],
                  (uint32_t)(ru(s >> 1) * 144 + 64 * (s & 1)));
-    };
-    const uint32_t s_voff = ((uint32_t)(m0 + 4 * MBK * wave + (lane >> 1)) * (uint32_t)UT) * 32u + 16u * (uint32_t)(lane & 1);
-    auto dma_s = [&](int u) __attribute__((always_inline)) {
-        if (lane < 8 * MBK) dma16_so(rs, lds0 + (uint32_t)(L::SB0 + (u % NSB) * L::SBS + wave * 128 * MBK), s_voff, (uint32_t)(ru(u) * 32));
     };
     const uint32_t h_voff = (uint32_t)(nw + (lane < 16 * NB ? lane : 0)) * rb;
     auto dma_h = [&](int u) __attribute__((always_inline)) {
@@ -166,18 +162,28 @@ __global__ void __launch_bounds__(RB_NT * PIPE) k_gemm_q4_k_rb(RbArgs g) {
     float rr[NB];
     u4v raw[NB], hd[NB];
     uint32_t sws[NB][2], pm[NB][4];
-    float cprev[NB];
+    float cprev[NB], xprev[NB][2];  // c of the previous super-block; -dmin m of its lane sub-blocks
 #pragma unroll
-    for (int j = 0; j < NB; j++) cprev[j] = 1.0f;
+    for (int j = 0; j < NB; j++) cprev[j] = 1.0f, xprev[j][0] = xprev[j][1] = 0.0f;
 
     auto read_hdr = [&](int u) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < NB; j++) hd[j] = rb_ld16(lds0 + (uint32_t)((u % NSB) * L::SBS) + hdr_lane + (uint32_t)(j * 256));
     };
-    // super-block values of column 16j + ln (from hd[j]; every lane of the column holds its header):
-    // scale words of sub-blocks 0-3 / 4-7 (zero where d = 0), the lane's min-term B fragment for
-    // sub-blocks 2lg, 2lg + 1 ((hi, hi), (lo, lo) bf16 pairs of x = -dmin m / c, matching the S
-    // fragment's (hi, lo), (hi, lo) pairs) and the column's rescale ratio c_{u-1} / c_u
+    // min-term B fragment of x0, x1 (sub-blocks 2lg, 2lg + 1): (hi, hi), (lo, lo) bf16 pairs, matching
+    // the S fragment's (hi, lo), (hi, lo) pairs
+    auto min_frag = [&](float x0, float x1) __attribute__((always_inline)) {
+        const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
+        const __bf16 l0 = (__bf16)(x0 - (float)h0), l1 = (__bf16)(x1 - (float)h1);
+        const uint32_t uh0 = __builtin_bit_cast(uint16_t, h0), uh1 = __builtin_bit_cast(uint16_t, h1);
+        const uint32_t ul0 = __builtin_bit_cast(uint16_t, l0), ul1 = __builtin_bit_cast(uint16_t, l1);
+        return __builtin_bit_cast(h8, u4v{uh0 * 0x10001u, ul0 * 0x10001u, uh1 * 0x10001u, ul1 * 0x10001u});
+    };
+    // super-block values of column 16j + ln (from hd[j] of super-block u; every lane of the column
+    // holds its header): scale words of sub-blocks 0-3 / 4-7 (zero where d = 0), the lane's min-term B
+    // fragment of the PREVIOUS super-block in units of c_u (x = -dmin_{u-1} m_{u-1} / c_u: its sums are
+    // whole only once its last stage is summed, so its min k-step runs at the start of u, after the
+    // rescale), and the column's rescale ratio c_{u-1} / c_u
     auto sb_col = [&](int j) __attribute__((always_inline)) {
         const u4v h = hd[j];
         uint32_t sw0, sw1, mw0, mw1;
@@ -188,15 +194,30 @@ __global__ void __launch_bounds__(RB_NT * PIPE) k_gemm_q4_k_rb(RbArgs g) {
         const uint32_t mw = lg < 2 ? mw0 : mw1;
         const float d = h2f((uint16_t)h.x), dmin = h2f((uint16_t)(h.x >> 16));
         const float c = d != 0.0f ? d : 1.0f, inv = 1.0f / c;
-        const float x0 = (-dmin * (float)byte_of(mw, 2 * (lg & 1))) * inv;
-        const float x1 = (-dmin * (float)byte_of(mw, 2 * (lg & 1) + 1)) * inv;
-        const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
-        const __bf16 l0 = (__bf16)(x0 - (float)h0), l1 = (__bf16)(x1 - (float)h1);
-        const uint32_t uh0 = __builtin_bit_cast(uint16_t, h0), uh1 = __builtin_bit_cast(uint16_t, h1);
-        const uint32_t ul0 = __builtin_bit_cast(uint16_t, l0), ul1 = __builtin_bit_cast(uint16_t, l1);
-        bm[j] = __builtin_bit_cast(h8, u4v{uh0 * 0x10001u, ul0 * 0x10001u, uh1 * 0x10001u, ul1 * 0x10001u});
+        bm[j] = min_frag(xprev[j][0] * inv, xprev[j][1] * inv);
+        xprev[j][0] = -dmin * (float)byte_of(mw, 2 * (lg & 1));
+        xprev[j][1] = -dmin * (float)byte_of(mw, 2 * (lg & 1) + 1);
         rr[j] = cprev[j] * inv;
         cprev[j] = c;
+    };
+    // activation sub-block sums (no pass over A before the kernel): in stage s = 2u + h, lane (r, b) of
+    // wave w sums row 16w + r (r = lane % 16) of the stage's tile over sub-block b = lane / 16 (fp32,
+    // the sum8 order) and stores it as a (hi, lo) bf16 pair in S(u)[row][4h + b] (the slot u % NSB
+    // that the min k-step of super-block u + 1 reads)
+    static_assert(MBK == 4 && RB_KS == 128, "one (row, sub-block) of the stage per lane of the 4 waves");
+    const int srow = 16 * wave + (lane & 15), sblk = lane >> 4;
+    u4v sx[4];
+    auto sums_rd = [&](int s) __attribute__((always_inline)) {
+        const uint32_t base = lds0 + (uint32_t)((s % NSTG) * L::STG + srow * 256);
+#pragma unroll
+        for (int c = 0; c < 4; c++) sx[c] = rb_ld16(base + (uint32_t)(((4 * sblk + c) ^ (srow & 15)) * 16));
+    };
+    auto sums_wr = [&](int s) __attribute__((always_inline)) {
+        const float v = sum8(sx[3], sum8(sx[2], sum8(sx[1], sum8(sx[0], 0.f))));
+        const __bf16 hi = (__bf16)v, lo = (__bf16)(v - (float)hi);
+        const uint32_t w = (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+        *(__attribute__((address_space(3))) uint32_t *)(uintptr_t)(lds0 + (uint32_t)(L::SB0 + ((s >> 1) % NSB) * L::SBS + srow * 32 +
+                                                                                     (4 * (s & 1) + sblk) * 4)) = w;
     };
     // main decode parameters of stage half h: the lane's quant group p = 2h + lg/2 covers sub-blocks
     // 2p (low nibbles: s, -1024 s) and 2p + 1 (high nibbles: s/16, -64 s)
@@ -232,53 +253,47 @@ __global__ void __launch_bounds__(RB_NT * PIPE) k_gemm_q4_k_rb(RbArgs g) {
         for (int j = 0; j < NB; j++) acc[i][j] *= rr[j];
     };
 
-    // vector-memory items issued in stage s = 2u + h for stage t = s + D (if t < S2): S, H of super-block
-    // t / 2 + 1 when t is even (one super-block early: its values are computed during stage t + 1), then A 0..MBK-1 and B 0..NB-1 of stage t. They are spread over the
-    // groups of the stage's first k-steps (h = 0: min k-step and main k-steps 0-1; h = 1: main
-    // k-steps 0-1). count_t = the instructions of stage t.
+    // vector-memory items issued in stage s = 2u + h for stage t = s + D (if t < S2): H of super-block
+    // t / 2 + 1 when t is even (one super-block early: its values are computed during stage t + 1),
+    // then A 0..MBK-1 and B 0..NB-1 of stage t. They are spread over the groups of the stage's first
+    // k-steps (h = 0: min k-step and main k-steps 0-1; h = 1: main k-steps 0-1). count_t = the
+    // instructions of stage t.
     auto count_t = [&](int t) __attribute__((always_inline)) {
-        return t < S2 ? MBK + NB + (((t & 1) == 0 && (t >> 1) + 1 < U) ? 2 : 0) : 0;
+        return t < S2 ? MBK + NB + (((t & 1) == 0 && (t >> 1) + 1 < U) ? 1 : 0) : 0;
     };
     auto issue_at = [&](int u, auto hc, auto fc) __attribute__((always_inline)) {
         constexpr int H = decltype(hc)::value, F = decltype(fc)::value;
         constexpr bool SH = ((H + D) & 1) == 0;
-        constexpr int NI = (SH ? 2 : 0) + MBK + NB, G = (H == 0 ? 3 : 2) * MBK;
+        constexpr int NI = (SH ? 1 : 0) + MBK + NB, G = (H == 0 ? 3 : 2) * MBK;
         static_assert(NI <= G, "issue slots");
         constexpr int n = (F * NI + G - 1) / G;
         if constexpr (n < NI && (n * G) / NI == F) {
             const int t = 2 * u + H + D;
             if (t < S2) {
-                constexpr int it = SH ? n : n + 2;  // 0 = S, 1 = H, 2.. = A, then B
+                constexpr int it = SH ? n : n + 1;  // 0 = H, 1.. = A, then B
                 if constexpr (it == 0) {
-                    if ((t >> 1) + 1 < U) dma_s((t >> 1) + 1);
-                } else if constexpr (it == 1) {
                     if ((t >> 1) + 1 < U) dma_h((t >> 1) + 1);
-                }
-                else if constexpr (it < 2 + MBK) {
-                    dma_a(t, it - 2);
+                } else if constexpr (it < 1 + MBK) {
+                    dma_a(t, it - 1);
                 } else {
-                    dma_b(t, it - 2 - MBK);
+                    dma_b(t, it - 1 - MBK);
                 }
             }
         }
     };
     auto sched_fence = []() __attribute__((always_inline)) { __builtin_amdgcn_sched_barrier(0); };
 
-    // ---- prologue: super-block 0's headers and sums, then stages 0 .. D - 1 as in the main loop
+    // ---- prologue: super-block 0's headers, then stages 0 .. D - 1 as in the main loop
     dma_h(0);
-    dma_s(0);
     int n_pro = 0;
     for (int t = 0; t < D && t < S2; t++) {
-        if ((t & 1) == 0 && (t >> 1) + 1 < U) {
-            dma_s((t >> 1) + 1);
-            dma_h((t >> 1) + 1);
-        }
+        if ((t & 1) == 0 && (t >> 1) + 1 < U) dma_h((t >> 1) + 1);
         for (int qq = 0; qq < MBK; qq++) dma_a(t, qq);
 #pragma unroll
         for (int j = 0; j < NB; j++) dma_b(t, j);
         n_pro += count_t(t);
     }
-    wait_vmcnt(1 + n_pro);  // H(0)
+    wait_vmcnt(n_pro);  // H(0)
     read_hdr(0);
 #pragma unroll
     for (int j = 0; j < NB; j++) sb_col(j);
@@ -289,11 +304,9 @@ __global__ void __launch_bounds__(RB_NT * PIPE) k_gemm_q4_k_rb(RbArgs g) {
     for (int j = 0; j < NB; j++) decode_j(0, j);
     rb_wait_lgkm();
     __syncthreads();
-    {
-        const uint32_t sb = s_base(0);
+    // (super-block 0's min k-step adds the zero term of a super-block -1)
 #pragma unroll
-        for (int i = 0; i < MBK; i++) fa[i] = rb_lds_pairs(sb + (uint32_t)(i * 16 * 32));
-    }
+    for (int i = 0; i < MBK; i++) fa[i] = h8{};
 
     // ---- k-steps: 8 groups (row blocks) each, pinned in order by scheduling fences
     // min k-step of super-block u (stage s = 2u): rescale + S x Bmin; reads stage s's kk = 0 A fragments
@@ -332,6 +345,8 @@ __global__ void __launch_bounds__(RB_NT * PIPE) k_gemm_q4_k_rb(RbArgs g) {
             fa[i] = rb_ld8(ab + (uint32_t)(i * 16 * 256));
             if constexpr ((i & 1) == 0 && (i >> 1) < NB) decode_j(KK + 1, i >> 1);
             if constexpr (KK < 2) issue_at(u, hc, std::integral_constant<int, (H == 0 ? MBK : 0) + MBK * KK + i>{});
+            if constexpr (KK == 0 && i == 1) sums_rd(s);
+            if constexpr (KK == 1 && i == 0) sums_wr(s);
             if constexpr (H == 1 && MORE) {
                 if constexpr (KK == 0 && i == 1) read_hdr(u + 1);
                 if constexpr (KK == 0 && i == 3)
@@ -371,7 +386,7 @@ __global__ void __launch_bounds__(RB_NT * PIPE) k_gemm_q4_k_rb(RbArgs g) {
         uint32_t nb = 0;
         constexpr uint32_t nstep = NSB ? 16u * 32u : 16u * 256u;
         if constexpr (MORE) {
-            nb = NSB ? s_base(u + 1) : a_base(s + 1, 0);
+            nb = NSB ? s_base(u) : a_base(s + 1, 0);
 #pragma unroll
             for (int i = 0; i < HG; i++) fa[i] = NSB ? rb_lds_pairs(nb + (uint32_t)i * nstep) : rb_ld8(nb + (uint32_t)i * nstep);
         }
@@ -408,6 +423,21 @@ __global__ void __launch_bounds__(RB_NT * PIPE) k_gemm_q4_k_rb(RbArgs g) {
     if (U >= 2) sb_body(std::integral_constant<int, 1>{}, U - 2);
     sb_body(std::integral_constant<int, 2>{}, U - 1);
 
+    // the last super-block's min k-step, in its own units (its sums were whole at the last hand-off)
+    {
+        const uint32_t sb = s_base(U - 1);
+#pragma unroll
+        for (int i = 0; i < MBK; i++) fa[i] = rb_lds_pairs(sb + (uint32_t)(i * 16 * 32));
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            const float inv = 1.0f / cprev[j];
+            bm[j] = min_frag(xprev[j][0] * inv, xprev[j][1] * inv);
+        }
+#pragma unroll
+        for (int i = 0; i < MBK; i++)
+#pragma unroll
+            for (int j = 0; j < NB; j++) acc[i][j] = mfma_bf16(fa[i], bm[j], acc[i][j]);
+    }
     // back to true units: x c of the last super-block (the lane's column of each block)
 #pragma unroll
     for (int j = 0; j < NB; j++)
@@ -463,13 +493,13 @@ int hq_rb_parts(int M, int N, int K, int n_cu) {
     return 0;
 }
 
-hipError_t hq_launch_gemm_rb(const hq_dev_mat *W, const uint16_t *A, const uint16_t *S, int M, void *C, int c_f32,
+hipError_t hq_launch_gemm_rb(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32,
                              int accumulate, int parts, float *partials, int *counters, hipStream_t st) {
     if (W->type != HQ_TYPE_Q4_K || !hq_rb_fits(M, (int)W->cols)) return hipErrorInvalidValue;
     if (parts < 1 || parts > 8 || (parts > 1 && (4 * parts > (int)W->cols / 256 || !partials || !counters)))
         return hipErrorInvalidValue;
     RbArgs g;
-    g.W = W->qs, g.row_bytes = (uint32_t)W->row_bytes, g.A = A, g.S = S;
+    g.W = W->qs, g.row_bytes = (uint32_t)W->row_bytes, g.A = A;
     g.M = M, g.N = (int)W->rows, g.K = (int)W->cols, g.C = C, g.c_f32 = c_f32, g.accumulate = accumulate;
     g.mt = 1;
     g.nt = (g.N + 63) / 64;

@@ -93,11 +93,11 @@ int hq_wr8_fits(const hq_dev_mat *W, int M);
 hipError_t hq_launch_gemm_wr8(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
                               int nt0, int nt1, hipStream_t st);
 // Mid-M Q4_K GEMM (hq_gemm_rb.hip): whether M, K suit it (33 <= M <= 64, K a multiple of 512,
-// 32-bit offsets), its workgroups per tile for a shape, and the launch (S = k_asums output for A in
-// the (hi, lo) pair layout; partials / counters as for the other K splits when parts > 1).
+// 32-bit offsets), its workgroups per tile for a shape, and the launch (no pre-pass: the kernel forms
+// the activation sub-block sums; partials / counters as for the other K splits when parts > 1).
 int hq_rb_fits(int M, int K);
 int hq_rb_parts(int M, int N, int K, int n_cu);  // 0: not this kernel; else workgroups per tile
-hipError_t hq_launch_gemm_rb(const hq_dev_mat *W, const uint16_t *A, const uint16_t *S, int M, void *C, int c_f32,
+hipError_t hq_launch_gemm_rb(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32,
                              int accumulate, int parts, float *partials, int *counters, hipStream_t st);
 // Mid-M Q8_0 GEMM (hq_gemm_rb.hip): workgroups per tile for a shape (0: not this kernel), and the
 // launch (no pre-pass; partials / counters as for the other K splits when parts > 1).

@@ -1005,7 +1005,7 @@ __global__ void __launch_bounds__(512) k_gemm_q4_k_w(GemmArgs g) {
 // fp32 sum of activations 256u + 32s .. +32 of row m, in fp16 (BF16 = false: the Stream-K kernel)
 // or bf16 (the full-K tile kernel). One thread per sub-block (four 16-byte loads, 32-bit index math;
 // M * K / 32 < 2^31 is checked by the launcher).
-template <bool BF16, bool PAIR = false>
+template <bool BF16>
 __global__ void __launch_bounds__(256) k_asums(const uint16_t *__restrict__ A, int M, int K,
                                                uint16_t *__restrict__ S) {
     const uint32_t kb = (uint32_t)K / 32u, n = (uint32_t)M * kb;
@@ -1024,15 +1024,10 @@ __global__ void __launch_bounds__(256) k_asums(const uint16_t *__restrict__ A, i
             hb = __builtin_bit_cast(uint16_t, hi);
             lb = __builtin_bit_cast(uint16_t, (_Float16)(v - (float)hi));
         }
-        if constexpr (PAIR) {  // [M][K/256][8][hi, lo] (mid-M kernel)
-            uint16_t *dst = S + ((size_t)m * (kb / 8) + s / 8) * 16 + 2 * (s % 8);
-            dst[0] = hb;
-            dst[1] = lb;
-        } else {  // [M][K/256][hi x 8, lo x 8]
-            uint16_t *dst = S + ((size_t)m * (kb / 8) + s / 8) * 16 + (s % 8);
-            dst[0] = hb;
-            dst[8] = lb;
-        }
+        // [M][K/256][hi x 8, lo x 8]
+        uint16_t *dst = S + ((size_t)m * (kb / 8) + s / 8) * 16 + (s % 8);
+        dst[0] = hb;
+        dst[8] = lb;
     }
 }
 
@@ -1502,7 +1497,7 @@ void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_by
         *counter_bytes = tiles * sizeof(int);
     }
     // (the Q4_K tile kernels wr, ws form their own)
-    *sums_bytes = (c.wide && !c.wr && !(c.ws_nb && W->type == HQ_TYPE_Q4_K)) || c.rbm ? (size_t)M * (W->cols / KC) * 32 : 0;
+    *sums_bytes = c.wide && !c.wr && !(c.ws_nb && W->type == HQ_TYPE_Q4_K) ? (size_t)M * (W->cols / KC) * 32 : 0;
     if (c.wr8) *partial_bytes = *counter_bytes = 0;  // (no K split)
     if (c.wr) {  // K split: one fp32 128 x wr_tw tile per (tile, part)
         const size_t tiles = (size_t)((M + 127) / 128) * ((W->rows + c.wr_tw - 1) / c.wr_tw);
@@ -1512,13 +1507,10 @@ void hq_gemm_work_bytes(const hq_dev_mat *W, int M, int n_cu, size_t *partial_by
 }
 
 // Pre-pass of a GEMM (the activation sub-block sums of the Q4_K kernels that read them from HBM;
-// nothing otherwise: the Q4_K tile kernels k_gemm_q4_k_wr and k_gemm_q4_k_ws form their own).
+// nothing otherwise: the Q4_K tile kernels k_gemm_q4_k_wr, k_gemm_q4_k_ws and k_gemm_q4_k_rb form
+// their own).
 hipError_t hq_launch_gemm_pre(const hq_dev_mat *W, const uint16_t *A, int M, const HqGemmWork &wk, hipStream_t st) {
     const GemmCfg c = gemm_cfg(W, M, wk.n_cu);
-    if (c.rbm) {
-        const size_t nsub = (size_t)M * (W->cols / 32);
-        k_asums<true, true><<<grid_for(nsub, 256, 16384), 256, 0, st>>>(A, M, (int)W->cols, wk.sums);
-    }
     if (c.wide && !c.wr && !(c.ws_nb && W->type == HQ_TYPE_Q4_K)) {
         const size_t nsub = (size_t)M * (W->cols / 32);
         if (nsub >= ((size_t)1 << 31)) return hipErrorInvalidValue;
@@ -1533,7 +1525,7 @@ hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, vo
                                const HqGemmWork &wk, hipStream_t st) {
     const GemmCfg c = gemm_cfg(W, M, wk.n_cu);
     if (c.nn) return hq_launch_gemm_nn(W, A, M, C, c_f32, accumulate, st);
-    if (c.rbm) return hq_launch_gemm_rb(W, A, wk.sums, M, C, c_f32, accumulate, c.rbm, wk.partials, wk.counters, st);
+    if (c.rbm) return hq_launch_gemm_rb(W, A, M, C, c_f32, accumulate, c.rbm, wk.partials, wk.counters, st);
     if (c.rb8) return hq_launch_gemm_rb8(W, A, M, C, c_f32, accumulate, c.rb8, wk.partials, wk.counters, st);
     if (c.bt) return hq_launch_gemm_bt(W, A, wk.sums, M, C, c_f32, accumulate, st);
     if (c.wr) return hq_launch_gemm_wr(W, A, M, C, c_f32, accumulate, 0, -1, c.wr_parts, wk.partials, wk.counters, st, c.wr_tw);
