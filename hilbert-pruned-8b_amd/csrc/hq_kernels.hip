@@ -1235,6 +1235,21 @@ hipError_t wr_launches(const WrPlan &pl, int M, int N, F &&launch) {
         }
     return hipSuccess;
 }
+// Launch plan of the Q4_K register-decode kernel over more than one round: 160-column tiles where
+// they need no more launches than 192-column ones (M = 512, N = 19456: two launches of 4 x 122 / 2
+// tiles, 244 of 256 CUs, instead of 204), and one launch where its tiles make two rounds on every XCD
+// with the second at least 60 % full (the gate/up pair GEMM at M = 512, I = 9728: one launch of
+// 4 x 122 tiles instead of two of 2 x 122, 68.5 -> 67.4 us in a same-box A/B)
+WrPlan wr4_plan(int M, int N, int n_cu) {
+    WrPlan pl = wr_plan(M, N, n_cu);
+    const WrPlan p160 = wr_plan(M, N, n_cu, 160);
+    if (p160.fill && p160.launches <= pl.launches) pl = p160;
+    const int mt = (M + 127) / 128, nt = (N + pl.tw - 1) / pl.tw, per_xcd = std::max(1, n_cu / 8);
+    const int on_xcd = mt * ((nt + 7) / 8);
+    if (pl.fill && on_xcd > per_xcd && on_xcd <= 2 * per_xcd && 5 * on_xcd >= 8 * per_xcd)
+        pl.row_tiles = mt, pl.col_tiles = nt, pl.launches = 1;
+    return pl;
+}
 }  // namespace
 
 namespace {
@@ -1254,6 +1269,7 @@ struct GemmCfg {
     bool wr;        // Q4_K, one round of full-K tiles: the 128 x 192 tile kernel k_gemm_q4_k_wr (hq_gemm_wr.hip)
     int wr_parts;   // with wr: workgroups per tile (K split), 1: whole K
     int wr_tw;      // with wr: tile width, 192 or 160 columns (k_gemm_q4_k_wr160)
+    bool wr_multi;  // with wr: launches of at most one round each (wr4_plan), no K split
     bool wr8;       // Q8_0, the same: k_gemm_q8_0_wr (hq_gemm_wr8.hip)
     bool nn;        // Q4_K with N <= 32 and many rows: k_gemm_q4_k_nn (hq_gemm_nn.hip)
 };
@@ -1345,6 +1361,19 @@ GemmCfg gemm_cfg(const hq_dev_mat *W, int M, int n_cu) {
     if (c.wide && !c.ws_nb && hq_bt_fits(W, M)) {
         const long t = (long)((M + 255) / 256) * (((long)W->rows + 255) / 256), rounds = (t + n_cu - 1) / n_cu;
         c.bt = 4 * t >= 3 * rounds * n_cu;
+    }
+    // Q4_K where the Stream-K wide kernel would run otherwise (N beyond one round at M ~512, M of
+    // several hundred rows and more at N ~10k, short of the 256 x 256 kernel's rule): the register-
+    // decode kernel as launches of at most one round each (wr4_plan), when they fill at least 70 % of
+    // the CU time. Per call against Stream-K in a same-box A/B (K = 2560): M = 512, N = 19456 80.9 ->
+    // 63.6 us; M = 384, N = 19456 66.4 -> 60.0; M = 512, N = 14336 65.4 -> 58.0; M = 768, N = 9728
+    // 66.0 -> 59.8; M = 1024 81.5 -> 63.3; M = 2048 140.6 -> 127.2; M = 4096, N = 2560 88.2 -> 71.4;
+    // M = 2048, N = 4096 60.6 -> 61.6. Against the 256 x 256 kernel it was no faster (M = 1536, N = 9728:
+    // 95.6 -> 96.0; M = 3072: 181.8 -> 191.0), so that one keeps its shapes.
+    c.wr_multi = false;
+    if (!c.wr && !c.bt && c.wide && W->type == HQ_TYPE_Q4_K && !(c.ws_nb && c.ws_parts > 1) && hq_wr_fits(W, M)) {
+        const WrPlan pl = wr4_plan(M, (int)W->rows, n_cu);
+        if (pl.fill) c.wr = c.wr_multi = true, c.wr_tw = pl.tw, c.ws_nb = 0;
     }
     // Q8_0 with M > 64: the Q8_0 tile kernel when its tiles fill at least half of the CU time
     // (rounds of tiles included; M = 128, N = 9728: 152 tiles of 128 x 64, 21.7 us against 24.9 for
@@ -1528,6 +1557,13 @@ hipError_t hq_launch_gemm_main(const hq_dev_mat *W, const uint16_t *A, int M, vo
     if (c.rbm) return hq_launch_gemm_rb(W, A, M, C, c_f32, accumulate, c.rbm, wk.partials, wk.counters, st);
     if (c.rb8) return hq_launch_gemm_rb8(W, A, M, C, c_f32, accumulate, c.rb8, wk.partials, wk.counters, st);
     if (c.bt) return hq_launch_gemm_bt(W, A, wk.sums, M, C, c_f32, accumulate, st);
+    if (c.wr && c.wr_multi) {
+        const size_t K = W->cols, N = W->rows, esize = c_f32 ? 4 : 2;
+        return wr_launches(wr4_plan(M, (int)N, wk.n_cu), M, (int)N, [&](int m0, int rows, int t0, int t1) {
+            return hq_launch_gemm_wr(W, A + (size_t)m0 * K, rows, (char *)C + (size_t)m0 * N * esize, c_f32, accumulate, t0, t1, 1,
+                                     nullptr, nullptr, st, c.wr_tw);
+        });
+    }
     if (c.wr) return hq_launch_gemm_wr(W, A, M, C, c_f32, accumulate, 0, -1, c.wr_parts, wk.partials, wk.counters, st, c.wr_tw);
     if (c.wr8) {
         const size_t K = W->cols, N = W->rows, esize = c_f32 ? 4 : 2;
@@ -1584,18 +1620,15 @@ hipError_t hq_launch_gemm_swiglu(const hq_dev_mat *W, const uint16_t *A, int M, 
     // The Q4_K kernel takes 160-column tiles where they need no more launches than 192-column ones
     // (M = 512, I = 9728: two launches of 4 x 122 / 2 tiles, 244 of 256 CUs, instead of 204)
     const bool wr8 = W->type == HQ_TYPE_Q8_0 && hq_wr8_fits(W, M), wr4 = W->type == HQ_TYPE_Q4_K && W->tab && hq_wr_fits(W, M);
-    WrPlan pl = wr_plan(M, N, wk.n_cu);
-    if (wr4) {
-        const WrPlan p160 = wr_plan(M, N, wk.n_cu, 160);
-        if (p160.fill && p160.launches <= pl.launches) pl = p160;
-    }
-    // and as one launch where its tiles make two rounds on every XCD, the second at least 60 % full
-    // (M = 512, I = 9728: one launch of 4 x 122 tiles instead of two of 2 x 122; Q4_K 68.5 -> 67.4 us,
-    // Q8_0 63.8 -> 62.9 in a same-box A/B)
-    if (pl.fill && (wr8 || wr4)) {
+    // (wr4_plan; the Q8_0 kernel takes the same plan with 192-column tiles only: one launch of two
+    // rounds, 63.8 -> 62.9 us at M = 512, I = 9728)
+    WrPlan pl = wr4 ? wr4_plan(M, N, wk.n_cu) : wr_plan(M, N, wk.n_cu);
+    if (wr8 && pl.fill) {
         const int mt = (M + 127) / 128, nt = (N + pl.tw - 1) / pl.tw, per_xcd = std::max(1, wk.n_cu / 8);
         const int on_xcd = mt * ((nt + 7) / 8);
         if (on_xcd > per_xcd && on_xcd <= 2 * per_xcd && 5 * on_xcd >= 8 * per_xcd) pl.row_tiles = mt, pl.col_tiles = nt, pl.launches = 1;
+    }
+    if (pl.fill && (wr8 || wr4)) {
         *fused = 1;
         return wr_launches(pl, M, N, [&](int m0, int rows, int t0, int t1) {
             const uint16_t *Am = A + (size_t)m0 * K;

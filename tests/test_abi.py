@@ -86,8 +86,11 @@ def test_gemm_workspace_bytes():
     # over 4 workgroups, no sub-block sums)
     pb, cb, sb, fits = hq.gemm_workspace_bytes(synth.Q4_K, 512, 2560, 9728)
     assert (pb, cb, sb, fits) == (64 * 4 * 128 * 160 * 4, 64 * 4, 0, True)
-    pb, cb, sb, fits = hq.gemm_workspace_bytes(synth.Q4_K, 4096, 2560, 9728)
-    assert (pb, cb, fits) == (2 * 256 * 128 * 256 * 4, 32 * 10 * 4, True)
+    # (M = 4095, N = 32: the Stream-K kernel, 4096 / 128 x 1 tiles; M = 4096, N = 2560, K = 9728: the
+    # register-decode kernel as launches of one round each, no workspace)
+    pb, cb, sb, fits = hq.gemm_workspace_bytes(synth.Q4_K, 4095, 32, 2560)
+    assert (pb, cb, fits) == (2 * 256 * 128 * 256 * 4, 32 * 4, True)
+    assert hq.gemm_workspace_bytes(synth.Q4_K, 4096, 2560, 9728) == (0, 0, 0, True)
     assert hq.gemm_workspace_bytes(synth.Q4_K, 4096, 9728, 2560) == (0, 0, 4096 * 10 * 32, True)
     # the 128 x 192 loader-wave kernel (M = 512, N = 9728): one round of tiles; its loader waves form
     # the sub-block sums in LDS, so no workspace at all
@@ -118,13 +121,14 @@ def test_gemm_kernel_names():
              (synth.Q6_K, 96, 9728, 2560): "k_gemm_kq_ws<14, 3>", (synth.Q4_K, 128, 9728, 2560): "k_gemm_q4_k_ws<3>",
              (synth.Q4_K, 200, 9728, 2560): "k_gemm_q4_k_wr_ks160", (synth.Q5_K, 96, 9728, 2560): "k_gemm_q5_k_ws<3>",
              (synth.Q4_K, 4096, 9728, 2560): "k_gemm_q4_k_bt", (synth.Q4_K, 16384, 2560, 9216): "k_gemm_q4_k_bt",
-             (synth.Q4_K, 16384, 1024, 2560): "k_gemm_q4_k_bt", (synth.Q4_K, 2048, 9728, 2560): "k_gemm_q4_k_w<8>",
+             (synth.Q4_K, 16384, 1024, 2560): "k_gemm_q4_k_bt", (synth.Q4_K, 2048, 9728, 2560): "k_gemm_q4_k_wr160",
              (synth.Q4_K, 64, 9728, 2560): "k_gemm_q4_k_rb<1, 4, 3, 2>",
              (synth.Q4_K, 64, 2560, 9728): "k_gemm_q4_k_rb<1, 4, 3, 2>", (synth.Q4_K, 64, 1024, 2560): "k_gemm_q4_k<4, 2>", (synth.Q4_K, 32, 9728, 2560): "k_gemm_q4_k<2, 2>",
              (synth.Q4_K, 64, 9728, 2304): "k_gemm_q4_k<4, 2>",
              (synth.Q4_K, 512, 2560, 9728): "k_gemm_q4_k_wr_ks160",
              (synth.Q4_K, 100, 10996, 5120): "k_gemm_q4_k_wr_ks<3>", (synth.Q4_K, 256, 2560, 9728): "k_gemm_q4_k_ws<3>",
-             (synth.Q4_K, 512, 1024, 2560): "k_gemm_q4_k_w<8>", (synth.Q4_K, 4096, 2560, 9728): "k_gemm_q4_k_w<8>",
+             (synth.Q4_K, 512, 1024, 2560): "k_gemm_q4_k_w<8>", (synth.Q4_K, 4096, 2560, 9728): "k_gemm_q4_k_wr160",
+             (synth.Q4_K, 512, 19456, 2560): "k_gemm_q4_k_wr160", (synth.Q4_K, 1536, 9728, 2560): "k_gemm_q4_k_bt",
              (synth.Q8_0, 512, 2560, 9728): "k_gemm_q8_0_ws<5>", (synth.Q8_0, 256, 2560, 9728): "k_gemm_q8_0_ws<3>",
              (synth.Q8_0, 16, 9728, 2560): "k_gemm_q8_0_rb<1, 3, 2>", (synth.Q8_0, 64, 9728, 2560): "k_gemm_q8_0_rb<4, 3, 2>",
              (synth.Q8_0, 16, 2560, 9728): "k_gemm_q8_0_rb<1, 3, 2>", (synth.Q8_0, 16, 1024, 1024): "k_gemm_q8_0<1, 2>", (synth.Q4_K, 1, 9728, 2560): "k_gemv_q4_k_r<4>",
@@ -160,9 +164,10 @@ def test_gemm_tile_selection():
             assert r in (16, 32, 64, 128, 256)
             assert r >= min(M, 128)
             if gtype == synth.Q4_K and M > 64:
-                # Q4_K above M = 64: full-K tiles of 128 x 32NB when they fill the CUs (128 x 192 with
-                # loader waves when one round of them does), 256 x 256 full-K tiles at large M when
-                # their rounds fill the CUs, else the 8-wave Stream-K kernel (128 x 256)
+                # Q4_K above M = 64: full-K tiles of 128 x 32NB when they fill the CUs (128 x 192 or
+                # 128 x 160 with loader waves when one round of them does, or launches of one round
+                # each do), 256 x 256 full-K tiles at large M when their rounds fill the CUs, else the
+                # 8-wave Stream-K kernel (128 x 256)
                 assert (r, c) in ((128, 256), (256, 256), (128, 192)) or (r == 128 and c in (64, 96, 128, 160))
             elif gtype == synth.Q8_0 and M > 64:
                 # Q8_0 above M = 64: full-K tiles of 128 x 32NB when they fill >= 50 % of the CU
@@ -185,11 +190,13 @@ def test_gemm_tile_selection():
     assert hq.gemm_tiles(synth.Q8_0, 2048, 9728) == (128, 192)
     assert hq.gemm_tiles(synth.Q8_0, 256, 9728) == (128, 96)
     assert hq.gemm_tiles(synth.Q4_K, 65, 9728) == (128, 256)
-    # full-K tiles: 4 x 61 tiles of 128 x 160 on 256 CUs; more tiles than CUs: Stream-K, or at large
-    # M the 256 x 256 tiles when their rounds fill >= 3/4 of the CU time (M = 4096: 608 tiles in 3
-    # rounds; M = 2048: 304 tiles in 2 rounds, 59 %)
+    # full-K tiles: 4 x 61 tiles of 128 x 160 on 256 CUs; more tiles than CUs: at large M the 256 x 256
+    # tiles when their rounds fill >= 3/4 of the CU time (M = 4096: 608 tiles in 3 rounds), else the
+    # 128 x 160 tiles as launches of one round each (M = 2048: 16 x 61 in 4 launches; the 256 x 256
+    # tiles would make 304 tiles in 2 rounds, 59 %), Stream-K where those fill < 70 % of the CU time
     assert hq.gemm_tiles(synth.Q4_K, 512, 9728) == (128, 160)  # k_gemm_q4_k_wr160: 244 tiles in one round
-    assert hq.gemm_tiles(synth.Q4_K, 2048, 9728) == (128, 256)
+    assert hq.gemm_tiles(synth.Q4_K, 2048, 9728) == (128, 160)
+    assert hq.gemm_tiles(synth.Q4_K, 512, 1024) == (128, 256)
     assert hq.gemm_tiles(synth.Q4_K, 4096, 9728) == (256, 256)
 
 

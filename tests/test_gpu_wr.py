@@ -8,7 +8,8 @@ N = 9672 (60 whole 160-column tiles and a ragged one of 72: wave 0's and wave 1'
 wave 2's first half valid, the rest and both half blocks past N) or 9674 (N not a multiple of 4: the
 element-wise store path); N = 13000 / 12996 for the 192-column kernel (67 whole tiles and a ragged one
 of 136 / 132 columns); K = 256 (one super-block: no rescale between super-blocks), 512, 1024, 2560
-and 4096 (the record ring of three slots wraps). The per-super-block column tables come from the
+and 4096 (the record ring of three slots wraps); more tiles than one round as launches of one round
+each, or one launch of two rounds (test_wr_launches). The per-super-block column tables come from the
 upload (k_q4k_tables), so every test also checks them. Bars as in test_gpu_parity.py: rel-L2 <= 1e-3
 and max-abs <= 2e-3 (Q4_K); against the float64 product, 2^-13 |W| @ |a| per output.
 """
@@ -83,6 +84,23 @@ def test_wr_accumulate_and_fp16_output(hqlib, oracle, M, N, K):
     acc16 = acc16.view(np.float16).astype(np.float32)
     want = plain + c16.view(np.float16).astype(np.float32)[rows]
     assert np.all(np.abs(acc16[rows] - want) <= 1e-2 + np.abs(want) * 2.0 ** -11)
+
+
+# more tiles than one round (wr4_plan): M = 1100 at N = 9672 as three launches of 4 row tiles (the
+# last 76 rows) x 61 column tiles (the last ragged); M = 512, N = 19448 as one launch of two rounds
+# (4 x 122 tiles, the last column tile ragged); M = 4096, N = 2560 as two launches of 16 x 16 tiles.
+# Rows sampled for the oracle; fp32 output, then fp16 through the same launches.
+@pytest.mark.parametrize("M,N,K", [(1100, 9672, 1024), (512, 19448, 1024), (4096, 2560, 1024)])
+def test_wr_launches(hqlib, oracle, M, N, K):
+    blocks = synth.random_blocks(synth.Q4_K, synth.Rng(201 + M), N, K)
+    a = synth.activations_f16(synth.Rng(202 + N), M, K)
+    rows = sample_rows(M)
+    ref = oracle.matmul(blocks, synth.Q4_K, N, K, oracle.f16_to_f32(a[rows]))
+    got = run(hqlib, blocks, a, N, K, "wr launches")
+    check(got[rows], ref, f"wr launches M={M} N={N}")
+    assert np.all(np.isfinite(got))
+    got16 = run(hqlib, blocks, a, N, K, "wr launches fp16 out", c_f32=False).view(np.float16).astype(np.float32)
+    assert np.all(np.abs(got16[rows] - ref) <= 1e-2 + np.abs(ref) * 2.0 ** -11)
 
 
 def test_wr_positive_activations(hqlib, oracle):
