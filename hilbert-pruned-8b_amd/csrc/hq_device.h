@@ -277,6 +277,32 @@ DEV void tile_store_rows(const char *lds, char *Ct, int rows, uint32_t pitch, ui
     }
 }
 
+// Output values n .. n + 7 of row m (n < N) of C [rows][N] (fp32 or fp16, plain or added to):
+// one 16-byte (fp16) or two (fp32) stores where the row holds all 8 and C allows it (wide), else
+// element by element.
+DEV void store8_out(void *C, int N, int m, int n, f4 v0, f4 v1, bool wide, int c_f32, int accumulate) {
+    const size_t idx = (size_t)m * N + n;
+    if (wide && n + 8 <= N) {
+        if (c_f32) {
+            f4 *q = (f4 *)((float *)C + idx);
+            q[0] = accumulate ? q[0] + v0 : v0;
+            q[1] = accumulate ? q[1] + v1 : v1;
+        } else {
+            h8 *q = (h8 *)((_Float16 *)C + idx);
+            if (accumulate) {
+                const h8 o = *q;
+                v0 += f4{(float)o[0], (float)o[1], (float)o[2], (float)o[3]};
+                v1 += f4{(float)o[4], (float)o[5], (float)o[6], (float)o[7]};
+            }
+            *q = h8{(_Float16)v0.x, (_Float16)v0.y, (_Float16)v0.z, (_Float16)v0.w,
+                    (_Float16)v1.x, (_Float16)v1.y, (_Float16)v1.z, (_Float16)v1.w};
+        }
+    } else {
+        const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        for (int e = 0; e < 8 && n + e < N; e++) store_out(C, idx + e, v[e], c_f32, accumulate);
+    }
+}
+
 // End of a full-K tile kernel's tile, held in LDS as fp32 rows of LD floats (BM x BN, NT threads).
 // parts == 1: stored to C. parts > 1 (a K split, at most MAXP parts): every part stores its tile to
 // partials[tile][part] with device-scope (sc1) 16-byte stores, waits for them and counts itself in
@@ -305,6 +331,7 @@ DEV void tile_finish(const char *lds, const Args &g, int m0, int n0, int tile, i
             buf_store16(rp, *(const f4 *)(lds + (row * LD + 8 * ch) * 4), own + off);
             buf_store16(rp, *(const f4 *)(lds + (row * LD + 8 * ch + 4) * 4), own + off + NCH * 16u);
         }
+        if (!g.counters) return;  // parts stored only: a kernel of its own adds them (k_tile_reduce)
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (threadIdx.x == 0) {
@@ -373,26 +400,7 @@ DEV void tile_finish(const char *lds, const Args &g, int m0, int n0, int tile, i
             v1 = *(const f4 *)(lds + (row * LD + 8 * ch + 4) * 4);
         }
         if (m >= M || n >= N) continue;
-        const size_t idx = (size_t)m * N + n;
-        if (wide && n + 8 <= N) {
-            if (g.c_f32) {
-                f4 *q = (f4 *)((float *)g.C + idx);
-                q[0] = g.accumulate ? q[0] + v0 : v0;
-                q[1] = g.accumulate ? q[1] + v1 : v1;
-            } else {
-                h8 *q = (h8 *)((_Float16 *)g.C + idx);
-                if (g.accumulate) {
-                    const h8 o = *q;
-                    v0 += f4{(float)o[0], (float)o[1], (float)o[2], (float)o[3]};
-                    v1 += f4{(float)o[4], (float)o[5], (float)o[6], (float)o[7]};
-                }
-                *q = h8{(_Float16)v0.x, (_Float16)v0.y, (_Float16)v0.z, (_Float16)v0.w,
-                        (_Float16)v1.x, (_Float16)v1.y, (_Float16)v1.z, (_Float16)v1.w};
-            }
-        } else {
-            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-            for (int e = 0; e < 8 && n + e < N; e++) store_out(g.C, idx + e, v[e], g.c_f32, g.accumulate);
-        }
+        store8_out(g.C, N, m, n, v0, v1, wide, g.c_f32, g.accumulate);
     }
 }
 

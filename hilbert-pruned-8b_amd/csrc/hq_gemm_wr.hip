@@ -679,6 +679,32 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr_ks160(WrArgs g) { wr_til
 // super-block (F = 1). The GEMM accumulates super-block v in units of c_v, rescales by F after it and
 // adds its min term in the next units (the last super-block's in its own; -dmin * m_i is exact in
 // fp32).
+// The K split's sum: the parts' tiles (tile_finish's layout: 16-byte piece h of 8-value chunk c of
+// tile t, part p at ((t parts + p) TILE) + (h NCH + c) 16 bytes) added in part order, as tile_finish's
+// last part would, by one thread per chunk over all CUs, then stored to C
+template <int BN>
+__global__ void __launch_bounds__(256) k_tile_reduce(const float *__restrict__ partials, int parts, int ntiles, int mt,
+                                                     int M, int N, void *C, int c_f32, int accumulate) {
+    constexpr int CH = BN / 8, NCH = WR_BM * CH;
+    constexpr size_t TILE = (size_t)WR_BM * BN * 4;
+    const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+    if (t >= (uint32_t)ntiles * (uint32_t)NCH) return;
+    const int tile = (int)(t / NCH), c = (int)(t - (uint32_t)tile * NCH), row = c / CH, ch = c - row * CH;
+    const int nt_i = tile / mt, mt_i = tile - nt_i * mt, m = mt_i * WR_BM + row, n = nt_i * BN + 8 * ch;
+    if (m >= M || n >= N) return;
+    const char *base = (const char *)partials + (size_t)tile * parts * TILE + (size_t)c * 16;
+    f4 pv[4][2];
+#pragma unroll
+    for (int p = 0; p < 4; p++)
+        if (p < parts) pv[p][0] = *(const f4 *)(base + p * TILE), pv[p][1] = *(const f4 *)(base + p * TILE + NCH * 16);
+    f4 v0 = f4{0.f, 0.f, 0.f, 0.f}, v1 = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < 4; p++)
+        if (p < parts) v0 += pv[p][0], v1 += pv[p][1];
+    const bool wide = (N & 7) == 0 && ((uintptr_t)C & 15u) == 0;
+    store8_out(C, N, m, n, v0, v1, wide, c_f32, accumulate);
+}
+
 __global__ void __launch_bounds__(256) k_q4k_tables(const uint8_t *W, uint32_t rows, uint32_t nb, uint32_t row_bytes,
                                                     uint8_t *tab) {
     const uint32_t n = blockIdx.x * 256u + threadIdx.x;
@@ -751,8 +777,15 @@ hipError_t hq_launch_gemm_wr(const hq_dev_mat *W, const uint16_t *A, int M, void
     // fp32 or fp16 C, or the SwiGLU output of a gate/up pair matrix (N a multiple of 16, no accumulate)
     if (c_f32 != 0 && c_f32 != 1 && !(c_f32 == HQ_OUT_SWIGLU && W->rows % 16 == 0 && !accumulate)) return hipErrorInvalidValue;
     const unsigned grid = (unsigned)(8 * (((g.nt - g.nt0) * parts + 7) / 8) * g.mt);
-    if (parts > 1 && tw == 160) k_gemm_q4_k_wr_ks160<<<grid, WR_NT, 0, st>>>(g);
-    else if (parts > 1) k_gemm_q4_k_wr_ks<NB><<<grid, WR_NT, 0, st>>>(g);
+    if (parts > 1) {
+        // every part stores its tile; k_tile_reduce adds them
+        g.counters = nullptr;
+        if (tw == 160) k_gemm_q4_k_wr_ks160<<<grid, WR_NT, 0, st>>>(g);
+        else k_gemm_q4_k_wr_ks<NB><<<grid, WR_NT, 0, st>>>(g);
+        const unsigned rgrid = (unsigned)(((size_t)g.ntiles * WR_BM * (tw / 8) + 255) / 256);
+        if (tw == 160) k_tile_reduce<160><<<rgrid, 256, 0, st>>>(partials, parts, g.ntiles, g.mt, M, g.N, C, c_f32, accumulate);
+        else k_tile_reduce<192><<<rgrid, 256, 0, st>>>(partials, parts, g.ntiles, g.mt, M, g.N, C, c_f32, accumulate);
+    }
     else if (tw == 160) k_gemm_q4_k_wr160<<<grid, WR_NT, 0, st>>>(g);
     else k_gemm_q4_k_wr<NB><<<grid, WR_NT, 0, st>>>(g);
     return hipGetLastError();
