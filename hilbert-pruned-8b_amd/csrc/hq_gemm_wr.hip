@@ -672,13 +672,7 @@ __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr_ks(WrArgs g) {
 __global__ void __launch_bounds__(WR_NT) k_gemm_q4_k_wr_ks160(WrArgs g) { wr_tile<true, 160>(g); }
 }  // namespace
 
-// Per-column tables of every super-block of a Q4_K matrix (one thread per row, super-blocks in order):
-// for super-block v, Bmin [rows][32 B] = bf16 hi[8], lo[8] of x_i = -dmin * m_i / c_{v+1} at
-// v * rows * 48, then records [rows][16 B] = scale words sw0, sw1 (zero where d = 0),
-// F = c_v / c_{v+1}, CN = c_{v+1}; c_v = d_v, or 1 where d_v = 0, and c_{v+1} reads c_v for the last
-// super-block (F = 1). The GEMM accumulates super-block v in units of c_v, rescales by F after it and
-// adds its min term in the next units (the last super-block's in its own; -dmin * m_i is exact in
-// fp32).
+namespace {
 // The K split's sum: the parts' tiles (tile_finish's layout: 16-byte piece h of 8-value chunk c of
 // tile t, part p at ((t parts + p) TILE) + (h NCH + c) 16 bytes) added in part order, as tile_finish's
 // last part would, by one thread per chunk over all CUs, then stored to C
@@ -704,7 +698,29 @@ __global__ void __launch_bounds__(256) k_tile_reduce(const float *__restrict__ p
     const bool wide = (N & 7) == 0 && ((uintptr_t)C & 15u) == 0;
     store8_out(C, N, m, n, v0, v1, wide, c_f32, accumulate);
 }
+}  // namespace
 
+// the launch of k_tile_reduce for the register-decode kernel's tile widths (160, 192). (The LDS-decode
+// tile kernels keep the last-part sum of tile_finish: their parts of a tile share one XCD's L2, and a
+// separate sum measured slower there, e.g. Q8_0 M = 128, N = 9728, two parts: 19.2 -> 20.3 us.)
+hipError_t hq_launch_tile_reduce(const float *partials, int parts, int ntiles, int mt, int bn, int M, int N, void *C, int c_f32,
+                                 int accumulate, hipStream_t st) {
+    if (parts < 2 || parts > 4 || mt < 1 || ntiles < 1) return hipErrorInvalidValue;
+    const unsigned grid = (unsigned)(((size_t)ntiles * WR_BM * (bn / 8) + 255) / 256);
+    if (bn == 160) k_tile_reduce<160><<<grid, 256, 0, st>>>(partials, parts, ntiles, mt, M, N, C, c_f32, accumulate);
+    else if (bn == 192) k_tile_reduce<192><<<grid, 256, 0, st>>>(partials, parts, ntiles, mt, M, N, C, c_f32, accumulate);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+
+// Per-column tables of every super-block of a Q4_K matrix (one thread per row, super-blocks in order):
+// for super-block v, Bmin [rows][32 B] = bf16 hi[8], lo[8] of x_i = -dmin * m_i / c_{v+1} at
+// v * rows * 48, then records [rows][16 B] = scale words sw0, sw1 (zero where d = 0),
+// F = c_v / c_{v+1}, CN = c_{v+1}; c_v = d_v, or 1 where d_v = 0, and c_{v+1} reads c_v for the last
+// super-block (F = 1). The GEMM accumulates super-block v in units of c_v, rescales by F after it and
+// adds its min term in the next units (the last super-block's in its own; -dmin * m_i is exact in
+// fp32).
 __global__ void __launch_bounds__(256) k_q4k_tables(const uint8_t *W, uint32_t rows, uint32_t nb, uint32_t row_bytes,
                                                     uint8_t *tab) {
     const uint32_t n = blockIdx.x * 256u + threadIdx.x;
@@ -782,9 +798,7 @@ hipError_t hq_launch_gemm_wr(const hq_dev_mat *W, const uint16_t *A, int M, void
         g.counters = nullptr;
         if (tw == 160) k_gemm_q4_k_wr_ks160<<<grid, WR_NT, 0, st>>>(g);
         else k_gemm_q4_k_wr_ks<NB><<<grid, WR_NT, 0, st>>>(g);
-        const unsigned rgrid = (unsigned)(((size_t)g.ntiles * WR_BM * (tw / 8) + 255) / 256);
-        if (tw == 160) k_tile_reduce<160><<<rgrid, 256, 0, st>>>(partials, parts, g.ntiles, g.mt, M, g.N, C, c_f32, accumulate);
-        else k_tile_reduce<192><<<rgrid, 256, 0, st>>>(partials, parts, g.ntiles, g.mt, M, g.N, C, c_f32, accumulate);
+        return hq_launch_tile_reduce(partials, parts, g.ntiles, g.mt, tw, M, g.N, C, c_f32, accumulate, st);
     }
     else if (tw == 160) k_gemm_q4_k_wr160<<<grid, WR_NT, 0, st>>>(g);
     else k_gemm_q4_k_wr<NB><<<grid, WR_NT, 0, st>>>(g);

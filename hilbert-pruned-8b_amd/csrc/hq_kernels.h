@@ -86,6 +86,10 @@ hipError_t hq_launch_gemm_bt(const hq_dev_mat *W, const uint16_t *A, const uint1
 // tiles nt0 .. nt1 - 1 (nt1 < 0: to the last); the Q4_K one also with each tile's K split over
 // `parts` workgroups (partials / counters as for the other K splits).
 int hq_wr_fits(const hq_dev_mat *W, int M);
+// The sum of a K split's part tiles (128-row tiles of bn = 160 or 192 columns in tile_finish's layout,
+// stored by every part of a kernel launched with no counters), added in part order and stored to C.
+hipError_t hq_launch_tile_reduce(const float *partials, int parts, int ntiles, int mt, int bn, int M, int N, void *C, int c_f32,
+                                 int accumulate, hipStream_t st);
 hipError_t hq_launch_gemm_wr(const hq_dev_mat *W, const uint16_t *A, int M, void *C, int c_f32, int accumulate,
                              int nt0, int nt1, int parts, float *partials, int *counters, hipStream_t st, int tw = 192);
 // The same tile shape for Q8_0 (hq_gemm_wr8.hip; K a multiple of 256, no workspace).
